@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Benchmark of the causal-MHA hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A *step* is one fused causal-attention forward + backward over the whole batch
+of config C3 (B=8, H=16, T=2048, D=64, bf16 Q/K/V,
+fp32 accumulation, LSE and gradients), the configuration the north star's
+throughput target is quoted on.  Inputs are synthetic (seeded N(0,1)*0.5,
+rounded to bf16) and resident in HBM before timing starts.
+
+value = algorithmic causal FLOPs (7*B*H*T^2*D per fwd+bwd) / step time, in
+TFLOP/s.  The same JSON line carries:
+  roofline      -- the dominant kernel: its algorithmic FLOPs per launch over
+                   its average launch time (HIP events on the launch stream)
+                   against the 2516.6 TFLOP/s dense-bf16 MFMA peak;
+  cpu_baseline  -- the NumPy restatement of the reference (oracle/, the
+                   reference's own NumPy semantics) timed on this host on a
+                   bounded sample of (b,h) slices of the same workload;
+  also          -- config C1 (fp32, B=32,H=8,T=256,D=64) on the same kernels,
+                   and per-phase timings.
+Only one GPU is used: --gpus > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+PEAK_BF16 = 2516.6  # TFLOP/s, dense bf16 MFMA, MI355X
+PEAK_FP32 = 157.3   # TFLOP/s, fp32 MFMA
+PEAK_HBM = 8000.0   # GB/s
+
+
+def attn_flops(B, H, T, D):
+    """Algorithmic causal FLOPs: fwd 2*B*H*T^2*D, bwd 5*B*H*T^2*D."""
+    u = B * H * T * T * D
+    return 2 * u, 5 * u
+
+
+def _events():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_loop(fn, steps, warmup):
+    """Average ms per call of fn() over `steps` calls after `warmup` calls,
+    bracketed by device synchronisation and HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def make_inputs(B, H, T, D, dtype, seed, scale_qkv):
+    """Seeded inputs, drawn q, k, v, dO in that order; bf16 rounding (RNE) by
+    the device cast.  Returns (host fp32 copies of the device values, device
+    tensors)."""
+    import torch
+
+    rng = np.random.default_rng(seed)
+    shp = (B, H, T, D)
+    arrs = [scale_qkv * rng.standard_normal(shp, dtype=np.float32) for _ in range(3)]
+    arrs.append(rng.standard_normal(shp, dtype=np.float32))
+    dev = [torch.from_numpy(a).to("cuda").to(dtype) for a in arrs]
+    host = [t.float().cpu().numpy() for t in dev]
+    return host, dev
+
+
+def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup):
+    import torch
+    from minitorch_amd import _lib as L
+    from minitorch_amd import kernels as K
+
+    arrs, (q, k, v, do) = make_inputs(B, H, T, D, dtype, seed, scale_qkv)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = K.attn_fwd(q, k, v, scale, True)
+    dq, dk, dv = K.attn_bwd(q, k, v, o, do, lse, scale, True)
+    ws = torch.empty(L.lib().mtx_attn_bwd_workspace_bytes(B, H, T), dtype=torch.uint8, device="cuda")
+
+    def step():
+        K.attn_fwd(q, k, v, scale, True, out=o, lse=lse)
+        K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk, dv=dv, workspace=ws)
+
+    ms_step = time_loop(step, steps, warmup)
+    # per-kernel averages (each phase is one kernel launch)
+    ms_fwd = time_loop(lambda: K.attn_fwd(q, k, v, scale, True, out=o, lse=lse), steps, 2)
+    ph = {}
+    for name, mask in (("delta", L.ATTN_BWD_DELTA), ("dkdv", L.ATTN_BWD_DKDV), ("dq", L.ATTN_BWD_DQ)):
+        ph[name] = time_loop(lambda m=mask: K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk,
+                                                       dv=dv, workspace=ws, phases=m), steps, 2)
+    torch.cuda.synchronize()
+    return dict(ms_step=ms_step, ms_fwd=ms_fwd, **{f"ms_{k}": v for k, v in ph.items()}), arrs
+
+
+def cpu_baseline_attention(arrs, T, D, budget_s=15.0):
+    """Time the NumPy restatement of the reference sub-graph (fwd + autograd
+    bwd, transformer.py:36-44 with its float64 promotion) over successive
+    (b,h) slices of the same inputs until `budget_s` seconds are spent."""
+    from oracle.attention import reference_attention
+
+    q, k, v, do = arrs
+    B, H = q.shape[:2]
+    slices = [(b, h) for b in range(B) for h in range(H)]
+    done = 0
+    t0 = time.perf_counter()
+    for b, h in slices:
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        reference_attention(q[sl], k[sl], v[sl], do[sl], 1.0 / math.sqrt(D), True)
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    f, bwd = attn_flops(1, done, T, D)
+    return (f + bwd) / dt / 1e12, done, dt
+
+
+def blas_threads():
+    for var in ("OPENBLAS_NUM_THREADS", "OMP_NUM_THREADS", "MKL_NUM_THREADS"):
+        if os.environ.get(var):
+            return int(os.environ[var])
+    try:
+        return len(os.sched_getaffinity(0))
+    except Exception:
+        return os.cpu_count() or 1
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(attention shards by (b,h) with no exchange; see DESIGN.md). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    # ---- C3: headline ----
+    B, H, T, D = 8, 16, 2048, 64
+    print(f"[bench] C3 bf16 B={B} H={H} T={T} D={D}: {args.warmup} warmup + {args.steps} steps",
+          file=sys.stderr, flush=True)
+    r3, arrs3 = bench_attention(B, H, T, D, torch.bfloat16, 3, 0.5, args.steps, args.warmup)
+    f3, b3 = attn_flops(B, H, T, D)
+    tflops = (f3 + b3) / (r3["ms_step"] * 1e-3) / 1e12
+    # dominant kernel and its algorithmic FLOPs: fwd kernel = 2u; dK/dV pass =
+    # S, dP, dV, dK = 4u; dQ pass = the dQ product only (its S/dP recompute is
+    # already counted in the dK/dV pass) = 1u; delta pass = none (HBM-bound).
+    u = B * H * T * T * D
+    kern = {"attn_fwd": (r3["ms_fwd"], 2 * u), "attn_dkdv": (r3["ms_dkdv"], 4 * u),
+            "attn_dq": (r3["ms_dq"], 1 * u)}
+    dom = max(kern, key=lambda k_: kern[k_][0])
+    ms_dom, fl_dom = kern[dom]
+    achieved = fl_dom / (ms_dom * 1e-3) / 1e12
+    print(f"[bench] C3 step {r3['ms_step']:.3f} ms = {tflops:.1f} TFLOP/s; phases {r3}",
+          file=sys.stderr, flush=True)
+
+    # ---- C1: fp32 ----
+    print("[bench] C1 fp32 B=32 H=8 T=256 D=64", file=sys.stderr, flush=True)
+    r1, _ = bench_attention(32, 8, 256, 64, torch.float32, 1, 1.0, args.steps, args.warmup)
+    f1, b1 = attn_flops(32, 8, 256, 64)
+    tflops1 = (f1 + b1) / (r1["ms_step"] * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu:
+        print(f"[bench] CPU baseline (NumPy restatement, ~{args.cpu_budget:.0f}s)", file=sys.stderr, flush=True)
+        cv, nsl, dt = cpu_baseline_attention(arrs3, T, D, args.cpu_budget)
+        cpu = {"value": round(cv, 6), "unit": "TFLOP/s", "cores": blas_threads(), "kind": "port",
+               "sample": f"{nsl} of {B * H} (b,h) slices of C3 (T=2048, D=64), fwd+bwd through the "
+                         f"NumPy restatement of the reference sub-graph (fp32 q@k^T, fp64 from the "
+                         f"scale on), {dt:.1f}s; TFLOP/s on the algorithmic causal count",
+               "host": platform.processor() or platform.machine(),
+               "numpy": np.__version__}
+
+    line = {
+        "metric": "causal-MHA fwd+bwd TFLOP/s (C3: B=8,H=16,T=2048,D=64 bf16)",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r3["ms_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 q/k/v, N(0,1) dO, rounded to bf16)",
+        "config": {"workload": "C3 causal MHA fwd+bwd", "B": B, "H": H, "T": T, "D": D,
+                   "causal": True, "parallelism": "none (1 GPU)"},
+        "pct_of_peak": round(100 * tflops / PEAK_BF16, 2),
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4),
+                     "traffic": None, "ms_per_launch": round(ms_dom, 4),
+                     "flops_per_launch": fl_dom},
+        "cpu_baseline": cpu,
+        "also": {
+            "C3_phase_ms": {k_: round(v_, 4) for k_, v_ in r3.items()},
+            "C1_fp32": {"tflops": round(tflops1, 3), "pct_of_fp32_peak": round(100 * tflops1 / PEAK_FP32, 2),
+                        "ms_per_step": round(r1["ms_step"], 4),
+                        "phase_ms": {k_: round(v_, 4) for k_, v_ in r1.items()}},
+        },
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,122 @@
+"""ctypes binding of libmtx_hip.so (the C ABI declared in include/mtx.h).
+
+This module is the only place that touches the shared library.  It loads the
+in-tree build (``minitorch_amd/libmtx_hip.so``), declares every exported
+signature, turns non-zero status codes into Python exceptions and converts
+torch device tensors (used purely as device-memory handles) into pointers,
+element strides and the current HIP stream.
+
+There is no fallback: if the library is missing or a call fails, an exception
+is raised.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = _PKG / "libmtx_hip.so"
+
+MTX_OK, MTX_ERR_ARG, MTX_ERR_SHAPE, MTX_ERR_DTYPE, MTX_ERR_HIP = range(5)
+MTX_F32, MTX_BF16 = 0, 1
+ATTN_BWD_DELTA, ATTN_BWD_DKDV, ATTN_BWD_DQ, ATTN_BWD_ALL = 1, 2, 4, 7
+
+_P = C.c_void_p
+_I = C.c_int
+_I64P = C.POINTER(C.c_int64)
+_F = C.c_float
+_SZ = C.c_size_t
+
+# name -> (restype, argtypes); mirrors include/mtx.h
+SIGNATURES = {
+    "mtx_last_error": (C.c_char_p, []),
+    "mtx_version": (C.c_char_p, []),
+    "mtx_attn_fwd": (_I, [_I, _I, _I, _I, _I, _I,
+                          _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
+                          _P, _F, _I, _P]),
+    "mtx_attn_bwd_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "mtx_attn_bwd": (_I, [_I, _I, _I, _I, _I, _I,
+                          _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
+                          _P,
+                          _P, _I64P, _P, _I64P, _P, _I64P,
+                          _P, _SZ, _F, _I, _I, _P]),
+    "mtx_attn_bwd_phase": (_I, [_I, _I, _I, _I, _I, _I, _I,
+                                _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
+                                _P,
+                                _P, _I64P, _P, _I64P, _P, _I64P,
+                                _P, _SZ, _F, _I, _I, _P]),
+}
+
+
+class MtxError(RuntimeError):
+    """A libmtx_hip call returned a non-zero status."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed (status {code}): {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def lib():
+    """Load (once) and return the CDLL with all signatures declared."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `python -m minitorch_amd.build` "
+                "(minitorch_amd has no CPU fallback)")
+        handle = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def exported_symbols():
+    return list(SIGNATURES)
+
+
+def check(fn_name: str, status: int) -> None:
+    if status != MTX_OK:
+        msg = lib().mtx_last_error().decode(errors="replace")
+        if status in (MTX_ERR_ARG, MTX_ERR_SHAPE, MTX_ERR_DTYPE):
+            raise ValueError(f"{fn_name}: {msg}")
+        raise MtxError(fn_name, status, msg)
+
+
+def call(fn_name: str, *args) -> None:
+    check(fn_name, getattr(lib(), fn_name)(*args))
+
+
+# ---------------------------------------------------------------------------
+# torch plumbing helpers (device memory + streams only)
+# ---------------------------------------------------------------------------
+
+def strides(t) -> C.Array:
+    s = t.stride()
+    return (C.c_int64 * len(s))(*s)
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def stream_handle(device=None):
+    import torch
+
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dtype_code(t) -> int:
+    import torch
+
+    if t.dtype == torch.float32:
+        return MTX_F32
+    if t.dtype == torch.bfloat16:
+        return MTX_BF16
+    raise ValueError(f"unsupported dtype {t.dtype} (float32 or bfloat16)")

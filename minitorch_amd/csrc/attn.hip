@@ -1,0 +1,836 @@
+// Fused causal multi-head attention for gfx950 (MI355X): forward, and a
+// deterministic two-pass backward.
+//
+// Replaces the reference's composed attention sub-graph, transformer.py:36-44
+// (q @ k^T, * 1/sqrt(D), + triu(-1e9), F.softmax, @ v) and the backward
+// closures of those nodes (tensor.py:210-218, 152-156, 115-119;
+// functional.py:69-73).
+//
+// Design (all kernels: 256 threads = 4 wave64s, 16x16 MFMA tiles):
+//  * "Transposed" products.  The forward and the dQ pass compute S^T = K Q^T, so
+//    a lane's accumulator column is one query: lane l owns query l%16 and keys
+//    4*(l/16)+r of each 16-key sub-tile.  Row max / row sum then need only two
+//    xor-shuffles, the O rescale is per lane, and the probabilities are already
+//    in the B-operand layout of O^T += V^T P^T (no LDS round trip for P).
+//  * The dK/dV pass computes S = Q K^T (lane owns a key) so that P and dS feed
+//    dV^T += dO^T P and dK^T += Q^T dS straight from registers, accumulating
+//    dK/dV for the workgroup's key block in registers over all query tiles.
+//  * dQ is a separate query-outer pass (recomputes S and dP) instead of fp32
+//    atomics: deterministic, and no dQ workspace traffic.
+//  * K/V (or Q/dO) tiles are staged through LDS; bf16 tiles that feed a
+//    transposed operand are also written transposed so each lane reads two
+//    8-byte words per MFMA operand.
+//  * Causal: tiles above the diagonal are skipped at workgroup and wave level;
+//    only diagonal tiles pay for the per-element mask.  Blocks are issued
+//    longest-first and all blocks of one (b,h) go to one XCD (workgroup ids are
+//    dealt round-robin over the 8 XCDs), so K/V re-reads hit that XCD's L2.
+#include "mtx_common.h"
+
+#include <cmath>
+
+namespace mtx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+
+struct Str3 {
+  int64_t b, h, t;  // element strides; the d stride is 1
+};
+
+struct FwdArgs {
+  const void* q; Str3 sq;
+  const void* k; Str3 sk;
+  const void* v; Str3 sv;
+  void* o; Str3 so;
+  float* lse;
+  int B, H, Tq, Tk;
+  float scale;
+  int causal;
+};
+
+struct BwdArgs {
+  const void* q; Str3 sq;
+  const void* k; Str3 sk;
+  const void* v; Str3 sv;
+  const void* o; Str3 so;
+  const void* dout; Str3 sdo;
+  const float* lse;
+  float* delta;
+  float* dq; Str3 sdq;
+  float* dk; Str3 sdk;
+  float* dv; Str3 sdv;
+  int B, H, Tq, Tk;
+  float scale;
+  int causal;
+  int accumulate;
+};
+
+// Work mapping: block id -> (tile index, bh).  Blocks of one bh share an XCD
+// (xcd = id % 8) and, for causal, the heaviest tiles are issued first.
+__device__ __forceinline__ void map_block(int bid, int ntile, int BH, bool heavy_last,
+                                          int& tile, int& bh) {
+  int rank;
+  if ((BH & 7) == 0) {
+    const int x = bid & 7, local = bid >> 3, per = BH >> 3;
+    bh = (local % per) * 8 + x;
+    rank = local / per;
+  } else {
+    bh = bid % BH;
+    rank = bid / BH;
+  }
+  tile = heavy_last ? (ntile - 1 - rank) : rank;
+}
+
+// ---------------------------------------------------------------------------
+// LDS tile staging
+// ---------------------------------------------------------------------------
+// Copy rows [r0, r0+R) x [0, D) of a row-strided global slice into LDS.  Rows
+// >= nrows read as zero.  ROW: row-major copy (row stride rld).  TRANS (bf16
+// only): transposed copy, tbuf[d * tld + row].
+template <typename T, int R, int D, bool ROW, bool TRANS>
+__device__ __forceinline__ void stage_tile(T* __restrict__ rowbuf, int rld,
+                                           T* __restrict__ tbuf, int tld,
+                                           const T* __restrict__ g, int64_t ts,
+                                           int r0, int nrows, int tid) {
+  constexpr int V = Elem<T>::kVec;
+  constexpr int CPR = D / V;  // 16-byte chunks per row
+  if constexpr (!TRANS) {
+#pragma unroll
+    for (int c = tid; c < R * CPR; c += kThreads) {
+      const int r = c / CPR, cc = c % CPR;
+      const int row = r0 + r;
+      uint4 val = make_uint4(0u, 0u, 0u, 0u);
+      if (row < nrows) val = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
+      *reinterpret_cast<uint4*>(rowbuf + r * rld + cc * V) = val;
+    }
+  } else {
+    static_assert(sizeof(T) == 2, "transposed staging is for bf16 tiles");
+#pragma unroll
+    for (int c = tid; c < (R / 2) * CPR; c += kThreads) {
+      const int rp = c / CPR, cc = c % CPR;
+      const int row = r0 + 2 * rp;
+      uint4 v0 = make_uint4(0u, 0u, 0u, 0u), v1 = v0;
+      if (row < nrows) v0 = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
+      if (row + 1 < nrows) v1 = *reinterpret_cast<const uint4*>(g + (int64_t)(row + 1) * ts + cc * V);
+      if constexpr (ROW) {
+        *reinterpret_cast<uint4*>(rowbuf + (2 * rp) * rld + cc * V) = v0;
+        *reinterpret_cast<uint4*>(rowbuf + (2 * rp + 1) * rld + cc * V) = v1;
+      }
+      const uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w};
+      const uint32_t b[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = (a[w] & 0xffffu) | (b[w] << 16);
+        const uint32_t hi = (a[w] >> 16) | (b[w] & 0xffff0000u);
+        *reinterpret_cast<uint32_t*>(tbuf + (cc * 8 + 2 * w) * tld + 2 * rp) = lo;
+        *reinterpret_cast<uint32_t*>(tbuf + (cc * 8 + 2 * w + 1) * tld + 2 * rp) = hi;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA operand fragments
+// ---------------------------------------------------------------------------
+// Contraction over the head dim uses the "quarter" k-map: lane group g covers
+// d in [g*D/4, (g+1)*D/4), chunk kc covers KPL consecutive d of that quarter.
+template <typename T, int D>
+struct DMap {
+  static constexpr int QPL = D / 4;
+  static constexpr int KPL = Mfma<T>::KPL;
+  static constexpr int KC = (QPL + KPL - 1) / KPL;
+};
+
+// Fragment of a row stored row-major (in LDS or global): row pointer p.
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::frag dfrag(const T* __restrict__ p, int g, int kc) {
+  constexpr int QPL = D / 4;
+  if constexpr (sizeof(T) == 4) {
+    return p[g * QPL + kc];
+  } else if constexpr (QPL >= 8) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p + g * QPL + 8 * kc);
+    return __builtin_bit_cast(bf16x8, u);
+  } else {  // D == 16: 4 real elements, 4 zeros
+    const uint2 u = *reinterpret_cast<const uint2*>(p + g * QPL);
+    const uint4 w = make_uint4(u.x, u.y, 0u, 0u);
+    return __builtin_bit_cast(bf16x8, w);
+  }
+}
+
+// A operand X^T[d = dcol][j] for k-step s over the j (key or query) dimension,
+// where the matching B operand comes from C-layout accumulators (see pfrag).
+//   fp32: step s covers j = 16*(s/4) + 4g + (s%4): read row-major X[j][dcol].
+//   bf16: step s covers j = 32s + 16*(e/4) + 4g + (e%4): read transposed Xt[dcol][j].
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag tfrag(const T* __restrict__ rowbuf, int rld,
+                                                        const T* __restrict__ tbuf, int tld,
+                                                        int dcol, int g, int s) {
+  if constexpr (sizeof(T) == 4) {
+    return rowbuf[(16 * (s >> 2) + 4 * g + (s & 3)) * rld + dcol];
+  } else {
+    const T* p = tbuf + dcol * tld + 32 * s + 4 * g;
+    const uint2 lo = *reinterpret_cast<const uint2*>(p);
+    const uint2 hi = *reinterpret_cast<const uint2*>(p + 16);
+    return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+  }
+}
+
+// B operand from C-layout accumulators c[j16] (16x16 sub-tiles along j), step s.
+template <typename T, int NJ16>
+__device__ __forceinline__ typename Mfma<T>::frag pfrag(const f32x4 (&c)[NJ16], int s) {
+  if constexpr (sizeof(T) == 4) {
+    return c[s >> 2][s & 3];
+  } else {
+    const f32x4 a = c[2 * s], b = c[2 * s + 1];
+    bf16x8 f;
+    f[0] = (__bf16)a[0]; f[1] = (__bf16)a[1]; f[2] = (__bf16)a[2]; f[3] = (__bf16)a[3];
+    f[4] = (__bf16)b[0]; f[5] = (__bf16)b[1]; f[6] = (__bf16)b[2]; f[7] = (__bf16)b[3];
+    return f;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* __restrict__ p, f32x4 v) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<f32x4*>(p) = v;
+  } else {
+    uint2 u;
+    u.x = pack_bf2(v[0], v[1]);
+    u.y = pack_bf2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(p) = u;
+  }
+}
+
+__device__ __forceinline__ void store_grad4(float* __restrict__ p, f32x4 v, bool acc) {
+  if (acc) {
+    const f32x4 old = *reinterpret_cast<const f32x4*>(p);
+    v += old;
+  }
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <typename T, int D, int NQ>
+__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const FwdArgs a) {
+  using MF = Mfma<T>;
+  using frag = typename MF::frag;
+  using DM = DMap<T, D>;
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int KC = DM::KC;
+  constexpr int DT = D / 16;
+  constexpr int BQ = kWaves * NQ * 16;
+  constexpr int BK = 64;
+  constexpr int NS = BK / MF::KI;             // k-steps of the PV product per tile
+  constexpr int LDR = D + 16 / (int)sizeof(T);  // row-major LDS stride
+  constexpr int LDT = BK + 4;                 // transposed LDS stride (bf16)
+  __shared__ __attribute__((aligned(16))) T Ks[BK * LDR];
+  __shared__ __attribute__((aligned(16))) T Vs[BF ? D * LDT : BK * LDR];
+
+  const int BH = a.B * a.H;
+  const int nqb = (a.Tq + BQ - 1) / BQ;
+  int qb, bh;
+  map_block(blockIdx.x, nqb, BH, a.causal != 0, qb, bh);
+  const int b = bh / a.H, h = bh % a.H;
+  const T* __restrict__ qp = static_cast<const T*>(a.q) + b * a.sq.b + h * a.sq.h;
+  const T* __restrict__ kp = static_cast<const T*>(a.k) + b * a.sk.b + h * a.sk.h;
+  const T* __restrict__ vp = static_cast<const T*>(a.v) + b * a.sv.b + h * a.sv.h;
+  T* __restrict__ op = static_cast<T*>(a.o) + b * a.so.b + h * a.so.h;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int q0 = qb * BQ;
+  const int qw0 = q0 + wid * NQ * 16;
+  const int off = a.Tk - a.Tq;
+  const float c = a.scale * kLog2e;
+
+  // Q fragments (B operand of S^T = K Q^T), straight from global memory
+  frag qf[NQ][KC];
+#pragma unroll
+  for (int qs = 0; qs < NQ; ++qs) {
+    const int row = qw0 + 16 * qs + n;
+    const int rr = row < a.Tq ? row : a.Tq - 1;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      frag f = dfrag<T, D>(qp + (int64_t)rr * a.sq.t, g, kc);
+      if (row >= a.Tq) f = frag{};
+      qf[qs][kc] = f;
+    }
+  }
+
+  f32x4 acc[NQ][DT];
+  float m[NQ], l[NQ];
+#pragma unroll
+  for (int qs = 0; qs < NQ; ++qs) {
+    m[qs] = -INFINITY;
+    l[qs] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[qs][dt] = zero4();
+  }
+
+  const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
+  for (int kb = 0; kb < kend; kb += BK) {
+    __syncthreads();
+    stage_tile<T, BK, D, true, false>(Ks, LDR, nullptr, 0, kp, a.sk.t, kb, a.Tk, tid);
+    if constexpr (BF)
+      stage_tile<T, BK, D, false, true>(nullptr, 0, Vs, LDT, vp, a.sv.t, kb, a.Tk, tid);
+    else
+      stage_tile<T, BK, D, true, false>(Vs, LDR, nullptr, 0, vp, a.sv.t, kb, a.Tk, tid);
+    __syncthreads();
+
+    if (a.causal && kb > qw0 + NQ * 16 - 1 + off) continue;  // nothing visible for this wave
+    const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
+
+    f32x4 s[NQ][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      frag kf[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) kf[kc] = dfrag<T, D>(Ks + (16 * kt + n) * LDR, g, kc);
+#pragma unroll
+      for (int qs = 0; qs < NQ; ++qs) {
+        f32x4 t = zero4();
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) t = MF::mma(kf[kc], qf[qs][kc], t);
+        s[qs][kt] = t;
+      }
+    }
+
+    frag pf[NQ][NS];
+#pragma unroll
+    for (int qs = 0; qs < NQ; ++qs) {
+      if (need_mask) {
+        const int qi = qw0 + 16 * qs + n;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int kj = kb + 16 * kt + 4 * g + r;
+            if (kj >= a.Tk || (a.causal && kj > qi + off)) s[qs][kt][r] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[qs][kt][r]);
+      mx = fmaxf(mx, shfl_xor(mx, 16));
+      mx = fmaxf(mx, shfl_xor(mx, 32));
+      const float mnew = fmaxf(m[qs], mx * c);
+      const float alpha = __builtin_amdgcn_exp2f(m[qs] - mnew);
+      m[qs] = mnew;
+      float ls = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[qs][kt][r], c, -mnew));
+          s[qs][kt][r] = p;
+          ls += p;
+        }
+      l[qs] = fmaf(l[qs], alpha, ls);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[qs][dt] *= alpha;
+#pragma unroll
+      for (int st = 0; st < NS; ++st) pf[qs][st] = pfrag<T, 4>(s[qs], st);
+    }
+
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        const frag vf = tfrag<T>(Vs, LDR, Vs, LDT, 16 * dt + n, g, st);
+#pragma unroll
+        for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(vf, pf[qs][st], acc[qs][dt]);
+      }
+  }
+
+  // finalize: O = acc / l, lse = (m + log2 l) * ln2
+#pragma unroll
+  for (int qs = 0; qs < NQ; ++qs) {
+    float lt = l[qs];
+    lt += shfl_xor(lt, 16);
+    lt += shfl_xor(lt, 32);
+    const int qi = qw0 + 16 * qs + n;
+    if (qi < a.Tq) {
+      const float inv = 1.0f / lt;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        store4<T>(op + (int64_t)qi * a.so.t + 16 * dt + 4 * g, acc[qs][dt] * inv);
+      if (g == 0) a.lse[(int64_t)bh * a.Tq + qi] = (m[qs] + __log2f(lt)) * kLn2;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward, pass 0: delta[i] = sum_d dO[i,d] * O[i,d]
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void attn_delta_kernel(const BwdArgs a) {
+  const int64_t rows = (int64_t)a.B * a.H * a.Tq;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= rows) return;
+  const int t = (int)(i % a.Tq);
+  const int64_t bh = i / a.Tq;
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const T* op = static_cast<const T*>(a.o) + b * a.so.b + h * a.so.h + (int64_t)t * a.so.t;
+  const T* dp = static_cast<const T*>(a.dout) + b * a.sdo.b + h * a.sdo.h + (int64_t)t * a.sdo.t;
+  constexpr int V = Elem<T>::kVec;
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < D / V; ++c) {
+    const uint4 ou = *reinterpret_cast<const uint4*>(op + c * V);
+    const uint4 du = *reinterpret_cast<const uint4*>(dp + c * V);
+    const T* oe = reinterpret_cast<const T*>(&ou);
+    const T* de = reinterpret_cast<const T*>(&du);
+#pragma unroll
+    for (int e = 0; e < V; ++e) sum = fmaf(Elem<T>::to_f(oe[e]), Elem<T>::to_f(de[e]), sum);
+  }
+  a.delta[i] = sum;
+}
+
+// ---------------------------------------------------------------------------
+// backward, pass 1: dK, dV (key-outer).  Each wave owns NK*16 keys.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int NK>
+__global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const BwdArgs a) {
+  using MF = Mfma<T>;
+  using frag = typename MF::frag;
+  using DM = DMap<T, D>;
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int KC = DM::KC;
+  constexpr int DT = D / 16;
+  constexpr int BKV = kWaves * NK * 16;
+  constexpr int BQ = 64;
+  constexpr int NS = BQ / MF::KI;
+  constexpr int LDR = D + 16 / (int)sizeof(T);
+  constexpr int LDT = BQ + 4;
+  __shared__ __attribute__((aligned(16))) T Qs[BQ * LDR];
+  __shared__ __attribute__((aligned(16))) T Ds[BQ * LDR];
+  __shared__ __attribute__((aligned(16))) T Qt[BF ? D * LDT : 1];
+  __shared__ __attribute__((aligned(16))) T Dt[BF ? D * LDT : 1];
+  __shared__ float lse_s[BQ];
+  __shared__ float del_s[BQ];
+
+  const int BH = a.B * a.H;
+  const int nkb = (a.Tk + BKV - 1) / BKV;
+  int kbk, bh;
+  map_block(blockIdx.x, nkb, BH, false, kbk, bh);
+  const int b = bh / a.H, h = bh % a.H;
+  const T* __restrict__ qp = static_cast<const T*>(a.q) + b * a.sq.b + h * a.sq.h;
+  const T* __restrict__ kp = static_cast<const T*>(a.k) + b * a.sk.b + h * a.sk.h;
+  const T* __restrict__ vp = static_cast<const T*>(a.v) + b * a.sv.b + h * a.sv.h;
+  const T* __restrict__ dop = static_cast<const T*>(a.dout) + b * a.sdo.b + h * a.sdo.h;
+  const float* __restrict__ lsep = a.lse + (int64_t)bh * a.Tq;
+  const float* __restrict__ delp = a.delta + (int64_t)bh * a.Tq;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int k0 = kbk * BKV;
+  const int kw0 = k0 + wid * NK * 16;
+  const int off = a.Tk - a.Tq;
+  const float c = a.scale * kLog2e;
+
+  // K and V fragments of this wave's keys (B operands of S = Q K^T, dP = dO V^T)
+  frag kf[NK][KC], vf[NK][KC];
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks) {
+    const int row = kw0 + 16 * ks + n;
+    const int rr = row < a.Tk ? row : a.Tk - 1;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      frag fk = dfrag<T, D>(kp + (int64_t)rr * a.sk.t, g, kc);
+      frag fv = dfrag<T, D>(vp + (int64_t)rr * a.sv.t, g, kc);
+      if (row >= a.Tk) { fk = frag{}; fv = frag{}; }
+      kf[ks][kc] = fk;
+      vf[ks][kc] = fv;
+    }
+  }
+
+  f32x4 dka[NK][DT], dva[NK][DT];
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) { dka[ks][dt] = zero4(); dva[ks][dt] = zero4(); }
+
+  int qstart = a.causal ? max(0, k0 - off) : 0;
+  qstart = (qstart / BQ) * BQ;
+  for (int qt = qstart; qt < a.Tq; qt += BQ) {
+    __syncthreads();
+    if constexpr (BF) {
+      stage_tile<T, BQ, D, true, true>(Qs, LDR, Qt, LDT, qp, a.sq.t, qt, a.Tq, tid);
+      stage_tile<T, BQ, D, true, true>(Ds, LDR, Dt, LDT, dop, a.sdo.t, qt, a.Tq, tid);
+    } else {
+      stage_tile<T, BQ, D, true, false>(Qs, LDR, nullptr, 0, qp, a.sq.t, qt, a.Tq, tid);
+      stage_tile<T, BQ, D, true, false>(Ds, LDR, nullptr, 0, dop, a.sdo.t, qt, a.Tq, tid);
+    }
+    if (tid < BQ) {
+      const int qi = qt + tid;
+      lse_s[tid] = qi < a.Tq ? lsep[qi] * kLog2e : INFINITY;
+      del_s[tid] = qi < a.Tq ? delp[qi] : 0.f;
+    }
+    __syncthreads();
+
+    // wave-level causal skip: every key of the wave is after every query of the tile
+    if (a.causal && kw0 > qt + BQ - 1 + off) continue;
+    const bool need_mask = a.causal && (kw0 + NK * 16 - 1 > qt + off);
+
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) {
+      f32x4 p[4], ds[4];
+#pragma unroll
+      for (int qs = 0; qs < 4; ++qs) {
+        f32x4 sv = zero4(), dpv = zero4();
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          sv = MF::mma(dfrag<T, D>(Qs + (16 * qs + n) * LDR, g, kc), kf[ks][kc], sv);
+          dpv = MF::mma(dfrag<T, D>(Ds + (16 * qs + n) * LDR, g, kc), vf[ks][kc], dpv);
+        }
+        const int kj = kw0 + 16 * ks + n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int ql = 16 * qs + 4 * g + r;
+          float pv = __builtin_amdgcn_exp2f(fmaf(sv[r], c, -lse_s[ql]));
+          if (need_mask && kj > qt + ql + off) pv = 0.f;
+          p[qs][r] = pv;
+          ds[qs][r] = pv * (dpv[r] - del_s[ql]);
+        }
+      }
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        const frag pb = pfrag<T, 4>(p, st);
+        const frag db = pfrag<T, 4>(ds, st);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          dva[ks][dt] = MF::mma(tfrag<T>(Ds, LDR, Dt, LDT, 16 * dt + n, g, st), pb, dva[ks][dt]);
+          dka[ks][dt] = MF::mma(tfrag<T>(Qs, LDR, Qt, LDT, 16 * dt + n, g, st), db, dka[ks][dt]);
+        }
+      }
+    }
+  }
+
+  float* __restrict__ dkp = a.dk + b * a.sdk.b + h * a.sdk.h;
+  float* __restrict__ dvp = a.dv + b * a.sdv.b + h * a.sdv.h;
+  const bool accf = a.accumulate != 0;
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks) {
+    const int kj = kw0 + 16 * ks + n;
+    if (kj < a.Tk) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        store_grad4(dkp + (int64_t)kj * a.sdk.t + 16 * dt + 4 * g, dka[ks][dt] * a.scale, accf);
+        store_grad4(dvp + (int64_t)kj * a.sdv.t + 16 * dt + 4 * g, dva[ks][dt], accf);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward, pass 2: dQ (query-outer, transposed products like the forward)
+// ---------------------------------------------------------------------------
+template <typename T, int D, int NQ>
+__global__ __launch_bounds__(kThreads) void attn_dq_kernel(const BwdArgs a) {
+  using MF = Mfma<T>;
+  using frag = typename MF::frag;
+  using DM = DMap<T, D>;
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int KC = DM::KC;
+  constexpr int DT = D / 16;
+  constexpr int BQ = kWaves * NQ * 16;
+  constexpr int BK = 64;
+  constexpr int NS = BK / MF::KI;
+  constexpr int LDR = D + 16 / (int)sizeof(T);
+  constexpr int LDT = BK + 4;
+  __shared__ __attribute__((aligned(16))) T Ks[BK * LDR];
+  __shared__ __attribute__((aligned(16))) T Vs[BK * LDR];
+  __shared__ __attribute__((aligned(16))) T Kt[BF ? D * LDT : 1];
+
+  const int BH = a.B * a.H;
+  const int nqb = (a.Tq + BQ - 1) / BQ;
+  int qb, bh;
+  map_block(blockIdx.x, nqb, BH, a.causal != 0, qb, bh);
+  const int b = bh / a.H, h = bh % a.H;
+  const T* __restrict__ qp = static_cast<const T*>(a.q) + b * a.sq.b + h * a.sq.h;
+  const T* __restrict__ kp = static_cast<const T*>(a.k) + b * a.sk.b + h * a.sk.h;
+  const T* __restrict__ vp = static_cast<const T*>(a.v) + b * a.sv.b + h * a.sv.h;
+  const T* __restrict__ dop = static_cast<const T*>(a.dout) + b * a.sdo.b + h * a.sdo.h;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int q0 = qb * BQ;
+  const int qw0 = q0 + wid * NQ * 16;
+  const int off = a.Tk - a.Tq;
+  const float c = a.scale * kLog2e;
+
+  frag qf[NQ][KC], df[NQ][KC];
+  float lse2[NQ], del[NQ];
+#pragma unroll
+  for (int qs = 0; qs < NQ; ++qs) {
+    const int row = qw0 + 16 * qs + n;
+    const bool ok = row < a.Tq;
+    const int rr = ok ? row : a.Tq - 1;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      frag fq = dfrag<T, D>(qp + (int64_t)rr * a.sq.t, g, kc);
+      frag fd = dfrag<T, D>(dop + (int64_t)rr * a.sdo.t, g, kc);
+      if (!ok) { fq = frag{}; fd = frag{}; }
+      qf[qs][kc] = fq;
+      df[qs][kc] = fd;
+    }
+    lse2[qs] = ok ? a.lse[(int64_t)bh * a.Tq + row] * kLog2e : INFINITY;
+    del[qs] = ok ? a.delta[(int64_t)bh * a.Tq + row] : 0.f;
+  }
+
+  f32x4 acc[NQ][DT];
+#pragma unroll
+  for (int qs = 0; qs < NQ; ++qs)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[qs][dt] = zero4();
+
+  const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
+  for (int kb = 0; kb < kend; kb += BK) {
+    __syncthreads();
+    if constexpr (BF)
+      stage_tile<T, BK, D, true, true>(Ks, LDR, Kt, LDT, kp, a.sk.t, kb, a.Tk, tid);
+    else
+      stage_tile<T, BK, D, true, false>(Ks, LDR, nullptr, 0, kp, a.sk.t, kb, a.Tk, tid);
+    stage_tile<T, BK, D, true, false>(Vs, LDR, nullptr, 0, vp, a.sv.t, kb, a.Tk, tid);
+    __syncthreads();
+
+    if (a.causal && kb > qw0 + NQ * 16 - 1 + off) continue;
+    const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
+
+    f32x4 ds[NQ][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      frag kfr[KC], vfr[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        kfr[kc] = dfrag<T, D>(Ks + (16 * kt + n) * LDR, g, kc);
+        vfr[kc] = dfrag<T, D>(Vs + (16 * kt + n) * LDR, g, kc);
+      }
+#pragma unroll
+      for (int qs = 0; qs < NQ; ++qs) {
+        f32x4 sv = zero4(), dpv = zero4();
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          sv = MF::mma(kfr[kc], qf[qs][kc], sv);
+          dpv = MF::mma(vfr[kc], df[qs][kc], dpv);
+        }
+        const int qi = qw0 + 16 * qs + n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float pv = __builtin_amdgcn_exp2f(fmaf(sv[r], c, -lse2[qs]));
+          if (need_mask) {
+            const int kj = kb + 16 * kt + 4 * g + r;
+            if (kj >= a.Tk || (a.causal && kj > qi + off)) pv = 0.f;
+          }
+          ds[qs][kt][r] = pv * (dpv[r] - del[qs]);
+        }
+      }
+    }
+
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      frag db[NQ];
+#pragma unroll
+      for (int qs = 0; qs < NQ; ++qs) db[qs] = pfrag<T, 4>(ds[qs], st);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const frag kt_f = tfrag<T>(Ks, LDR, Kt, LDT, 16 * dt + n, g, st);
+#pragma unroll
+        for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(kt_f, db[qs], acc[qs][dt]);
+      }
+    }
+  }
+
+  float* __restrict__ dqp = a.dq + b * a.sdq.b + h * a.sdq.h;
+  const bool accf = a.accumulate != 0;
+#pragma unroll
+  for (int qs = 0; qs < NQ; ++qs) {
+    const int qi = qw0 + 16 * qs + n;
+    if (qi < a.Tq) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        store_grad4(dqp + (int64_t)qi * a.sdq.t + 16 * dt + 4 * g, acc[qs][dt] * a.scale, accf);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+// tile parameters per dtype
+template <typename T> struct Cfg;
+template <> struct Cfg<float> { static constexpr int NQ = 1, NK = 1; };
+template <> struct Cfg<bf16_t> { static constexpr int NQ = 2, NK = 2; };
+
+int check_bhtd(const char* name, const void* p, const int64_t* s, int esize) {
+  MTX_CHECK_ARG(p != nullptr, "%s: null pointer", name);
+  MTX_CHECK_ARG(s != nullptr, "%s: null strides", name);
+  MTX_CHECK_ARG(s[3] == 1, "%s: the d stride must be 1 (got %lld)", name, (long long)s[3]);
+  const int vec = 16 / esize;
+  for (int i = 0; i < 3; ++i)
+    MTX_CHECK_ARG(s[i] >= 0 && s[i] % vec == 0,
+                  "%s: stride[%d]=%lld must be a non-negative multiple of %d elements", name, i,
+                  (long long)s[i], vec);
+  MTX_CHECK_ARG(((uintptr_t)p & 15u) == 0, "%s: pointer must be 16-byte aligned", name);
+  return MTX_OK;
+}
+
+int check_dims(int dtype, int B, int H, int Tq, int Tk, int D, int causal) {
+  if (dtype != MTX_F32 && dtype != MTX_BF16) return fail(MTX_ERR_DTYPE, "unsupported dtype %d", dtype);
+  MTX_CHECK_SHAPE(B >= 1 && H >= 1 && Tq >= 1 && Tk >= 1, "B,H,Tq,Tk must be >= 1 (got %d,%d,%d,%d)",
+                  B, H, Tq, Tk);
+  MTX_CHECK_SHAPE(D == 16 || D == 32 || D == 64 || D == 128, "head dim D=%d not in {16,32,64,128}", D);
+  MTX_CHECK_SHAPE(!causal || Tq <= Tk, "causal attention needs Tq <= Tk (got %d > %d)", Tq, Tk);
+  MTX_CHECK_SHAPE((int64_t)B * H <= (1 << 24) && Tq <= (1 << 24) && Tk <= (1 << 24), "shape too large");
+  return MTX_OK;
+}
+
+Str3 s3(const int64_t* s) { return Str3{s[0], s[1], s[2]}; }
+
+template <typename T, int D>
+int launch_fwd(const FwdArgs& a, hipStream_t st) {
+  constexpr int NQ = Cfg<T>::NQ;
+  constexpr int BQ = kWaves * NQ * 16;
+  const int grid = cdiv(a.Tq, BQ) * a.B * a.H;
+  hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQ>), dim3(grid), dim3(kThreads), 0, st, a);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+template <typename T, int D>
+int launch_bwd(const BwdArgs& a, int phases, hipStream_t st) {
+  constexpr int NQ = Cfg<T>::NQ, NK = Cfg<T>::NK;
+  if (phases & MTX_ATTN_BWD_DELTA) {
+    const int64_t rows = (int64_t)a.B * a.H * a.Tq;
+    hipLaunchKernelGGL((attn_delta_kernel<T, D>), dim3((unsigned)((rows + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, st, a);
+    MTX_LAUNCHED();
+  }
+  if (phases & MTX_ATTN_BWD_DKDV) {
+    const int gk = cdiv(a.Tk, kWaves * NK * 16) * a.B * a.H;
+    hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK>), dim3(gk), dim3(kThreads), 0, st, a);
+    MTX_LAUNCHED();
+  }
+  if (phases & MTX_ATTN_BWD_DQ) {
+    const int gq = cdiv(a.Tq, kWaves * NQ * 16) * a.B * a.H;
+    hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ>), dim3(gq), dim3(kThreads), 0, st, a);
+    MTX_LAUNCHED();
+  }
+  return MTX_OK;
+}
+
+template <typename T>
+int dispatch_fwd(int D, const FwdArgs& a, hipStream_t st) {
+  switch (D) {
+    case 16: return launch_fwd<T, 16>(a, st);
+    case 32: return launch_fwd<T, 32>(a, st);
+    case 64: return launch_fwd<T, 64>(a, st);
+    default: return launch_fwd<T, 128>(a, st);
+  }
+}
+
+template <typename T>
+int dispatch_bwd(int D, const BwdArgs& a, int phases, hipStream_t st) {
+  switch (D) {
+    case 16: return launch_bwd<T, 16>(a, phases, st);
+    case 32: return launch_bwd<T, 32>(a, phases, st);
+    case 64: return launch_bwd<T, 64>(a, phases, st);
+    default: return launch_bwd<T, 128>(a, phases, st);
+  }
+}
+
+}  // namespace
+}  // namespace mtx
+
+using namespace mtx;
+
+extern "C" int mtx_attn_fwd(int dtype, int B, int H, int Tq, int Tk, int D,
+                            const void* q, const int64_t* q_strides,
+                            const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides,
+                            void* o, const int64_t* o_strides,
+                            float* lse, float scale, int causal, void* stream) {
+  int rc = check_dims(dtype, B, H, Tq, Tk, D, causal);
+  if (rc) return rc;
+  const int es = dtype == MTX_F32 ? 4 : 2;
+  if ((rc = check_bhtd("q", q, q_strides, es))) return rc;
+  if ((rc = check_bhtd("k", k, k_strides, es))) return rc;
+  if ((rc = check_bhtd("v", v, v_strides, es))) return rc;
+  if ((rc = check_bhtd("o", o, o_strides, es))) return rc;
+  MTX_CHECK_ARG(lse != nullptr, "lse: null pointer");
+  MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
+  FwdArgs a{q, s3(q_strides), k, s3(k_strides), v, s3(v_strides), o, s3(o_strides),
+            lse, B, H, Tq, Tk, scale, causal ? 1 : 0};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dtype == MTX_F32 ? dispatch_fwd<float>(D, a, st) : dispatch_fwd<bf16_t>(D, a, st);
+}
+
+extern "C" size_t mtx_attn_bwd_workspace_bytes(int B, int H, int Tq) {
+  if (B < 1 || H < 1 || Tq < 1) return 0;
+  return (size_t)B * H * Tq * sizeof(float);
+}
+
+extern "C" int mtx_attn_bwd_phase(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
+                            const void* q, const int64_t* q_strides,
+                            const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides,
+                            const void* o, const int64_t* o_strides,
+                            const void* dout, const int64_t* do_strides,
+                            const float* lse,
+                            float* dq, const int64_t* dq_strides,
+                            float* dk, const int64_t* dk_strides,
+                            float* dv, const int64_t* dv_strides,
+                            void* workspace, size_t workspace_bytes,
+                            float scale, int causal, int accumulate, void* stream) {
+  MTX_CHECK_ARG(phases > 0 && (phases & ~MTX_ATTN_BWD_ALL) == 0, "bad phase mask %d", phases);
+  int rc = check_dims(dtype, B, H, Tq, Tk, D, causal);
+  if (rc) return rc;
+  const int es = dtype == MTX_F32 ? 4 : 2;
+  if ((rc = check_bhtd("q", q, q_strides, es))) return rc;
+  if ((rc = check_bhtd("k", k, k_strides, es))) return rc;
+  if ((rc = check_bhtd("v", v, v_strides, es))) return rc;
+  if ((rc = check_bhtd("o", o, o_strides, es))) return rc;
+  if ((rc = check_bhtd("dout", dout, do_strides, es))) return rc;
+  if ((rc = check_bhtd("dq", dq, dq_strides, 4))) return rc;
+  if ((rc = check_bhtd("dk", dk, dk_strides, 4))) return rc;
+  if ((rc = check_bhtd("dv", dv, dv_strides, 4))) return rc;
+  MTX_CHECK_ARG(lse != nullptr, "lse: null pointer");
+  MTX_CHECK_ARG(workspace != nullptr, "workspace: null pointer");
+  MTX_CHECK_ARG(workspace_bytes >= mtx_attn_bwd_workspace_bytes(B, H, Tq),
+                "workspace too small: %zu < %zu bytes", workspace_bytes,
+                mtx_attn_bwd_workspace_bytes(B, H, Tq));
+  MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
+  BwdArgs a{q, s3(q_strides), k, s3(k_strides), v, s3(v_strides), o, s3(o_strides),
+            dout, s3(do_strides), lse, static_cast<float*>(workspace),
+            dq, s3(dq_strides), dk, s3(dk_strides), dv, s3(dv_strides),
+            B, H, Tq, Tk, scale, causal ? 1 : 0, accumulate ? 1 : 0};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dtype == MTX_F32 ? dispatch_bwd<float>(D, a, phases, st)
+                          : dispatch_bwd<bf16_t>(D, a, phases, st);
+}
+
+extern "C" int mtx_attn_bwd(int dtype, int B, int H, int Tq, int Tk, int D,
+                            const void* q, const int64_t* q_strides,
+                            const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides,
+                            const void* o, const int64_t* o_strides,
+                            const void* dout, const int64_t* do_strides,
+                            const float* lse,
+                            float* dq, const int64_t* dq_strides,
+                            float* dk, const int64_t* dk_strides,
+                            float* dv, const int64_t* dv_strides,
+                            void* workspace, size_t workspace_bytes,
+                            float scale, int causal, int accumulate, void* stream) {
+  return mtx_attn_bwd_phase(MTX_ATTN_BWD_ALL, dtype, B, H, Tq, Tk, D, q, q_strides, k, k_strides,
+                            v, v_strides, o, o_strides, dout, do_strides, lse, dq, dq_strides,
+                            dk, dk_strides, dv, dv_strides, workspace, workspace_bytes, scale,
+                            causal, accumulate, stream);
+}

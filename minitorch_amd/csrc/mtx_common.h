@@ -1,0 +1,124 @@
+// Shared device/host helpers for the minitorch_amd HIP library (gfx950 only).
+//
+// Everything here is internal to libmtx_hip.so; the public C ABI is declared in
+// include/mtx.h.  Status codes, the thread-local error string and the MFMA
+// fragment helpers used by the attention, GEMM and row kernels live here.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string>
+
+#include "../../include/mtx.h"
+
+namespace mtx {
+
+// ---------------------------------------------------------------------------
+// error plumbing (host)
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+
+#define MTX_CHECK_ARG(cond, ...)                                  \
+  do {                                                            \
+    if (!(cond)) return ::mtx::fail(MTX_ERR_ARG, __VA_ARGS__);    \
+  } while (0)
+#define MTX_CHECK_SHAPE(cond, ...)                                \
+  do {                                                            \
+    if (!(cond)) return ::mtx::fail(MTX_ERR_SHAPE, __VA_ARGS__);  \
+  } while (0)
+#define MTX_HIP(expr)                                                           \
+  do {                                                                          \
+    hipError_t _e = (expr);                                                     \
+    if (_e != hipSuccess)                                                       \
+      return ::mtx::fail(MTX_ERR_HIP, "%s: %s", #expr, hipGetErrorString(_e));  \
+  } while (0)
+// check the launch that was just issued
+#define MTX_LAUNCHED()                                                          \
+  do {                                                                          \
+    hipError_t _e = hipGetLastError();                                          \
+    if (_e != hipSuccess)                                                       \
+      return ::mtx::fail(MTX_ERR_HIP, "launch: %s", hipGetErrorString(_e));     \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// vector types
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t bf16_t;  // storage type of bf16 in global memory
+
+__device__ __forceinline__ float bf2f(bf16_t x) {
+  return __uint_as_float(((uint32_t)x) << 16);
+}
+// round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950)
+__device__ __forceinline__ bf16_t f2bf(float x) {
+  __bf16 b = (__bf16)x;
+  return __builtin_bit_cast(bf16_t, b);
+}
+
+// ---------------------------------------------------------------------------
+// element type traits: loads of 16-byte chunks, conversions
+// ---------------------------------------------------------------------------
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kVec = 4;  // elements per 16-byte chunk
+  __device__ __forceinline__ static float to_f(float x) { return x; }
+  __device__ __forceinline__ static float from_f(float x) { return x; }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int kVec = 8;
+  __device__ __forceinline__ static float to_f(bf16_t x) { return bf2f(x); }
+  __device__ __forceinline__ static bf16_t from_f(float x) { return f2bf(x); }
+};
+
+// ---------------------------------------------------------------------------
+// 16x16 MFMA family.  For every instruction used here lane l supplies
+// A[row = l%16][k = kmap(l/16, e)] and B[k = kmap(l/16, e)][col = l%16] for its
+// e = 0..KPL-1 operand elements, with the same k-map for A and B, and receives
+// C[row = 4*(l/16) + r][col = l%16], r = 0..3.  Because the k-map is shared by
+// both operands, the kernels only need to feed matching k-sets to A and B; the
+// concrete k-map of the hardware never matters.
+// ---------------------------------------------------------------------------
+template <typename T> struct Mfma;
+template <> struct Mfma<float> {
+  static constexpr int KI = 4;   // k per instruction
+  static constexpr int KPL = 1;  // operand elements per lane
+  typedef float frag;
+  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<bf16_t> {
+  static constexpr int KI = 32;
+  static constexpr int KPL = 8;
+  typedef bf16x8 frag;
+  __device__ __forceinline__ static f32x4 mma(frag a, frag b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// XOR shuffles inside a wave64 (ds_bpermute based)
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+// 32-bit LDS/global helpers --------------------------------------------------
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+  bf16x2 v;
+  v[0] = (__bf16)a;
+  v[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace mtx

@@ -1,0 +1,223 @@
+"""NumPy restatement of the reference's causal attention sub-graph (oracle).
+
+TEST INFRASTRUCTURE ONLY -- imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg; never by the product.
+
+The reference computes attention inside ``MultiHeadAttention.forward``
+(transformer.py:36-44) from generic autograd ops:
+
+    scores = (q @ k.transpose(-2, -1)) * (1.0 / np.sqrt(head_dim))
+    scores = scores + Tensor(np.triu(np.ones((T, T), float32), k=1) * -1e9)
+    attn   = F.softmax(scores, axis=-1)
+    out    = attn @ v
+
+Under NumPy 2 (the reference's pinned version) ``1.0/np.sqrt(D)`` is an
+``np.float64`` scalar, ``Tensor.__init__`` keeps it as a 0-d float64 array
+(tensor.py:53-54), and ``float32 array * float64 0-d array`` promotes to float64.
+So q@k^T is an fp32 sgemm, and everything from the scale on is float64.
+Gradient holders follow the dtype of the tensor they belong to
+(``_accum_grad`` zero-inits with ``zeros_like(data)`` then adds in place,
+tensor.py:29-33), so the grad of the fp32 ``q@k^T`` node is rounded to fp32
+before the matmul backward produces dq and dk in fp32.
+
+``reference_attention`` restates exactly that flow.  ``attention_f64`` is the
+same mathematics carried out entirely in float64, and ``flash_forward`` /
+``flash_backward`` the log-sum-exp formulation the GPU kernels implement.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+F64 = np.float64
+
+
+def causal_mask(Tq: int, Tk: int) -> np.ndarray:
+    """Boolean (Tq, Tk) mask of *hidden* entries.
+
+    For Tq == Tk this is ``np.triu(ones, k=1) != 0`` (transformer.py:39).  For
+    Tq < Tk the queries are the last Tq positions (bottom-right alignment), the
+    rule the GPU library uses: key j is visible to query i iff j <= i + Tk - Tq.
+    """
+    i = np.arange(Tq)[:, None]
+    j = np.arange(Tk)[None, :]
+    return j > i + (Tk - Tq)
+
+
+def _softmax_lastdim(x: np.ndarray) -> np.ndarray:
+    """F.softmax forward, functional.py:62-66 (max-shift, exp, divide by sum)."""
+    shifted = x - x.max(axis=-1, keepdims=True)
+    exps = np.exp(shifted)
+    return exps / exps.sum(axis=-1, keepdims=True)
+
+
+def _softmax_backward(p: np.ndarray, gout: np.ndarray) -> np.ndarray:
+    """F.softmax backward closure, functional.py:69-73."""
+    g = gout * p
+    return g - p * g.sum(axis=-1, keepdims=True)
+
+
+def reference_attention(q, k, v, dout=None, scale=None, causal=True):
+    """The reference's attention sub-graph with its exact dtype flow.
+
+    q, k, v: (..., T, D) float32 (the _split_heads views, transformer.py:26-28).
+    dout: upstream gradient of ``out`` or None (forward only).
+    Returns (out, dq, dk, dv); grads are None when dout is None.
+
+    Forward: transformer.py:36-44, with matmul tensor.py:207-208, the scalar
+    multiply tensor.py:148-150 (fp32 * fp64 0-d -> fp64), mask add
+    tensor.py:111-113, softmax functional.py:62-66.
+    Backward: the closures in reverse topological order -- matmul
+    tensor.py:210-218 (attn @ v), softmax functional.py:69-73, add
+    tensor.py:115-119 (identity for scores), mul tensor.py:152-156
+    (other.data * out.grad, accumulated into the fp32 q@k^T node's grad),
+    matmul tensor.py:210-218 (q @ k^T), transpose tensor.py:338-340.
+    """
+    q = np.asarray(q, dtype=F32)
+    k = np.asarray(k, dtype=F32)
+    v = np.asarray(v, dtype=F32)
+    Tq, D = q.shape[-2], q.shape[-1]
+    Tk = k.shape[-2]
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)  # np.float64, as in transformer.py:36
+    scale64 = np.asarray(np.float64(scale))
+    kt = np.swapaxes(k, -1, -2)
+    qk = q @ kt  # fp32 (sgemm)
+    scores = qk * scale64  # -> float64
+    if causal:
+        mask = (causal_mask(Tq, Tk).astype(F32) * F32(-1e9)).astype(F32)
+        scores = scores + mask
+    attn = _softmax_lastdim(scores)  # float64
+    out = attn @ v  # float64 @ float32 -> float64
+    if dout is None:
+        return out, None, None, None
+    gout = np.asarray(dout, dtype=F64)
+    # attn @ v backward (tensor.py:213-218); v's grad holder is fp32
+    d_attn = gout @ np.swapaxes(v, -1, -2)
+    dv = (np.swapaxes(attn, -1, -2) @ gout).astype(F32)
+    # softmax backward -> grad of scores (float64 node)
+    d_scores = _softmax_backward(attn, d_attn)
+    # mask add: identity; mul by scale: grad flows into the fp32 q@k^T node
+    d_qk = (scale64 * d_scores).astype(F32)
+    # q @ kt backward in fp32
+    dq = (d_qk @ k).astype(F32)
+    d_kt = np.swapaxes(q, -1, -2) @ d_qk
+    dk = np.swapaxes(d_kt, -1, -2).astype(F32)
+    return out, dq, dk, dv
+
+
+def attention_f64(q, k, v, dout=None, scale=None, causal=True):
+    """Same mathematics as reference_attention, entirely in float64.
+
+    Returns (out, p, dq, dk, dv, ds) where p is the probability matrix and ds
+    the score gradient (grad w.r.t. scale * q k^T + mask), for invariant checks.
+    """
+    q = np.asarray(q, dtype=F64)
+    k = np.asarray(k, dtype=F64)
+    v = np.asarray(v, dtype=F64)
+    Tq, D = q.shape[-2], q.shape[-1]
+    Tk = k.shape[-2]
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    s = (q @ np.swapaxes(k, -1, -2)) * scale
+    if causal:
+        s = np.where(causal_mask(Tq, Tk), -np.inf, s)
+    p = _softmax_lastdim(s)
+    out = p @ v
+    if dout is None:
+        return out, p, None, None, None, None
+    g = np.asarray(dout, dtype=F64)
+    dv = np.swapaxes(p, -1, -2) @ g
+    dp = g @ np.swapaxes(v, -1, -2)
+    ds = _softmax_backward(p, dp)
+    dq = scale * (ds @ k)
+    dk = scale * (np.swapaxes(ds, -1, -2) @ q)
+    return out, p, dq, dk, dv, ds
+
+
+def flash_forward(q, k, v, scale, causal=True):
+    """Log-sum-exp form: returns (out, lse) with lse_i = log sum_j exp(s_ij),
+    s = scale * q k^T over visible keys.  Float64."""
+    q = np.asarray(q, dtype=F64)
+    k = np.asarray(k, dtype=F64)
+    v = np.asarray(v, dtype=F64)
+    s = (q @ np.swapaxes(k, -1, -2)) * scale
+    if causal:
+        s = np.where(causal_mask(q.shape[-2], k.shape[-2]), -np.inf, s)
+    m = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - m)
+    l = e.sum(axis=-1, keepdims=True)
+    out = (e @ v) / l
+    lse = (m + np.log(l))[..., 0]
+    return out, lse
+
+
+def flash_backward(q, k, v, out, dout, lse, scale, causal=True):
+    """Backward from saved (out, lse): P = exp(s - lse), delta = rowsum(dO*O),
+    dS = P * (dO V^T - delta).  Float64.  Returns (dq, dk, dv)."""
+    q = np.asarray(q, dtype=F64)
+    k = np.asarray(k, dtype=F64)
+    v = np.asarray(v, dtype=F64)
+    out = np.asarray(out, dtype=F64)
+    g = np.asarray(dout, dtype=F64)
+    s = (q @ np.swapaxes(k, -1, -2)) * scale
+    p = np.exp(s - np.asarray(lse, dtype=F64)[..., None])
+    if causal:
+        p = np.where(causal_mask(q.shape[-2], k.shape[-2]), 0.0, p)
+    delta = (g * out).sum(axis=-1, keepdims=True)
+    dp = g @ np.swapaxes(v, -1, -2)
+    ds = p * (dp - delta)
+    dq = scale * (ds @ k)
+    dk = scale * (np.swapaxes(ds, -1, -2) @ q)
+    dv = np.swapaxes(p, -1, -2) @ g
+    return dq, dk, dv
+
+
+def reference_attention_chunked(q, k, v, dout=None, scale=None, causal=True, chunk=1):
+    """reference_attention over the leading (B, H) axes in chunks of `chunk`
+    (b, h) slices, to bound memory at long T (one fp64 (T, T) matrix per
+    slice).  Results are identical to the unchunked call: every slice is
+    independent."""
+    B, H = q.shape[0], q.shape[1]
+    outs = []
+    for b in range(B):
+        row = []
+        for h0 in range(0, H, chunk):
+            sl = (slice(b, b + 1), slice(h0, h0 + chunk))
+            row.append(reference_attention(q[sl], k[sl], v[sl],
+                                           None if dout is None else dout[sl],
+                                           scale, causal))
+        outs.append([np.concatenate([r[i] for r in row], axis=1) if row[0][i] is not None else None
+                     for i in range(4)])
+    return tuple(np.concatenate([o[i] for o in outs], axis=0) if outs[0][i] is not None else None
+                 for i in range(4))
+
+
+def numerical_gradient(f, inputs, eps=1e-5):
+    """Central differences in float64, one element at a time -- the method of
+    the reference's grad_check.numerical_gradient (grad_check.py:5-38)."""
+    grads = []
+    for idx_in, x in enumerate(inputs):
+        g = np.zeros_like(x, dtype=F64)
+        it = np.nditer(x, flags=["multi_index"])
+        while not it.finished:
+            i = it.multi_index
+            old = x[i]
+            x[i] = old + eps
+            fp = f()
+            x[i] = old - eps
+            fm = f()
+            x[i] = old
+            g[i] = (fp - fm) / (2 * eps)
+            it.iternext()
+        grads.append(g)
+    return grads
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to bfloat16 (round-to-nearest-even) and return them
+    as float32.  NaN/inf are not expected in the inputs."""
+    x = np.ascontiguousarray(x, dtype=F32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(F32)

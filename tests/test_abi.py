@@ -1,0 +1,101 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/mtx.h declares, the ctypes table matches the header, and invalid
+arguments are rejected on the host before any HIP call."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from minitorch_amd import _lib as L
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mtx.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mtx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_something():
+    names = declared_functions()
+    assert "mtx_attn_fwd" in names and "mtx_attn_bwd" in names
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = L.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in mtx.h but not exported"
+        assert name in L.SIGNATURES, f"{name} has no ctypes signature in _lib.py"
+    assert set(L.SIGNATURES) == set(declared_functions())
+
+
+def test_version():
+    assert b"gfx950" in L.lib().mtx_version()
+
+
+def _strides(*s):
+    return (C.c_int64 * 4)(*s)
+
+
+def _fwd(**over):
+    args = dict(dtype=L.MTX_F32, B=1, H=1, Tq=8, Tk=8, D=64, q=16, qs=(512, 512, 64, 1),
+                k=16, ks=(512, 512, 64, 1), v=16, vs=(512, 512, 64, 1), o=16, os=(512, 512, 64, 1),
+                lse=16, scale=0.125, causal=1)
+    args.update(over)
+    a = args
+    # fake (never dereferenced) device addresses: validation fails before any HIP call
+    p = lambda x: C.c_void_p(x) if x else None
+    return L.lib().mtx_attn_fwd(a["dtype"], a["B"], a["H"], a["Tq"], a["Tk"], a["D"],
+                                p(a["q"]), _strides(*a["qs"]), p(a["k"]), _strides(*a["ks"]),
+                                p(a["v"]), _strides(*a["vs"]), p(a["o"]), _strides(*a["os"]),
+                                p(a["lse"]), a["scale"], a["causal"], None)
+
+
+@pytest.mark.parametrize("over,code,frag", [
+    (dict(dtype=7), L.MTX_ERR_DTYPE, "dtype"),
+    (dict(D=48), L.MTX_ERR_SHAPE, "head dim"),
+    (dict(Tq=0), L.MTX_ERR_SHAPE, ">= 1"),
+    (dict(Tq=9, Tk=8), L.MTX_ERR_SHAPE, "Tq <= Tk"),
+    (dict(q=0), L.MTX_ERR_ARG, "null"),
+    (dict(lse=0), L.MTX_ERR_ARG, "lse"),
+    (dict(ks=(512, 512, 64, 2)), L.MTX_ERR_ARG, "d stride"),
+    (dict(vs=(512, 512, 66, 1)), L.MTX_ERR_ARG, "multiple"),
+    (dict(o=24), L.MTX_ERR_ARG, "aligned"),
+    (dict(scale=-1.0), L.MTX_ERR_ARG, "scale"),
+])
+def test_attn_fwd_rejects_bad_arguments(over, code, frag):
+    rc = _fwd(**over)
+    assert rc == code
+    assert frag in L.lib().mtx_last_error().decode()
+
+
+def test_attn_bwd_rejects_small_workspace():
+    s = _strides(512, 512, 64, 1)
+    p = C.c_void_p(16)
+    rc = L.lib().mtx_attn_bwd(L.MTX_F32, 1, 1, 8, 8, 64, p, s, p, s, p, s, p, s, p, s, p,
+                              p, s, p, s, p, s, p, 4, 0.125, 1, 0, None)
+    assert rc == L.MTX_ERR_ARG
+    assert "workspace" in L.lib().mtx_last_error().decode()
+
+
+def test_attn_bwd_phase_mask_checked():
+    s = _strides(512, 512, 64, 1)
+    p = C.c_void_p(16)
+    rc = L.lib().mtx_attn_bwd_phase(8, L.MTX_F32, 1, 1, 8, 8, 64, p, s, p, s, p, s, p, s, p, s, p,
+                                    p, s, p, s, p, s, p, 1 << 20, 0.125, 1, 0, None)
+    assert rc == L.MTX_ERR_ARG
+
+
+def test_workspace_query():
+    assert L.lib().mtx_attn_bwd_workspace_bytes(2, 3, 5) == 2 * 3 * 5 * 4
+    assert L.lib().mtx_attn_bwd_workspace_bytes(0, 3, 5) == 0
+
+
+def test_python_wrapper_raises_value_error():
+    s = _strides(512, 512, 64, 1)
+    p = C.c_void_p(16)
+    with pytest.raises(ValueError, match="phase"):
+        L.call("mtx_attn_bwd_phase", 0, L.MTX_F32, 1, 1, 8, 8, 64, p, s, p, s, p, s, p, s, p, s, p,
+               p, s, p, s, p, s, p, 1 << 20, 0.125, 1, 0, None)
