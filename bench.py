@@ -130,6 +130,18 @@ def cpu_baseline_attention(arrs, T, D, budget_s=15.0):
     return (f + bwd) / dt / 1e12, done, dt
 
 
+def pmc_traffic(kernel):
+    """HBM bytes per launch of `kernel` at C3 from the committed rocprofv3 PMC
+    summary (profiles/pmc_traffic.json), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)["bytes_per_launch"][kernel]
+        return int(rec["read"] + rec["write"])
+    except Exception:
+        return None
+
+
 def blas_threads():
     for var in ("OPENBLAS_NUM_THREADS", "OMP_NUM_THREADS", "MKL_NUM_THREADS"):
         if os.environ.get(var):
@@ -147,6 +159,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--only", choices=("all", "c3", "c1"), default="all",
+                    help="profiling aid: run only one attention config and print no JSON line")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="profiling aid: run 5 device copies of MIB MiB (a kernel of known HBM "
+                         "traffic, for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -159,6 +176,20 @@ def main():
     if not torch.cuda.is_available():
         print("no GPU visible", file=sys.stderr)
         sys.exit(1)
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copied {args.calibrate_copy} MiB x5", file=sys.stderr)
+        return
+    if args.only == "c1":
+        r1, _ = bench_attention(32, 8, 256, 64, torch.float32, 1, 1.0, args.steps, args.warmup)
+        print(f"[bench] C1 {r1}", file=sys.stderr)
+        return
 
     # ---- C3: headline ----
     B, H, T, D = 8, 16, 2048, 64
@@ -178,6 +209,8 @@ def main():
     achieved = fl_dom / (ms_dom * 1e-3) / 1e12
     print(f"[bench] C3 step {r3['ms_step']:.3f} ms = {tflops:.1f} TFLOP/s; phases {r3}",
           file=sys.stderr, flush=True)
+    if args.only == "c3":
+        return
 
     # ---- C1: fp32 ----
     print("[bench] C1 fp32 B=32 H=8 T=256 D=64", file=sys.stderr, flush=True)
@@ -214,7 +247,7 @@ def main():
         "pct_of_peak": round(100 * tflops / PEAK_BF16, 2),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                      "peak": PEAK_BF16, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4),
-                     "traffic": None, "ms_per_launch": round(ms_dom, 4),
+                     "traffic": pmc_traffic(dom), "ms_per_launch": round(ms_dom, 4),
                      "flops_per_launch": fl_dom},
         "cpu_baseline": cpu,
         "also": {

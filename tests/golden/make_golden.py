@@ -1,0 +1,171 @@
+#!/usr/bin/env python3
+"""Write the golden fixtures in tests/golden/ by running the REFERENCE itself.
+
+Run in the build container only (the reference is mounted at
+/root/reference; it never travels to the GPU box and nothing else imports it):
+
+    python tests/golden/make_golden.py            # attention, MHA, C0 train, greedy
+    python tests/golden/make_golden.py --c2       # also the C2 20-step loss curve (slow)
+
+These are the functions no closed form, finite difference or library
+cross-check pins (the composed training step as the reference executes it,
+with NumPy 2's float64 promotion and float32 gradient holders; the greedy
+sequence its forward produces).  Each fixture stores its inputs' seeds and the
+reference's outputs.  Inputs are generated with the same helpers the oracle
+uses (oracle.gpt.init_params / draw_batch), and the reference model's
+state_dict keys are checked against oracle.gpt.param_spec first.
+"""
+from __future__ import annotations
+
+import argparse
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+REFERENCE = Path("/root/reference")
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(REFERENCE))
+
+import minitorch as mt  # noqa: E402  (the reference)
+from minitorch import functional as RF  # noqa: E402
+
+from oracle.gpt import C0, C2, GPTConfig, draw_batch, init_params, param_spec  # noqa: E402
+
+
+def ref_model(cfg: GPTConfig, rng):
+    model = mt.GPT(cfg.vocab, cfg.block, cfg.n_embd, cfg.n_head, cfg.n_layer, dropout=0.0)
+    names = [n for n, _, _ in param_spec(cfg)]
+    sd = model.state_dict()
+    assert list(sd.keys()) == names, "state_dict key order differs from oracle.gpt.param_spec"
+    for n, shp, _ in param_spec(cfg):
+        assert sd[n].shape == shp, (n, sd[n].shape, shp)
+    model.load_state_dict(init_params(cfg, rng))
+    return model
+
+
+def attention_subgraph(path):
+    """transformer.py:36-44 through the reference's Tensor ops, B=2,H=3,T=17,D=16."""
+    rng = np.random.default_rng(200)
+    B, H, T, D = 2, 3, 17, 16
+    q, k, v, do = (rng.standard_normal((B, H, T, D), dtype=np.float32) for _ in range(4))
+    tq, tk, tv = (mt.Tensor(a.copy(), requires_grad=True) for a in (q, k, v))
+    scores = (tq @ tk.transpose(-2, -1)) * (1.0 / np.sqrt(D))
+    mask = np.triu(np.ones((T, T), dtype=np.float32), k=1) * -1e9
+    scores = scores + mt.Tensor(mask)
+    attn = RF.softmax(scores, axis=-1)
+    out = attn @ tv
+    (out * mt.Tensor(do)).sum().backward()
+    np.savez(path, q=q, k=k, v=v, do=do, out=out.data, dq=tq.grad, dk=tk.grad, dv=tv.grad,
+             out_dtype=str(out.data.dtype), dq_dtype=str(tq.grad.dtype))
+    print(f"wrote {path.name}: out {out.data.dtype}, dq {tq.grad.dtype}")
+
+
+def mha_module(path):
+    """A whole MultiHeadAttention (transformer.py:14-46), n_embd=48, 3 heads,
+    x (2,17,48); loss = sum(y * dy)."""
+    rng = np.random.default_rng(201)
+    C, H, B, T = 48, 3, 2, 17
+    mha = mt.MultiHeadAttention(C, H, dropout=0.0)
+    w = {}
+    for name in ("q_proj", "k_proj", "v_proj", "out_proj"):
+        w[name + ".weight"] = (rng.standard_normal((C, C)) * 0.1).astype(np.float32)
+        w[name + ".bias"] = (rng.standard_normal(C) * 0.1).astype(np.float32)
+    mha.load_state_dict(w)
+    x = rng.standard_normal((B, T, C), dtype=np.float32)
+    dy = rng.standard_normal((B, T, C), dtype=np.float32)
+    tx = mt.Tensor(x.copy(), requires_grad=True)
+    y = mha(tx)
+    (y * mt.Tensor(dy)).sum().backward()
+    grads = {f"grad.{n}": getattr(getattr(mha, n.split(".")[0]), n.split(".")[1]).grad for n in w}
+    np.savez(path, x=x, dy=dy, y=y.data, dx=tx.grad, **{f"param.{k}": v for k, v in w.items()}, **grads)
+    print(f"wrote {path.name}: y {y.data.dtype}, dx {tx.grad.dtype}")
+
+
+def sample_index(shape, n, seed):
+    r = np.random.default_rng(seed)
+    return np.stack([r.integers(0, s, n) for s in shape], axis=1)
+
+
+def train_curve(cfg: GPTConfig, seed: int, B: int, steps: int, path, full_grads_max=4096):
+    """The harness loop (char_transformer.py:70-77) on the reference: loss per
+    step; at step 0 the logits of batch row 0, every parameter's gradient L2
+    norm, full gradients of small parameters and 64 sampled entries of each
+    large one."""
+    rng = np.random.default_rng(seed)
+    model = ref_model(cfg, rng)
+    opt = mt.Adam(model.parameters(), lr=3e-4)
+    model.train()
+    names = [n for n, _, _ in param_spec(cfg)]
+    losses, extra = [], {}
+    t0 = time.time()
+    for it in range(steps):
+        x, y = draw_batch(rng, cfg.vocab, B, cfg.block)
+        logits = model(x)
+        Bb, T, V = logits.shape
+        loss = mt.cross_entropy_loss(logits.reshape(Bb * T, V), mt.Tensor(y.reshape(-1)))
+        opt.zero_grad()
+        loss.backward()
+        if it == 0:
+            extra["logits0_row0"] = logits.data[0]
+            extra["logits_dtype"] = str(logits.data.dtype)
+            norms = []
+            for n, p in zip(names, model.parameters()):
+                g = p.grad.astype(np.float64)
+                norms.append(np.sqrt((g * g).sum()))
+                if p.grad.size <= full_grads_max:
+                    extra[f"grad.{n}"] = p.grad.copy()
+                else:
+                    ix = sample_index(p.grad.shape, 64, 7)
+                    extra[f"gidx.{n}"] = ix
+                    extra[f"gval.{n}"] = p.grad[tuple(ix.T)]
+            extra["grad_norms"] = np.array(norms)
+        opt.step()
+        losses.append(float(loss.data))
+        print(f"  step {it:2d} loss {losses[-1]:.10f}  ({time.time() - t0:.1f}s)", flush=True)
+    np.savez(path, losses=np.array(losses), seed=seed, B=B, steps=steps, names=np.array(names), **extra)
+    print(f"wrote {path.name}")
+
+
+def greedy(path, seed=100, B=4, T0=8, n_new=24):
+    """Greedy decoding harness over the reference forward: argmax of
+    model(idx[:, -block:]).data[:, -1, :] (transformer.py:97-98), eval mode,
+    no_grad; C0-size model."""
+    rng = np.random.default_rng(seed)
+    model = ref_model(C0, rng)
+    model.eval()
+    prompts = rng.integers(0, C0.vocab, (B, T0))
+    idx = prompts.copy()
+    margins = []
+    with mt.no_grad():
+        for _ in range(n_new):
+            logits = model(idx[:, -C0.block:]).data[:, -1, :]
+            nxt = np.argmax(logits, axis=-1)
+            top2 = np.sort(logits, axis=-1)[:, -2:]
+            margins.append(top2[:, 1] - top2[:, 0])
+            idx = np.concatenate([idx, nxt[:, None]], axis=1)
+    np.savez(path, prompts=prompts, tokens=idx, margins=np.stack(margins, 1), seed=seed)
+    print(f"wrote {path.name}: min top-2 margin {np.min(margins):.3e}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--c2", action="store_true", help="also run the C2 20-step curve (slow)")
+    ap.add_argument("--only-c2", action="store_true")
+    args = ap.parse_args()
+    if not args.only_c2:
+        attention_subgraph(HERE / "attn_subgraph.npz")
+        mha_module(HERE / "mha_module.npz")
+        print("C0 training, 20 steps")
+        train_curve(C0, 0, 16, 20, HERE / "c0_train.npz")
+        greedy(HERE / "greedy_c0.npz")
+    if args.c2 or args.only_c2:
+        print("C2 training, 20 steps")
+        train_curve(C2, 2, 64, 20, HERE / "c2_train.npz")
+
+
+if __name__ == "__main__":
+    main()
