@@ -127,6 +127,140 @@ int mtx_attn_bwd_phase(int phases, int dtype, int B, int H, int Tq, int Tk, int 
                        void* workspace, size_t workspace_bytes,
                        float scale, int causal, int accumulate, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* GEMM                                                                     */
+/* ------------------------------------------------------------------------ */
+/*
+ * Strided-batched fp32 GEMM on MFMA: for b < batch,
+ *   C[b] = alpha * A[b] @ B[b] + beta * C[b] + bias (bias[n], may be NULL).
+ * A is M x K with element (m,k) at a + b*sa_b + m*sa_m + k*sa_k (sa_m or sa_k
+ * must be 1); B is K x N likewise (sb_k or sb_n must be 1); C is M x N.  A
+ * batch stride of 0 broadcasts that operand.  Replaces Tensor.__matmul__
+ * (tensor.py:207-208) and its backward products (tensor.py:210-218, transposes
+ * as stride swaps) and Linear.forward (layers.py:31-37, bias fused).  With a
+ * workspace of mtx_gemm_workspace_bytes() bytes, long-K products are split
+ * over K and reduced deterministically; without one they run unsplit.
+ */
+size_t mtx_gemm_workspace_bytes(int M, int N, int K, int batch);
+int mtx_gemm_f32(int M, int N, int K, int batch,
+                 float alpha, const float* a, int64_t sa_m, int64_t sa_k, int64_t sa_b,
+                 const float* b, int64_t sb_k, int64_t sb_n, int64_t sb_b,
+                 float beta, float* c, int64_t sc_m, int64_t sc_n, int64_t sc_b,
+                 const float* bias, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Elementwise and reductions                                               */
+/* ------------------------------------------------------------------------ */
+enum mtx_ew_op {
+  MTX_EW_COPY = 0,         /* a                         (strided copy)        */
+  MTX_EW_ADD = 1,          /* a + b                     tensor.py:113         */
+  MTX_EW_SUB = 2,          /* a - b                     tensor.py:131         */
+  MTX_EW_MUL = 3,          /* a * b                     tensor.py:150         */
+  MTX_EW_DIV = 4,          /* a / b                     tensor.py:168         */
+  MTX_EW_POW = 5,          /* a ** b                    tensor.py:188         */
+  MTX_EW_AXPBY = 6,        /* alpha*a + beta*b                                */
+  MTX_EW_SCALE_SHIFT = 7,  /* alpha*a + beta                                  */
+  MTX_EW_EXP = 8,          /* exp(a)                    tensor.py:393         */
+  MTX_EW_LOG = 9,          /* log(max(a, 1e-12))        tensor.py:405         */
+  MTX_EW_TANH = 10,        /* tanh(a)                   functional.py:41      */
+  MTX_EW_NEG = 11,         /* -a                                              */
+  MTX_EW_RECIP_CLAMP = 12, /* 1/max(a, 1e-12)           tensor.py:410         */
+  MTX_EW_TANH_GRAD = 13,   /* (1 - a*a) * b             functional.py:46      */
+  MTX_EW_SQUARE = 14,      /* a*a                                             */
+  MTX_EW_SQRT = 15,        /* sqrt(a)                                         */
+  MTX_EW_FILL = 16,        /* alpha (a unused)                                */
+  MTX_EW_MAXIMUM = 17,     /* max(a, b)                                       */
+  MTX_EW_EQ = 18,          /* a == b ? 1 : 0            tensor.py:284         */
+  MTX_EW_GT = 19,          /* a > b ? 1 : 0                                   */
+  MTX_EW_ABS = 20,         /* |a|                       tensor.py:440         */
+  MTX_EW_SIGN = 21,        /* sign(a)                   tensor.py:444         */
+  MTX_EW_NUM_OPS = 22
+};
+/*
+ * out = op(a, b) (+ out if accumulate) over an ndim <= 8 index space `shape`;
+ * each operand has its own element strides (0 = broadcast).  Unary ops ignore
+ * b.  The accumulate form is the reference's _accum_grad (tensor.py:29-33).
+ */
+int mtx_ewise_f32(int op, int ndim, const int64_t* shape,
+                  const float* a, const int64_t* a_strides,
+                  const float* b, const int64_t* b_strides,
+                  float* out, const int64_t* out_strides,
+                  float alpha, float beta, int accumulate, void* stream);
+
+enum mtx_red_op { MTX_RED_SUM = 0, MTX_RED_MAX = 1 };
+/*
+ * out = alpha * reduce(a over the axes with reduce_mask[d] != 0) (+ out).
+ * out is contiguous over the kept axes in order.  Replaces Tensor.sum / mean
+ * (alpha = 1/count) / max (tensor.py:227-294) and _sum_to_shape
+ * (tensor.py:20-26).  Deterministic; long reductions use the workspace.
+ */
+size_t mtx_reduce_workspace_bytes(int ndim, const int64_t* shape, const int* reduce_mask);
+int mtx_reduce_f32(int op, int ndim, const int64_t* shape, const float* a, const int64_t* a_strides,
+                   const int* reduce_mask, float* out, float alpha, int accumulate,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Row kernels (last axis contiguous; rows with a leading stride)           */
+/* ------------------------------------------------------------------------ */
+/*
+ * Softmax (log_mode = 0, functional.py:62-66) or log_softmax (log_mode = 1,
+ * functional.py:81-86) over rows of length L.  causal_tq > 0 treats the rows
+ * as stacked (causal_tq, L) score matrices and hides column j of row i when
+ * j > i + (L - causal_tq): the reference's triu(-1e9) mask (transformer.py:39-40)
+ * with its exact-zero result.
+ */
+int mtx_softmax_fwd_f32(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows, int L,
+                        int causal_tq, int log_mode, void* stream);
+/* Backward: softmax functional.py:69-73, log_softmax functional.py:88-92. */
+int mtx_softmax_bwd_f32(const float* y, int64_t ldy, const float* dy, int64_t lddy, float* dx, int64_t lddx,
+                        int64_t rows, int L, int log_mode, int accumulate, void* stream);
+
+/* LayerNorm, layers.py:82-86 as one pass; saves per-row mean and std. C <= 2048. */
+int mtx_layernorm_fwd_f32(const float* x, int64_t ldx, const float* gamma, const float* beta,
+                          float* y, int64_t ldy, float* mean, float* std_, int64_t rows, int C,
+                          float eps, void* stream);
+size_t mtx_layernorm_bwd_workspace_bytes(int64_t rows, int C);
+/* LayerNorm backward: dx (if non-NULL) and dgamma/dbeta (if non-NULL). */
+int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* gamma, const float* mean,
+                          const float* std_, const float* dy, int64_t lddy, float* dx, int64_t lddx,
+                          float* dgamma, float* dbeta, int64_t rows, int C, int accumulate,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* GELU (tanh form, functional.py:54-59), contiguous n elements. */
+int mtx_gelu_fwd_f32(const float* x, float* y, int64_t n, void* stream);
+int mtx_gelu_bwd_f32(const float* x, const float* dy, float* dx, int64_t n, int accumulate, void* stream);
+
+/*
+ * Softmax cross-entropy with integer labels (loss.py:17-27): per-row
+ * row_loss = lse - logits[label] and lse.  Backward: dlogits = g * scale *
+ * (softmax - onehot), g read from device memory (the upstream scalar grad).
+ */
+int mtx_xent_fwd_f32(const float* logits, int64_t ld, const int64_t* labels, float* row_loss,
+                     float* lse, int64_t rows, int V, void* stream);
+int mtx_xent_bwd_f32(const float* logits, int64_t ld, const int64_t* labels, const float* lse,
+                     const float* gscalar, float scale, float* dlogits, int64_t ldd, int64_t rows, int V,
+                     int accumulate, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Embedding and optimizer                                                  */
+/* ------------------------------------------------------------------------ */
+/* out[i, :] = weight[idx[i], :]   (layers.py:102-104 -> tensor.py:374-375) */
+int mtx_embedding_fwd_f32(const float* weight, int64_t ldw, int64_t V, const int64_t* idx, int64_t n,
+                          float* out, int64_t ldo, int C, void* stream);
+/* dweight[v, :] (+)= sum_{i: idx[i]==v} grad[i, :]  (np.add.at, tensor.py:382); deterministic */
+int mtx_embedding_bwd_f32(const int64_t* idx, int64_t n, const float* grad, int64_t ldg, float* dweight,
+                          int64_t lddw, int64_t V, int C, int accumulate, void* stream);
+
+/*
+ * Adam over many tensors in one launch (optim.py:37-59).  `table` is a device
+ * array of ntensors entries {float* p; const float* g; float* m; float* v;
+ * int64_t n; int64_t block0}, block0 from mtx_adam_blocks (host helper);
+ * total_blocks = last block0 + ceil(last n / 256).
+ */
+int mtx_adam_blocks(const int64_t* sizes, int ntensors, int64_t* block0_out);
+int mtx_adam_f32(const void* table, int ntensors, int64_t total_blocks, double lr, double beta1,
+                 double beta2, double eps, double weight_decay, int step, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,27 @@
 """minitorch_amd -- MI355X-native causal-attention hot path for minitorch.
 
-Kernels live in libmtx_hip.so (HIP, gfx950), reached through the C ABI in
-include/mtx.h via ctypes (``minitorch_amd._lib``).
+The public surface mirrors the reference package (minitorch/__init__.py):
+Tensor, no_grad, Module, Sequential, Linear, LayerNorm, Embedding, GELU,
+Dropout, GPT, TransformerBlock, MultiHeadAttention, cross_entropy_loss, Adam,
+F.  Every operation runs in libmtx_hip.so (HIP, gfx950) through the C ABI in
+include/mtx.h; torch is used only for device memory and streams.
 """
 __version__ = "0.1.0"
+
+from . import functional as F  # noqa: E402
+from .layers import GELU, Dropout, Embedding, LayerNorm, Linear, ReLU, Sigmoid, Softmax, Tanh  # noqa: E402
+from .loss import cross_entropy_loss, mse_loss  # noqa: E402
+from .module import Module, Sequential  # noqa: E402
+from .optim import SGD, Adam  # noqa: E402
+from .tensor import Tensor, cat, no_grad, stack  # noqa: E402
+from .transformer import GPT, MultiHeadAttention, TransformerBlock  # noqa: E402
+
+__all__ = [
+    "Tensor", "no_grad", "cat", "stack",
+    "Module", "Sequential",
+    "Linear", "ReLU", "Sigmoid", "Tanh", "Softmax", "Dropout", "GELU", "LayerNorm", "Embedding",
+    "GPT", "TransformerBlock", "MultiHeadAttention",
+    "mse_loss", "cross_entropy_loss",
+    "SGD", "Adam",
+    "F",
+]

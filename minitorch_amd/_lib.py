@@ -27,6 +27,14 @@ _I = C.c_int
 _I64P = C.POINTER(C.c_int64)
 _F = C.c_float
 _SZ = C.c_size_t
+_I64 = C.c_int64
+_IP = C.POINTER(C.c_int)
+_D = C.c_double
+
+EW = dict(COPY=0, ADD=1, SUB=2, MUL=3, DIV=4, POW=5, AXPBY=6, SCALE_SHIFT=7, EXP=8, LOG=9, TANH=10,
+          NEG=11, RECIP_CLAMP=12, TANH_GRAD=13, SQUARE=14, SQRT=15, FILL=16, MAXIMUM=17, EQ=18, GT=19,
+          ABS=20, SIGN=21)
+RED_SUM, RED_MAX = 0, 1
 
 # name -> (restype, argtypes); mirrors include/mtx.h
 SIGNATURES = {
@@ -46,6 +54,29 @@ SIGNATURES = {
                                 _P,
                                 _P, _I64P, _P, _I64P, _P, _I64P,
                                 _P, _SZ, _F, _I, _I, _P]),
+    "mtx_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "mtx_gemm_f32": (_I, [_I, _I, _I, _I,
+                          _F, _P, _I64, _I64, _I64,
+                          _P, _I64, _I64, _I64,
+                          _F, _P, _I64, _I64, _I64,
+                          _P, _P, _SZ, _P]),
+    "mtx_ewise_f32": (_I, [_I, _I, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _F, _F, _I, _P]),
+    "mtx_reduce_workspace_bytes": (_SZ, [_I, _I64P, _IP]),
+    "mtx_reduce_f32": (_I, [_I, _I, _I64P, _P, _I64P, _IP, _P, _F, _I, _P, _SZ, _P]),
+    "mtx_softmax_fwd_f32": (_I, [_P, _I64, _P, _I64, _I64, _I, _I, _I, _P]),
+    "mtx_softmax_bwd_f32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I, _I, _I, _P]),
+    "mtx_layernorm_fwd_f32": (_I, [_P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _I, _F, _P]),
+    "mtx_layernorm_bwd_workspace_bytes": (_SZ, [_I64, _I]),
+    "mtx_layernorm_bwd_f32": (_I, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _I64, _I, _I,
+                                   _P, _SZ, _P]),
+    "mtx_gelu_fwd_f32": (_I, [_P, _P, _I64, _P]),
+    "mtx_gelu_bwd_f32": (_I, [_P, _P, _P, _I64, _I, _P]),
+    "mtx_xent_fwd_f32": (_I, [_P, _I64, _P, _P, _P, _I64, _I, _P]),
+    "mtx_xent_bwd_f32": (_I, [_P, _I64, _P, _P, _P, _F, _P, _I64, _I64, _I, _I, _P]),
+    "mtx_embedding_fwd_f32": (_I, [_P, _I64, _I64, _P, _I64, _P, _I64, _I, _P]),
+    "mtx_embedding_bwd_f32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I, _I, _P]),
+    "mtx_adam_blocks": (_I, [_I64P, _I, _I64P]),
+    "mtx_adam_f32": (_I, [_P, _I, _I64, _D, _D, _D, _D, _D, _I, _P]),
 }
 
 

@@ -1,0 +1,141 @@
+// Embedding gather / deterministic scatter-add, and multi-tensor Adam (fp32).
+//
+// Embedding.forward is Tensor.__getitem__ with an index array
+// (layers.py:102-104 -> tensor.py:374-387); its backward is
+// np.add.at(grad, idx, out.grad) (tensor.py:382).  Repeated ids must add up:
+// here one workgroup owns one table row and adds the matching token rows in
+// token order, so the result is deterministic (no atomics).
+//
+// Adam.step (optim.py:37-59) over every parameter tensor in one launch: the
+// caller passes a device table with one entry per tensor.  The arithmetic
+// follows the reference's float32 expression order:
+//   m = b1*m + (1-b1)*g;  v = b2*v + (1-b2)*(g*g)
+//   p -= (lr * (m / (1-b1^t))) / (sqrt(v / (1-b2^t)) + eps)
+#include "mtx_common.h"
+
+namespace mtx {
+namespace {
+
+__global__ __launch_bounds__(256) void embed_gather_kernel(const float* __restrict__ w, int64_t ldw,
+                                                           const int64_t* __restrict__ idx,
+                                                           float* __restrict__ out, int64_t ldo, int64_t n, int C,
+                                                           int64_t V) {
+  const int64_t total = n * C;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / C;
+    const int c = (int)(e % C);
+    int64_t r = idx[i];
+    r = r < 0 ? 0 : (r >= V ? V - 1 : r);  // ids are validated on the host
+    out[i * ldo + c] = w[r * ldw + c];
+  }
+}
+
+// dW[v, c] (+)= sum over tokens i with idx[i] == v of g[i, c], in token order
+__global__ __launch_bounds__(256) void embed_scatter_kernel(const int64_t* __restrict__ idx,
+                                                            const float* __restrict__ g, int64_t ldg,
+                                                            float* __restrict__ dw, int64_t lddw, int64_t n, int C,
+                                                            int accumulate) {
+  __shared__ int64_t ids[256];
+  const int64_t v = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  float acc = 0.f;
+  for (int64_t base = 0; base < n; base += 256) {
+    const int64_t i = base + threadIdx.x;
+    __syncthreads();
+    ids[threadIdx.x] = i < n ? idx[i] : -1;
+    __syncthreads();
+    const int cnt = (int)min<int64_t>(256, n - base);
+    if (c < C) {
+      for (int j = 0; j < cnt; ++j)
+        if (ids[j] == v) acc += g[(base + j) * ldg + c];
+    }
+  }
+  if (c < C) {
+    float* p = dw + v * lddw + c;
+    *p = accumulate ? *p + acc : acc;
+  }
+}
+
+struct AdamEntry {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  int64_t n;
+  int64_t block0;  // first block of this tensor
+};
+
+__global__ __launch_bounds__(256) void adam_kernel(const AdamEntry* __restrict__ tab, int ntab, float lr, float b1,
+                                                   float b2, float c1, float c2, float bc1, float bc2, float eps,
+                                                   float wd) {
+  // locate this block's tensor (tables are short: linear scan)
+  int t = 0;
+  while (t + 1 < ntab && tab[t + 1].block0 <= (int64_t)blockIdx.x) ++t;
+  const AdamEntry e = tab[t];
+  const int64_t i = ((int64_t)blockIdx.x - e.block0) * 256 + threadIdx.x;
+  if (i >= e.n) return;
+  float g = e.g[i];
+  if (wd != 0.f) g = g + wd * e.p[i];
+  const float m = b1 * e.m[i] + c1 * g;
+  const float v = b2 * e.v[i] + c2 * (g * g);
+  e.m[i] = m;
+  e.v[i] = v;
+  const float mh = m / bc1;
+  const float vh = v / bc2;
+  e.p[i] = e.p[i] - (lr * mh) / (sqrtf(vh) + eps);
+}
+
+}  // namespace
+}  // namespace mtx
+
+using namespace mtx;
+
+extern "C" int mtx_embedding_fwd_f32(const float* weight, int64_t ldw, int64_t V, const int64_t* idx, int64_t n,
+                                     float* out, int64_t ldo, int C, void* stream) {
+  MTX_CHECK_ARG(weight && idx && out, "embedding: null pointer");
+  MTX_CHECK_SHAPE(n >= 0 && C >= 1 && V >= 1 && ldw >= C && ldo >= C, "embedding: bad shape");
+  if (n == 0) return MTX_OK;
+  const int blocks = (int)std::min<int64_t>((n * C + 255) / 256, 16384);
+  hipLaunchKernelGGL(embed_gather_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), weight, ldw,
+                     idx, out, ldo, n, C, V);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_embedding_bwd_f32(const int64_t* idx, int64_t n, const float* grad, int64_t ldg, float* dweight,
+                                     int64_t lddw, int64_t V, int C, int accumulate, void* stream) {
+  MTX_CHECK_ARG(idx && grad && dweight, "embedding_bwd: null pointer");
+  MTX_CHECK_SHAPE(n >= 0 && C >= 1 && V >= 1 && V < (1 << 30) && ldg >= C && lddw >= C, "embedding_bwd: bad shape");
+  hipLaunchKernelGGL(embed_scatter_kernel, dim3((unsigned)V, (C + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), idx, grad, ldg, dweight, lddw, n, C, accumulate ? 1 : 0);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_adam_blocks(const int64_t* sizes, int ntensors, int64_t* block0_out) {
+  MTX_CHECK_ARG(sizes && block0_out && ntensors >= 0, "adam_blocks: bad argument");
+  int64_t b = 0;
+  for (int i = 0; i < ntensors; ++i) {
+    block0_out[i] = b;
+    b += (sizes[i] + 255) / 256;
+  }
+  return MTX_OK;
+}
+
+extern "C" int mtx_adam_f32(const void* table, int ntensors, int64_t total_blocks, double lr, double beta1,
+                            double beta2, double eps, double weight_decay, int step, void* stream) {
+  MTX_CHECK_ARG(table && ntensors >= 1, "adam: empty table");
+  MTX_CHECK_ARG(step >= 1, "adam: step must be >= 1");
+  MTX_CHECK_SHAPE(total_blocks >= 0 && total_blocks < (1LL << 31), "adam: bad block count");
+  if (total_blocks == 0) return MTX_OK;
+  // scalars rounded to float32 exactly as NumPy does for python-float * float32 array
+  const float c1 = (float)(1.0 - beta1), c2 = (float)(1.0 - beta2);
+  const float bc1 = (float)(1.0 - std::pow(beta1, (double)step));
+  const float bc2 = (float)(1.0 - std::pow(beta2, (double)step));
+  hipLaunchKernelGGL(adam_kernel, dim3((unsigned)total_blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const AdamEntry*>(table), ntensors, (float)lr, (float)beta1, (float)beta2, c1, c2,
+                     bc1, bc2, (float)eps, (float)weight_decay);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}

@@ -1,0 +1,426 @@
+// Row-wise fused kernels (fp32): softmax, log_softmax, LayerNorm, GELU and
+// softmax cross-entropy, forward and backward.
+//
+// Replaces, per row of the last axis:
+//   F.softmax        functional.py:62-78  (optionally with the causal mask of
+//                    transformer.py:39-40 applied as exact zeros)
+//   F.log_softmax    functional.py:81-97
+//   LayerNorm        layers.py:73-89 (biased variance, eps inside the sqrt,
+//                    x_hat = diff / std: the 9-node composite in one pass)
+//   F.gelu           functional.py:54-59 (tanh approximation with the float32
+//                    constants the reference's Tensor(scalar) produces)
+//   cross_entropy    loss.py:17-27 (log_softmax + one-hot NLL, mean over N)
+// One wave64 per row; rows are independent, so every result is deterministic.
+#include "mtx_common.h"
+
+namespace mtx {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// visible(j) for causal rows: row r of a stack of (Tq, L) matrices
+__device__ __forceinline__ int causal_limit(int64_t row, int causal_tq, int L) {
+  if (causal_tq <= 0) return L;
+  const int i = (int)(row % causal_tq);
+  return min(L, i + (L - causal_tq) + 1);
+}
+
+__global__ __launch_bounds__(256) void softmax_fwd_kernel(const float* __restrict__ x, int64_t ldx,
+                                                          float* __restrict__ y, int64_t ldy,
+                                                          int64_t rows, int L, int causal_tq, int log_mode) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* xr = x + row * ldx;
+  float* yr = y + row * ldy;
+  const int lim = causal_limit(row, causal_tq, L);
+  float mx = -INFINITY;
+  for (int j = lane; j < lim; j += 64) mx = fmaxf(mx, xr[j]);
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int j = lane; j < lim; j += 64) s += expf(xr[j] - mx);
+  s = wave_sum(s);
+  if (log_mode) {
+    const float lse = logf(s);
+    for (int j = lane; j < L; j += 64) yr[j] = j < lim ? (xr[j] - mx) - lse : -INFINITY;
+  } else {
+    for (int j = lane; j < L; j += 64) yr[j] = j < lim ? expf(xr[j] - mx) / s : 0.f;
+  }
+}
+
+// softmax:     dx = y * (dy - sum(y * dy))
+// log_softmax: dx = dy - exp(y) * sum(dy)
+__global__ __launch_bounds__(256) void softmax_bwd_kernel(const float* __restrict__ y, int64_t ldy,
+                                                          const float* __restrict__ dy, int64_t lddy,
+                                                          float* __restrict__ dx, int64_t lddx,
+                                                          int64_t rows, int L, int log_mode, int accumulate) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* yr = y + row * ldy;
+  const float* gr = dy + row * lddy;
+  float* dr = dx + row * lddx;
+  float s = 0.f;
+  if (log_mode) {
+    for (int j = lane; j < L; j += 64) s += gr[j];
+  } else {
+    for (int j = lane; j < L; j += 64) s += yr[j] * gr[j];
+  }
+  s = wave_sum(s);
+  for (int j = lane; j < L; j += 64) {
+    float v = log_mode ? gr[j] - expf(yr[j]) * s : yr[j] * (gr[j] - s);
+    if (accumulate) v += dr[j];
+    dr[j] = v;
+  }
+}
+
+// LayerNorm forward: y = (x - mean) / sqrt(var + eps) * gamma + beta.
+// Saves mean and std per row for the backward.
+template <int VPL>  // values per lane held in registers (C <= 64 * VPL)
+__global__ __launch_bounds__(256) void layernorm_fwd_kernel(const float* __restrict__ x, int64_t ldx,
+                                                            const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta,
+                                                            float* __restrict__ y, int64_t ldy,
+                                                            float* __restrict__ mean_out,
+                                                            float* __restrict__ std_out,
+                                                            int64_t rows, int C, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* xr = x + row * ldx;
+  float v[VPL];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int j = lane + 64 * i;
+    v[i] = j < C ? xr[j] : 0.f;
+    s += v[i];
+  }
+  const float mean = wave_sum(s) / (float)C;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int j = lane + 64 * i;
+    const float d = j < C ? v[i] - mean : 0.f;
+    v[i] = d;
+    q += d * d;
+  }
+  const float var = wave_sum(q) / (float)C;
+  const float sd = sqrtf(var + eps);
+  float* yr = y + row * ldy;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int j = lane + 64 * i;
+    if (j < C) yr[j] = (v[i] / sd) * gamma[j] + beta[j];
+  }
+  if (lane == 0) {
+    mean_out[row] = mean;
+    std_out[row] = sd;
+  }
+}
+
+// dx = (1/std) * (g - mean(g) - xh * mean(g * xh)), g = dy * gamma
+template <int VPL>
+__global__ __launch_bounds__(256) void layernorm_bwd_kernel(const float* __restrict__ x, int64_t ldx,
+                                                            const float* __restrict__ gamma,
+                                                            const float* __restrict__ mean_in,
+                                                            const float* __restrict__ std_in,
+                                                            const float* __restrict__ dy, int64_t lddy,
+                                                            float* __restrict__ dx, int64_t lddx,
+                                                            int64_t rows, int C, int accumulate) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float mean = mean_in[row], sd = std_in[row];
+  const float* xr = x + row * ldx;
+  const float* gr = dy + row * lddy;
+  float xh[VPL], gg[VPL];
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int j = lane + 64 * i;
+    if (j < C) {
+      xh[i] = (xr[j] - mean) / sd;
+      gg[i] = gr[j] * gamma[j];
+    } else {
+      xh[i] = 0.f;
+      gg[i] = 0.f;
+    }
+    s1 += gg[i];
+    s2 += gg[i] * xh[i];
+  }
+  s1 = wave_sum(s1) / (float)C;
+  s2 = wave_sum(s2) / (float)C;
+  float* dr = dx + row * lddx;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int j = lane + 64 * i;
+    if (j < C) {
+      float v = (gg[i] - s1 - xh[i] * s2) / sd;
+      if (accumulate) v += dr[j];
+      dr[j] = v;
+    }
+  }
+}
+
+// dgamma[c] = sum_r dy[r,c] * xh[r,c], dbeta[c] = sum_r dy[r,c]; rows split
+// into chunks, partials [split][2][C] in ws, combined in chunk order.
+__global__ __launch_bounds__(256) void layernorm_param_partial(const float* __restrict__ x, int64_t ldx,
+                                                               const float* __restrict__ mean_in,
+                                                               const float* __restrict__ std_in,
+                                                               const float* __restrict__ dy, int64_t lddy,
+                                                               float* __restrict__ ws, int64_t rows, int C,
+                                                               int64_t chunk) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int s = blockIdx.y;
+  if (c >= C) return;
+  const int64_t r0 = (int64_t)s * chunk, r1 = min(rows, r0 + chunk);
+  float ag = 0.f, ab = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float g = dy[r * lddy + c];
+    ag += g * ((x[r * ldx + c] - mean_in[r]) / std_in[r]);
+    ab += g;
+  }
+  ws[((int64_t)s * 2 + 0) * C + c] = ag;
+  ws[((int64_t)s * 2 + 1) * C + c] = ab;
+}
+
+__global__ __launch_bounds__(256) void layernorm_param_combine(const float* __restrict__ ws, int nsplit, int C,
+                                                               float* __restrict__ dgamma,
+                                                               float* __restrict__ dbeta, int accumulate) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  float ag = 0.f, ab = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    ag += ws[((int64_t)s * 2 + 0) * C + c];
+    ab += ws[((int64_t)s * 2 + 1) * C + c];
+  }
+  if (accumulate) { ag += dgamma[c]; ab += dbeta[c]; }
+  dgamma[c] = ag;
+  dbeta[c] = ab;
+}
+
+// GELU, tanh form with the reference's float32 constants
+__device__ __forceinline__ float gelu_c0() { return 0.7978845834732056f; }  // float32(sqrt(2/pi))
+__device__ __forceinline__ float gelu_c1() { return 0.044714998453855515f; }  // float32(0.044715)
+
+__global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = x[i];
+    const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
+    y[i] = v * 0.5f * (tanhf(inner) + 1.0f);
+  }
+}
+
+__global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__ x, const float* __restrict__ dy,
+                                                       float* __restrict__ dx, int64_t n, int accumulate) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = x[i];
+    const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
+    const float t = tanhf(inner);
+    const float d = 0.5f * (t + 1.0f) + 0.5f * v * (1.0f - t * t) * gelu_c0() * (1.0f + 3.0f * gelu_c1() * v * v);
+    float r = d * dy[i];
+    if (accumulate) r += dx[i];
+    dx[i] = r;
+  }
+}
+
+// Cross-entropy forward: per-row loss_i = lse_i - x[i, y_i]; lse saved.
+__global__ __launch_bounds__(256) void xent_fwd_kernel(const float* __restrict__ x, int64_t ldx,
+                                                       const int64_t* __restrict__ labels,
+                                                       float* __restrict__ row_loss, float* __restrict__ lse_out,
+                                                       int64_t rows, int V) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* xr = x + row * ldx;
+  float mx = -INFINITY;
+  for (int j = lane; j < V; j += 64) mx = fmaxf(mx, xr[j]);
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int j = lane; j < V; j += 64) s += expf(xr[j] - mx);
+  s = wave_sum(s);
+  if (lane == 0) {
+    const float lse = mx + logf(s);
+    int64_t y = labels[row];
+    y = y < 0 ? 0 : (y >= V ? V - 1 : y);  // labels are validated on the host
+    row_loss[row] = lse - xr[y];
+    lse_out[row] = lse;
+  }
+}
+
+// dx[i,j] = g * (exp(x[i,j] - lse_i) - [j == y_i]) * scale, g read from device
+__global__ __launch_bounds__(256) void xent_bwd_kernel(const float* __restrict__ x, int64_t ldx,
+                                                       const int64_t* __restrict__ labels,
+                                                       const float* __restrict__ lse,
+                                                       const float* __restrict__ gscalar, float scale,
+                                                       float* __restrict__ dx, int64_t lddx, int64_t rows, int V,
+                                                       int accumulate) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float g = gscalar[0] * scale;
+  const float l = lse[row];
+  const int64_t y = labels[row];
+  const float* xr = x + row * ldx;
+  float* dr = dx + row * lddx;
+  for (int j = lane; j < V; j += 64) {
+    float v = g * (expf(xr[j] - l) - (j == y ? 1.0f : 0.0f));
+    if (accumulate) v += dr[j];
+    dr[j] = v;
+  }
+}
+
+int rows_grid(int64_t rows) { return (int)((rows + 3) / 4); }
+
+template <template <int> class K>
+struct Dummy {};
+
+}  // namespace
+}  // namespace mtx
+
+using namespace mtx;
+
+extern "C" int mtx_softmax_fwd_f32(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows, int L,
+                                   int causal_tq, int log_mode, void* stream) {
+  MTX_CHECK_ARG(x && y, "softmax: null pointer");
+  MTX_CHECK_SHAPE(rows >= 0 && L >= 1 && ldx >= L && ldy >= L, "softmax: bad rows/L/ld");
+  MTX_CHECK_SHAPE(causal_tq >= 0 && causal_tq <= L, "softmax: causal_tq must be in [0, L]");
+  if (rows == 0) return MTX_OK;
+  MTX_CHECK_SHAPE(rows / 4 < (1LL << 31), "softmax: too many rows");
+  hipLaunchKernelGGL(softmax_fwd_kernel, dim3(rows_grid(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     x, ldx, y, ldy, rows, L, causal_tq, log_mode ? 1 : 0);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_softmax_bwd_f32(const float* y, int64_t ldy, const float* dy, int64_t lddy, float* dx,
+                                   int64_t lddx, int64_t rows, int L, int log_mode, int accumulate, void* stream) {
+  MTX_CHECK_ARG(y && dy && dx, "softmax_bwd: null pointer");
+  MTX_CHECK_SHAPE(rows >= 0 && L >= 1 && ldy >= L && lddy >= L && lddx >= L, "softmax_bwd: bad rows/L/ld");
+  if (rows == 0) return MTX_OK;
+  hipLaunchKernelGGL(softmax_bwd_kernel, dim3(rows_grid(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     y, ldy, dy, lddy, dx, lddx, rows, L, log_mode ? 1 : 0, accumulate ? 1 : 0);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_layernorm_fwd_f32(const float* x, int64_t ldx, const float* gamma, const float* beta,
+                                     float* y, int64_t ldy, float* mean, float* std_, int64_t rows, int C,
+                                     float eps, void* stream) {
+  MTX_CHECK_ARG(x && gamma && beta && y && mean && std_, "layernorm: null pointer");
+  MTX_CHECK_SHAPE(rows >= 0 && C >= 1 && C <= 64 * 32 && ldx >= C && ldy >= C,
+                  "layernorm: C must be in [1, 2048] and ld >= C");
+  if (rows == 0) return MTX_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int vpl = (C + 63) / 64;
+  dim3 gr(rows_grid(rows)), bl(256);
+#define LN_F(V) hipLaunchKernelGGL(layernorm_fwd_kernel<V>, gr, bl, 0, st, x, ldx, gamma, beta, y, ldy, mean, std_, rows, C, eps)
+  if (vpl <= 1) LN_F(1);
+  else if (vpl <= 2) LN_F(2);
+  else if (vpl <= 4) LN_F(4);
+  else if (vpl <= 8) LN_F(8);
+  else if (vpl <= 16) LN_F(16);
+  else LN_F(32);
+#undef LN_F
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" size_t mtx_layernorm_bwd_workspace_bytes(int64_t rows, int C) {
+  if (rows < 1 || C < 1) return 0;
+  const int64_t nsplit = std::min<int64_t>(256, (rows + 63) / 64);
+  return (size_t)nsplit * 2 * C * sizeof(float);
+}
+
+extern "C" int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* gamma, const float* mean,
+                                     const float* std_, const float* dy, int64_t lddy, float* dx, int64_t lddx,
+                                     float* dgamma, float* dbeta, int64_t rows, int C, int accumulate,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  MTX_CHECK_ARG(x && gamma && mean && std_ && dy, "layernorm_bwd: null pointer");
+  MTX_CHECK_SHAPE(rows >= 0 && C >= 1 && C <= 2048 && ldx >= C && lddy >= C, "layernorm_bwd: bad shape");
+  MTX_CHECK_ARG(!dx || lddx >= C, "layernorm_bwd: bad lddx");
+  MTX_CHECK_ARG((dgamma == nullptr) == (dbeta == nullptr), "layernorm_bwd: dgamma and dbeta go together");
+  if (rows == 0) return MTX_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dx) {
+    const int vpl = (C + 63) / 64;
+    dim3 gr(rows_grid(rows)), bl(256);
+#define LN_B(V) hipLaunchKernelGGL(layernorm_bwd_kernel<V>, gr, bl, 0, st, x, ldx, gamma, mean, std_, dy, lddy, dx, lddx, rows, C, accumulate ? 1 : 0)
+    if (vpl <= 1) LN_B(1);
+    else if (vpl <= 2) LN_B(2);
+    else if (vpl <= 4) LN_B(4);
+    else if (vpl <= 8) LN_B(8);
+    else if (vpl <= 16) LN_B(16);
+    else LN_B(32);
+#undef LN_B
+    MTX_LAUNCHED();
+  }
+  if (dgamma) {
+    const size_t need = mtx_layernorm_bwd_workspace_bytes(rows, C);
+    MTX_CHECK_ARG(workspace && workspace_bytes >= need, "layernorm_bwd: workspace too small (%zu < %zu)",
+                  workspace_bytes, need);
+    const int nsplit = (int)(need / (2 * C * sizeof(float)));
+    const int64_t chunk = (rows + nsplit - 1) / nsplit;
+    float* ws = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(layernorm_param_partial, dim3((C + 255) / 256, nsplit), dim3(256), 0, st, x, ldx, mean,
+                       std_, dy, lddy, ws, rows, C, chunk);
+    MTX_LAUNCHED();
+    hipLaunchKernelGGL(layernorm_param_combine, dim3((C + 255) / 256), dim3(256), 0, st, ws, nsplit, C, dgamma,
+                       dbeta, accumulate ? 1 : 0);
+    MTX_LAUNCHED();
+  }
+  return MTX_OK;
+}
+
+extern "C" int mtx_gelu_fwd_f32(const float* x, float* y, int64_t n, void* stream) {
+  MTX_CHECK_ARG(x && y && n >= 0, "gelu: bad argument");
+  if (n == 0) return MTX_OK;
+  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 16384);
+  hipLaunchKernelGGL(gelu_fwd_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x, y, n);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_gelu_bwd_f32(const float* x, const float* dy, float* dx, int64_t n, int accumulate,
+                                void* stream) {
+  MTX_CHECK_ARG(x && dy && dx && n >= 0, "gelu_bwd: bad argument");
+  if (n == 0) return MTX_OK;
+  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 16384);
+  hipLaunchKernelGGL(gelu_bwd_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), x, dy, dx, n,
+                     accumulate ? 1 : 0);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_xent_fwd_f32(const float* logits, int64_t ld, const int64_t* labels, float* row_loss,
+                                float* lse, int64_t rows, int V, void* stream) {
+  MTX_CHECK_ARG(logits && labels && row_loss && lse, "xent: null pointer");
+  MTX_CHECK_SHAPE(rows >= 0 && V >= 1 && ld >= V, "xent: bad shape");
+  if (rows == 0) return MTX_OK;
+  hipLaunchKernelGGL(xent_fwd_kernel, dim3(rows_grid(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     logits, ld, labels, row_loss, lse, rows, V);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_xent_bwd_f32(const float* logits, int64_t ld, const int64_t* labels, const float* lse,
+                                const float* gscalar, float scale, float* dlogits, int64_t ldd, int64_t rows, int V,
+                                int accumulate, void* stream) {
+  MTX_CHECK_ARG(logits && labels && lse && gscalar && dlogits, "xent_bwd: null pointer");
+  MTX_CHECK_SHAPE(rows >= 0 && V >= 1 && ld >= V && ldd >= V, "xent_bwd: bad shape");
+  if (rows == 0) return MTX_OK;
+  hipLaunchKernelGGL(xent_bwd_kernel, dim3(rows_grid(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     logits, ld, labels, lse, gscalar, scale, dlogits, ldd, rows, V, accumulate ? 1 : 0);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}

@@ -1,0 +1,256 @@
+"""Stateless differentiable functions (the reference's functional.py, plus the
+fused ops the GPU path adds).
+
+Reference functions, same names and semantics: relu, sigmoid, tanh, gelu,
+softmax, log_softmax (functional.py:9-97).  Added fused ops, each one autograd
+node with a hand-written backward (the precedent is the reference's Conv2d,
+conv.py:66-95):
+  linear(x, W, b)              x @ W + b with the bias in the GEMM epilogue
+  causal_attention(q, k, v)    transformer.py:36-44 as one flash kernel
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import device as dev
+from . import kernels as K
+from .device import DeviceArray
+from .tensor import Tensor, _accum_grad, _grad_target, grad_enabled
+
+
+def _track(*ts):
+    return grad_enabled() and any(t.requires_grad for t in ts)
+
+
+def _node(data, prev, op, backward, track):
+    out = Tensor(data, requires_grad=track)
+    if track:
+        out._backward = backward
+        out._prev = set(prev)
+        out._op = op
+    return out
+
+
+def relu(x):
+    """max(0, x) (functional.py:9-21)."""
+    data = dev.empty(x.shape)
+    K.ewise("MAXIMUM", data.t, x.data.t, dev.const(0.0).t)
+    out = None
+
+    def _backward():
+        if x.requires_grad:
+            g = dev.empty(x.shape)
+            K.ewise("GT", g.t, x.data.t, dev.const(0.0).t)
+            K.ewise("MUL", g.t, g.t, out.grad.t)
+            _accum_grad(x, g, owned=True)
+
+    out = _node(data, (x,), "relu", _backward, _track(x))
+    return out
+
+
+def sigmoid(x):
+    """1 / (1 + exp(-x)) (functional.py:24-36)."""
+    data = dev.empty(x.shape)
+    K.ewise("NEG", data.t, x.data.t)
+    K.ewise("EXP", data.t, data.t)
+    K.ewise("SCALE_SHIFT", data.t, data.t, alpha=1.0, beta=1.0)
+    K.ewise("DIV", data.t, dev.const(1.0).t.expand(x.shape), data.t)
+    out = None
+
+    def _backward():
+        if x.requires_grad:
+            g = dev.empty(x.shape)
+            K.ewise("SCALE_SHIFT", g.t, out.data.t, alpha=-1.0, beta=1.0)
+            K.ewise("MUL", g.t, g.t, out.data.t)
+            K.ewise("MUL", g.t, g.t, out.grad.t)
+            _accum_grad(x, g, owned=True)
+
+    out = _node(data, (x,), "sigmoid", _backward, _track(x))
+    return out
+
+
+def tanh(x):
+    """Hyperbolic tangent (functional.py:39-51)."""
+    data = dev.empty(x.shape)
+    K.ewise("TANH", data.t, x.data.t)
+    out = None
+
+    def _backward():
+        if x.requires_grad:
+            g = dev.empty(x.shape)
+            K.ewise("TANH_GRAD", g.t, out.data.t, out.grad.t)
+            _accum_grad(x, g, owned=True)
+
+    out = _node(data, (x,), "tanh", _backward, _track(x))
+    return out
+
+
+def gelu(x):
+    """GELU, tanh approximation (functional.py:54-59), as one fused node: the
+    same formula and float32 constants as the reference's 8-node composite."""
+    xc = x.data.contiguous()
+    data = dev.empty(x.shape)
+    K.gelu_fwd(xc.t, data.t)
+    out = None
+
+    def _backward():
+        if x.requires_grad:
+            target, acc = _grad_target(x)
+            K.gelu_bwd(xc.t, out.grad.contiguous().t, target.t, accumulate=acc)
+
+    out = _node(data, (x,), "gelu", _backward, _track(x))
+    return out
+
+
+def _last_axis(x, axis):
+    axis = axis % x.ndim
+    if axis != x.ndim - 1:
+        raise NotImplementedError("softmax over a non-last axis: transpose first")
+
+
+def softmax(x, axis=-1, causal=False):
+    """Softmax over the last axis (functional.py:62-78).  causal=True applies
+    the causal mask of transformer.py:39-40 to a (..., Tq, L) score tensor:
+    hidden entries come out exactly 0, as the reference's -1e9 add gives."""
+    _last_axis(x, axis)
+    xc = x.data.contiguous()
+    data = dev.empty(x.shape)
+    K.softmax_fwd(xc.t, data.t, causal_tq=x.shape[-2] if causal else 0)
+    out = None
+
+    def _backward():
+        if x.requires_grad:
+            target, acc = _grad_target(x)
+            K.softmax_bwd(out.data.t, out.grad.contiguous().t, target.t, accumulate=acc)
+
+    out = _node(data, (x,), "softmax", _backward, _track(x))
+    return out
+
+
+def log_softmax(x, axis=-1):
+    """log(softmax(x)) over the last axis (functional.py:81-97)."""
+    _last_axis(x, axis)
+    xc = x.data.contiguous()
+    data = dev.empty(x.shape)
+    K.softmax_fwd(xc.t, data.t, log=True)
+    out = None
+
+    def _backward():
+        if x.requires_grad:
+            target, acc = _grad_target(x)
+            K.softmax_bwd(out.data.t, out.grad.contiguous().t, target.t, log=True, accumulate=acc)
+
+    out = _node(data, (x,), "log_softmax", _backward, _track(x))
+    return out
+
+
+def linear(x, weight, bias=None):
+    """x @ W + b (layers.py:31-37) as one node: bias fused into the GEMM
+    epilogue; backward dX = dY W^T, dW = X^T dY (batch folded into the
+    contraction), db = column sums of dY."""
+    from .linalg import bmm, matmul_data, matmul_grad_b
+
+    if x.shape[-1] != weight.shape[0]:
+        raise AssertionError(f"Linear expects last dim {weight.shape[0]}, got {x.shape[-1]}")
+    N = weight.shape[1]
+    out_shape = tuple(x.shape[:-1]) + (N,)
+    data = dev.empty(out_shape)
+    xt = x.data.t if x.ndim >= 2 else x.data.t.unsqueeze(0)
+    ot = data.t if x.ndim >= 2 else data.t.unsqueeze(0)
+    bmm(xt, weight.data.t, ot, bias=bias.data.t if bias is not None else None)
+    prev = (x, weight) + ((bias,) if bias is not None else ())
+    out = None
+
+    def _backward():
+        g = out.grad
+        if x.requires_grad:
+            target, acc = _grad_target(x)
+            gt = g.t if x.ndim >= 2 else g.t.unsqueeze(0)
+            tt = target.t if x.ndim >= 2 else target.t.unsqueeze(0)
+            bmm(gt, weight.data.t.transpose(0, 1), tt, beta=1.0 if acc else 0.0)
+        if weight.requires_grad:
+            matmul_grad_b(x.data, g, weight)
+        if bias is not None and bias.requires_grad:
+            target, acc = _grad_target(bias)
+            K.reduce(g.t, list(range(g.ndim - 1)), target.t, accumulate=acc)
+
+    out = _node(data, prev, "linear", _backward, _track(*prev))
+    return out
+
+
+def causal_attention(q, k, v, scale=None):
+    """softmax(q k^T * scale + causal mask) @ v for (B, H, T, D) tensors --
+    exactly transformer.py:36-44 -- as one fused flash kernel (libmtx_hip
+    mtx_attn_fwd / mtx_attn_bwd).  q, k, v may be the strided views that
+    _split_heads makes (no copies); gradients come back in the same layout."""
+    D = q.shape[-1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    qt, kt, vt = q.data.t, k.data.t, v.data.t
+    o, lse = K.attn_fwd(qt, kt, vt, scale, True)
+    out = None
+
+    def _backward():
+        do = out.grad.contiguous().t
+        need = [t.requires_grad for t in (q, k, v)]
+        if not any(need):
+            return
+        tgt = []
+        for t in (q, k, v):
+            if t.requires_grad and t.grad is not None:
+                tgt.append((t.grad.t, True))
+            else:
+                buf = dev.DeviceArray(torch_empty_like(t.data.t))
+                tgt.append((buf.t, False))
+        acc_all = all(a for _, a in tgt)
+        none_acc = not any(a for _, a in tgt)
+        if acc_all or none_acc:
+            K.attn_bwd(qt, kt, vt, o, do, lse, scale, True, dq=tgt[0][0], dk=tgt[1][0], dv=tgt[2][0],
+                       accumulate=acc_all)
+            for t, (buf, acc) in zip((q, k, v), tgt):
+                if t.requires_grad and not acc:
+                    t.grad = DeviceArray(buf)
+        else:
+            dq, dk, dv = K.attn_bwd(qt, kt, vt, o, do, lse, scale, True)
+            for t, gbuf in zip((q, k, v), (dq, dk, dv)):
+                if t.requires_grad:
+                    _accum_grad(t, DeviceArray(gbuf), owned=True)
+
+    out = _node(DeviceArray(o), (q, k, v), "causal_attention", _backward, _track(q, k, v))
+    return out
+
+
+def torch_empty_like(t):
+    """An uninitialised buffer with t's shape and (dense) strides."""
+    import torch
+
+    return torch.empty_like(t, dtype=torch.float32)
+
+
+def cross_entropy(logits, labels):
+    """Mean softmax cross-entropy of (N, V) logits against integer labels
+    (loss.py:17-27: log_softmax + one-hot NLL, divided by N), fused."""
+    N, V = logits.shape
+    lab = np.asarray(labels).reshape(-1)
+    if lab.size != N:
+        raise ValueError("one label per row expected")
+    if lab.size and (lab.min() < 0 or lab.max() >= V):
+        raise IndexError("label out of range")
+    labels_d = dev.index_array(lab.astype(np.int64))
+    xc = logits.data.contiguous()
+    row_loss = dev.empty((N,))
+    lse = dev.empty((N,))
+    K.xent_fwd(xc.t, labels_d.t, row_loss.t, lse.t)
+    data = dev.empty(())
+    K.reduce(row_loss.t, [0], data.t.view(1), alpha=1.0 / N)
+    out = None
+
+    def _backward():
+        if logits.requires_grad:
+            target, acc = _grad_target(logits)
+            K.xent_bwd(xc.t, labels_d.t, lse.t, out.grad.t.view(1), 1.0 / N, target.t, accumulate=acc)
+
+    out = _node(data, (logits,), "cross_entropy", _backward, _track(logits))
+    return out

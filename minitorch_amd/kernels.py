@@ -87,3 +87,236 @@ def attn_bwd(q, k, v, out, dout, lse, scale: float, causal: bool = True,
            L.ptr(workspace), workspace.numel() * workspace.element_size(),
            float(scale), int(bool(causal)), int(bool(accumulate)), L.stream_handle(q.device))
     return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
+# generic elementwise / reductions
+# ---------------------------------------------------------------------------
+
+def _i64(seq):
+    seq = tuple(int(x) for x in seq)
+    return (L.C.c_int64 * max(1, len(seq)))(*seq)
+
+
+def _bstrides(t, shape):
+    """Element strides of `t` broadcast to `shape` (0 on broadcast axes)."""
+    nd = len(shape)
+    ts, tst = tuple(t.shape), tuple(t.stride())
+    pad = nd - len(ts)
+    if pad < 0:
+        raise ValueError(f"cannot broadcast shape {ts} to {tuple(shape)}")
+    out = []
+    for d in range(nd):
+        if d < pad:
+            out.append(0)
+            continue
+        sz = ts[d - pad]
+        if sz == shape[d]:
+            out.append(tst[d - pad] if sz != 1 else 0)
+        elif sz == 1:
+            out.append(0)
+        else:
+            raise ValueError(f"cannot broadcast shape {ts} to {tuple(shape)}")
+    return out
+
+
+def ewise(op: str, out, a=None, b=None, alpha: float = 1.0, beta: float = 0.0, accumulate=False):
+    """out (+)= op(a, b), broadcasting a and b to out's shape."""
+    shape = tuple(out.shape)
+    nd = len(shape)
+    if nd > 8:
+        raise ValueError("at most 8 dimensions")
+    sa = _i64(_bstrides(a, shape)) if a is not None else None
+    sb = _i64(_bstrides(b, shape)) if b is not None else None
+    L.call("mtx_ewise_f32", L.EW[op], nd, _i64(shape),
+           L.ptr(a) if a is not None else None, sa,
+           L.ptr(b) if b is not None else None, sb,
+           L.ptr(out), _i64(out.stride()), float(alpha), float(beta), int(bool(accumulate)),
+           L.stream_handle())
+    return out
+
+
+def fill(out, value: float):
+    shape = tuple(out.shape)
+    L.call("mtx_ewise_f32", L.EW["FILL"], len(shape), _i64(shape), None, None, None, None,
+           L.ptr(out), _i64(out.stride()), float(value), 0.0, 0, L.stream_handle())
+    return out
+
+
+def reduce(a, axes, out, op=L.RED_SUM, alpha: float = 1.0, accumulate=False):
+    """out (+)= alpha * reduce(a over `axes`); out is contiguous with the kept
+    axes of a in order (any shape with that many elements)."""
+    shape = tuple(a.shape)
+    nd = len(shape)
+    axes = {ax % nd for ax in axes} if nd else set()
+    mask = (L.C.c_int * max(1, nd))(*[1 if d in axes else 0 for d in range(nd)])
+    shp = _i64(shape)
+    ws_bytes = L.lib().mtx_reduce_workspace_bytes(nd, shp, mask)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
+    if not out.is_contiguous():
+        raise ValueError("reduce output must be contiguous")
+    L.call("mtx_reduce_f32", int(op), nd, shp, L.ptr(a), _i64(a.stride()), mask, L.ptr(out),
+           float(alpha), int(bool(accumulate)), L.ptr(ws) if ws is not None else None, ws_bytes,
+           L.stream_handle())
+    return out
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+
+def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=1,
+         sa=None, sb=None, sc=None):
+    """C = alpha*A@B + beta*C (+bias) with explicit (row, col, batch) strides
+    for each operand; defaults take them from 2-D/3-D tensors."""
+    if sa is None:
+        sa = (a.stride(-2), a.stride(-1), a.stride(0) if a.dim() == 3 else 0)
+    if sb is None:
+        sb = (b.stride(-2), b.stride(-1), b.stride(0) if b.dim() == 3 else 0)
+    if sc is None:
+        sc = (c.stride(-2), c.stride(-1), c.stride(0) if c.dim() == 3 else 0)
+    M = a.shape[-2] if M is None else M
+    K = a.shape[-1] if K is None else K
+    N = b.shape[-1] if N is None else N
+    # one operand stride must be unit; otherwise the caller passes a copy
+    ws_bytes = L.lib().mtx_gemm_workspace_bytes(M, N, K, batch)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=c.device) if ws_bytes else None
+    L.call("mtx_gemm_f32", int(M), int(N), int(K), int(batch),
+           float(alpha), L.ptr(a), int(sa[0]), int(sa[1]), int(sa[2]),
+           L.ptr(b), int(sb[0]), int(sb[1]), int(sb[2]),
+           float(beta), L.ptr(c), int(sc[0]), int(sc[1]), int(sc[2]),
+           L.ptr(bias) if bias is not None else None,
+           L.ptr(ws) if ws is not None else None, ws_bytes, L.stream_handle())
+    return c
+
+
+# ---------------------------------------------------------------------------
+# row kernels
+# ---------------------------------------------------------------------------
+
+def _rows(t):
+    """(rows, L, leading stride) of a tensor whose last axis is contiguous and
+    whose leading axes collapse to one row index."""
+    if t.stride(-1) != 1:
+        raise ValueError("last axis must be contiguous")
+    Lx = t.shape[-1]
+    rows = t.numel() // Lx if Lx else 0
+    if t.dim() == 1:
+        return 1, Lx, Lx
+    # leading axes must collapse with a single stride
+    ld = t.stride(-2)
+    expect = ld * t.shape[-2]
+    for d in range(t.dim() - 3, -1, -1):
+        if t.shape[d] != 1 and t.stride(d) != expect:
+            raise ValueError("leading axes do not collapse")
+        expect *= t.shape[d]
+    return rows, Lx, ld
+
+
+def softmax_fwd(x, y, causal_tq=0, log=False):
+    rx, Lx, ldx = _rows(x)
+    _, _, ldy = _rows(y)
+    L.call("mtx_softmax_fwd_f32", L.ptr(x), ldx, L.ptr(y), ldy, rx, Lx, int(causal_tq), int(log),
+           L.stream_handle())
+    return y
+
+
+def softmax_bwd(y, dy, dx, log=False, accumulate=False):
+    r, Lx, ldy = _rows(y)
+    _, _, lddy = _rows(dy)
+    _, _, lddx = _rows(dx)
+    L.call("mtx_softmax_bwd_f32", L.ptr(y), ldy, L.ptr(dy), lddy, L.ptr(dx), lddx, r, Lx, int(log),
+           int(bool(accumulate)), L.stream_handle())
+    return dx
+
+
+def layernorm_fwd(x, gamma, beta, y, mean, std, eps):
+    r, C, ldx = _rows(x)
+    _, _, ldy = _rows(y)
+    L.call("mtx_layernorm_fwd_f32", L.ptr(x), ldx, L.ptr(gamma), L.ptr(beta), L.ptr(y), ldy,
+           L.ptr(mean), L.ptr(std), r, C, float(eps), L.stream_handle())
+    return y
+
+
+def layernorm_bwd(x, gamma, mean, std, dy, dx=None, dgamma=None, dbeta=None, accumulate=False):
+    r, C, ldx = _rows(x)
+    _, _, lddy = _rows(dy)
+    lddx = _rows(dx)[2] if dx is not None else C
+    ws = None
+    ws_bytes = 0
+    if dgamma is not None:
+        ws_bytes = L.lib().mtx_layernorm_bwd_workspace_bytes(r, C)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    L.call("mtx_layernorm_bwd_f32", L.ptr(x), ldx, L.ptr(gamma), L.ptr(mean), L.ptr(std),
+           L.ptr(dy), lddy, L.ptr(dx) if dx is not None else None, lddx,
+           L.ptr(dgamma) if dgamma is not None else None, L.ptr(dbeta) if dbeta is not None else None,
+           r, C, int(bool(accumulate)), L.ptr(ws) if ws is not None else None, ws_bytes,
+           L.stream_handle())
+
+
+def gelu_fwd(x, y):
+    if not (x.is_contiguous() and y.is_contiguous()):
+        raise ValueError("gelu: contiguous tensors only")
+    L.call("mtx_gelu_fwd_f32", L.ptr(x), L.ptr(y), x.numel(), L.stream_handle())
+    return y
+
+
+def gelu_bwd(x, dy, dx, accumulate=False):
+    if not (x.is_contiguous() and dy.is_contiguous() and dx.is_contiguous()):
+        raise ValueError("gelu_bwd: contiguous tensors only")
+    L.call("mtx_gelu_bwd_f32", L.ptr(x), L.ptr(dy), L.ptr(dx), x.numel(), int(bool(accumulate)),
+           L.stream_handle())
+    return dx
+
+
+def xent_fwd(logits, labels, row_loss, lse):
+    r, V, ld = _rows(logits)
+    L.call("mtx_xent_fwd_f32", L.ptr(logits), ld, L.ptr(labels), L.ptr(row_loss), L.ptr(lse), r, V,
+           L.stream_handle())
+
+
+def xent_bwd(logits, labels, lse, gscalar, scale, dlogits, accumulate=False):
+    r, V, ld = _rows(logits)
+    _, _, ldd = _rows(dlogits)
+    L.call("mtx_xent_bwd_f32", L.ptr(logits), ld, L.ptr(labels), L.ptr(lse), L.ptr(gscalar),
+           float(scale), L.ptr(dlogits), ldd, r, V, int(bool(accumulate)), L.stream_handle())
+
+
+def embedding_fwd(weight, idx, out):
+    V, C = weight.shape
+    L.call("mtx_embedding_fwd_f32", L.ptr(weight), weight.stride(0), V, L.ptr(idx), idx.numel(),
+           L.ptr(out), C, C, L.stream_handle())
+    return out
+
+
+def embedding_bwd(idx, grad, dweight, accumulate=False):
+    V, C = dweight.shape
+    L.call("mtx_embedding_bwd_f32", L.ptr(idx), idx.numel(), L.ptr(grad), C, L.ptr(dweight),
+           dweight.stride(0), V, C, int(bool(accumulate)), L.stream_handle())
+    return dweight
+
+
+class AdamTable:
+    """Device table for the one-launch multi-tensor Adam (layout of the C
+    struct AdamEntry: p, g, m, v, n, block0 -- six 64-bit words)."""
+
+    def __init__(self, params, grads, ms, vs):
+        n = len(params)
+        sizes = (L.C.c_int64 * n)(*[p.numel() for p in params])
+        b0 = (L.C.c_int64 * n)()
+        L.call("mtx_adam_blocks", sizes, n, b0)
+        rows = []
+        for i in range(n):
+            rows.append([params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(),
+                         params[i].numel(), b0[i]])
+        import numpy as np
+
+        host = np.array(rows, dtype=np.int64)
+        self.table = torch.from_numpy(host).to(params[0].device)
+        self.n = n
+        self.total_blocks = int(b0[n - 1] + (params[n - 1].numel() + 255) // 256) if n else 0
+
+
+def adam_step(table: AdamTable, lr, beta1, beta2, eps, weight_decay, step):
+    L.call("mtx_adam_f32", L.ptr(table.table), table.n, table.total_blocks, float(lr), float(beta1),
+           float(beta2), float(eps), float(weight_decay), int(step), L.stream_handle())

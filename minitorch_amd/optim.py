@@ -1,0 +1,74 @@
+"""Optimisers (the reference's optim.py:5-59).
+
+Adam updates every parameter tensor in a single kernel launch (a device table
+of (param, grad, m, v) pointers), with the reference's float32 arithmetic.
+"""
+from __future__ import annotations
+
+from . import device as dev
+from . import kernels as K
+
+
+class Optimizer:
+    def __init__(self, params, lr=1e-3, weight_decay=0.0):
+        self.params = list(params)
+        self.lr = lr
+        self.weight_decay = weight_decay
+
+    def zero_grad(self):
+        for p in self.params:
+            p.grad = None
+
+    def step(self):
+        raise NotImplementedError
+
+
+class Adam(Optimizer):
+    """Bias-corrected Adam (optim.py:37-59)."""
+
+    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0):
+        super().__init__(params, lr, weight_decay)
+        self.beta1, self.beta2 = betas
+        self.eps = eps
+        self.t = 0
+        self.m = [dev.zeros(p.shape) for p in self.params]
+        self.v = [dev.zeros(p.shape) for p in self.params]
+        self._table = None
+        self._key = None
+
+    def step(self):
+        self.t += 1
+        live = [i for i, p in enumerate(self.params) if p.requires_grad and p.grad is not None]
+        if not live:
+            return
+        for i in live:
+            p = self.params[i]
+            if not p.grad.t.is_contiguous():
+                p.grad = p.grad.copy()
+        key = tuple((self.params[i].data.t.data_ptr(), self.params[i].grad.t.data_ptr()) for i in live)
+        if key != self._key:
+            self._table = K.AdamTable([self.params[i].data.t for i in live],
+                                      [self.params[i].grad.t for i in live],
+                                      [self.m[i].t for i in live], [self.v[i].t for i in live])
+            self._key = key
+        K.adam_step(self._table, self.lr, self.beta1, self.beta2, self.eps, self.weight_decay, self.t)
+
+
+class SGD(Optimizer):
+    """SGD with momentum (optim.py:19-34): v = mu*v + g; p -= lr*v."""
+
+    def __init__(self, params, lr=1e-3, momentum=0.0, weight_decay=0.0):
+        super().__init__(params, lr, weight_decay)
+        self.momentum = momentum
+        self.velocities = [dev.zeros(p.shape) for p in self.params]
+
+    def step(self):
+        for p, v in zip(self.params, self.velocities):
+            if not p.requires_grad or p.grad is None:
+                continue
+            g = p.grad
+            if self.weight_decay:
+                g = g.copy()
+                K.ewise("AXPBY", g.t, g.t, p.data.t, alpha=1.0, beta=self.weight_decay)
+            K.ewise("AXPBY", v.t, v.t, g.t, alpha=self.momentum, beta=1.0)
+            K.ewise("AXPBY", p.data.t, p.data.t, v.t, alpha=1.0, beta=-self.lr)

@@ -1,0 +1,106 @@
+"""GPT on the device (the reference's transformer.py:14-104).
+
+``MultiHeadAttention`` keeps the reference's constructor, attributes,
+state_dict names and forward contract; its score/mask/softmax/value block
+(transformer.py:36-44) is the fused ``F.causal_attention`` kernel, fed with
+the strided (B, H, T, D) views that ``_split_heads`` makes.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import functional as F
+from .layers import Dropout, Embedding, GELU, LayerNorm, Linear
+from .module import Module, Sequential
+from .tensor import Tensor, no_grad
+
+
+class MultiHeadAttention(Module):
+    def __init__(self, n_embd, n_head, dropout=0.0):
+        super().__init__()
+        assert n_embd % n_head == 0, "n_embd must be divisible by n_head"
+        self.n_head = n_head
+        self.head_dim = n_embd // n_head
+        self.q_proj = Linear(n_embd, n_embd)
+        self.k_proj = Linear(n_embd, n_embd)
+        self.v_proj = Linear(n_embd, n_embd)
+        self.out_proj = Linear(n_embd, n_embd)
+        self.attn_drop = Dropout(dropout)
+
+    def _split_heads(self, x, B, T):
+        # (B, T, C) -> (B, n_head, T, head_dim), a strided view
+        return x.reshape(B, T, self.n_head, self.head_dim).transpose(1, 2)
+
+    def forward(self, x):
+        B, T, C = x.shape
+        q = self._split_heads(self.q_proj(x), B, T)
+        k = self._split_heads(self.k_proj(x), B, T)
+        v = self._split_heads(self.v_proj(x), B, T)
+        if self.attn_drop.p > 0.0 and self.attn_drop._training:
+            raise NotImplementedError("attention dropout inside the fused kernel is not implemented; "
+                                      "use dropout=0.0 (the benchmark configurations do)")
+        out = F.causal_attention(q, k, v, scale=1.0 / math.sqrt(self.head_dim))
+        out = out.transpose(1, 2).reshape(B, T, C)
+        return self.out_proj(out)
+
+
+class TransformerBlock(Module):
+    """Pre-norm block: x + attn(ln1(x)), then x + mlp(ln2(x))."""
+
+    def __init__(self, n_embd, n_head, dropout=0.0):
+        super().__init__()
+        self.ln1 = LayerNorm(n_embd)
+        self.attn = MultiHeadAttention(n_embd, n_head, dropout)
+        self.ln2 = LayerNorm(n_embd)
+        self.mlp = Sequential(
+            Linear(n_embd, 4 * n_embd),
+            GELU(),
+            Linear(4 * n_embd, n_embd),
+            Dropout(dropout),
+        )
+
+    def forward(self, x):
+        x = x + self.attn(self.ln1(x))
+        x = x + self.mlp(self.ln2(x))
+        return x
+
+
+class GPT(Module):
+    def __init__(self, vocab_size, block_size, n_embd=64, n_head=4, n_layer=2, dropout=0.0):
+        super().__init__()
+        self.block_size = block_size
+        self.tok_emb = Embedding(vocab_size, n_embd)
+        self.pos_emb = Embedding(block_size, n_embd)
+        self.drop = Dropout(dropout)
+        self.blocks = [TransformerBlock(n_embd, n_head, dropout) for _ in range(n_layer)]
+        self.ln_f = LayerNorm(n_embd)
+        self.lm_head = Linear(n_embd, vocab_size)
+
+    def forward(self, idx):
+        idx = np.asarray(idx)
+        B, T = idx.shape
+        assert T <= self.block_size, f"sequence length {T} exceeds block_size {self.block_size}"
+        tok = self.tok_emb(idx)
+        pos = self.pos_emb(np.arange(T))
+        x = self.drop(tok + pos)
+        for block in self.blocks:
+            x = block(x)
+        x = self.ln_f(x)
+        return self.lm_head(x)
+
+    def generate(self, idx, max_new_tokens, temperature=1.0):
+        """Sample tokens as the reference does (transformer.py:93-104): full
+        forward over the cropped context, host softmax over the last logits,
+        np.random.choice per row."""
+        idx = np.asarray(idx)
+        for _ in range(max_new_tokens):
+            idx_cond = idx[:, -self.block_size:]
+            logits = self.forward(idx_cond).data[:, -1, :] / temperature
+            logits = logits - logits.max(axis=-1, keepdims=True)
+            probs = np.exp(logits)
+            probs = probs / probs.sum(axis=-1, keepdims=True)
+            next_ids = np.array([np.random.choice(probs.shape[-1], p=p) for p in probs])
+            idx = np.concatenate([idx, next_ids[:, None]], axis=1)
+        return idx

@@ -126,7 +126,9 @@ def train_curve(cfg: GPTConfig, seed: int, B: int, steps: int, path, full_grads_
         opt.step()
         losses.append(float(loss.data))
         print(f"  step {it:2d} loss {losses[-1]:.10f}  ({time.time() - t0:.1f}s)", flush=True)
-    np.savez(path, losses=np.array(losses), seed=seed, B=B, steps=steps, names=np.array(names), **extra)
+        # saved after every step so a long run leaves a usable prefix
+        np.savez(path, losses=np.array(losses), seed=seed, B=B, steps=len(losses), names=np.array(names),
+                 **extra)
     print(f"wrote {path.name}")
 
 

@@ -1,0 +1,292 @@
+"""GPU parity of the GEMM, elementwise, reduction, row, embedding and Adam
+kernels (through minitorch_amd.kernels and the Tensor API) against NumPy.
+
+fp32 bar: |gpu - ref| <= 1e-5 + 1e-4 * |ref| elementwise, except where a test
+states a looser, justified bound (long float32 dot products).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def T(x):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).cuda()
+
+
+def H(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def close(got, ref, rtol=1e-4, atol=1e-5, name=""):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    err = np.abs(got - ref)
+    lim = atol + rtol * np.abs(ref)
+    assert np.all(err <= lim), f"{name}: max err {err.max():.3e} (max |ref| {np.abs(ref).max():.3e})"
+
+
+def dot_tol(K):
+    """Elementwise tolerance for a float32 dot product of length K with N(0,1)
+    entries: rounding error grows like sqrt(K) * 2^-24 * |terms|."""
+    return 2e-6 * np.sqrt(K) * 4
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb,batch,bias", [
+    (1, 1, 1, False, False, 1, False),
+    (7, 5, 3, False, False, 1, True),
+    (64, 64, 64, False, False, 1, False),
+    (130, 70, 33, True, False, 1, True),
+    (129, 257, 100, False, True, 3, False),
+    (256, 65, 384, False, False, 1, True),
+    (384, 1536, 4096, True, False, 1, False),   # weight-gradient shape: split-K path
+    (33, 17, 2000, True, True, 2, False),
+])
+def test_gemm(dev, M, N, K, ta, tb, batch, bias):
+    import torch
+    from minitorch_amd import kernels as Kn
+
+    _say(f"[gemm] M={M} N={N} K={K} ta={ta} tb={tb} batch={batch} bias={bias}")
+    rng = np.random.default_rng(M * 7 + N + K)
+    a = rng.standard_normal((batch, K, M) if ta else (batch, M, K), dtype=np.float32)
+    b = rng.standard_normal((batch, N, K) if tb else (batch, K, N), dtype=np.float32)
+    c0 = rng.standard_normal((batch, M, N), dtype=np.float32)
+    bs = rng.standard_normal(N, dtype=np.float32)
+    ta_, tb_, tc = T(a), T(b), T(c0)
+    av = ta_.transpose(1, 2) if ta else ta_
+    bv = tb_.transpose(1, 2) if tb else tb_
+    Kn.gemm(av, bv, tc, alpha=0.5, beta=2.0, bias=T(bs) if bias else None, batch=batch)
+    A = np.swapaxes(a, 1, 2) if ta else a
+    B = np.swapaxes(b, 1, 2) if tb else b
+    ref = 0.5 * (A.astype(np.float64) @ B) + 2.0 * c0 + (bs if bias else 0)
+    close(H(tc), ref, rtol=1e-4, atol=dot_tol(K), name="gemm")
+
+
+def test_ewise_broadcast_and_accumulate(dev):
+    import torch
+    from minitorch_amd import kernels as Kn
+
+    _say("[ewise]")
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((4, 1, 6), dtype=np.float32)
+    b = rng.standard_normal((3, 1), dtype=np.float32) + 3.0
+    out = torch.empty((4, 3, 6), device="cuda")
+    for op, f in (("ADD", np.add), ("SUB", np.subtract), ("MUL", np.multiply), ("DIV", np.divide)):
+        Kn.ewise(op, out, T(a), T(b))
+        close(H(out), f(a.astype(np.float64), b), name=op)
+    Kn.ewise("POW", out, T(np.abs(a) + 0.5), T(b))
+    close(H(out), (np.abs(a) + 0.5).astype(np.float64) ** b, rtol=2e-6 * 10, name="pow")
+    for op, f in (("EXP", np.exp), ("TANH", np.tanh), ("NEG", np.negative),
+                  ("LOG", lambda x: np.log(np.maximum(x, 1e-12)))):
+        o = torch.empty((4, 1, 6), device="cuda")
+        Kn.ewise(op, o, T(a))
+        close(H(o), f(a.astype(np.float64)), rtol=1e-5, name=op)
+    # accumulate into a strided (transposed) output
+    base = rng.standard_normal((6, 5), dtype=np.float32)
+    ob = T(base)
+    src = rng.standard_normal((5, 6), dtype=np.float32)
+    Kn.ewise("COPY", ob.t(), T(src), accumulate=True)
+    close(H(ob), base + src.T, name="accumulate-strided")
+
+
+@pytest.mark.parametrize("shape,axes", [((5, 7), [0]), ((5, 7), [1]), ((3, 4, 5), [0, 1]),
+                                        ((16384, 384), [0]), ((2, 3, 4, 5), [1, 3]), ((7,), [0])])
+def test_reduce_sum(dev, shape, axes):
+    import torch
+    from minitorch_amd import kernels as Kn
+
+    _say(f"[reduce] {shape} {axes}")
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal(shape, dtype=np.float32)
+    kept = [s for i, s in enumerate(shape) if i not in axes]
+    out = torch.empty(kept if kept else (1,), device="cuda")
+    Kn.reduce(T(a), axes, out, alpha=0.5)
+    ref = 0.5 * a.astype(np.float64).sum(axis=tuple(axes))
+    R = int(np.prod([shape[i] for i in axes]))
+    close(H(out).reshape(np.shape(ref)), ref, atol=dot_tol(R), name="reduce")
+
+
+@pytest.mark.parametrize("rows,L,causal", [(3, 5, 0), (64, 65, 0), (40, 256, 256), (8, 1000, 0)])
+def test_softmax_and_log_softmax(dev, rows, L, causal):
+    import torch
+    from minitorch_amd import kernels as Kn
+    from oracle.attention import causal_mask
+
+    _say(f"[softmax] rows={rows} L={L} causal={causal}")
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((rows, L), dtype=np.float32) * 3
+    dy = rng.standard_normal((rows, L), dtype=np.float32)
+    xs = x.astype(np.float64)
+    if causal:
+        m = np.tile(causal_mask(causal, L), (rows // causal + 1, 1))[:rows]
+        xs = np.where(m, -np.inf, xs)
+    p = np.exp(xs - xs.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    y = torch.empty((rows, L), device="cuda")
+    Kn.softmax_fwd(T(x), y, causal_tq=causal)
+    close(H(y), p, name="softmax")
+    dx = torch.empty((rows, L), device="cuda")
+    Kn.softmax_bwd(y, T(dy), dx)
+    g = dy * p
+    close(H(dx), g - p * g.sum(-1, keepdims=True), name="softmax_bwd")
+    if not causal:
+        ly = torch.empty((rows, L), device="cuda")
+        Kn.softmax_fwd(T(x), ly, log=True)
+        lp = np.log(p)
+        close(H(ly), lp, atol=1e-5, name="log_softmax")
+        Kn.softmax_bwd(ly, T(dy), dx, log=True)
+        close(H(dx), dy - p * dy.sum(-1, keepdims=True), name="log_softmax_bwd")
+
+
+@pytest.mark.parametrize("rows,C", [(5, 64), (300, 384), (17, 1536), (3, 33)])
+def test_layernorm(dev, rows, C):
+    import torch
+    from minitorch_amd import kernels as Kn
+    from oracle.gpt import Holder, ln_bwd, ln_fwd
+
+    _say(f"[layernorm] rows={rows} C={C}")
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((rows, C), dtype=np.float32) * 2 + 1
+    gam = rng.standard_normal(C, dtype=np.float32)
+    bet = rng.standard_normal(C, dtype=np.float32)
+    dy = rng.standard_normal((rows, C), dtype=np.float32)
+    y = torch.empty((rows, C), device="cuda")
+    mean = torch.empty(rows, device="cuda")
+    std = torch.empty(rows, device="cuda")
+    tx = T(x)
+    Kn.layernorm_fwd(tx, T(gam), T(bet), y, mean, std, float(np.float32(1e-5)))
+    ry, cache = ln_fwd(x.astype(np.float64), gam, bet)
+    close(H(y), ry, name="ln_fwd")
+    dx = torch.empty((rows, C), device="cuda")
+    dg = torch.empty(C, device="cuda")
+    db = torch.empty(C, device="cuda")
+    Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dx=dx)
+    Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dgamma=dg, dbeta=db)
+    hx, hg, hb = Holder(x.shape, np.float64), Holder((C,), np.float64), Holder((C,), np.float64)
+    ln_bwd(dy.astype(np.float64), cache, hx, hg, hb)
+    close(H(dx), hx.g, atol=1e-4 * np.sqrt(C) / 10, name="ln_dx")
+    close(H(dg), hg.g, atol=dot_tol(rows), name="ln_dgamma")
+    close(H(db), hb.g, atol=dot_tol(rows), name="ln_dbeta")
+
+
+def test_gelu(dev):
+    import torch
+    from minitorch_amd import kernels as Kn
+    from oracle.gpt import Holder, gelu_bwd, gelu_fwd
+
+    _say("[gelu]")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(10001, dtype=np.float32) * 3
+    dy = rng.standard_normal(10001, dtype=np.float32)
+    y = torch.empty(10001, device="cuda")
+    Kn.gelu_fwd(T(x), y)
+    ry, cache = gelu_fwd(x.astype(np.float64))
+    close(H(y), ry, name="gelu")
+    dx = torch.empty(10001, device="cuda")
+    Kn.gelu_bwd(T(x), T(dy), dx)
+    h = Holder(x.shape, np.float64)
+    gelu_bwd(dy.astype(np.float64), cache, h)
+    close(H(dx), h.g, name="gelu_bwd")
+
+
+def test_cross_entropy_and_embedding(dev):
+    import torch
+    import minitorch_amd as mt
+    from oracle.gpt import cross_entropy, cross_entropy_bwd
+
+    _say("[xent+embedding]")
+    rng = np.random.default_rng(6)
+    N, V, C = 300, 65, 48
+    logits = rng.standard_normal((N, V), dtype=np.float32)
+    labels = rng.integers(0, V, N)
+    t = mt.Tensor(logits, requires_grad=True)
+    loss = mt.cross_entropy_loss(t, mt.Tensor(labels.astype(np.float32)))
+    loss.backward()
+    rl, cache = cross_entropy(logits.astype(np.float64), labels)
+    assert abs(float(loss) - float(rl)) < 1e-5 * abs(float(rl))
+    close(t.grad.numpy(), cross_entropy_bwd(cache), atol=1e-7, name="xent_grad")
+    W = rng.standard_normal((V, C), dtype=np.float32)
+    ids = rng.integers(0, V, (4, 75))
+    g = rng.standard_normal((4, 75, C), dtype=np.float32)
+    tw = mt.Tensor(W, requires_grad=True)
+    e = tw[ids]
+    close(e.numpy(), W[ids], rtol=0, atol=0, name="gather")
+    (e * mt.Tensor(g)).sum().backward()
+    ref = np.zeros_like(W, dtype=np.float64)
+    np.add.at(ref, ids, g)
+    close(tw.grad.numpy(), ref, atol=dot_tol(300), name="scatter_add")
+
+
+def test_adam_matches_oracle(dev):
+    import minitorch_amd as mt
+    from oracle.gpt import Adam as OAdam
+
+    _say("[adam]")
+    rng = np.random.default_rng(7)
+    shapes = [(5,), (33, 7), (300,), (2, 3, 4)]
+    ps = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+    tp = [mt.Tensor(p.copy(), requires_grad=True) for p in ps]
+    opt = mt.Adam(tp, lr=3e-4)
+    op = {str(i): p.copy() for i, p in enumerate(ps)}
+    oopt = OAdam(op, lr=3e-4)
+    for step in range(3):
+        gs = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+        for t, g in zip(tp, gs):
+            t.grad = mt.Tensor(g).data
+        opt.step()
+        oopt.step(op, {str(i): g for i, g in enumerate(gs)})
+    for i, t in enumerate(tp):
+        close(t.numpy(), op[str(i)], rtol=1e-6, atol=1e-7, name=f"adam p{i}")
+
+
+def test_tensor_autograd_like_reference_checks(dev):
+    """Analytic GPU gradients of the reference's test_grads.py cases
+    (add/mul broadcast 76-85, matmul-batched 96-99, matmul-broadcast-batch
+    102-105, mean-axis 116-119, reshape 150-153, transpose 156-159, tanh
+    176-179, softmax 188-191, log_softmax 194-197) against float64 NumPy."""
+    import minitorch_amd as mt
+    from minitorch_amd import functional as F
+
+    _say("[tensor autograd]")
+    rng = np.random.default_rng(8)
+
+    def run(f_gpu, f_np, *arrs):
+        ts = [mt.Tensor(a, requires_grad=True) for a in arrs]
+        out = f_gpu(*ts)
+        (out * mt.Tensor(np.ones(out.shape, np.float32))).sum().backward()
+        # numerical reference: float64 central differences of the NumPy form
+        from oracle.attention import numerical_gradient
+
+        xs = [a.astype(np.float64).copy() for a in arrs]
+        num = numerical_gradient(lambda: float(np.sum(f_np(*xs))), xs, eps=1e-6)
+        for t, n in zip(ts, num):
+            close(t.grad.numpy(), n, rtol=1e-3, atol=1e-4, name=f_gpu.__name__ if hasattr(f_gpu, "__name__") else "")
+
+    r = lambda *s: rng.standard_normal(s).astype(np.float32)
+    run(lambda a, b: a + b, lambda a, b: a + b, r(3, 4), r(4))
+    run(lambda a, b: a * b, lambda a, b: a * b, r(3, 4), r(3, 1))
+    run(lambda a, b: a / b, lambda a, b: a / b, r(3, 4), np.abs(r(3, 4)) + 0.5)
+    run(lambda a, b: a @ b, lambda a, b: a @ b, r(2, 3, 4), r(2, 4, 5))
+    run(lambda a, b: a @ b, lambda a, b: a @ b, r(2, 3, 4), r(4, 5))
+    run(lambda a: a.mean(axis=1), lambda a: a.mean(axis=1), r(3, 4))
+    run(lambda a: a.reshape(4, 3).transpose(), lambda a: a.reshape(4, 3).T, r(3, 4))
+    run(lambda a: F.tanh(a), np.tanh, r(3, 4))
+    run(lambda a: F.softmax(a) * mt.Tensor(np.arange(4, dtype=np.float32)),
+        lambda a: (np.exp(a) / np.exp(a).sum(-1, keepdims=True)) * np.arange(4), r(3, 4))
+    run(lambda a: F.log_softmax(a) * mt.Tensor(np.arange(4, dtype=np.float32)),
+        lambda a: (a - np.log(np.exp(a).sum(-1, keepdims=True))) * np.arange(4), r(3, 4))
+    run(lambda a: (a ** 3), lambda a: a ** 3, r(3, 4))
+    run(lambda a: a.exp(), np.exp, r(3, 4))
