@@ -130,6 +130,86 @@ def cpu_baseline_attention(arrs, T, D, budget_s=15.0):
     return (f + bwd) / dt / 1e12, done, dt
 
 
+C0_CFG = dict(vocab=65, block=32, n_embd=64, n_head=4, n_layer=2, B=16)
+C2_CFG = dict(vocab=65, block=256, n_embd=384, n_head=6, n_layer=6, B=64)
+
+
+def gpt_flops_per_step(c):
+    """Model FLOPs of one training step: 6 * (matmul params) * tokens plus the
+    causal attention products 3 * L * (2 * B * T^2 * C) (fwd 1x, bwd 2x of the
+    causal-halved 4*B*T^2*C)."""
+    C, V, L, B, T = c["n_embd"], c["vocab"], c["n_layer"], c["B"], c["block"]
+    n_mm = L * (4 * C * C + 8 * C * C) + C * V
+    return 6 * n_mm * B * T + 3 * L * (2 * B * T * T * C)
+
+
+def bench_gpt(c, seed, steps, warmup):
+    """Training steps (forward, cross-entropy, zero_grad, backward, Adam
+    lr 3e-4) on seeded synthetic token batches already resident on the GPU.
+    Returns ms per step and the losses of the timed steps."""
+    import torch
+
+    import minitorch_amd as mt
+    from minitorch_amd import device as D
+
+    rng = np.random.default_rng(seed)
+    model = mt.GPT(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"], dropout=0.0)
+    model.init_weights(rng)
+    opt = mt.Adam(model.parameters(), lr=3e-4)
+    model.train()
+    B, T, V = c["B"], c["block"], c["vocab"]
+    batches = []
+    for _ in range(warmup + steps):
+        ids = rng.integers(0, V, (B, T + 1))
+        batches.append((D.index_array(ids[:, :-1]), D.index_array(ids[:, 1:].reshape(-1))))
+    losses = []
+
+    def step(i):
+        x, y = batches[i]
+        logits = model(x)
+        loss = mt.cross_entropy_loss(logits.reshape(B * T, V), mt.Tensor(y))
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        return loss
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    e0.record()
+    last = []
+    for i in range(warmup, warmup + steps):
+        last.append(step(i))
+    e1.record()
+    torch.cuda.synchronize()
+    losses = [float(l_) for l_ in last]
+    return e0.elapsed_time(e1) / steps, losses
+
+
+def cpu_baseline_gpt(c, budget_s, B_sample):
+    """The NumPy restatement of the reference training step (oracle/gpt.py:
+    forward, cross-entropy, hand-derived backward with the reference's dtype
+    flow, Adam) on a batch of B_sample sequences, repeated until budget_s."""
+    from oracle.gpt import Adam, GPTConfig, draw_batch, gpt_loss_and_grads, init_params
+
+    cfg = GPTConfig(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"])
+    rng = np.random.default_rng(0)
+    P = init_params(cfg, rng)
+    opt = Adam(P, lr=3e-4)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        x, y = draw_batch(rng, cfg.vocab, B_sample, cfg.block)
+        _, _, G = gpt_loss_and_grads(P, x, y, cfg)
+        opt.step(P, G)
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return n * B_sample * cfg.block / dt, n, dt
+
+
 def pmc_traffic(kernel):
     """HBM bytes per launch of `kernel` at C3 from the committed rocprofv3 PMC
     summary (profiles/pmc_traffic.json), or None."""
@@ -159,7 +239,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=("all", "c3", "c1"), default="all",
+    ap.add_argument("--only", choices=("all", "c3", "c1", "gpt2", "gpt0"), default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run 5 device copies of MIB MiB (a kernel of known HBM "
@@ -185,6 +265,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(f"[bench] copied {args.calibrate_copy} MiB x5", file=sys.stderr)
+        return
+    if args.only in ("gpt2", "gpt0"):
+        c = C2_CFG if args.only == "gpt2" else C0_CFG
+        ms, losses = bench_gpt(c, 2, args.steps, args.warmup)
+        print(f"[bench] {args.only}: {ms:.3f} ms/step, {c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, "
+              f"losses {losses}", file=sys.stderr)
         return
     if args.only == "c1":
         r1, _ = bench_attention(32, 8, 256, 64, torch.float32, 1, 1.0, args.steps, args.warmup)
@@ -218,7 +304,19 @@ def main():
     f1, b1 = attn_flops(32, 8, 256, 64)
     tflops1 = (f1 + b1) / (r1["ms_step"] * 1e-3) / 1e12
 
+    # ---- GPT training: C2 (GPT-small char model) and C0 (tiny) ----
+    print("[bench] GPT C2 training (B=64, T=256, 6x384)", file=sys.stderr, flush=True)
+    ms_c2, losses_c2 = bench_gpt(C2_CFG, 2, max(3, args.steps // 4), 2)
+    tok_c2 = C2_CFG["B"] * C2_CFG["block"] / (ms_c2 * 1e-3)
+    fl_c2 = gpt_flops_per_step(C2_CFG)
+    print(f"[bench] C2 {ms_c2:.2f} ms/step = {tok_c2:.0f} tokens/s, losses {losses_c2}", file=sys.stderr,
+          flush=True)
+    print("[bench] GPT C0 training (B=16, T=32, 2x64)", file=sys.stderr, flush=True)
+    ms_c0, _ = bench_gpt(C0_CFG, 0, args.steps, 3)
+    tok_c0 = C0_CFG["B"] * C0_CFG["block"] / (ms_c0 * 1e-3)
+
     cpu = None
+    cpu_gpt = None
     if not args.no_cpu:
         print(f"[bench] CPU baseline (NumPy restatement, ~{args.cpu_budget:.0f}s)", file=sys.stderr, flush=True)
         cv, nsl, dt = cpu_baseline_attention(arrs3, T, D, args.cpu_budget)
@@ -228,6 +326,14 @@ def main():
                          f"scale on), {dt:.1f}s; TFLOP/s on the algorithmic causal count",
                "host": platform.processor() or platform.machine(),
                "numpy": np.__version__}
+        print("[bench] CPU baseline, GPT C2 step on 1 sequence (NumPy restatement)", file=sys.stderr, flush=True)
+        tps2, n2, dt2 = cpu_baseline_gpt(C2_CFG, args.cpu_budget / 2, 1)
+        tps0, n0, dt0 = cpu_baseline_gpt(C0_CFG, 3.0, C0_CFG["B"])
+        cpu_gpt = {"C2_tokens_per_s": round(tps2, 2), "C0_tokens_per_s": round(tps0, 1),
+                   "cores": blas_threads(), "kind": "port",
+                   "sample": f"C2 model, {n2} training steps on 1 sequence of 256 tokens ({dt2:.1f}s); "
+                             f"C0, {n0} full B=16 steps ({dt0:.1f}s); NumPy restatement of the "
+                             f"reference step (oracle/gpt.py)"}
 
     line = {
         "metric": "causal-MHA fwd+bwd TFLOP/s (C3: B=8,H=16,T=2048,D=64 bf16)",
@@ -255,6 +361,16 @@ def main():
             "C1_fp32": {"tflops": round(tflops1, 3), "pct_of_fp32_peak": round(100 * tflops1 / PEAK_FP32, 2),
                         "ms_per_step": round(r1["ms_step"], 4),
                         "phase_ms": {k_: round(v_, 4) for k_, v_ in r1.items()}},
+            "gpt_train": {
+                "C2": {"tokens_per_s": round(tok_c2, 1), "ms_per_step": round(ms_c2, 3),
+                       "model_tflops": round(fl_c2 / (ms_c2 * 1e-3) / 1e12, 2),
+                       "pct_of_fp32_peak": round(100 * fl_c2 / (ms_c2 * 1e-3) / 1e12 / PEAK_FP32, 2),
+                       "config": "vocab 65, n_embd 384, 6 heads, 6 layers, T=256, B=64, fp32, Adam 3e-4",
+                       "losses": [round(x, 5) for x in losses_c2]},
+                "C0": {"tokens_per_s": round(tok_c0, 1), "ms_per_step": round(ms_c0, 3),
+                       "config": "vocab 65, n_embd 64, 4 heads, 2 layers, T=32, B=16, fp32"},
+                "cpu_baseline": cpu_gpt,
+            },
         },
     }
     print(json.dumps(line), flush=True)

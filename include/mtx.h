@@ -252,6 +252,13 @@ int mtx_embedding_bwd_f32(const int64_t* idx, int64_t n, const float* grad, int6
                           int64_t lddw, int64_t V, int C, int accumulate, void* stream);
 
 /*
+ * One-hot rows: out[i, v] = (idx[i] == v) as float32, (n, V) row-major.  With
+ * a GEMM, dweight = onehot^T @ grad is the embedding backward for small
+ * vocabularies (np.add.at, tensor.py:382) on MFMA, deterministic.
+ */
+int mtx_onehot_f32(const int64_t* idx, int64_t n, int64_t V, float* out, void* stream);
+
+/*
  * Adam over many tensors in one launch (optim.py:37-59).  `table` is a device
  * array of ntensors entries {float* p; const float* g; float* m; float* v;
  * int64_t n; int64_t block0}, block0 from mtx_adam_blocks (host helper);

@@ -76,6 +76,7 @@ SIGNATURES = {
     "mtx_embedding_fwd_f32": (_I, [_P, _I64, _I64, _P, _I64, _P, _I64, _I, _P]),
     "mtx_embedding_bwd_f32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I, _I, _P]),
     "mtx_adam_blocks": (_I, [_I64P, _I, _I64P]),
+    "mtx_onehot_f32": (_I, [_P, _I64, _I64, _P, _P]),
     "mtx_adam_f32": (_I, [_P, _I, _I64, _D, _D, _D, _D, _D, _I, _P]),
 }
 

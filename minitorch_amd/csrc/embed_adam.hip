@@ -57,6 +57,17 @@ __global__ __launch_bounds__(256) void embed_scatter_kernel(const int64_t* __res
   }
 }
 
+// out[i, v] = (idx[i] == v), row-major (n, V)
+__global__ __launch_bounds__(256) void onehot_kernel(const int64_t* __restrict__ idx, int64_t n, int64_t V,
+                                                     float* __restrict__ out) {
+  const int64_t total = n * V;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / V, v = e % V;
+    out[e] = idx[i] == v ? 1.0f : 0.0f;
+  }
+}
+
 struct AdamEntry {
   float* p;
   const float* g;
@@ -109,6 +120,16 @@ extern "C" int mtx_embedding_bwd_f32(const int64_t* idx, int64_t n, const float*
   MTX_CHECK_SHAPE(n >= 0 && C >= 1 && V >= 1 && V < (1 << 30) && ldg >= C && lddw >= C, "embedding_bwd: bad shape");
   hipLaunchKernelGGL(embed_scatter_kernel, dim3((unsigned)V, (C + 255) / 256), dim3(256), 0,
                      static_cast<hipStream_t>(stream), idx, grad, ldg, dweight, lddw, n, C, accumulate ? 1 : 0);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_onehot_f32(const int64_t* idx, int64_t n, int64_t V, float* out, void* stream) {
+  MTX_CHECK_ARG(idx && out, "onehot: null pointer");
+  MTX_CHECK_SHAPE(n >= 0 && V >= 1, "onehot: bad shape");
+  if (n == 0) return MTX_OK;
+  const int blocks = (int)std::min<int64_t>((n * V + 255) / 256, 16384);
+  hipLaunchKernelGGL(onehot_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), idx, n, V, out);
   MTX_LAUNCHED();
   return MTX_OK;
 }

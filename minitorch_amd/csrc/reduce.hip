@@ -56,52 +56,76 @@ __device__ __forceinline__ int64_t red_offset(const RedArgs& g, int64_t r) {
   return off;
 }
 
+// Block = 64 outputs (threadIdx.x) x 4 reduction lanes (threadIdx.y).  When
+// the kept axes are innermost, the 64 outputs of a block are consecutive in
+// memory, so every reduction step is a coalesced 256-byte read.
 __global__ __launch_bounds__(256) void reduce_kernel(const RedArgs g) {
-  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  __shared__ float part[4][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t o = (int64_t)blockIdx.x * 64 + tx;
   const int s = blockIdx.y;
-  if (o >= g.nout) return;
-  const float* base = g.a + kept_offset(g, o);
-  const int64_t r0 = (int64_t)s * g.chunk;
-  const int64_t r1 = min(g.nred, r0 + g.chunk);
-  float acc = g.op == MTX_RED_MAX ? -INFINITY : 0.f;
-  if (g.nr == 1) {
-    const int64_t st = g.rstr[0];
-    for (int64_t r = r0; r < r1; ++r) {
-      const float v = base[r * st];
-      acc = g.op == MTX_RED_MAX ? fmaxf(acc, v) : acc + v;
-    }
-  } else {
-    for (int64_t r = r0; r < r1; ++r) {
-      const float v = base[red_offset(g, r)];
-      acc = g.op == MTX_RED_MAX ? fmaxf(acc, v) : acc + v;
+  const bool is_max = g.op == MTX_RED_MAX;
+  float acc = is_max ? -INFINITY : 0.f;
+  if (o < g.nout) {
+    const float* base = g.a + kept_offset(g, o);
+    const int64_t r0 = (int64_t)s * g.chunk;
+    const int64_t r1 = min(g.nred, r0 + g.chunk);
+    if (g.nr == 1) {
+      const int64_t st = g.rstr[0];
+      for (int64_t r = r0 + ty; r < r1; r += 4) {
+        const float v = base[r * st];
+        acc = is_max ? fmaxf(acc, v) : acc + v;
+      }
+    } else {
+      for (int64_t r = r0 + ty; r < r1; r += 4) {
+        const float v = base[red_offset(g, r)];
+        acc = is_max ? fmaxf(acc, v) : acc + v;
+      }
     }
   }
+  part[ty][tx] = acc;
+  __syncthreads();
+  if (ty != 0 || o >= g.nout) return;
+  float t = part[0][tx];
+#pragma unroll
+  for (int j = 1; j < 4; ++j) t = is_max ? fmaxf(t, part[j][tx]) : t + part[j][tx];
   if (g.nsplit > 1) {
-    g.ws[(int64_t)s * g.nout + o] = acc;
+    g.ws[(int64_t)s * g.nout + o] = t;
   } else {
-    float v = g.alpha * acc;
+    float v = g.alpha * t;
     if (g.accumulate) v += g.out[o];
     g.out[o] = v;
   }
 }
 
 __global__ __launch_bounds__(256) void reduce_combine_kernel(const RedArgs g) {
-  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (o >= g.nout) return;
-  float acc = g.op == MTX_RED_MAX ? -INFINITY : 0.f;
-  for (int s = 0; s < g.nsplit; ++s) {
-    const float v = g.ws[(int64_t)s * g.nout + o];
-    acc = g.op == MTX_RED_MAX ? fmaxf(acc, v) : acc + v;
+  __shared__ float part[4][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t o = (int64_t)blockIdx.x * 64 + tx;
+  const bool is_max = g.op == MTX_RED_MAX;
+  float acc = is_max ? -INFINITY : 0.f;
+  if (o < g.nout) {
+    for (int s = ty; s < g.nsplit; s += 4) {
+      const float v = g.ws[(int64_t)s * g.nout + o];
+      acc = is_max ? fmaxf(acc, v) : acc + v;
+    }
   }
-  float v = g.alpha * acc;
+  part[ty][tx] = acc;
+  __syncthreads();
+  if (ty != 0 || o >= g.nout) return;
+  float t = part[0][tx];
+#pragma unroll
+  for (int j = 1; j < 4; ++j) t = is_max ? fmaxf(t, part[j][tx]) : t + part[j][tx];
+  float v = g.alpha * t;
   if (g.accumulate) v += g.out[o];
   g.out[o] = v;
 }
 
 int plan_splits(int64_t nout, int64_t nred) {
-  // aim for >= ~64K threads in flight, chunks of >= 64 elements
+  // enough blocks (64 outputs each) to fill the GPU, >= 64 reduced elements per split
+  const int64_t bx = (nout + 63) / 64;
   int64_t s = 1;
-  while (nout * s < 65536 && nred / (s * 2) >= 64 && s < 256) s *= 2;
+  while (bx * s < 1024 && nred / (s * 2) >= 64 && s < 512) s *= 2;
   return (int)s;
 }
 
@@ -145,8 +169,8 @@ extern "C" int mtx_reduce_f32(int op, int ndim, const int64_t* shape, const floa
   g.chunk = (nred + s - 1) / s;
   g.ws = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int bx = (int)((nout + 255) / 256);
-  MTX_CHECK_SHAPE(bx < (1 << 30), "reduce: too many outputs");
+  const int bx = (int)((nout + 63) / 64);
+  MTX_CHECK_SHAPE((nout + 63) / 64 < (1 << 30), "reduce: too many outputs");
   hipLaunchKernelGGL(reduce_kernel, dim3(bx, s), dim3(256), 0, st, g);
   MTX_LAUNCHED();
   if (s > 1) {

@@ -172,41 +172,60 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(const float* __restr
   }
 }
 
-// dgamma[c] = sum_r dy[r,c] * xh[r,c], dbeta[c] = sum_r dy[r,c]; rows split
-// into chunks, partials [split][2][C] in ws, combined in chunk order.
+// dgamma[c] = sum_r dy[r,c] * xh[r,c], dbeta[c] = sum_r dy[r,c].  Block = 64
+// columns x 4 row lanes over one chunk of rows; partials [split][2][C] go to
+// the workspace and are combined in split order (deterministic).
 __global__ __launch_bounds__(256) void layernorm_param_partial(const float* __restrict__ x, int64_t ldx,
                                                                const float* __restrict__ mean_in,
                                                                const float* __restrict__ std_in,
                                                                const float* __restrict__ dy, int64_t lddy,
                                                                float* __restrict__ ws, int64_t rows, int C,
                                                                int64_t chunk) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
+  __shared__ float pg[4][64], pb[4][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + tx;
   const int s = blockIdx.y;
-  if (c >= C) return;
   const int64_t r0 = (int64_t)s * chunk, r1 = min(rows, r0 + chunk);
   float ag = 0.f, ab = 0.f;
-  for (int64_t r = r0; r < r1; ++r) {
-    const float g = dy[r * lddy + c];
-    ag += g * ((x[r * ldx + c] - mean_in[r]) / std_in[r]);
-    ab += g;
+  if (c < C) {
+    for (int64_t r = r0 + ty; r < r1; r += 4) {
+      const float g = dy[r * lddy + c];
+      ag += g * ((x[r * ldx + c] - mean_in[r]) / std_in[r]);
+      ab += g;
+    }
   }
-  ws[((int64_t)s * 2 + 0) * C + c] = ag;
-  ws[((int64_t)s * 2 + 1) * C + c] = ab;
+  pg[ty][tx] = ag;
+  pb[ty][tx] = ab;
+  __syncthreads();
+  if (ty == 0 && c < C) {
+    ws[((int64_t)s * 2 + 0) * C + c] = pg[0][tx] + pg[1][tx] + pg[2][tx] + pg[3][tx];
+    ws[((int64_t)s * 2 + 1) * C + c] = pb[0][tx] + pb[1][tx] + pb[2][tx] + pb[3][tx];
+  }
 }
 
 __global__ __launch_bounds__(256) void layernorm_param_combine(const float* __restrict__ ws, int nsplit, int C,
                                                                float* __restrict__ dgamma,
                                                                float* __restrict__ dbeta, int accumulate) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= C) return;
+  __shared__ float pg[4][64], pb[4][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + tx;
   float ag = 0.f, ab = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    ag += ws[((int64_t)s * 2 + 0) * C + c];
-    ab += ws[((int64_t)s * 2 + 1) * C + c];
+  if (c < C) {
+    for (int s = ty; s < nsplit; s += 4) {
+      ag += ws[((int64_t)s * 2 + 0) * C + c];
+      ab += ws[((int64_t)s * 2 + 1) * C + c];
+    }
   }
-  if (accumulate) { ag += dgamma[c]; ab += dbeta[c]; }
-  dgamma[c] = ag;
-  dbeta[c] = ab;
+  pg[ty][tx] = ag;
+  pb[ty][tx] = ab;
+  __syncthreads();
+  if (ty == 0 && c < C) {
+    ag = pg[0][tx] + pg[1][tx] + pg[2][tx] + pg[3][tx];
+    ab = pb[0][tx] + pb[1][tx] + pb[2][tx] + pb[3][tx];
+    if (accumulate) { ag += dgamma[c]; ab += dbeta[c]; }
+    dgamma[c] = ag;
+    dbeta[c] = ab;
+  }
 }
 
 // GELU, tanh form with the reference's float32 constants
@@ -338,7 +357,10 @@ extern "C" int mtx_layernorm_fwd_f32(const float* x, int64_t ldx, const float* g
 
 extern "C" size_t mtx_layernorm_bwd_workspace_bytes(int64_t rows, int C) {
   if (rows < 1 || C < 1) return 0;
-  const int64_t nsplit = std::min<int64_t>(256, (rows + 63) / 64);
+  // enough (64-column x split) blocks to fill the GPU, >= 64 rows per split
+  const int64_t bx = (C + 63) / 64;
+  int64_t nsplit = 1;
+  while (bx * nsplit < 1024 && rows / (nsplit * 2) >= 64 && nsplit < 512) nsplit *= 2;
   return (size_t)nsplit * 2 * C * sizeof(float);
 }
 
@@ -372,10 +394,10 @@ extern "C" int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* g
     const int nsplit = (int)(need / (2 * C * sizeof(float)));
     const int64_t chunk = (rows + nsplit - 1) / nsplit;
     float* ws = static_cast<float*>(workspace);
-    hipLaunchKernelGGL(layernorm_param_partial, dim3((C + 255) / 256, nsplit), dim3(256), 0, st, x, ldx, mean,
+    hipLaunchKernelGGL(layernorm_param_partial, dim3((C + 63) / 64, nsplit), dim3(256), 0, st, x, ldx, mean,
                        std_, dy, lddy, ws, rows, C, chunk);
     MTX_LAUNCHED();
-    hipLaunchKernelGGL(layernorm_param_combine, dim3((C + 255) / 256), dim3(256), 0, st, ws, nsplit, C, dgamma,
+    hipLaunchKernelGGL(layernorm_param_combine, dim3((C + 63) / 64), dim3(256), 0, st, ws, nsplit, C, dgamma,
                        dbeta, accumulate ? 1 : 0);
     MTX_LAUNCHED();
   }

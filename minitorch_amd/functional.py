@@ -233,12 +233,20 @@ def cross_entropy(logits, labels):
     """Mean softmax cross-entropy of (N, V) logits against integer labels
     (loss.py:17-27: log_softmax + one-hot NLL, divided by N), fused."""
     N, V = logits.shape
-    lab = np.asarray(labels).reshape(-1)
-    if lab.size != N:
-        raise ValueError("one label per row expected")
-    if lab.size and (lab.min() < 0 or lab.max() >= V):
-        raise IndexError("label out of range")
-    labels_d = dev.index_array(lab.astype(np.int64))
+    if isinstance(labels, DeviceArray):
+        # device-resident labels: range is the caller's responsibility (the
+        # kernel clamps; it never reads out of bounds)
+        labels_d = dev.index_array(labels)
+        if labels_d.size != N:
+            raise ValueError("one label per row expected")
+        labels_d = labels_d.reshape(N)
+    else:
+        lab = np.asarray(labels).reshape(-1)
+        if lab.size != N:
+            raise ValueError("one label per row expected")
+        if lab.size and (lab.min() < 0 or lab.max() >= V):
+            raise IndexError("label out of range")
+        labels_d = dev.index_array(lab.astype(np.int64))
     xc = logits.data.contiguous()
     row_loss = dev.empty((N,))
     lse = dev.empty((N,))

@@ -290,7 +290,17 @@ def embedding_fwd(weight, idx, out):
 
 
 def embedding_bwd(idx, grad, dweight, accumulate=False):
+    """dweight (+)= scatter-add of grad rows by idx.  Small tables use a
+    one-hot GEMM on MFMA (onehot^T @ grad); large ones the row-owner kernel.
+    Both are deterministic."""
     V, C = dweight.shape
+    n = idx.numel()
+    if V <= 4096 and n * V <= (1 << 27):
+        onehot = torch.empty((n, V), dtype=torch.float32, device=grad.device)
+        L.call("mtx_onehot_f32", L.ptr(idx), n, V, L.ptr(onehot), L.stream_handle())
+        gemm(onehot.t(), grad, dweight, beta=1.0 if accumulate else 0.0, M=V, N=C, K=n, batch=1,
+             sa=(1, V, 0), sb=(grad.stride(0), grad.stride(1), 0), sc=(dweight.stride(0), dweight.stride(1), 0))
+        return dweight
     L.call("mtx_embedding_bwd_f32", L.ptr(idx), idx.numel(), L.ptr(grad), C, L.ptr(dweight),
            dweight.stride(0), V, C, int(bool(accumulate)), L.stream_handle())
     return dweight

@@ -13,6 +13,7 @@ import numpy as np
 from . import device as dev
 from . import functional as F
 from . import kernels as K
+from .device import DeviceArray
 from .module import Module
 from .tensor import Tensor, _grad_target, grad_enabled
 
@@ -128,6 +129,8 @@ class Embedding(Module):
                              requires_grad=True)
 
     def forward(self, idx):
+        if isinstance(idx, DeviceArray):
+            return self.weight[idx]
         return self.weight[np.asarray(idx)]
 
 

@@ -457,12 +457,15 @@ class Tensor:
         out = None
         if isinstance(key, (np.ndarray, list, DeviceArray)) and not (
                 isinstance(key, np.ndarray) and key.dtype == bool):
-            idx = dev.index_array(key)
             if self.ndim != 2:
                 raise NotImplementedError("index arrays are supported on 2-D tensors (embedding tables)")
-            ids = np.asarray(key) if not isinstance(key, DeviceArray) else key.numpy()
-            if ids.size and (ids.min() < 0 or ids.max() >= self.shape[0]):
-                raise IndexError(f"index out of range for axis 0 of size {self.shape[0]}")
+            if not isinstance(key, DeviceArray):
+                # host ids are range-checked here; device-resident ids are the
+                # caller's responsibility (the kernel clamps, it never reads out of bounds)
+                ids = np.asarray(key)
+                if ids.size and (ids.min() < 0 or ids.max() >= self.shape[0]):
+                    raise IndexError(f"index out of range for axis 0 of size {self.shape[0]}")
+            idx = dev.index_array(key)
             C = self.shape[1]
             data = dev.empty(tuple(idx.shape) + (C,))
             K.embedding_fwd(self.data.t, idx.t.reshape(-1), data.t.view(-1, C))

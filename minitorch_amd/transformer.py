@@ -11,7 +11,9 @@ import math
 
 import numpy as np
 
+from . import device as dev
 from . import functional as F
+from .device import DeviceArray
 from .layers import Dropout, Embedding, GELU, LayerNorm, Linear
 from .module import Module, Sequential
 from .tensor import Tensor, no_grad
@@ -78,12 +80,36 @@ class GPT(Module):
         self.ln_f = LayerNorm(n_embd)
         self.lm_head = Linear(n_embd, vocab_size)
 
+    def init_weights(self, rng, std=0.02):
+        """Harness initialisation used by the benchmark configurations: in
+        state_dict order, every Linear weight and Embedding table ~ N(0, std)
+        (float64 standard normals * std, cast to float32), biases 0, LayerNorm
+        gamma 1 / beta 0.  `rng` is a numpy Generator."""
+        state = {}
+        for name, arr in self.state_dict().items():
+            if name.endswith(".gamma"):
+                state[name] = np.ones(arr.shape, np.float32)
+            elif name.endswith(".beta") or name.endswith(".bias"):
+                state[name] = np.zeros(arr.shape, np.float32)
+            else:
+                state[name] = (rng.standard_normal(arr.shape) * std).astype(np.float32)
+        self.load_state_dict(state)
+        return self
+
+    def _positions(self, T):
+        cache = self.__dict__.setdefault("_pos_ids", {})
+        if T not in cache:
+            cache[T] = dev.index_array(np.arange(T))
+        return cache[T]
+
     def forward(self, idx):
-        idx = np.asarray(idx)
+        """idx: (B, T) token ids, host ints or a device int64 DeviceArray."""
+        if not isinstance(idx, DeviceArray):
+            idx = np.asarray(idx)
         B, T = idx.shape
         assert T <= self.block_size, f"sequence length {T} exceeds block_size {self.block_size}"
         tok = self.tok_emb(idx)
-        pos = self.pos_emb(np.arange(T))
+        pos = self.pos_emb(self._positions(T))
         x = self.drop(tok + pos)
         for block in self.blocks:
             x = block(x)

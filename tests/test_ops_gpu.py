@@ -290,3 +290,22 @@ def test_tensor_autograd_like_reference_checks(dev):
         lambda a: (a - np.log(np.exp(a).sum(-1, keepdims=True))) * np.arange(4), r(3, 4))
     run(lambda a: (a ** 3), lambda a: a ** 3, r(3, 4))
     run(lambda a: a.exp(), np.exp, r(3, 4))
+
+
+def test_embedding_backward_both_paths(dev):
+    """Small tables take the one-hot GEMM path, large ones (V > 4096) the
+    row-owner scatter kernel; both must equal np.add.at with repeated ids."""
+    import torch
+    from minitorch_amd import kernels as Kn
+
+    for V, n, C in ((65, 5000, 96), (5000, 700, 40)):
+        _say(f"[embedding bwd] V={V} n={n} C={C}")
+        rng = np.random.default_rng(V)
+        ids = rng.integers(0, min(V, 50), n)  # heavy repetition
+        g = rng.standard_normal((n, C), dtype=np.float32)
+        base = rng.standard_normal((V, C), dtype=np.float32)
+        dw = T(base)
+        Kn.embedding_bwd(torch.from_numpy(ids).cuda(), T(g), dw, accumulate=True)
+        ref = base.astype(np.float64).copy()
+        np.add.at(ref, ids, g)
+        close(H(dw), ref, atol=dot_tol(n), name=f"embedding_bwd V={V}")
