@@ -48,6 +48,31 @@ class MultiHeadAttention(Module):
         return self.out_proj(out)
 
 
+    def forward_cached(self, x, cache, t0):
+        """Inference-only step over positions [t0, t0 + T) of x (B, T, C):
+        keys/values of these positions are written into cache = (k, v), each a
+        (B, Tmax, C) DeviceArray, and attention runs against cache[:, :t0 + T]
+        (bottom-right causal: query i sees keys <= t0 + i)."""
+        from . import kernels as K
+
+        B, T, C = x.shape
+        H, D = self.n_head, self.head_dim
+        q = self.q_proj(x)
+        k = self.k_proj(x)
+        v = self.v_proj(x)
+        kc, vc = cache
+        K.ewise("COPY", kc.t[:, t0:t0 + T, :], k.data.t)
+        K.ewise("COPY", vc.t[:, t0:t0 + T, :], v.data.t)
+        Tk = t0 + T
+        heads = lambda t: t.view(t.shape[0], t.shape[1], H, D).transpose(1, 2)
+        qh = heads(q.data.t)
+        kh = heads(kc.t[:, :Tk, :])
+        vh = heads(vc.t[:, :Tk, :])
+        out = dev.empty((B, T, H, D))
+        K.attn_fwd(qh, kh, vh, 1.0 / math.sqrt(D), True, out=out.t.transpose(1, 2))
+        return self.out_proj(Tensor(out.reshape(B, T, C)))
+
+
 class TransformerBlock(Module):
     """Pre-norm block: x + attn(ln1(x)), then x + mlp(ln2(x))."""
 
@@ -65,6 +90,11 @@ class TransformerBlock(Module):
 
     def forward(self, x):
         x = x + self.attn(self.ln1(x))
+        x = x + self.mlp(self.ln2(x))
+        return x
+
+    def forward_cached(self, x, cache, t0):
+        x = x + self.attn.forward_cached(self.ln1(x), cache, t0)
         x = x + self.mlp(self.ln2(x))
         return x
 
@@ -115,6 +145,43 @@ class GPT(Module):
             x = block(x)
         x = self.ln_f(x)
         return self.lm_head(x)
+
+    def generate_greedy(self, idx, max_new_tokens, return_margins=False):
+        """Greedy decoding: argmax (first maximum, as np.argmax) of the last
+        position's logits -- the C4 harness over transformer.py:93-104 -- with
+        a KV cache: one prefill over the prompt, then one-token steps whose
+        attention runs on the device against the cached keys and values
+        (1 query vs the growing prefix).  Needs T0 + max_new_tokens <=
+        block_size (beyond it the reference crops the context and recomputes
+        positions, which a cache cannot reuse; use generate() then).
+        Returns ids (B, T0 + n) and, if asked, the top-2 logit margins (B, n)."""
+        idx = np.asarray(idx)
+        B, T0 = idx.shape
+        Tmax = T0 + max_new_tokens
+        if Tmax > self.block_size:
+            raise ValueError(f"prompt + new tokens = {Tmax} exceeds block_size {self.block_size}")
+        C = self.tok_emb.weight.shape[1]
+        caches = [(dev.empty((B, Tmax, C)), dev.empty((B, Tmax, C))) for _ in self.blocks]
+        out = np.empty((B, Tmax), dtype=np.int64)
+        out[:, :T0] = idx
+        margins = np.empty((B, max_new_tokens), dtype=np.float64)
+        with no_grad():
+            t0, cur = 0, idx
+            for step in range(max_new_tokens):
+                T = cur.shape[1]
+                x = self.tok_emb(cur) + self.pos_emb(np.arange(t0, t0 + T))
+                for block, cache in zip(self.blocks, caches):
+                    x = block.forward_cached(x, cache, t0)
+                x = self.ln_f(x)
+                last = Tensor(x.data.t[:, T - 1:T, :])
+                logits = self.lm_head(last).data.numpy()[:, 0, :]
+                nxt = np.argmax(logits, axis=-1)
+                top2 = np.sort(logits, axis=-1)[:, -2:]
+                margins[:, step] = top2[:, 1] - top2[:, 0]
+                out[:, T0 + step] = nxt
+                t0 += T
+                cur = nxt[:, None]
+        return (out, margins) if return_margins else out
 
     def generate(self, idx, max_new_tokens, temperature=1.0):
         """Sample tokens as the reference does (transformer.py:93-104): full

@@ -441,3 +441,62 @@ def greedy_generate(P, cfg: GPTConfig, prompts, n_new):
         margins.append(top2[:, 1] - top2[:, 0])
         idx = np.concatenate([idx, nxt[:, None]], axis=1)
     return idx, np.stack(margins, axis=1)
+
+
+def greedy_generate_cached(P, cfg: GPTConfig, prompts, n_new):
+    """greedy_generate computed incrementally: a prefill forward over the
+    prompt that keeps each layer's k/v, then one-token steps attending to the
+    cached k/v.  The same per-row arithmetic as the full recompute (attention
+    of one query over its prefix, same dtype flow), so the argmax sequence is
+    the reference's up to last-bit summation-order differences; pinned against
+    greedy_generate (itself pinned by the reference's tokens)."""
+    idx = np.asarray(prompts)
+    B, T0 = idx.shape
+    H, D = cfg.n_head, cfg.head_dim
+    cache = [[None, None] for _ in range(cfg.n_layer)]
+    margins = []
+
+    def run(tokens, t0):
+        T = tokens.shape[1]
+        x = P["tok_emb.weight"][tokens] + P["pos_emb.weight"][np.arange(t0, t0 + T)]
+        for i in range(cfg.n_layer):
+            pre = f"blocks.{i}."
+            h, _ = ln_fwd(x, P[pre + "ln1.gamma"], P[pre + "ln1.beta"])
+            a = pre + "attn."
+            q, _ = linear_fwd(h, P[a + "q_proj.weight"], P[a + "q_proj.bias"])
+            k, _ = linear_fwd(h, P[a + "k_proj.weight"], P[a + "k_proj.bias"])
+            v, _ = linear_fwd(h, P[a + "v_proj.weight"], P[a + "v_proj.bias"])
+            split = lambda t: t.reshape(B, T, H, D).transpose(0, 2, 1, 3)
+            kc = split(k) if cache[i][0] is None else np.concatenate([cache[i][0], split(k)], axis=2)
+            vc = split(v) if cache[i][1] is None else np.concatenate([cache[i][1], split(v)], axis=2)
+            cache[i] = [kc, vc]
+            qh = split(q)
+            sc = np.asarray(np.float64(1.0 / np.sqrt(D)))
+            s = (qh @ kc.swapaxes(-1, -2)) * sc
+            Tk = kc.shape[2]
+            mask = (np.triu(np.ones((T, Tk), dtype=F32), k=1 + (Tk - T)) * -1e9).astype(F32)
+            s = s + mask
+            e = np.exp(s - s.max(axis=-1, keepdims=True))
+            p = e / e.sum(axis=-1, keepdims=True)
+            o = (p @ vc).transpose(0, 2, 1, 3).reshape(B, T, cfg.n_embd)
+            y, _ = linear_fwd(o, P[a + "out_proj.weight"], P[a + "out_proj.bias"])
+            x = x + y
+            h2, _ = ln_fwd(x, P[pre + "ln2.gamma"], P[pre + "ln2.beta"])
+            f1, _ = linear_fwd(h2, P[pre + "mlp.layers.0.weight"], P[pre + "mlp.layers.0.bias"])
+            gl, _ = gelu_fwd(f1)
+            f2, _ = linear_fwd(gl, P[pre + "mlp.layers.2.weight"], P[pre + "mlp.layers.2.bias"])
+            x = x + f2
+        xf, _ = ln_fwd(x, P["ln_f.gamma"], P["ln_f.beta"])
+        logits, _ = linear_fwd(xf[:, -1:, :], P["lm_head.weight"], P["lm_head.bias"])
+        return logits[:, 0, :]
+
+    t0, cur = 0, idx
+    for _ in range(n_new):
+        logits = run(cur, t0)
+        nxt = np.argmax(logits, axis=-1)
+        top2 = np.sort(logits, axis=-1)[:, -2:]
+        margins.append(top2[:, 1] - top2[:, 0])
+        t0 += cur.shape[1]
+        idx = np.concatenate([idx, nxt[:, None]], axis=1)
+        cur = nxt[:, None]
+    return idx, np.stack(margins, axis=1)

@@ -165,3 +165,52 @@ def test_greedy_matches_reference(dev):
             logits = model(idx[:, -C0.block:]).data[:, -1, :]
             idx = np.concatenate([idx, np.argmax(logits, axis=-1)[:, None]], axis=1)
     np.testing.assert_array_equal(idx, g["tokens"])
+
+
+def test_kv_cache_greedy_matches_recompute_and_oracle(dev):
+    """KV-cache greedy decoding (prefill + one-token steps with the fused
+    attention at Tq=1) gives the same tokens as full-recompute decoding and as
+    the oracle's cached greedy on a 3-layer model."""
+    import minitorch_amd as mt
+    from oracle.gpt import GPTConfig, greedy_generate_cached, init_params
+
+    _say("[gpt] KV-cache greedy vs recompute vs oracle")
+    cfg = GPTConfig(vocab=65, block=48, n_embd=96, n_head=6, n_layer=3)
+    rng = np.random.default_rng(31)
+    P = init_params(cfg, rng)
+    prompts = rng.integers(0, cfg.vocab, (3, 8))
+    model = gpu_gpt(cfg, P)
+    model.eval()
+    toks, margins = model.generate_greedy(prompts, 30, return_margins=True)
+    ref, rmarg = greedy_generate_cached(P, cfg, prompts, 30)
+    np.testing.assert_array_equal(toks, ref)
+    np.testing.assert_allclose(margins, rmarg, rtol=0, atol=1e-4)
+    idx = prompts.copy()
+    with mt.no_grad():
+        for _ in range(30):
+            logits = model(idx).data[:, -1, :]
+            idx = np.concatenate([idx, np.argmax(logits, axis=-1)[:, None]], axis=1)
+    np.testing.assert_array_equal(toks, idx)
+
+
+def test_c4_greedy_full_config(dev):
+    """Config C4 at full size: 64 prompts x 32 tokens, +224 greedy tokens with
+    the C2 model, tokens identical to the oracle's (fixture
+    tests/golden/c4_greedy.npz, made by tests/golden/make_c4_fixture.py).  On a
+    mismatch the first differing position and its oracle top-2 margin are
+    reported."""
+    from oracle.gpt import C2, init_params
+
+    _say("[gpt] C4 greedy, 64 x (32 + 224) tokens")
+    g = load("c4_greedy.npz")
+    model = gpu_gpt(C2, init_params(C2, np.random.default_rng(2)))
+    model.eval()
+    toks, margins = model.generate_greedy(g["prompts"], 224, return_margins=True)
+    ref = g["tokens"]
+    bad = np.argwhere(toks != ref)
+    if bad.size:
+        r, c = bad[0]
+        raise AssertionError(f"{len(np.unique(bad[:, 0]))} rows differ; first at row {r} pos {c}: "
+                             f"gpu {toks[r, c]} vs oracle {ref[r, c]}, oracle top-2 margin "
+                             f"{g['margins'][r, c - 32]:.3e}, gpu margin {margins[r, c - 32]:.3e}")
+    _say(f"  all {ref.shape[0] * 224} greedy tokens identical; min oracle margin {g['margins'].min():.2e}")

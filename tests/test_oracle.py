@@ -259,3 +259,27 @@ def test_c2_step0_matches_reference_golden():
     names = list(g["names"])
     norms = np.array([np.sqrt((grads[n].astype(np.float64) ** 2).sum()) for n in names])
     np.testing.assert_allclose(norms, g["grad_norms"], rtol=1e-5, atol=1e-10)
+
+
+def test_cached_greedy_matches_reference_golden():
+    """The KV-cache form of greedy decoding gives the reference's tokens."""
+    g = load("greedy_c0.npz")
+    rng = np.random.default_rng(int(g["seed"]))
+    P = G.init_params(G.C0, rng)
+    prompts = rng.integers(0, G.C0.vocab, g["prompts"].shape)
+    toks, margins = G.greedy_generate_cached(P, G.C0, prompts, g["tokens"].shape[1] - prompts.shape[1])
+    np.testing.assert_array_equal(toks, g["tokens"])
+    # block 0 runs in float32 (the reference's dtype flow); a (B*T, C) product
+    # and a (B, 1, C) product round differently, so margins agree to ~1e-7
+    np.testing.assert_allclose(margins, g["margins"], rtol=0, atol=2e-6)
+
+
+def test_cached_greedy_equals_recompute_on_larger_model():
+    cfg = G.GPTConfig(vocab=65, block=48, n_embd=96, n_head=6, n_layer=3)
+    rng = np.random.default_rng(31)
+    P = G.init_params(cfg, rng)
+    prompts = rng.integers(0, cfg.vocab, (3, 8))
+    a, ma = G.greedy_generate(P, cfg, prompts, 20)
+    b, mb = G.greedy_generate_cached(P, cfg, prompts, 20)
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_allclose(ma, mb, rtol=0, atol=2e-6)
