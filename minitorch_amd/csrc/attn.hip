@@ -130,6 +130,74 @@ __device__ __forceinline__ void stage_tile(T* __restrict__ rowbuf, int rld,
   }
 }
 
+// A tile in flight: global -> registers (fetch) and registers -> LDS (put),
+// so the next tile's global loads overlap the current tile's MFMA work.
+// ROW: row-major copy; TRANS (bf16): transposed copy (optionally both).
+template <typename T, int R, int D, bool ROW, bool TRANS>
+struct TileRegs {
+  static constexpr int V = Elem<T>::kVec;
+  static constexpr int CPR = D / V;  // 16-byte chunks per row
+  static constexpr int NCH = TRANS ? (R / 2) * CPR : R * CPR;      // work items
+  static constexpr int PER = (NCH + kThreads - 1) / kThreads;      // items per thread
+  static constexpr int NR = TRANS ? 2 * PER : PER;                 // uint4 registers
+  uint4 r[NR];
+
+  __device__ __forceinline__ void fetch(const T* __restrict__ g, int64_t ts, int r0, int nrows, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * kThreads;
+      uint4 v0 = make_uint4(0u, 0u, 0u, 0u), v1 = v0;
+      if (c < NCH) {
+        if constexpr (TRANS) {
+          const int rp = c / CPR, cc = c % CPR;
+          const int row = r0 + 2 * rp;
+          if (row < nrows) v0 = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
+          if (row + 1 < nrows) v1 = *reinterpret_cast<const uint4*>(g + (int64_t)(row + 1) * ts + cc * V);
+        } else {
+          const int rr = c / CPR, cc = c % CPR;
+          const int row = r0 + rr;
+          if (row < nrows) v0 = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
+        }
+      }
+      if constexpr (TRANS) {
+        r[2 * i] = v0;
+        r[2 * i + 1] = v1;
+      } else {
+        r[i] = v0;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void put(T* __restrict__ rowbuf, int rld, T* __restrict__ tbuf, int tld,
+                                      int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * kThreads;
+      if (c >= NCH) continue;
+      if constexpr (TRANS) {
+        const int rp = c / CPR, cc = c % CPR;
+        const uint4 v0 = r[2 * i], v1 = r[2 * i + 1];
+        if constexpr (ROW) {
+          *reinterpret_cast<uint4*>(rowbuf + (2 * rp) * rld + cc * V) = v0;
+          *reinterpret_cast<uint4*>(rowbuf + (2 * rp + 1) * rld + cc * V) = v1;
+        }
+        const uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w};
+        const uint32_t b[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t lo = (a[w] & 0xffffu) | (b[w] << 16);
+          const uint32_t hi = (a[w] >> 16) | (b[w] & 0xffff0000u);
+          *reinterpret_cast<uint32_t*>(tbuf + (cc * 8 + 2 * w) * tld + 2 * rp) = lo;
+          *reinterpret_cast<uint32_t*>(tbuf + (cc * 8 + 2 * w + 1) * tld + 2 * rp) = hi;
+        }
+      } else {
+        const int rr = c / CPR, cc = c % CPR;
+        *reinterpret_cast<uint4*>(rowbuf + rr * rld + cc * V) = r[i];
+      }
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // MFMA operand fragments
 // ---------------------------------------------------------------------------
@@ -214,7 +282,7 @@ __device__ __forceinline__ void store_grad4(float* __restrict__ p, f32x4 v, bool
 // forward
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NQ>
-__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
@@ -226,8 +294,10 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const FwdArgs a) {
   constexpr int NS = BK / MF::KI;             // k-steps of the PV product per tile
   constexpr int LDR = D + 16 / (int)sizeof(T);  // row-major LDS stride
   constexpr int LDT = BK + 4;                 // transposed LDS stride (bf16)
-  __shared__ __attribute__((aligned(16))) T Ks[BK * LDR];
-  __shared__ __attribute__((aligned(16))) T Vs[BF ? D * LDT : BK * LDR];
+  constexpr int KSZ = BK * LDR, VSZ = BF ? D * LDT : BK * LDR;
+  constexpr int NBUF = (KSZ + VSZ) * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) T Ks[NBUF * KSZ];
+  __shared__ __attribute__((aligned(16))) T Vs[NBUF * VSZ];
 
   const int BH = a.B * a.H;
   const int nqb = (a.Tq + BQ - 1) / BQ;
@@ -272,14 +342,25 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const FwdArgs a) {
   }
 
   const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
-  for (int kb = 0; kb < kend; kb += BK) {
+  const int ntile = (kend + BK - 1) / BK;
+  TileRegs<T, BK, D, true, false> kreg;
+  TileRegs<T, BK, D, !BF, BF> vreg;
+  if (ntile > 0) {
+    kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
+    vreg.fetch(vp, a.sv.t, 0, a.Tk, tid);
+  }
+  for (int it = 0; it < ntile; ++it) {
+    const int kb = it * BK;
+    T* __restrict__ Kb = Ks + (NBUF == 2 ? (it & 1) : 0) * KSZ;
+    T* __restrict__ Vb = Vs + (NBUF == 2 ? (it & 1) : 0) * VSZ;
+    if constexpr (NBUF == 1) __syncthreads();
+    kreg.put(Kb, LDR, nullptr, 0, tid);
+    vreg.put(Vb, LDR, Vb, LDT, tid);
     __syncthreads();
-    stage_tile<T, BK, D, true, false>(Ks, LDR, nullptr, 0, kp, a.sk.t, kb, a.Tk, tid);
-    if constexpr (BF)
-      stage_tile<T, BK, D, false, true>(nullptr, 0, Vs, LDT, vp, a.sv.t, kb, a.Tk, tid);
-    else
-      stage_tile<T, BK, D, true, false>(Vs, LDR, nullptr, 0, vp, a.sv.t, kb, a.Tk, tid);
-    __syncthreads();
+    if (it + 1 < ntile) {
+      kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
+      vreg.fetch(vp, a.sv.t, kb + BK, a.Tk, tid);
+    }
 
     if (a.causal && kb > qw0 + NQ * 16 - 1 + off) continue;  // nothing visible for this wave
     const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
@@ -289,7 +370,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const FwdArgs a) {
     for (int kt = 0; kt < 4; ++kt) {
       frag kf[KC];
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) kf[kc] = dfrag<T, D>(Ks + (16 * kt + n) * LDR, g, kc);
+      for (int kc = 0; kc < KC; ++kc) kf[kc] = dfrag<T, D>(Kb + (16 * kt + n) * LDR, g, kc);
 #pragma unroll
       for (int qs = 0; qs < NQ; ++qs) {
         f32x4 t = zero4();
@@ -332,8 +413,10 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const FwdArgs a) {
           ls += p;
         }
       l[qs] = fmaf(l[qs], alpha, ls);
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {  // wave-uniform; exact skip
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[qs][dt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) acc[qs][dt] *= alpha;
+      }
 #pragma unroll
       for (int st = 0; st < NS; ++st) pf[qs][st] = pfrag<T, 4>(s[qs], st);
     }
@@ -342,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const FwdArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
-        const frag vf = tfrag<T>(Vs, LDR, Vs, LDT, 16 * dt + n, g, st);
+        const frag vf = tfrag<T>(Vb, LDR, Vb, LDT, 16 * dt + n, g, st);
 #pragma unroll
         for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(vf, pf[qs][st], acc[qs][dt]);
       }
@@ -396,7 +479,7 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const BwdArgs a) {
 // backward, pass 1: dK, dV (key-outer).  Each wave owns NK*16 keys.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NK>
-__global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
@@ -408,12 +491,14 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const BwdArgs a) {
   constexpr int NS = BQ / MF::KI;
   constexpr int LDR = D + 16 / (int)sizeof(T);
   constexpr int LDT = BQ + 4;
-  __shared__ __attribute__((aligned(16))) T Qs[BQ * LDR];
-  __shared__ __attribute__((aligned(16))) T Ds[BQ * LDR];
-  __shared__ __attribute__((aligned(16))) T Qt[BF ? D * LDT : 1];
-  __shared__ __attribute__((aligned(16))) T Dt[BF ? D * LDT : 1];
-  __shared__ float lse_s[BQ];
-  __shared__ float del_s[BQ];
+  constexpr int RSZ = BQ * LDR, TSZ = BF ? D * LDT : 0;
+  constexpr int NBUF = (2 * RSZ + 2 * TSZ) * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) T Qs[NBUF * RSZ];
+  __shared__ __attribute__((aligned(16))) T Ds[NBUF * RSZ];
+  __shared__ __attribute__((aligned(16))) T Qt[BF ? NBUF * TSZ : 1];
+  __shared__ __attribute__((aligned(16))) T Dt[BF ? NBUF * TSZ : 1];
+  __shared__ float lse_s[NBUF * BQ];
+  __shared__ float del_s[NBUF * BQ];
 
   const int BH = a.B * a.H;
   const int nkb = (a.Tk + BKV - 1) / BKV;
@@ -459,55 +544,98 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const BwdArgs a) {
 
   int qstart = a.causal ? max(0, k0 - off) : 0;
   qstart = (qstart / BQ) * BQ;
-  for (int qt = qstart; qt < a.Tq; qt += BQ) {
-    __syncthreads();
-    if constexpr (BF) {
-      stage_tile<T, BQ, D, true, true>(Qs, LDR, Qt, LDT, qp, a.sq.t, qt, a.Tq, tid);
-      stage_tile<T, BQ, D, true, true>(Ds, LDR, Dt, LDT, dop, a.sdo.t, qt, a.Tq, tid);
-    } else {
-      stage_tile<T, BQ, D, true, false>(Qs, LDR, nullptr, 0, qp, a.sq.t, qt, a.Tq, tid);
-      stage_tile<T, BQ, D, true, false>(Ds, LDR, nullptr, 0, dop, a.sdo.t, qt, a.Tq, tid);
-    }
+  const int ntile = qstart < a.Tq ? (a.Tq - qstart + BQ - 1) / BQ : 0;
+  TileRegs<T, BQ, D, true, BF> qreg, dreg;
+  float lse_r = 0.f, del_r = 0.f;
+  auto fetch = [&](int qt) {
+    qreg.fetch(qp, a.sq.t, qt, a.Tq, tid);
+    dreg.fetch(dop, a.sdo.t, qt, a.Tq, tid);
     if (tid < BQ) {
       const int qi = qt + tid;
-      lse_s[tid] = qi < a.Tq ? lsep[qi] * kLog2e : INFINITY;
-      del_s[tid] = qi < a.Tq ? delp[qi] : 0.f;
+      lse_r = qi < a.Tq ? lsep[qi] * kLog2e : INFINITY;
+      del_r = qi < a.Tq ? delp[qi] : 0.f;
+    }
+  };
+  if (ntile > 0) fetch(qstart);
+  for (int it = 0; it < ntile; ++it) {
+    const int qt = qstart + it * BQ;
+    const int bsel = NBUF == 2 ? (it & 1) : 0;
+    T* __restrict__ Qb = Qs + bsel * RSZ;
+    T* __restrict__ Db = Ds + bsel * RSZ;
+    T* __restrict__ Qtb = Qt + bsel * TSZ;
+    T* __restrict__ Dtb = Dt + bsel * TSZ;
+    float* __restrict__ lse_b = lse_s + bsel * BQ;
+    float* __restrict__ del_b = del_s + bsel * BQ;
+    if constexpr (NBUF == 1) __syncthreads();
+    qreg.put(Qb, LDR, Qtb, LDT, tid);
+    dreg.put(Db, LDR, Dtb, LDT, tid);
+    if (tid < BQ) {
+      lse_b[tid] = lse_r;
+      del_b[tid] = del_r;
     }
     __syncthreads();
+    if (it + 1 < ntile) fetch(qt + BQ);
 
     // wave-level causal skip: every key of the wave is after every query of the tile
     if (a.causal && kw0 > qt + BQ - 1 + off) continue;
     const bool need_mask = a.causal && (kw0 + NK * 16 - 1 > qt + off);
 
+    // The 64-query tile is walked in groups of GQ 16-query sub-tiles, one
+    // group per dV/dK MFMA k-step (bf16: 32 queries; fp32: 16 queries = 4
+    // steps).  Every LDS fragment is read once and feeds all NK key
+    // sub-blocks of the wave; only one group's P / dS is live at a time.
+    constexpr int GQ = MF::KI >= 16 ? MF::KI / 16 : 1;
+    constexpr int NG = 4 / GQ;
+    constexpr int SPG = NS / NG;
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) {
-      f32x4 p[4], ds[4];
+    for (int gq = 0; gq < NG; ++gq) {
+      f32x4 p[NK][GQ], ds[NK][GQ];
 #pragma unroll
-      for (int qs = 0; qs < 4; ++qs) {
-        f32x4 sv = zero4(), dpv = zero4();
+      for (int j = 0; j < GQ; ++j) {
+        const int qs = gq * GQ + j;
+        frag qa[KC], da[KC];
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
-          sv = MF::mma(dfrag<T, D>(Qs + (16 * qs + n) * LDR, g, kc), kf[ks][kc], sv);
-          dpv = MF::mma(dfrag<T, D>(Ds + (16 * qs + n) * LDR, g, kc), vf[ks][kc], dpv);
+          qa[kc] = dfrag<T, D>(Qb + (16 * qs + n) * LDR, g, kc);
+          da[kc] = dfrag<T, D>(Db + (16 * qs + n) * LDR, g, kc);
         }
-        const int kj = kw0 + 16 * ks + n;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int ql = 16 * qs + 4 * g + r;
-          float pv = __builtin_amdgcn_exp2f(fmaf(sv[r], c, -lse_s[ql]));
-          if (need_mask && kj > qt + ql + off) pv = 0.f;
-          p[qs][r] = pv;
-          ds[qs][r] = pv * (dpv[r] - del_s[ql]);
+        for (int ks = 0; ks < NK; ++ks) {
+          f32x4 sv = zero4(), dpv = zero4();
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc) {
+            sv = MF::mma(qa[kc], kf[ks][kc], sv);
+            dpv = MF::mma(da[kc], vf[ks][kc], dpv);
+          }
+          const int kj = kw0 + 16 * ks + n;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int ql = 16 * qs + 4 * g + r;
+            float pv = __builtin_amdgcn_exp2f(fmaf(sv[r], c, -lse_b[ql]));
+            if (need_mask && kj > qt + ql + off) pv = 0.f;
+            p[ks][j][r] = pv;
+            ds[ks][j][r] = pv * (dpv[r] - del_b[ql]);
+          }
         }
       }
 #pragma unroll
-      for (int st = 0; st < NS; ++st) {
-        const frag pb = pfrag<T, 4>(p, st);
-        const frag db = pfrag<T, 4>(ds, st);
+      for (int ls = 0; ls < SPG; ++ls) {
+        const int st = gq * SPG + ls;
+        frag pb[NK], db[NK];
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) {
+          pb[ks] = pfrag<T, GQ>(p[ks], ls);
+          db[ks] = pfrag<T, GQ>(ds[ks], ls);
+        }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          dva[ks][dt] = MF::mma(tfrag<T>(Ds, LDR, Dt, LDT, 16 * dt + n, g, st), pb, dva[ks][dt]);
-          dka[ks][dt] = MF::mma(tfrag<T>(Qs, LDR, Qt, LDT, 16 * dt + n, g, st), db, dka[ks][dt]);
+          const frag dof = tfrag<T>(Db, LDR, Dtb, LDT, 16 * dt + n, g, st);
+          const frag qf2 = tfrag<T>(Qb, LDR, Qtb, LDT, 16 * dt + n, g, st);
+#pragma unroll
+          for (int ks = 0; ks < NK; ++ks) {
+            dva[ks][dt] = MF::mma(dof, pb[ks], dva[ks][dt]);
+            dka[ks][dt] = MF::mma(qf2, db[ks], dka[ks][dt]);
+          }
         }
       }
     }
@@ -533,7 +661,7 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const BwdArgs a) {
 // backward, pass 2: dQ (query-outer, transposed products like the forward)
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NQ>
-__global__ __launch_bounds__(kThreads) void attn_dq_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
@@ -545,9 +673,11 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const BwdArgs a) {
   constexpr int NS = BK / MF::KI;
   constexpr int LDR = D + 16 / (int)sizeof(T);
   constexpr int LDT = BK + 4;
-  __shared__ __attribute__((aligned(16))) T Ks[BK * LDR];
-  __shared__ __attribute__((aligned(16))) T Vs[BK * LDR];
-  __shared__ __attribute__((aligned(16))) T Kt[BF ? D * LDT : 1];
+  constexpr int RSZ = BK * LDR, TSZ = BF ? D * LDT : 0;
+  constexpr int NBUF = (2 * RSZ + TSZ) * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) T Ks[NBUF * RSZ];
+  __shared__ __attribute__((aligned(16))) T Vs[NBUF * RSZ];
+  __shared__ __attribute__((aligned(16))) T Kt[BF ? NBUF * TSZ : 1];
 
   const int BH = a.B * a.H;
   const int nqb = (a.Tq + BQ - 1) / BQ;
@@ -593,14 +723,27 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const BwdArgs a) {
     for (int dt = 0; dt < DT; ++dt) acc[qs][dt] = zero4();
 
   const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
-  for (int kb = 0; kb < kend; kb += BK) {
+  const int ntile = (kend + BK - 1) / BK;
+  TileRegs<T, BK, D, true, BF> kreg;
+  TileRegs<T, BK, D, true, false> vreg;
+  if (ntile > 0) {
+    kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
+    vreg.fetch(vp, a.sv.t, 0, a.Tk, tid);
+  }
+  for (int it = 0; it < ntile; ++it) {
+    const int kb = it * BK;
+    const int bsel = NBUF == 2 ? (it & 1) : 0;
+    T* __restrict__ Kb = Ks + bsel * RSZ;
+    T* __restrict__ Vb = Vs + bsel * RSZ;
+    T* __restrict__ Ktb = Kt + bsel * TSZ;
+    if constexpr (NBUF == 1) __syncthreads();
+    kreg.put(Kb, LDR, Ktb, LDT, tid);
+    vreg.put(Vb, LDR, nullptr, 0, tid);
     __syncthreads();
-    if constexpr (BF)
-      stage_tile<T, BK, D, true, true>(Ks, LDR, Kt, LDT, kp, a.sk.t, kb, a.Tk, tid);
-    else
-      stage_tile<T, BK, D, true, false>(Ks, LDR, nullptr, 0, kp, a.sk.t, kb, a.Tk, tid);
-    stage_tile<T, BK, D, true, false>(Vs, LDR, nullptr, 0, vp, a.sv.t, kb, a.Tk, tid);
-    __syncthreads();
+    if (it + 1 < ntile) {
+      kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
+      vreg.fetch(vp, a.sv.t, kb + BK, a.Tk, tid);
+    }
 
     if (a.causal && kb > qw0 + NQ * 16 - 1 + off) continue;
     const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
@@ -611,8 +754,8 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const BwdArgs a) {
       frag kfr[KC], vfr[KC];
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        kfr[kc] = dfrag<T, D>(Ks + (16 * kt + n) * LDR, g, kc);
-        vfr[kc] = dfrag<T, D>(Vs + (16 * kt + n) * LDR, g, kc);
+        kfr[kc] = dfrag<T, D>(Kb + (16 * kt + n) * LDR, g, kc);
+        vfr[kc] = dfrag<T, D>(Vb + (16 * kt + n) * LDR, g, kc);
       }
 #pragma unroll
       for (int qs = 0; qs < NQ; ++qs) {
@@ -642,7 +785,7 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const BwdArgs a) {
       for (int qs = 0; qs < NQ; ++qs) db[qs] = pfrag<T, 4>(ds[qs], st);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const frag kt_f = tfrag<T>(Ks, LDR, Kt, LDT, 16 * dt + n, g, st);
+        const frag kt_f = tfrag<T>(Kb, LDR, Ktb, LDT, 16 * dt + n, g, st);
 #pragma unroll
         for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(kt_f, db[qs], acc[qs][dt]);
       }
@@ -666,9 +809,16 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const BwdArgs a) {
 // host side
 // ---------------------------------------------------------------------------
 // tile parameters per dtype
-template <typename T> struct Cfg;
-template <> struct Cfg<float> { static constexpr int NQ = 1, NK = 1; };
-template <> struct Cfg<bf16_t> { static constexpr int NQ = 2, NK = 2; };
+// NQ: 16-query sub-tiles per wave (forward, dQ); NK: 16-key sub-tiles per
+// wave (dK/dV).  Larger values reuse each LDS fragment for more MFMAs; they
+// are capped where the accumulators would no longer fit 2 waves per SIMD.
+template <typename T, int D> struct Cfg;
+template <int D> struct Cfg<float, D> { static constexpr int NQ = 1, NK = 1, NQF = 1; };
+template <int D> struct Cfg<bf16_t, D> {
+  static constexpr int NQ = D <= 64 ? 2 : 1;
+  static constexpr int NQF = 2;
+  static constexpr int NK = D <= 64 ? 2 : 1;
+};
 
 int check_bhtd(const char* name, const void* p, const int64_t* s, int esize) {
   MTX_CHECK_ARG(p != nullptr, "%s: null pointer", name);
@@ -697,7 +847,7 @@ Str3 s3(const int64_t* s) { return Str3{s[0], s[1], s[2]}; }
 
 template <typename T, int D>
 int launch_fwd(const FwdArgs& a, hipStream_t st) {
-  constexpr int NQ = Cfg<T>::NQ;
+  constexpr int NQ = Cfg<T, D>::NQF;
   constexpr int BQ = kWaves * NQ * 16;
   const int grid = cdiv(a.Tq, BQ) * a.B * a.H;
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQ>), dim3(grid), dim3(kThreads), 0, st, a);
@@ -707,7 +857,7 @@ int launch_fwd(const FwdArgs& a, hipStream_t st) {
 
 template <typename T, int D>
 int launch_bwd(const BwdArgs& a, int phases, hipStream_t st) {
-  constexpr int NQ = Cfg<T>::NQ, NK = Cfg<T>::NK;
+  constexpr int NQ = Cfg<T, D>::NQ, NK = Cfg<T, D>::NK;
   if (phases & MTX_ATTN_BWD_DELTA) {
     const int64_t rows = (int64_t)a.B * a.H * a.Tq;
     hipLaunchKernelGGL((attn_delta_kernel<T, D>), dim3((unsigned)((rows + kThreads - 1) / kThreads)),
