@@ -226,21 +226,30 @@ __device__ __forceinline__ typename Mfma<T>::frag dfrag(const T* __restrict__ p,
   }
 }
 
-// A operand X^T[d = dcol][j] for k-step s over the j (key or query) dimension,
-// where the matching B operand comes from C-layout accumulators (see pfrag).
-//   fp32: step s covers j = 16*(s/4) + 4g + (s%4): read row-major X[j][dcol].
-//   bf16: step s covers j = 32s + 16*(e/4) + 4g + (e%4): read transposed Xt[dcol][j].
+// A operand X^T[d][j] for k-step s over the j (key or query) dimension of a
+// row-major LDS tile X[j][d] (row stride rld), for d = 16*dt + n, where the
+// matching B operand comes from C-layout accumulators (see pfrag).
+//   fp32: step s covers j = 16*(s/4) + 4g + (s%4): one scalar read.
+//   bf16: step s covers j = 32s + 16*(e/4) + 4g + (e%4), e = 0..7, read with
+//   two gfx950 transposing LDS loads (ds_read_b64_tr_b16).  Within each
+//   16-lane group, element i of lane k's result is element (k%4) of the 8-byte
+//   chunk addressed by lane 4i + k/4 of the group, so lane (g, n) addresses
+//   X[32s + 4g + n/4][16dt + 4(n%4)] (and 16 rows further for e = 4..7) and
+//   receives X[32s + 4g + i][16dt + n], i = 0..3.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
 template <typename T>
-__device__ __forceinline__ typename Mfma<T>::frag tfrag(const T* __restrict__ rowbuf, int rld,
-                                                        const T* __restrict__ tbuf, int tld,
-                                                        int dcol, int g, int s) {
+__device__ __forceinline__ typename Mfma<T>::frag tfrag(const T* __restrict__ rowbuf, int rld, int dt, int n,
+                                                        int g, int s) {
   if constexpr (sizeof(T) == 4) {
-    return rowbuf[(16 * (s >> 2) + 4 * g + (s & 3)) * rld + dcol];
+    return rowbuf[(16 * (s >> 2) + 4 * g + (s & 3)) * rld + 16 * dt + n];
   } else {
-    const T* p = tbuf + dcol * tld + 32 * s + 4 * g;
-    const uint2 lo = *reinterpret_cast<const uint2*>(p);
-    const uint2 hi = *reinterpret_cast<const uint2*>(p + 16);
-    return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+    const T* p = rowbuf + (32 * s + 4 * g + (n >> 2)) * rld + 16 * dt + 4 * (n & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 16 * rld));
+    const uint2 ul = __builtin_bit_cast(uint2, lo), uh = __builtin_bit_cast(uint2, hi);
+    return __builtin_bit_cast(bf16x8, make_uint4(ul.x, ul.y, uh.x, uh.y));
   }
 }
 
@@ -293,8 +302,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
   constexpr int BK = 64;
   constexpr int NS = BK / MF::KI;             // k-steps of the PV product per tile
   constexpr int LDR = D + 16 / (int)sizeof(T);  // row-major LDS stride
-  constexpr int LDT = BK + 4;                 // transposed LDS stride (bf16)
-  constexpr int KSZ = BK * LDR, VSZ = BF ? D * LDT : BK * LDR;
+  constexpr int KSZ = BK * LDR, VSZ = BK * LDR;
   constexpr int NBUF = (KSZ + VSZ) * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) T Ks[NBUF * KSZ];
   __shared__ __attribute__((aligned(16))) T Vs[NBUF * VSZ];
@@ -343,8 +351,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
 
   const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
   const int ntile = (kend + BK - 1) / BK;
-  TileRegs<T, BK, D, true, false> kreg;
-  TileRegs<T, BK, D, !BF, BF> vreg;
+  TileRegs<T, BK, D, true, false> kreg, vreg;
   if (ntile > 0) {
     kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
     vreg.fetch(vp, a.sv.t, 0, a.Tk, tid);
@@ -355,7 +362,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
     T* __restrict__ Vb = Vs + (NBUF == 2 ? (it & 1) : 0) * VSZ;
     if constexpr (NBUF == 1) __syncthreads();
     kreg.put(Kb, LDR, nullptr, 0, tid);
-    vreg.put(Vb, LDR, Vb, LDT, tid);
+    vreg.put(Vb, LDR, nullptr, 0, tid);
     __syncthreads();
     if (it + 1 < ntile) {
       kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
@@ -425,7 +432,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
-        const frag vf = tfrag<T>(Vb, LDR, Vb, LDT, 16 * dt + n, g, st);
+        const frag vf = tfrag<T>(Vb, LDR, dt, n, g, st);
 #pragma unroll
         for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(vf, pf[qs][st], acc[qs][dt]);
       }
@@ -490,13 +497,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   constexpr int BQ = 64;
   constexpr int NS = BQ / MF::KI;
   constexpr int LDR = D + 16 / (int)sizeof(T);
-  constexpr int LDT = BQ + 4;
-  constexpr int RSZ = BQ * LDR, TSZ = BF ? D * LDT : 0;
-  constexpr int NBUF = (2 * RSZ + 2 * TSZ) * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  constexpr int RSZ = BQ * LDR;
+  constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) T Qs[NBUF * RSZ];
   __shared__ __attribute__((aligned(16))) T Ds[NBUF * RSZ];
-  __shared__ __attribute__((aligned(16))) T Qt[BF ? NBUF * TSZ : 1];
-  __shared__ __attribute__((aligned(16))) T Dt[BF ? NBUF * TSZ : 1];
   __shared__ float lse_s[NBUF * BQ];
   __shared__ float del_s[NBUF * BQ];
 
@@ -545,7 +549,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   int qstart = a.causal ? max(0, k0 - off) : 0;
   qstart = (qstart / BQ) * BQ;
   const int ntile = qstart < a.Tq ? (a.Tq - qstart + BQ - 1) / BQ : 0;
-  TileRegs<T, BQ, D, true, BF> qreg, dreg;
+  TileRegs<T, BQ, D, true, false> qreg, dreg;
   float lse_r = 0.f, del_r = 0.f;
   auto fetch = [&](int qt) {
     qreg.fetch(qp, a.sq.t, qt, a.Tq, tid);
@@ -562,13 +566,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
     const int bsel = NBUF == 2 ? (it & 1) : 0;
     T* __restrict__ Qb = Qs + bsel * RSZ;
     T* __restrict__ Db = Ds + bsel * RSZ;
-    T* __restrict__ Qtb = Qt + bsel * TSZ;
-    T* __restrict__ Dtb = Dt + bsel * TSZ;
     float* __restrict__ lse_b = lse_s + bsel * BQ;
     float* __restrict__ del_b = del_s + bsel * BQ;
     if constexpr (NBUF == 1) __syncthreads();
-    qreg.put(Qb, LDR, Qtb, LDT, tid);
-    dreg.put(Db, LDR, Dtb, LDT, tid);
+    qreg.put(Qb, LDR, nullptr, 0, tid);
+    dreg.put(Db, LDR, nullptr, 0, tid);
     if (tid < BQ) {
       lse_b[tid] = lse_r;
       del_b[tid] = del_r;
@@ -629,8 +631,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const frag dof = tfrag<T>(Db, LDR, Dtb, LDT, 16 * dt + n, g, st);
-          const frag qf2 = tfrag<T>(Qb, LDR, Qtb, LDT, 16 * dt + n, g, st);
+          const frag dof = tfrag<T>(Db, LDR, dt, n, g, st);
+          const frag qf2 = tfrag<T>(Qb, LDR, dt, n, g, st);
 #pragma unroll
           for (int ks = 0; ks < NK; ++ks) {
             dva[ks][dt] = MF::mma(dof, pb[ks], dva[ks][dt]);
@@ -672,12 +674,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
   constexpr int BK = 64;
   constexpr int NS = BK / MF::KI;
   constexpr int LDR = D + 16 / (int)sizeof(T);
-  constexpr int LDT = BK + 4;
-  constexpr int RSZ = BK * LDR, TSZ = BF ? D * LDT : 0;
-  constexpr int NBUF = (2 * RSZ + TSZ) * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  constexpr int RSZ = BK * LDR;
+  constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) T Ks[NBUF * RSZ];
   __shared__ __attribute__((aligned(16))) T Vs[NBUF * RSZ];
-  __shared__ __attribute__((aligned(16))) T Kt[BF ? NBUF * TSZ : 1];
 
   const int BH = a.B * a.H;
   const int nqb = (a.Tq + BQ - 1) / BQ;
@@ -724,8 +724,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
 
   const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
   const int ntile = (kend + BK - 1) / BK;
-  TileRegs<T, BK, D, true, BF> kreg;
-  TileRegs<T, BK, D, true, false> vreg;
+  TileRegs<T, BK, D, true, false> kreg, vreg;
   if (ntile > 0) {
     kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
     vreg.fetch(vp, a.sv.t, 0, a.Tk, tid);
@@ -735,9 +734,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
     const int bsel = NBUF == 2 ? (it & 1) : 0;
     T* __restrict__ Kb = Ks + bsel * RSZ;
     T* __restrict__ Vb = Vs + bsel * RSZ;
-    T* __restrict__ Ktb = Kt + bsel * TSZ;
     if constexpr (NBUF == 1) __syncthreads();
-    kreg.put(Kb, LDR, Ktb, LDT, tid);
+    kreg.put(Kb, LDR, nullptr, 0, tid);
     vreg.put(Vb, LDR, nullptr, 0, tid);
     __syncthreads();
     if (it + 1 < ntile) {
@@ -785,7 +783,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
       for (int qs = 0; qs < NQ; ++qs) db[qs] = pfrag<T, 4>(ds[qs], st);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const frag kt_f = tfrag<T>(Kb, LDR, Ktb, LDT, 16 * dt + n, g, st);
+        const frag kt_f = tfrag<T>(Kb, LDR, dt, n, g, st);
 #pragma unroll
         for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(kt_f, db[qs], acc[qs][dt]);
       }
