@@ -27,6 +27,13 @@
 #include "mtx_common.h"
 
 #include <cmath>
+#include <type_traits>
+
+// 1: the dK/dV tile body is instantiated twice (masked diagonal tiles,
+// unmasked interior tiles); 0: one body with a run-time mask test
+#ifndef MTX_DKDV_SPLIT
+#define MTX_DKDV_SPLIT 1
+#endif
 
 namespace mtx {
 namespace {
@@ -142,21 +149,30 @@ struct TileRegs {
   static constexpr int NR = TRANS ? 2 * PER : PER;                 // uint4 registers
   uint4 r[NR];
 
+  // `full` (wave-uniform): every row of the tile is < nrows, so loads need no guard
   __device__ __forceinline__ void fetch(const T* __restrict__ g, int64_t ts, int r0, int nrows, int tid) {
+    const bool full = r0 + R <= nrows;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * kThreads;
       uint4 v0 = make_uint4(0u, 0u, 0u, 0u), v1 = v0;
-      if (c < NCH) {
+      if (NCH % kThreads == 0 || c < NCH) {
         if constexpr (TRANS) {
           const int rp = c / CPR, cc = c % CPR;
           const int row = r0 + 2 * rp;
-          if (row < nrows) v0 = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
-          if (row + 1 < nrows) v1 = *reinterpret_cast<const uint4*>(g + (int64_t)(row + 1) * ts + cc * V);
+          const T* p0 = g + (int64_t)row * ts + cc * V;
+          if (full) {
+            v0 = *reinterpret_cast<const uint4*>(p0);
+            v1 = *reinterpret_cast<const uint4*>(p0 + ts);
+          } else {
+            if (row < nrows) v0 = *reinterpret_cast<const uint4*>(p0);
+            if (row + 1 < nrows) v1 = *reinterpret_cast<const uint4*>(p0 + ts);
+          }
         } else {
           const int rr = c / CPR, cc = c % CPR;
           const int row = r0 + rr;
-          if (row < nrows) v0 = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
+          const T* p0 = g + (int64_t)row * ts + cc * V;
+          if (full || row < nrows) v0 = *reinterpret_cast<const uint4*>(p0);
         }
       }
       if constexpr (TRANS) {
@@ -173,7 +189,7 @@ struct TileRegs {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * kThreads;
-      if (c >= NCH) continue;
+      if (NCH % kThreads != 0 && c >= NCH) continue;
       if constexpr (TRANS) {
         const int rp = c / CPR, cc = c % CPR;
         const uint4 v0 = r[2 * i], v1 = r[2 * i + 1];
@@ -195,6 +211,19 @@ struct TileRegs {
         *reinterpret_cast<uint4*>(rowbuf + rr * rld + cc * V) = r[i];
       }
     }
+  }
+};
+
+// xor-shuffles across the 16-lane groups of a wave64 through ds_bpermute, with
+// the byte addresses computed once per kernel
+struct Xor1632 {
+  int a16, a32;
+  __device__ __forceinline__ explicit Xor1632(int lane) : a16((lane ^ 16) << 2), a32((lane ^ 32) << 2) {}
+  __device__ __forceinline__ float x16(float v) const {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(a16, __float_as_int(v)));
+  }
+  __device__ __forceinline__ float x32(float v) const {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(a32, __float_as_int(v)));
   }
 };
 
@@ -287,6 +316,16 @@ __device__ __forceinline__ void store_grad4(float* __restrict__ p, f32x4 v, bool
   *reinterpret_cast<f32x4*>(p) = v;
 }
 
+// Row padding (elements) of LDS tiles: keeps 16-byte row alignment and
+// spreads rows over the LDS banks.
+#ifndef MTX_BF16_LDS_PAD
+#define MTX_BF16_LDS_PAD 8
+#endif
+template <typename T>
+__host__ __device__ constexpr int lds_pad() {
+  return sizeof(T) == 2 ? MTX_BF16_LDS_PAD : 4;
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
@@ -301,7 +340,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
   constexpr int BQ = kWaves * NQ * 16;
   constexpr int BK = 64;
   constexpr int NS = BK / MF::KI;             // k-steps of the PV product per tile
-  constexpr int LDR = D + 16 / (int)sizeof(T);  // row-major LDS stride
+  constexpr int LDR = D + lds_pad<T>();  // row-major LDS stride
   constexpr int KSZ = BK * LDR, VSZ = BK * LDR;
   constexpr int NBUF = (KSZ + VSZ) * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) T Ks[NBUF * KSZ];
@@ -318,12 +357,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
   T* __restrict__ op = static_cast<T*>(a.o) + b * a.so.b + h * a.so.h;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wid = tid >> 6;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int n = lane & 15, g = lane >> 4;
   const int q0 = qb * BQ;
   const int qw0 = q0 + wid * NQ * 16;
   const int off = a.Tk - a.Tq;
   const float c = a.scale * kLog2e;
+  const Xor1632 xs(lane);
 
   // Q fragments (B operand of S^T = K Q^T), straight from global memory
   frag qf[NQ][KC];
@@ -391,22 +432,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
 #pragma unroll
     for (int qs = 0; qs < NQ; ++qs) {
       if (need_mask) {
+        // key kb + 16kt + 4g + r is visible iff 16kt + r <= lim
         const int qi = qw0 + 16 * qs + n;
+        int lim = a.Tk - 1 - kb - 4 * g;
+        if (a.causal) lim = min(lim, qi + off - kb - 4 * g);
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int kj = kb + 16 * kt + 4 * g + r;
-            if (kj >= a.Tk || (a.causal && kj > qi + off)) s[qs][kt][r] = -INFINITY;
-          }
+          for (int r = 0; r < 4; ++r)
+            if (16 * kt + r > lim) s[qs][kt][r] = -INFINITY;
       }
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[qs][kt][r]);
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
+      mx = fmaxf(mx, xs.x16(mx));
+      mx = fmaxf(mx, xs.x32(mx));
       const float mnew = fmaxf(m[qs], mx * c);
       const float alpha = __builtin_amdgcn_exp2f(m[qs] - mnew);
       m[qs] = mnew;
@@ -442,8 +484,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
 #pragma unroll
   for (int qs = 0; qs < NQ; ++qs) {
     float lt = l[qs];
-    lt += shfl_xor(lt, 16);
-    lt += shfl_xor(lt, 32);
+    lt += xs.x16(lt);
+    lt += xs.x32(lt);
     const int qi = qw0 + 16 * qs + n;
     if (qi < a.Tq) {
       const float inv = 1.0f / lt;
@@ -496,7 +538,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   constexpr int BKV = kWaves * NK * 16;
   constexpr int BQ = 64;
   constexpr int NS = BQ / MF::KI;
-  constexpr int LDR = D + 16 / (int)sizeof(T);
+  constexpr int LDR = D + lds_pad<T>();
   constexpr int RSZ = BQ * LDR;
   constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) T Qs[NBUF * RSZ];
@@ -517,7 +559,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   const float* __restrict__ delp = a.delta + (int64_t)bh * a.Tq;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wid = tid >> 6;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int k0 = kbk * BKV;
   const int kw0 = k0 + wid * NK * 16;
@@ -581,6 +624,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
     // wave-level causal skip: every key of the wave is after every query of the tile
     if (a.causal && kw0 > qt + BQ - 1 + off) continue;
     const bool need_mask = a.causal && (kw0 + NK * 16 - 1 > qt + off);
+    auto tile = [&](auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
 
     // The 64-query tile is walked in groups of GQ 16-query sub-tiles, one
     // group per dV/dK MFMA k-step (bf16: 32 queries; fp32: 16 queries = 4
@@ -609,12 +654,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
             sv = MF::mma(qa[kc], kf[ks][kc], sv);
             dpv = MF::mma(da[kc], vf[ks][kc], dpv);
           }
-          const int kj = kw0 + 16 * ks + n;
+          // key kj is hidden from query qt + ql iff r < kj - qt - off - 16qs - 4g
+          const int hid = kw0 + 16 * ks + n - qt - off - 16 * qs - 4 * g;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int ql = 16 * qs + 4 * g + r;
             float pv = __builtin_amdgcn_exp2f(fmaf(sv[r], c, -lse_b[ql]));
-            if (need_mask && kj > qt + ql + off) pv = 0.f;
+            if (MASKED && need_mask && r < hid) pv = 0.f;
             p[ks][j][r] = pv;
             ds[ks][j][r] = pv * (dpv[r] - del_b[ql]);
           }
@@ -641,6 +687,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
         }
       }
     }
+      };
+#if MTX_DKDV_SPLIT
+    if (need_mask) tile(std::true_type{});
+    else tile(std::false_type{});
+#else
+    tile(std::true_type{});
+#endif
   }
 
   float* __restrict__ dkp = a.dk + b * a.sdk.b + h * a.sdk.h;
@@ -673,7 +726,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
   constexpr int BQ = kWaves * NQ * 16;
   constexpr int BK = 64;
   constexpr int NS = BK / MF::KI;
-  constexpr int LDR = D + 16 / (int)sizeof(T);
+  constexpr int LDR = D + lds_pad<T>();
   constexpr int RSZ = BK * LDR;
   constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) T Ks[NBUF * RSZ];
@@ -690,7 +743,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
   const T* __restrict__ dop = static_cast<const T*>(a.dout) + b * a.sdo.b + h * a.sdo.h;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wid = tid >> 6;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int q0 = qb * BQ;
   const int qw0 = q0 + wid * NQ * 16;
@@ -745,6 +799,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
 
     if (a.causal && kb > qw0 + NQ * 16 - 1 + off) continue;
     const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
+    auto tile = [&](auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
 
     f32x4 ds[NQ][4];
 #pragma unroll
@@ -763,13 +819,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
           sv = MF::mma(kfr[kc], qf[qs][kc], sv);
           dpv = MF::mma(vfr[kc], df[qs][kc], dpv);
         }
-        const int qi = qw0 + 16 * qs + n;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float pv = __builtin_amdgcn_exp2f(fmaf(sv[r], c, -lse2[qs]));
-          if (need_mask) {
-            const int kj = kb + 16 * kt + 4 * g + r;
-            if (kj >= a.Tk || (a.causal && kj > qi + off)) pv = 0.f;
+          if constexpr (MASKED) {
+            // key kb + 16kt + 4g + r is visible iff r <= lim
+            int lim = a.Tk - 1 - kb - 16 * kt - 4 * g;
+            if (a.causal) lim = min(lim, qw0 + 16 * qs + n + off - kb - 16 * kt - 4 * g);
+            if (r > lim) pv = 0.f;
           }
           ds[qs][kt][r] = pv * (dpv[r] - del[qs]);
         }
@@ -788,6 +845,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
         for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(kt_f, db[qs], acc[qs][dt]);
       }
     }
+      };
+    if (need_mask) tile(std::true_type{});
+    else tile(std::false_type{});
   }
 
   float* __restrict__ dqp = a.dq + b * a.sdq.b + h * a.sdq.h;
@@ -810,12 +870,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
 // NQ: 16-query sub-tiles per wave (forward, dQ); NK: 16-key sub-tiles per
 // wave (dK/dV).  Larger values reuse each LDS fragment for more MFMAs; they
 // are capped where the accumulators would no longer fit 2 waves per SIMD.
+// Compile-time tuning knobs (bf16, D <= 64), overridable with -D for sweeps.
+#ifndef MTX_FWD_NQ_BF16
+#define MTX_FWD_NQ_BF16 2
+#endif
+#ifndef MTX_DQ_NQ_BF16
+#define MTX_DQ_NQ_BF16 2
+#endif
+#ifndef MTX_DKDV_NK_BF16
+#define MTX_DKDV_NK_BF16 2
+#endif
 template <typename T, int D> struct Cfg;
 template <int D> struct Cfg<float, D> { static constexpr int NQ = 1, NK = 1, NQF = 1; };
 template <int D> struct Cfg<bf16_t, D> {
-  static constexpr int NQ = D <= 64 ? 2 : 1;
-  static constexpr int NQF = 2;
-  static constexpr int NK = D <= 64 ? 2 : 1;
+  static constexpr int NQ = D <= 64 ? MTX_DQ_NQ_BF16 : 1;
+  static constexpr int NQF = D <= 64 ? MTX_FWD_NQ_BF16 : 2;
+  static constexpr int NK = D <= 64 ? MTX_DKDV_NK_BF16 : 1;
 };
 
 int check_bhtd(const char* name, const void* p, const int64_t* s, int esize) {

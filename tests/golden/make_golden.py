@@ -126,9 +126,11 @@ def train_curve(cfg: GPTConfig, seed: int, B: int, steps: int, path, full_grads_
         opt.step()
         losses.append(float(loss.data))
         print(f"  step {it:2d} loss {losses[-1]:.10f}  ({time.time() - t0:.1f}s)", flush=True)
-        # saved after every step so a long run leaves a usable prefix
-        np.savez(path, losses=np.array(losses), seed=seed, B=B, steps=len(losses), names=np.array(names),
+        # saved after every step (write + rename) so a long run leaves a usable prefix
+        tmp = path.with_name(path.stem + ".part.npz")
+        np.savez(tmp, losses=np.array(losses), seed=seed, B=B, steps=len(losses), names=np.array(names),
                  **extra)
+        tmp.replace(path)
     print(f"wrote {path.name}")
 
 
