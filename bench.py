@@ -98,10 +98,11 @@ def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup):
         K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk, dv=dv, workspace=ws)
 
     ms_step = time_loop(step, steps, warmup)
-    # per-kernel averages (each phase is one kernel launch)
+    # per-kernel averages (each phase is one kernel launch; the dQ pass also
+    # computes delta = rowsum(dO*O), which the dK/dV pass reads)
     ms_fwd = time_loop(lambda: K.attn_fwd(q, k, v, scale, True, out=o, lse=lse), steps, 2)
     ph = {}
-    for name, mask in (("delta", L.ATTN_BWD_DELTA), ("dkdv", L.ATTN_BWD_DKDV), ("dq", L.ATTN_BWD_DQ)):
+    for name, mask in (("dq", L.ATTN_BWD_DELTA | L.ATTN_BWD_DQ), ("dkdv", L.ATTN_BWD_DKDV)):
         ph[name] = time_loop(lambda m=mask: K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk,
                                                        dv=dv, workspace=ws, phases=m), steps, 2)
     torch.cuda.synchronize()
@@ -286,7 +287,7 @@ def main():
     tflops = (f3 + b3) / (r3["ms_step"] * 1e-3) / 1e12
     # dominant kernel and its algorithmic FLOPs: fwd kernel = 2u; dK/dV pass =
     # S, dP, dV, dK = 4u; dQ pass = the dQ product only (its S/dP recompute is
-    # already counted in the dK/dV pass) = 1u; delta pass = none (HBM-bound).
+    # already counted in the dK/dV pass, and its delta rowsum is O(T*D)) = 1u.
     u = B * H * T * T * D
     kern = {"attn_fwd": (r3["ms_fwd"], 2 * u), "attn_dkdv": (r3["ms_dkdv"], 4 * u),
             "attn_dq": (r3["ms_dq"], 1 * u)}

@@ -102,10 +102,12 @@ int mtx_attn_bwd(int dtype, int B, int H, int Tq, int Tk, int D,
                  float scale, int causal, int accumulate, void* stream);
 
 /*
- * The three passes of mtx_attn_bwd, selectable by a bit mask, so a caller can
- * time them separately or run the dK/dV and dQ passes on two streams once the
- * delta pass has finished.  Same arguments as mtx_attn_bwd.  DELTA writes the
- * workspace; DKDV and DQ read it.  (No reference counterpart: the reference
+ * The passes of mtx_attn_bwd, selectable by a bit mask, so a caller can time
+ * them separately.  Same arguments as mtx_attn_bwd.  DELTA writes
+ * delta = rowsum(dO*O) to the workspace; DKDV and DQ read it.  When DELTA and
+ * DQ are both selected they run as one kernel (the dQ pass computes delta for
+ * its rows and stores it); selected passes run in the order DELTA, DQ, DKDV,
+ * and mtx_attn_bwd is DELTA|DQ|DKDV.  (No reference counterpart: the reference
  * runs this backward as the per-node closures listed at mtx_attn_bwd.)
  */
 enum mtx_attn_bwd_phases {

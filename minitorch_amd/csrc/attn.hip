@@ -31,6 +31,10 @@
 
 // 1: the dK/dV tile body is instantiated twice (masked diagonal tiles,
 // unmasked interior tiles); 0: one body with a run-time mask test
+// waves per SIMD the forward kernel is compiled for
+#ifndef MTX_FWD_WAVES
+#define MTX_FWD_WAVES 2
+#endif
 #ifndef MTX_DKDV_SPLIT
 #define MTX_DKDV_SPLIT 1
 #endif
@@ -282,6 +286,34 @@ __device__ __forceinline__ typename Mfma<T>::frag tfrag(const T* __restrict__ ro
   }
 }
 
+// Operand fragment multiplied by c (rounded back to T).
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag scale_frag(typename Mfma<T>::frag f, float c) {
+  if constexpr (sizeof(T) == 4) {
+    return f * c;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (__bf16)((float)f[e] * c);
+    return f;
+  }
+}
+
+// acc + sum of the elements of an operand fragment (bf16: v_dot2 with ones).
+template <typename T>
+__device__ __forceinline__ float frag_sum(typename Mfma<T>::frag f, float acc) {
+  if constexpr (sizeof(T) == 4) {
+    return acc + f;
+  } else {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const bf16x2 pr = {f[e], f[e + 1]};
+      acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+    }
+    return acc;
+  }
+}
+
 // B operand from C-layout accumulators c[j16] (16x16 sub-tiles along j), step s.
 template <typename T, int NJ16>
 __device__ __forceinline__ typename Mfma<T>::frag pfrag(const f32x4 (&c)[NJ16], int s) {
@@ -330,7 +362,7 @@ __host__ __device__ constexpr int lds_pad() {
 // forward
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NQ>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const FwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
@@ -366,7 +398,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
   const float c = a.scale * kLog2e;
   const Xor1632 xs(lane);
 
-  // Q fragments (B operand of S^T = K Q^T), straight from global memory
+  // Q fragments (B operand of S^T = K Q^T), straight from global memory and
+  // pre-multiplied by c = scale*log2(e), so the MFMA yields log2-unit scores
   frag qf[NQ][KC];
 #pragma unroll
   for (int qs = 0; qs < NQ; ++qs) {
@@ -374,18 +407,27 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
     const int rr = row < a.Tq ? row : a.Tq - 1;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      frag f = dfrag<T, D>(qp + (int64_t)rr * a.sq.t, g, kc);
+      frag f = scale_frag<T>(dfrag<T, D>(qp + (int64_t)rr * a.sq.t, g, kc), c);
       if (row >= a.Tq) f = frag{};
       qf[qs][kc] = f;
     }
   }
 
+  // Online softmax against a reference m per query (log2 units) that moves
+  // lazily: the S MFMA starts from -m, so it yields x = s*c - m and p =
+  // exp2(x) directly.  m moves to the row max only on the row's first tile
+  // or when a tile's max exceeds it by more than kTau (so p <= 2^kTau);
+  // that path is taken by the whole wave (wave-uniform branch).  Any m gives
+  // the same O = acc / l and lse = (m + log2 l) * ln2.
+  constexpr float kTau = 8.f;
   f32x4 acc[NQ][DT];
+  f32x4 cin[NQ];
   float m[NQ], l[NQ];
 #pragma unroll
   for (int qs = 0; qs < NQ; ++qs) {
     m[qs] = -INFINITY;
     l[qs] = 0.f;
+    cin[qs] = zero4();
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[qs][dt] = zero4();
   }
@@ -421,7 +463,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
       for (int kc = 0; kc < KC; ++kc) kf[kc] = dfrag<T, D>(Kb + (16 * kt + n) * LDR, g, kc);
 #pragma unroll
       for (int qs = 0; qs < NQ; ++qs) {
-        f32x4 t = zero4();
+        f32x4 t = cin[qs];
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) t = MF::mma(kf[kc], qf[qs][kc], t);
         s[qs][kt] = t;
@@ -449,25 +491,31 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdArgs a) 
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[qs][kt][r]);
       mx = fmaxf(mx, xs.x16(mx));
       mx = fmaxf(mx, xs.x32(mx));
-      const float mnew = fmaxf(m[qs], mx * c);
-      const float alpha = __builtin_amdgcn_exp2f(m[qs] - mnew);
-      m[qs] = mnew;
-      float ls = 0.f;
+      const bool keep = m[qs] != -INFINITY && mx <= kTau;
+      if (__builtin_amdgcn_ballot_w64(!keep) != 0ull) {
+        // move this lane's reference up by d (0 for lanes that keep theirs);
+        // everything is updated in place
+        const float d = (keep || mx == -INFINITY) ? 0.f : mx;
+        const bool fresh = m[qs] == -INFINITY;
+        const float alpha = fresh ? 0.f : __builtin_amdgcn_exp2f(-d);
+        m[qs] = fresh ? (mx == -INFINITY ? -INFINITY : d) : m[qs] + d;
+        const float cm = m[qs] == -INFINITY ? 0.f : -m[qs];
+        cin[qs] = f32x4{cm, cm, cm, cm};
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[qs][kt][r], c, -mnew));
-          s[qs][kt][r] = p;
-          ls += p;
-        }
-      l[qs] = fmaf(l[qs], alpha, ls);
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {  // wave-uniform; exact skip
+        for (int kt = 0; kt < 4; ++kt) s[qs][kt] -= d;
+        l[qs] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[qs][dt] *= alpha;
       }
 #pragma unroll
-      for (int st = 0; st < NS; ++st) pf[qs][st] = pfrag<T, 4>(s[qs], st);
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[qs][kt][r] = __builtin_amdgcn_exp2f(s[qs][kt][r]);
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        pf[qs][st] = pfrag<T, 4>(s[qs], st);
+        l[qs] = frag_sum<T>(pf[qs][st], l[qs]);
+      }
     }
 
 #pragma unroll
@@ -543,8 +591,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) T Qs[NBUF * RSZ];
   __shared__ __attribute__((aligned(16))) T Ds[NBUF * RSZ];
-  __shared__ float lse_s[NBUF * BQ];
-  __shared__ float del_s[NBUF * BQ];
+  // per query of the tile: -lse*log2(e) and -delta, the starting accumulators
+  // of the S and dP MFMAs, so they yield log2(P) and dP - delta directly
+  __shared__ __attribute__((aligned(16))) float lse_s[NBUF * BQ];
+  __shared__ __attribute__((aligned(16))) float del_s[NBUF * BQ];
 
   const int BH = a.B * a.H;
   const int nkb = (a.Tk + BKV - 1) / BKV;
@@ -567,7 +617,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   const int off = a.Tk - a.Tq;
   const float c = a.scale * kLog2e;
 
-  // K and V fragments of this wave's keys (B operands of S = Q K^T, dP = dO V^T)
+  // K and V fragments of this wave's keys (B operands of S = Q K^T, dP = dO V^T);
+  // K pre-multiplied by c = scale*log2(e), so S comes out in log2 units
   frag kf[NK][KC], vf[NK][KC];
 #pragma unroll
   for (int ks = 0; ks < NK; ++ks) {
@@ -575,7 +626,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
     const int rr = row < a.Tk ? row : a.Tk - 1;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      frag fk = dfrag<T, D>(kp + (int64_t)rr * a.sk.t, g, kc);
+      frag fk = scale_frag<T>(dfrag<T, D>(kp + (int64_t)rr * a.sk.t, g, kc), c);
       frag fv = dfrag<T, D>(vp + (int64_t)rr * a.sv.t, g, kc);
       if (row >= a.Tk) { fk = frag{}; fv = frag{}; }
       kf[ks][kc] = fk;
@@ -599,8 +650,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
     dreg.fetch(dop, a.sdo.t, qt, a.Tq, tid);
     if (tid < BQ) {
       const int qi = qt + tid;
-      lse_r = qi < a.Tq ? lsep[qi] * kLog2e : INFINITY;
-      del_r = qi < a.Tq ? delp[qi] : 0.f;
+      lse_r = qi < a.Tq ? -lsep[qi] * kLog2e : -INFINITY;
+      del_r = qi < a.Tq ? -delp[qi] : 0.f;
     }
   };
   if (ntile > 0) fetch(qstart);
@@ -646,9 +697,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
           qa[kc] = dfrag<T, D>(Qb + (16 * qs + n) * LDR, g, kc);
           da[kc] = dfrag<T, D>(Db + (16 * qs + n) * LDR, g, kc);
         }
+        const f32x4 nlse = *reinterpret_cast<const f32x4*>(lse_b + 16 * qs + 4 * g);
+        const f32x4 ndel = *reinterpret_cast<const f32x4*>(del_b + 16 * qs + 4 * g);
 #pragma unroll
         for (int ks = 0; ks < NK; ++ks) {
-          f32x4 sv = zero4(), dpv = zero4();
+          f32x4 sv = nlse, dpv = ndel;
 #pragma unroll
           for (int kc = 0; kc < KC; ++kc) {
             sv = MF::mma(qa[kc], kf[ks][kc], sv);
@@ -658,11 +711,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
           const int hid = kw0 + 16 * ks + n - qt - off - 16 * qs - 4 * g;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int ql = 16 * qs + 4 * g + r;
-            float pv = __builtin_amdgcn_exp2f(fmaf(sv[r], c, -lse_b[ql]));
+            float pv = __builtin_amdgcn_exp2f(sv[r]);
             if (MASKED && need_mask && r < hid) pv = 0.f;
             p[ks][j][r] = pv;
-            ds[ks][j][r] = pv * (dpv[r] - del_b[ql]);
+            ds[ks][j][r] = pv * dpv[r];
           }
         }
       }
@@ -715,7 +767,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
 // ---------------------------------------------------------------------------
 // backward, pass 2: dQ (query-outer, transposed products like the forward)
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NQ>
+// FD: also computes delta[i] = sum_d dO[i,d] O[i,d] for its rows (from the
+// same fragments it loads anyway) and writes it for the dK/dV pass.
+template <typename T, int D, int NQ, bool FD>
 __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
@@ -750,9 +804,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
   const int qw0 = q0 + wid * NQ * 16;
   const int off = a.Tk - a.Tq;
   const float c = a.scale * kLog2e;
+  const Xor1632 xs(lane);
 
+  // Q pre-multiplied by c = scale*log2(e); the S and dP MFMAs start from
+  // -lse*log2(e) and -delta, so they yield log2(P) and dP - delta directly
   frag qf[NQ][KC], df[NQ][KC];
-  float lse2[NQ], del[NQ];
+  f32x4 nlse[NQ], ndel[NQ];
 #pragma unroll
   for (int qs = 0; qs < NQ; ++qs) {
     const int row = qw0 + 16 * qs + n;
@@ -760,14 +817,37 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
     const int rr = ok ? row : a.Tq - 1;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      frag fq = dfrag<T, D>(qp + (int64_t)rr * a.sq.t, g, kc);
+      frag fq = scale_frag<T>(dfrag<T, D>(qp + (int64_t)rr * a.sq.t, g, kc), c);
       frag fd = dfrag<T, D>(dop + (int64_t)rr * a.sdo.t, g, kc);
       if (!ok) { fq = frag{}; fd = frag{}; }
       qf[qs][kc] = fq;
       df[qs][kc] = fd;
     }
-    lse2[qs] = ok ? a.lse[(int64_t)bh * a.Tq + row] * kLog2e : INFINITY;
-    del[qs] = ok ? a.delta[(int64_t)bh * a.Tq + row] : 0.f;
+    const float nl = ok ? -a.lse[(int64_t)bh * a.Tq + row] * kLog2e : -INFINITY;
+    float dl;
+    if constexpr (FD) {
+      // this lane's quarter of the row, then the sum over the 4 lanes of the row
+      const T* __restrict__ orow = static_cast<const T*>(a.o) + b * a.so.b + h * a.so.h + (int64_t)rr * a.so.t;
+      dl = 0.f;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const frag fo = dfrag<T, D>(orow, g, kc);
+        if constexpr (sizeof(T) == 4) {
+          dl = fmaf(fo, df[qs][kc], dl);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dl = fmaf((float)fo[e], (float)df[qs][kc][e], dl);
+        }
+      }
+      dl += xs.x16(dl);
+      dl += xs.x32(dl);
+      if (ok && g == 0) a.delta[(int64_t)bh * a.Tq + row] = dl;
+    } else {
+      dl = ok ? a.delta[(int64_t)bh * a.Tq + row] : 0.f;
+    }
+    const float nd = ok ? -dl : 0.f;
+    nlse[qs] = f32x4{nl, nl, nl, nl};
+    ndel[qs] = f32x4{nd, nd, nd, nd};
   }
 
   f32x4 acc[NQ][DT];
@@ -813,7 +893,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
       }
 #pragma unroll
       for (int qs = 0; qs < NQ; ++qs) {
-        f32x4 sv = zero4(), dpv = zero4();
+        f32x4 sv = nlse[qs], dpv = ndel[qs];
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
           sv = MF::mma(kfr[kc], qf[qs][kc], sv);
@@ -821,14 +901,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float pv = __builtin_amdgcn_exp2f(fmaf(sv[r], c, -lse2[qs]));
+          float pv = __builtin_amdgcn_exp2f(sv[r]);
           if constexpr (MASKED) {
             // key kb + 16kt + 4g + r is visible iff r <= lim
             int lim = a.Tk - 1 - kb - 16 * kt - 4 * g;
             if (a.causal) lim = min(lim, qw0 + 16 * qs + n + off - kb - 16 * kt - 4 * g);
             if (r > lim) pv = 0.f;
           }
-          ds[qs][kt][r] = pv * (dpv[r] - del[qs]);
+          ds[qs][kt][r] = pv * dpv[r];
         }
       }
     }
@@ -923,23 +1003,30 @@ int launch_fwd(const FwdArgs& a, hipStream_t st) {
   return MTX_OK;
 }
 
+// Phase order: delta, dQ, dK/dV.  DELTA together with DQ runs as one
+// kernel (the dQ pass computes delta for its rows and stores it), which the
+// dK/dV pass then reads.
 template <typename T, int D>
 int launch_bwd(const BwdArgs& a, int phases, hipStream_t st) {
   constexpr int NQ = Cfg<T, D>::NQ, NK = Cfg<T, D>::NK;
-  if (phases & MTX_ATTN_BWD_DELTA) {
+  const bool fuse = (phases & MTX_ATTN_BWD_DELTA) && (phases & MTX_ATTN_BWD_DQ);
+  if ((phases & MTX_ATTN_BWD_DELTA) && !fuse) {
     const int64_t rows = (int64_t)a.B * a.H * a.Tq;
     hipLaunchKernelGGL((attn_delta_kernel<T, D>), dim3((unsigned)((rows + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, st, a);
     MTX_LAUNCHED();
   }
+  if (phases & MTX_ATTN_BWD_DQ) {
+    const int gq = cdiv(a.Tq, kWaves * NQ * 16) * a.B * a.H;
+    if (fuse)
+      hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ, true>), dim3(gq), dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ, false>), dim3(gq), dim3(kThreads), 0, st, a);
+    MTX_LAUNCHED();
+  }
   if (phases & MTX_ATTN_BWD_DKDV) {
     const int gk = cdiv(a.Tk, kWaves * NK * 16) * a.B * a.H;
     hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK>), dim3(gk), dim3(kThreads), 0, st, a);
-    MTX_LAUNCHED();
-  }
-  if (phases & MTX_ATTN_BWD_DQ) {
-    const int gq = cdiv(a.Tq, kWaves * NQ * 16) * a.B * a.H;
-    hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ>), dim3(gq), dim3(kThreads), 0, st, a);
     MTX_LAUNCHED();
   }
   return MTX_OK;

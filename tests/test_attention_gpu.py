@@ -178,6 +178,40 @@ def test_accumulate_flag(dev):
         np.testing.assert_allclose(a.cpu().numpy(), 2 * b.cpu().numpy(), rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("dtype_name", ["float32", "bfloat16"])
+def test_phases_split_match_fused(dev, dtype_name):
+    """mtx_attn_bwd_phase run as three calls (standalone delta kernel, then
+    dQ, then dK/dV) gives the oracle's gradients and agrees with the fused
+    DELTA|DQ path of mtx_attn_bwd up to the summation order of delta."""
+    import torch
+    from minitorch_amd import _lib as L
+    from minitorch_amd import kernels as K
+
+    dtype = getattr(torch, dtype_name)
+    _say(f"[attn phases split vs fused] {dtype_name}")
+    rng = np.random.default_rng(17)
+    B, H, Tq, Tk, D = 2, 3, 150, 190, 64
+    arrs = [rng.standard_normal((B, H, T, D), dtype=np.float32) for T in (Tq, Tk, Tk, Tq)]
+    if dtype == torch.bfloat16:
+        arrs = [bf16_round(0.5 * x) for x in arrs]
+    q, k, v, do = (_to_dev(x, dev, dtype) for x in arrs)
+    o, lse = K.attn_fwd(q, k, v, 0.125, True)
+    fused = K.attn_bwd(q, k, v, o, do, lse, 0.125, True)
+    split = [torch.full_like(t, float("nan")) for t in fused]
+    ws = torch.empty(L.lib().mtx_attn_bwd_workspace_bytes(B, H, Tq), dtype=torch.uint8, device=dev)
+    for ph in (L.ATTN_BWD_DELTA, L.ATTN_BWD_DQ, L.ATTN_BWD_DKDV):
+        K.attn_bwd(q, k, v, o, do, lse, 0.125, True, dq=split[0], dk=split[1], dv=split[2],
+                   workspace=ws, phases=ph)
+    torch.cuda.synchronize()
+    refs = reference_attention(*arrs, 0.125, True)[1:]
+    for name, a, b, r in zip(("dq", "dk", "dv"), fused, split, refs):
+        a, b = a.cpu().numpy(), b.cpu().numpy()
+        assert np.all(np.isfinite(b)), name
+        scale = float(np.abs(r).max())
+        assert np.abs(a - b).max() <= 1e-5 * scale, (name, float(np.abs(a - b).max()), scale)
+        (_fp32_bar if dtype == torch.float32 else _bf16_bar)(b, r, name)
+
+
 def test_c1_full(dev):
     """Config C1: B=32, H=8, T=256, D=64 fp32, q,k,v,dO ~ N(0,1) drawn in that
     order from default_rng(1); scale 1/8.  Full tensors vs the oracle."""
