@@ -10,16 +10,17 @@
 //  * "Transposed" products.  The forward and the dQ pass compute S^T = K Q^T, so
 //    a lane's accumulator column is one query: lane l owns query l%16 and keys
 //    4*(l/16)+r of each 16-key sub-tile.  Row max / row sum then need only two
-//    xor-shuffles, the O rescale is per lane, and the probabilities are already
+//    lane swaps (v_permlane16/32_swap), the O rescale is per lane, and the probabilities are already
 //    in the B-operand layout of O^T += V^T P^T (no LDS round trip for P).
 //  * The dK/dV pass computes S = Q K^T (lane owns a key) so that P and dS feed
 //    dV^T += dO^T P and dK^T += Q^T dS straight from registers, accumulating
 //    dK/dV for the workgroup's key block in registers over all query tiles.
 //  * dQ is a separate query-outer pass (recomputes S and dP) instead of fp32
 //    atomics: deterministic, and no dQ workspace traffic.
-//  * K/V (or Q/dO) tiles are staged through LDS; bf16 tiles that feed a
-//    transposed operand are also written transposed so each lane reads two
-//    8-byte words per MFMA operand.
+//  * K/V (or Q/dO) tiles are staged through LDS row-major (global -> registers
+//    -> LDS, double-buffered, one barrier per tile); operands that need the
+//    transposed tile are read with gfx950's transposing LDS load
+//    (ds_read_b64_tr_b16), so each tile is stored once.
 //  * Causal: tiles above the diagonal are skipped at workgroup and wave level;
 //    only diagonal tiles pay for the per-element mask.  Blocks are issued
 //    longest-first and all blocks of one (b,h) go to one XCD (workgroup ids are
@@ -96,140 +97,62 @@ __device__ __forceinline__ void map_block(int bid, int ntile, int BH, bool heavy
 // ---------------------------------------------------------------------------
 // LDS tile staging
 // ---------------------------------------------------------------------------
-// Copy rows [r0, r0+R) x [0, D) of a row-strided global slice into LDS.  Rows
-// >= nrows read as zero.  ROW: row-major copy (row stride rld).  TRANS (bf16
-// only): transposed copy, tbuf[d * tld + row].
-template <typename T, int R, int D, bool ROW, bool TRANS>
-__device__ __forceinline__ void stage_tile(T* __restrict__ rowbuf, int rld,
-                                           T* __restrict__ tbuf, int tld,
-                                           const T* __restrict__ g, int64_t ts,
-                                           int r0, int nrows, int tid) {
-  constexpr int V = Elem<T>::kVec;
-  constexpr int CPR = D / V;  // 16-byte chunks per row
-  if constexpr (!TRANS) {
-#pragma unroll
-    for (int c = tid; c < R * CPR; c += kThreads) {
-      const int r = c / CPR, cc = c % CPR;
-      const int row = r0 + r;
-      uint4 val = make_uint4(0u, 0u, 0u, 0u);
-      if (row < nrows) val = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
-      *reinterpret_cast<uint4*>(rowbuf + r * rld + cc * V) = val;
-    }
-  } else {
-    static_assert(sizeof(T) == 2, "transposed staging is for bf16 tiles");
-#pragma unroll
-    for (int c = tid; c < (R / 2) * CPR; c += kThreads) {
-      const int rp = c / CPR, cc = c % CPR;
-      const int row = r0 + 2 * rp;
-      uint4 v0 = make_uint4(0u, 0u, 0u, 0u), v1 = v0;
-      if (row < nrows) v0 = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
-      if (row + 1 < nrows) v1 = *reinterpret_cast<const uint4*>(g + (int64_t)(row + 1) * ts + cc * V);
-      if constexpr (ROW) {
-        *reinterpret_cast<uint4*>(rowbuf + (2 * rp) * rld + cc * V) = v0;
-        *reinterpret_cast<uint4*>(rowbuf + (2 * rp + 1) * rld + cc * V) = v1;
-      }
-      const uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w};
-      const uint32_t b[4] = {v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = (a[w] & 0xffffu) | (b[w] << 16);
-        const uint32_t hi = (a[w] >> 16) | (b[w] & 0xffff0000u);
-        *reinterpret_cast<uint32_t*>(tbuf + (cc * 8 + 2 * w) * tld + 2 * rp) = lo;
-        *reinterpret_cast<uint32_t*>(tbuf + (cc * 8 + 2 * w + 1) * tld + 2 * rp) = hi;
-      }
-    }
-  }
-}
-
-// A tile in flight: global -> registers (fetch) and registers -> LDS (put),
-// so the next tile's global loads overlap the current tile's MFMA work.
-// ROW: row-major copy; TRANS (bf16): transposed copy (optionally both).
-template <typename T, int R, int D, bool ROW, bool TRANS>
+// A tile in flight: global -> registers (fetch) and registers -> LDS (put,
+// row-major with row stride ld), so the next tile's global loads overlap the
+// current tile's MFMA work.
+template <typename T, int R, int D>
 struct TileRegs {
   static constexpr int V = Elem<T>::kVec;
-  static constexpr int CPR = D / V;  // 16-byte chunks per row
-  static constexpr int NCH = TRANS ? (R / 2) * CPR : R * CPR;      // work items
-  static constexpr int PER = (NCH + kThreads - 1) / kThreads;      // items per thread
-  static constexpr int NR = TRANS ? 2 * PER : PER;                 // uint4 registers
-  uint4 r[NR];
+  static constexpr int CPR = D / V;                           // 16-byte chunks per row
+  static constexpr int NCH = R * CPR;                         // chunks per tile
+  static constexpr int PER = (NCH + kThreads - 1) / kThreads;  // chunks per thread
+  uint4 r[PER];
 
-  // `full` (wave-uniform): every row of the tile is < nrows, so loads need no guard
+  // rows >= nrows read as zero; `full` (wave-uniform): every row of the tile is
+  // < nrows, so loads need no guard
   __device__ __forceinline__ void fetch(const T* __restrict__ g, int64_t ts, int r0, int nrows, int tid) {
     const bool full = r0 + R <= nrows;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * kThreads;
-      uint4 v0 = make_uint4(0u, 0u, 0u, 0u), v1 = v0;
+      uint4 v0 = make_uint4(0u, 0u, 0u, 0u);
       if (NCH % kThreads == 0 || c < NCH) {
-        if constexpr (TRANS) {
-          const int rp = c / CPR, cc = c % CPR;
-          const int row = r0 + 2 * rp;
-          const T* p0 = g + (int64_t)row * ts + cc * V;
-          if (full) {
-            v0 = *reinterpret_cast<const uint4*>(p0);
-            v1 = *reinterpret_cast<const uint4*>(p0 + ts);
-          } else {
-            if (row < nrows) v0 = *reinterpret_cast<const uint4*>(p0);
-            if (row + 1 < nrows) v1 = *reinterpret_cast<const uint4*>(p0 + ts);
-          }
-        } else {
-          const int rr = c / CPR, cc = c % CPR;
-          const int row = r0 + rr;
-          const T* p0 = g + (int64_t)row * ts + cc * V;
-          if (full || row < nrows) v0 = *reinterpret_cast<const uint4*>(p0);
-        }
+        const int rr = c / CPR, cc = c % CPR;
+        const int row = r0 + rr;
+        if (full || row < nrows) v0 = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
       }
-      if constexpr (TRANS) {
-        r[2 * i] = v0;
-        r[2 * i + 1] = v1;
-      } else {
-        r[i] = v0;
-      }
+      r[i] = v0;
     }
   }
 
-  __device__ __forceinline__ void put(T* __restrict__ rowbuf, int rld, T* __restrict__ tbuf, int tld,
-                                      int tid) const {
+  __device__ __forceinline__ void put(T* __restrict__ buf, int ld, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * kThreads;
       if (NCH % kThreads != 0 && c >= NCH) continue;
-      if constexpr (TRANS) {
-        const int rp = c / CPR, cc = c % CPR;
-        const uint4 v0 = r[2 * i], v1 = r[2 * i + 1];
-        if constexpr (ROW) {
-          *reinterpret_cast<uint4*>(rowbuf + (2 * rp) * rld + cc * V) = v0;
-          *reinterpret_cast<uint4*>(rowbuf + (2 * rp + 1) * rld + cc * V) = v1;
-        }
-        const uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w};
-        const uint32_t b[4] = {v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t lo = (a[w] & 0xffffu) | (b[w] << 16);
-          const uint32_t hi = (a[w] >> 16) | (b[w] & 0xffff0000u);
-          *reinterpret_cast<uint32_t*>(tbuf + (cc * 8 + 2 * w) * tld + 2 * rp) = lo;
-          *reinterpret_cast<uint32_t*>(tbuf + (cc * 8 + 2 * w + 1) * tld + 2 * rp) = hi;
-        }
-      } else {
-        const int rr = c / CPR, cc = c % CPR;
-        *reinterpret_cast<uint4*>(rowbuf + rr * rld + cc * V) = r[i];
-      }
+      const int rr = c / CPR, cc = c % CPR;
+      *reinterpret_cast<uint4*>(buf + rr * ld + cc * V) = r[i];
     }
   }
 };
 
-// xor-shuffles across the 16-lane groups of a wave64 through ds_bpermute, with
-// the byte addresses computed once per kernel
-struct Xor1632 {
-  int a16, a32;
-  __device__ __forceinline__ explicit Xor1632(int lane) : a16((lane ^ 16) << 2), a32((lane ^ 32) << 2) {}
-  __device__ __forceinline__ float x16(float v) const {
-    return __int_as_float(__builtin_amdgcn_ds_bpermute(a16, __float_as_int(v)));
-  }
-  __device__ __forceinline__ float x32(float v) const {
-    return __int_as_float(__builtin_amdgcn_ds_bpermute(a32, __float_as_int(v)));
-  }
-};
+// Reductions over the 4 lanes l, l^16, l^32, l^48 of a wave64 with the gfx950
+// lane swaps: v_permlane16_swap / v_permlane32_swap leave {v[l], v[l^16]}
+// (resp. l^32) in the two results, in some order, on every lane, so a
+// commutative op of the two needs no lane select.  Every lane of the group
+// gets the same bits.
+__device__ __forceinline__ float max4l(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum4l(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // ---------------------------------------------------------------------------
 // MFMA operand fragments
@@ -396,7 +319,6 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
   const int qw0 = q0 + wid * NQ * 16;
   const int off = a.Tk - a.Tq;
   const float c = a.scale * kLog2e;
-  const Xor1632 xs(lane);
 
   // Q fragments (B operand of S^T = K Q^T), straight from global memory and
   // pre-multiplied by c = scale*log2(e), so the MFMA yields log2-unit scores
@@ -434,7 +356,7 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
 
   const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
   const int ntile = (kend + BK - 1) / BK;
-  TileRegs<T, BK, D, true, false> kreg, vreg;
+  TileRegs<T, BK, D> kreg, vreg;
   if (ntile > 0) {
     kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
     vreg.fetch(vp, a.sv.t, 0, a.Tk, tid);
@@ -444,8 +366,8 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
     T* __restrict__ Kb = Ks + (NBUF == 2 ? (it & 1) : 0) * KSZ;
     T* __restrict__ Vb = Vs + (NBUF == 2 ? (it & 1) : 0) * VSZ;
     if constexpr (NBUF == 1) __syncthreads();
-    kreg.put(Kb, LDR, nullptr, 0, tid);
-    vreg.put(Vb, LDR, nullptr, 0, tid);
+    kreg.put(Kb, LDR, tid);
+    vreg.put(Vb, LDR, tid);
     __syncthreads();
     if (it + 1 < ntile) {
       kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
@@ -489,8 +411,7 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[qs][kt][r]);
-      mx = fmaxf(mx, xs.x16(mx));
-      mx = fmaxf(mx, xs.x32(mx));
+      mx = max4l(mx);
       const bool keep = m[qs] != -INFINITY && mx <= kTau;
       if (__builtin_amdgcn_ballot_w64(!keep) != 0ull) {
         // move this lane's reference up by d (0 for lanes that keep theirs);
@@ -532,8 +453,7 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
 #pragma unroll
   for (int qs = 0; qs < NQ; ++qs) {
     float lt = l[qs];
-    lt += xs.x16(lt);
-    lt += xs.x32(lt);
+    lt = sum4l(lt);
     const int qi = qw0 + 16 * qs + n;
     if (qi < a.Tq) {
       const float inv = 1.0f / lt;
@@ -643,7 +563,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   int qstart = a.causal ? max(0, k0 - off) : 0;
   qstart = (qstart / BQ) * BQ;
   const int ntile = qstart < a.Tq ? (a.Tq - qstart + BQ - 1) / BQ : 0;
-  TileRegs<T, BQ, D, true, false> qreg, dreg;
+  TileRegs<T, BQ, D> qreg, dreg;
   float lse_r = 0.f, del_r = 0.f;
   auto fetch = [&](int qt) {
     qreg.fetch(qp, a.sq.t, qt, a.Tq, tid);
@@ -663,8 +583,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
     float* __restrict__ lse_b = lse_s + bsel * BQ;
     float* __restrict__ del_b = del_s + bsel * BQ;
     if constexpr (NBUF == 1) __syncthreads();
-    qreg.put(Qb, LDR, nullptr, 0, tid);
-    dreg.put(Db, LDR, nullptr, 0, tid);
+    qreg.put(Qb, LDR, tid);
+    dreg.put(Db, LDR, tid);
     if (tid < BQ) {
       lse_b[tid] = lse_r;
       del_b[tid] = del_r;
@@ -804,7 +724,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
   const int qw0 = q0 + wid * NQ * 16;
   const int off = a.Tk - a.Tq;
   const float c = a.scale * kLog2e;
-  const Xor1632 xs(lane);
 
   // Q pre-multiplied by c = scale*log2(e); the S and dP MFMAs start from
   // -lse*log2(e) and -delta, so they yield log2(P) and dP - delta directly
@@ -839,8 +758,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
           for (int e = 0; e < 8; ++e) dl = fmaf((float)fo[e], (float)df[qs][kc][e], dl);
         }
       }
-      dl += xs.x16(dl);
-      dl += xs.x32(dl);
+      dl = sum4l(dl);
       if (ok && g == 0) a.delta[(int64_t)bh * a.Tq + row] = dl;
     } else {
       dl = ok ? a.delta[(int64_t)bh * a.Tq + row] : 0.f;
@@ -858,7 +776,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
 
   const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
   const int ntile = (kend + BK - 1) / BK;
-  TileRegs<T, BK, D, true, false> kreg, vreg;
+  TileRegs<T, BK, D> kreg, vreg;
   if (ntile > 0) {
     kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
     vreg.fetch(vp, a.sv.t, 0, a.Tk, tid);
@@ -869,8 +787,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
     T* __restrict__ Kb = Ks + bsel * RSZ;
     T* __restrict__ Vb = Vs + bsel * RSZ;
     if constexpr (NBUF == 1) __syncthreads();
-    kreg.put(Kb, LDR, nullptr, 0, tid);
-    vreg.put(Vb, LDR, nullptr, 0, tid);
+    kreg.put(Kb, LDR, tid);
+    vreg.put(Vb, LDR, tid);
     __syncthreads();
     if (it + 1 < ntile) {
       kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
