@@ -129,6 +129,54 @@ int mtx_attn_bwd_phase(int phases, int dtype, int B, int H, int Tq, int Tk, int 
                        void* workspace, size_t workspace_bytes,
                        float scale, int causal, int accumulate, void* stream);
 
+/*
+ * Decode-step attention: one query per (b, h) against its L cached keys,
+ * o = softmax(scale * q k^T) v, lse = log sum_j exp(scale * q.k_j).  This is
+ * the reference's attention sub-graph (transformer.py:36-44) at the last
+ * position, which GPT.generate recomputes per token (transformer.py:93-104);
+ * with a KV cache it is the whole attention work of a step.  q and o are
+ * (B, H, 1, D), k and v (B, H, L, D) views (4 element strides each, the t
+ * stride of q/o unused, unit d stride, so (B, T, C) caches pass as head views).
+ * lengths: optional device int32[B]; sequence b then uses its first
+ * min(lengths[b], L) keys (ragged batches; a length of 0 gives o = 0,
+ * lse = -inf), so one call shape serves every step of a decode loop.
+ * lse may be NULL.  0 <= L <= 8192; D in {16, 32, 64, 128}; fp32 or bf16.
+ */
+int mtx_attn_decode(int dtype, int B, int H, int L, int D,
+                    const void* q, const int64_t* q_strides,
+                    const void* k, const int64_t* k_strides,
+                    const void* v, const int64_t* v_strides,
+                    void* o, const int64_t* o_strides,
+                    float* lse, const int* lengths, float scale, void* stream);
+
+/*
+ * Greedy pick over rows of x (rows, cols; row stride ld): idx[r * idx_stride]
+ * = first index of the row maximum (np.argmax, the build's greedy harness over
+ * the logits of transformer.py:97-98) and, if margin != NULL,
+ * margin[r * margin_stride] = largest - second largest value (0 on ties).
+ */
+int mtx_argmax_f32(int rows, int cols, const float* x, int64_t ld, int64_t* idx, int64_t idx_stride,
+                   float* margin, int64_t margin_stride, void* stream);
+
+/*
+ * KV-cache append for a decode step: cache[b, lengths[b] - 1, :] = x[b, :] for
+ * b < B (C floats; rows with lengths[b] - 1 outside [0, T) are skipped), the
+ * position read on the device.  Replaces, for cached decoding, the k/v
+ * projections' recomputation over the whole context that GPT.generate does per
+ * token (transformer.py:93-104 through transformer.py:33-35).
+ */
+int mtx_kv_append_f32(int B, int C, int T, const float* x, int64_t x_stride_b, float* cache,
+                      int64_t cache_stride_b, int64_t cache_stride_t, const int* lengths, void* stream);
+
+/*
+ * End of a decode step: lengths[b] += 1 for b < B and, if pos != NULL,
+ * pos[0] += 1 (the position index of the next token).  With mtx_kv_append_f32
+ * and the lengths argument of mtx_attn_decode it lets a recorded step replay
+ * unchanged for every token.  (No reference counterpart: the reference's loop
+ * grows idx on the host, transformer.py:95-103.)
+ */
+int mtx_decode_advance(int B, int* lengths, int64_t* pos, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* GEMM                                                                     */
 /* ------------------------------------------------------------------------ */

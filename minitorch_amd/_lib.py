@@ -54,6 +54,12 @@ SIGNATURES = {
                                 _P,
                                 _P, _I64P, _P, _I64P, _P, _I64P,
                                 _P, _SZ, _F, _I, _I, _P]),
+    "mtx_attn_decode": (_I, [_I, _I, _I, _I, _I,
+                             _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
+                             _P, _P, _F, _P]),
+    "mtx_argmax_f32": (_I, [_I, _I, _P, _I64, _P, _I64, _P, _I64, _P]),
+    "mtx_kv_append_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _P]),
+    "mtx_decode_advance": (_I, [_I, _P, _P, _P]),
     "mtx_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "mtx_gemm_f32": (_I, [_I, _I, _I, _I,
                           _F, _P, _I64, _I64, _I64,

@@ -1,0 +1,322 @@
+// Decode-time attention (one new query per sequence against its cached keys)
+// and the device-side greedy pick, for gfx950 (MI355X).
+//
+// mtx_attn_decode replaces, for the incremental step of generation, the
+// reference's attention sub-graph (transformer.py:36-44) evaluated at the last
+// position: o = softmax(scale * q k^T) v over the L cached keys.  The
+// reference recomputes the whole forward per token (GPT.generate,
+// transformer.py:93-104); with a KV cache the step's attention is this
+// product, which reads K and V once and is HBM / cache bound.
+//
+// One workgroup per (b, h):
+//   phase 1: thread t owns keys t, t+256, ...; it reads the key row (D
+//            contiguous elements) and forms s = (c q).k in registers, where
+//            c = scale*log2(e); scores go to LDS, the max and the sum of
+//            exp2(s - max) are reduced over the workgroup;
+//   phase 2: thread t owns output element d = t % D for the key group
+//            t / D; each wave reads a value row per key (coalesced) and
+//            accumulates p_j v[j][d]; the key groups are summed through LDS.
+// mtx_argmax_f32 is np.argmax over rows (first maximum) plus the top-2 margin,
+// the greedy harness's pick, so decoding needs no host round trip per token.
+// mtx_kv_append_f32 and mtx_decode_advance keep a decode step's positions in
+// device memory, so one recorded step (a HIP graph) replays for every token.
+#include "mtx_common.h"
+
+#include <cmath>
+
+namespace mtx {
+namespace {
+
+constexpr int kDecThreads = 256;
+constexpr int kDecMaxL = 8192;  // scores held in LDS: 32 KiB
+
+struct DecStr {
+  int64_t b, h, t;  // element strides; the d stride is 1
+};
+
+struct DecArgs {
+  const void* q; DecStr sq;
+  const void* k; DecStr sk;
+  const void* v; DecStr sv;
+  void* o; DecStr so;
+  float* lse;
+  const int* lengths;
+  int B, H, L;
+  float scale;
+};
+
+template <typename T, int E>
+__device__ __forceinline__ void load_row(const T* __restrict__ p, float* out) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int e = 0; e < E; e += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(p + e);
+      out[e] = v[0]; out[e + 1] = v[1]; out[e + 2] = v[2]; out[e + 3] = v[3];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; e += 8) {
+      const uint4 u = *reinterpret_cast<const uint4*>(p + e);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[e + 2 * i] = __uint_as_float(w[i] << 16);
+        out[e + 2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float load1(const T* p) {
+  if constexpr (sizeof(T) == 4) return *p;
+  else return bf2f(*p);
+}
+
+template <typename T>
+__device__ __forceinline__ void store1(T* p, float x) {
+  if constexpr (sizeof(T) == 4) *p = x;
+  else *p = f2bf(x);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecArgs a) {
+  extern __shared__ float smem[];  // [L] scores, then reduction scratch
+  __shared__ float red[kDecThreads / 64];
+  __shared__ float part[kDecThreads];
+
+  const int bh = blockIdx.x;
+  const int b = bh / a.H, h = bh % a.H;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  int L = a.L;
+  if (a.lengths != nullptr) L = min(max(a.lengths[b], 0), a.L);
+  const T* __restrict__ qp = static_cast<const T*>(a.q) + b * a.sq.b + h * a.sq.h;
+  const T* __restrict__ kp = static_cast<const T*>(a.k) + b * a.sk.b + h * a.sk.h;
+  const T* __restrict__ vp = static_cast<const T*>(a.v) + b * a.sv.b + h * a.sv.h;
+  T* __restrict__ op = static_cast<T*>(a.o) + b * a.so.b + h * a.so.h;
+  const float c = a.scale * kLog2e;
+
+  // ---- phase 1: scores (log2 units) ----
+  float q[D];
+  load_row<T, D>(qp, q);
+#pragma unroll
+  for (int d = 0; d < D; ++d) q[d] *= c;
+  float mx = -INFINITY;
+  for (int j = tid; j < L; j += kDecThreads) {
+    const T* __restrict__ kr = kp + (int64_t)j * a.sk.t;
+    float s = 0.f;
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += 16) {
+      float kc[16];
+      load_row<T, 16>(kr + d0, kc);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s = fmaf(q[d0 + e], kc[e], s);
+    }
+    smem[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[wid] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.f;
+  for (int j = tid; j < L; j += kDecThreads) {
+    const float p = __builtin_amdgcn_exp2f(smem[j] - mx);
+    smem[j] = p;
+    sum += p;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[wid] = sum;
+  __syncthreads();  // also publishes every p_j
+  const float l = (red[0] + red[1]) + (red[2] + red[3]);
+
+  // ---- phase 2: o[d] = sum_j p_j v[j][d] / l ----
+  constexpr int NG = kDecThreads / D;  // key groups
+  const int d = tid % D, kg = tid / D;
+  float acc = 0.f;
+  for (int j = kg; j < L; j += NG) acc = fmaf(smem[j], load1<T>(vp + (int64_t)j * a.sv.t + d), acc);
+  part[tid] = acc;
+  __syncthreads();
+  if (tid < D) {
+    float o = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) o += part[g * D + tid];
+    store1<T>(op + tid, L > 0 ? o / l : 0.f);
+    if (tid == 0 && a.lse != nullptr) a.lse[bh] = L > 0 ? (mx + __log2f(l)) * kLn2 : -INFINITY;
+  }
+}
+
+// ---- greedy pick: first maximum per row and top-2 margin ----
+struct Top2 {
+  float m1, m2;
+  int i1;
+};
+
+__device__ __forceinline__ Top2 merge(Top2 x, Top2 y) {
+  Top2 r;
+  r.m1 = fmaxf(x.m1, y.m1);
+  r.i1 = x.m1 > y.m1 ? x.i1 : (y.m1 > x.m1 ? y.i1 : min(x.i1, y.i1));
+  r.m2 = x.m1 >= y.m1 ? fmaxf(x.m2, y.m1) : fmaxf(x.m1, y.m2);
+  return r;
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(int rows, int cols, const float* __restrict__ x,
+                                                     int64_t ld, int64_t* __restrict__ idx, int64_t idx_stride,
+                                                     float* __restrict__ margin, int64_t margin_stride) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;  // wave-uniform
+  const float* __restrict__ xr = x + (int64_t)row * ld;
+  Top2 t{-INFINITY, -INFINITY, cols};
+  for (int c = lane; c < cols; c += 64) {
+    const float v = xr[c];
+    if (v > t.m1) {
+      t.m2 = t.m1;
+      t.m1 = v;
+      t.i1 = c;
+    } else if (v > t.m2) {
+      t.m2 = v;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    Top2 o;
+    o.m1 = __shfl_xor(t.m1, m, 64);
+    o.m2 = __shfl_xor(t.m2, m, 64);
+    o.i1 = __shfl_xor(t.i1, m, 64);
+    t = merge(t, o);
+  }
+  if (lane == 0) {
+    idx[(int64_t)row * idx_stride] = t.i1;
+    if (margin != nullptr) margin[(int64_t)row * margin_stride] = t.m1 - t.m2;
+  }
+}
+
+// cache[b, lengths[b] - 1, :] = x[b, :] (rows outside [0, T) are skipped)
+__global__ __launch_bounds__(256) void kv_append_kernel(int B, int C, int T, const float* __restrict__ x,
+                                                        int64_t sxb, float* __restrict__ cache, int64_t scb,
+                                                        int64_t sct, const int* __restrict__ lengths) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)B * C) return;
+  const int b = (int)(i / C), c = (int)(i % C);
+  const int t = lengths[b] - 1;
+  if (t < 0 || t >= T) return;
+  cache[b * scb + (int64_t)t * sct + c] = x[b * sxb + c];
+}
+
+// lengths[b] += 1 for every b; pos[0] += 1
+__global__ void advance_kernel(int B, int* __restrict__ lengths, int64_t* __restrict__ pos) {
+  const int i = threadIdx.x + blockIdx.x * blockDim.x;
+  if (i < B) lengths[i] += 1;
+  if (i == 0 && pos != nullptr) pos[0] += 1;
+}
+
+int check_row3(const char* name, const void* p, const int64_t* s, int esize) {
+  MTX_CHECK_ARG(p != nullptr, "%s: null pointer", name);
+  MTX_CHECK_ARG(s != nullptr, "%s: null strides", name);
+  MTX_CHECK_ARG(s[3] == 1, "%s: the d stride must be 1 (got %lld)", name, (long long)s[3]);
+  const int vec = 16 / esize;
+  for (int i = 0; i < 3; ++i)
+    MTX_CHECK_ARG(s[i] >= 0 && s[i] % vec == 0,
+                  "%s: stride[%d]=%lld must be a non-negative multiple of %d elements", name, i,
+                  (long long)s[i], vec);
+  MTX_CHECK_ARG(((uintptr_t)p & 15u) == 0, "%s: pointer must be 16-byte aligned", name);
+  return MTX_OK;
+}
+
+template <typename T, int D>
+int launch_decode(const DecArgs& a, hipStream_t st) {
+  const size_t lds = (size_t)(a.L > 0 ? a.L : 1) * sizeof(float);
+  hipLaunchKernelGGL((attn_decode_kernel<T, D>), dim3(a.B * a.H), dim3(kDecThreads), lds, st, a);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+template <typename T>
+int dispatch_decode(int D, const DecArgs& a, hipStream_t st) {
+  switch (D) {
+    case 16: return launch_decode<T, 16>(a, st);
+    case 32: return launch_decode<T, 32>(a, st);
+    case 64: return launch_decode<T, 64>(a, st);
+    default: return launch_decode<T, 128>(a, st);
+  }
+}
+
+}  // namespace
+}  // namespace mtx
+
+using namespace mtx;
+
+extern "C" int mtx_attn_decode(int dtype, int B, int H, int L, int D,
+                               const void* q, const int64_t* q_strides,
+                               const void* k, const int64_t* k_strides,
+                               const void* v, const int64_t* v_strides,
+                               void* o, const int64_t* o_strides,
+                               float* lse, const int* lengths, float scale, void* stream) {
+  if (dtype != MTX_F32 && dtype != MTX_BF16) return fail(MTX_ERR_DTYPE, "unsupported dtype %d", dtype);
+  MTX_CHECK_SHAPE(B >= 1 && H >= 1 && (int64_t)B * H <= (1 << 24), "B,H must be >= 1 (got %d,%d)", B, H);
+  MTX_CHECK_SHAPE(L >= 0 && L <= kDecMaxL, "decode needs 0 <= L <= %d cached keys (got %d)", kDecMaxL, L);
+  MTX_CHECK_SHAPE(D == 16 || D == 32 || D == 64 || D == 128, "head dim D=%d not in {16,32,64,128}", D);
+  const int es = dtype == MTX_F32 ? 4 : 2;
+  int rc;
+  if ((rc = check_row3("q", q, q_strides, es))) return rc;
+  if ((rc = check_row3("k", k, k_strides, es))) return rc;
+  if ((rc = check_row3("v", v, v_strides, es))) return rc;
+  if ((rc = check_row3("o", o, o_strides, es))) return rc;
+  MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
+  DecArgs a{q, {q_strides[0], q_strides[1], q_strides[2]},
+            k, {k_strides[0], k_strides[1], k_strides[2]},
+            v, {v_strides[0], v_strides[1], v_strides[2]},
+            o, {o_strides[0], o_strides[1], o_strides[2]},
+            lse, lengths, B, H, L, scale};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return dtype == MTX_F32 ? dispatch_decode<float>(D, a, st) : dispatch_decode<bf16_t>(D, a, st);
+}
+
+extern "C" int mtx_argmax_f32(int rows, int cols, const float* x, int64_t ld, int64_t* idx,
+                              int64_t idx_stride, float* margin, int64_t margin_stride, void* stream) {
+  MTX_CHECK_SHAPE(rows >= 1 && cols >= 1, "rows, cols must be >= 1 (got %d, %d)", rows, cols);
+  MTX_CHECK_ARG(x != nullptr && idx != nullptr, "x, idx: null pointer");
+  MTX_CHECK_ARG(ld >= cols, "ld=%lld < cols=%d", (long long)ld, cols);
+  hipLaunchKernelGGL(argmax_kernel, dim3((rows + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     rows, cols, x, ld, idx, idx_stride, margin, margin_stride);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_kv_append_f32(int B, int C, int T, const float* x, int64_t x_stride_b, float* cache,
+                                 int64_t cache_stride_b, int64_t cache_stride_t, const int* lengths,
+                                 void* stream) {
+  MTX_CHECK_SHAPE(B >= 1 && C >= 1 && T >= 1, "B, C, T must be >= 1 (got %d, %d, %d)", B, C, T);
+  MTX_CHECK_ARG(x != nullptr && cache != nullptr && lengths != nullptr, "x, cache, lengths: null pointer");
+  MTX_CHECK_ARG(x_stride_b >= C && cache_stride_t >= C && cache_stride_b >= (int64_t)T * cache_stride_t,
+                "strides must not overlap rows (x %lld, cache b %lld, t %lld for C=%d, T=%d)",
+                (long long)x_stride_b, (long long)cache_stride_b, (long long)cache_stride_t, C, T);
+  const int64_t n = (int64_t)B * C;
+  hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), B, C, T, x, x_stride_b, cache, cache_stride_b,
+                     cache_stride_t, lengths);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_decode_advance(int B, int* lengths, int64_t* pos, void* stream) {
+  MTX_CHECK_SHAPE(B >= 1, "B must be >= 1 (got %d)", B);
+  MTX_CHECK_ARG(lengths != nullptr, "lengths: null pointer");
+  hipLaunchKernelGGL(advance_kernel, dim3((B + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), B,
+                     lengths, pos);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}

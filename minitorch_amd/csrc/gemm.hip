@@ -289,6 +289,17 @@ Plan plan_gemm(int M, int N, int K, int batch, size_t ws_bytes) {
       p.kchunk = cdiv(cdiv(K, want), BK) * BK;
       p.ksplit = cdiv(K, p.kchunk);
     }
+  } else if (t < 64 && K >= 128) {
+    // skinny products (decode steps: M = sequences): too few output tiles to
+    // cover the CUs, so split K into chunks of >= 64
+    int want = (int)std::min<int64_t>(16, (256 + t - 1) / t);
+    want = std::min(want, K / 64);
+    const size_t need = (size_t)want * batch * (size_t)M * N * sizeof(float);
+    if (want > 1 && need <= ws_bytes) {
+      p.ksplit = want;
+      p.kchunk = cdiv(cdiv(K, want), BK) * BK;
+      p.ksplit = cdiv(K, p.kchunk);
+    }
   }
   return p;
 }

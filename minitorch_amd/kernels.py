@@ -52,6 +52,80 @@ def attn_fwd(q, k, v, scale: float, causal: bool = True, out=None, lse=None):
     return out, lse
 
 
+def attn_decode(q, k, v, scale: float, out=None, lse=None, lengths=None):
+    """Decode-step attention: q (B,H,1,D) against k/v (B,H,L,D) (any strides
+    with a contiguous last dim, e.g. head views of (B,T,C) caches).  lengths:
+    optional int32 device tensor (B,): sequence b uses its first lengths[b]
+    keys.  Returns (out (B,H,1,D) like q, lse fp32 (B,H) or None)."""
+    _need_cuda(q, k, v)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _bhtd(name, t)
+    B, H, Tq, D = q.shape
+    Lk = k.shape[2]
+    if Tq != 1 or k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
+        raise ValueError(f"shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    if out is None:
+        out = torch.empty((B, H, 1, D), dtype=q.dtype, device=q.device)
+    _bhtd("out", out)
+    if lse is not None and (not lse.is_contiguous() or lse.shape != (B, H) or lse.dtype != torch.float32):
+        raise ValueError("lse must be a contiguous fp32 (B,H) tensor")
+    if lengths is not None and (lengths.dtype != torch.int32 or lengths.shape != (B,)
+                                or not lengths.is_contiguous() or not lengths.is_cuda):
+        raise ValueError("lengths must be a contiguous int32 device tensor of shape (B,)")
+    L.call("mtx_attn_decode", L.dtype_code(q), B, H, Lk, D,
+           L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
+           L.ptr(out), L.strides(out), L.ptr(lse) if lse is not None else None,
+           L.ptr(lengths) if lengths is not None else None, float(scale),
+           L.stream_handle(q.device))
+    return out, lse
+
+
+def argmax_rows(x, idx=None, margin=None):
+    """First-maximum index of each row of a fp32 (rows, cols) device tensor
+    (np.argmax) and, if `margin` is given, largest - second largest.  idx:
+    int64 (rows,) or a strided column view; returns (idx, margin)."""
+    _need_cuda(x)
+    if x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be a fp32 (rows, cols) tensor with contiguous rows")
+    rows, cols = x.shape
+    if idx is None:
+        idx = torch.empty((rows,), dtype=torch.int64, device=x.device)
+    if idx.dtype != torch.int64 or idx.numel() != rows:
+        raise ValueError("idx must be int64 with one entry per row")
+    if margin is not None and (margin.dtype != torch.float32 or margin.numel() != rows):
+        raise ValueError("margin must be fp32 with one entry per row")
+    L.call("mtx_argmax_f32", rows, cols, L.ptr(x), x.stride(0), L.ptr(idx), idx.stride(0) if idx.dim() else 1,
+           L.ptr(margin) if margin is not None else None, margin.stride(0) if margin is not None else 0,
+           L.stream_handle(x.device))
+    return idx, margin
+
+
+def kv_append(x, cache, lengths):
+    """cache[b, lengths[b] - 1, :] = x[b, 0, :]: x (B, 1, C) fp32, cache
+    (B, T, C) fp32 with contiguous rows, lengths int32 device (B,)."""
+    _need_cuda(x, cache, lengths)
+    B, T, C = cache.shape
+    if x.dtype != torch.float32 or cache.dtype != torch.float32 or x.shape != (B, 1, C):
+        raise ValueError(f"kv_append: x{tuple(x.shape)} / cache{tuple(cache.shape)} mismatch (fp32 needed)")
+    if x.stride(2) != 1 or cache.stride(2) != 1 or lengths.dtype != torch.int32 or lengths.shape != (B,):
+        raise ValueError("kv_append: contiguous rows and int32 lengths (B,) needed")
+    L.call("mtx_kv_append_f32", B, C, T, L.ptr(x), x.stride(0), L.ptr(cache), cache.stride(0), cache.stride(1),
+           L.ptr(lengths), L.stream_handle(x.device))
+
+
+def decode_advance(lengths, pos=None):
+    """lengths += 1 (int32 device (B,)) and pos += 1 (int64 device (1,))."""
+    _need_cuda(lengths)
+    if lengths.dtype != torch.int32 or lengths.dim() != 1 or not lengths.is_contiguous():
+        raise ValueError("lengths must be a contiguous int32 device vector")
+    if pos is not None and (pos.dtype != torch.int64 or not pos.is_cuda):
+        raise ValueError("pos must be an int64 device tensor")
+    L.call("mtx_decode_advance", lengths.numel(), L.ptr(lengths), L.ptr(pos) if pos is not None else None,
+           L.stream_handle(lengths.device))
+
+
 def attn_bwd(q, k, v, out, dout, lse, scale: float, causal: bool = True,
              dq=None, dk=None, dv=None, accumulate: bool = False, workspace=None,
              phases: int = L.ATTN_BWD_ALL):

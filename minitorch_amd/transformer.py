@@ -10,6 +10,7 @@ from __future__ import annotations
 import math
 
 import numpy as np
+import torch
 
 from . import device as dev
 from . import functional as F
@@ -30,6 +31,7 @@ class MultiHeadAttention(Module):
         self.v_proj = Linear(n_embd, n_embd)
         self.out_proj = Linear(n_embd, n_embd)
         self.attn_drop = Dropout(dropout)
+        self._qkv = None  # fused q/k/v projection for decode steps (fuse_qkv)
 
     def _split_heads(self, x, B, T):
         # (B, T, C) -> (B, n_head, T, head_dim), a strided view
@@ -69,8 +71,44 @@ class MultiHeadAttention(Module):
         kh = heads(kc.t[:, :Tk, :])
         vh = heads(vc.t[:, :Tk, :])
         out = dev.empty((B, T, H, D))
-        K.attn_fwd(qh, kh, vh, 1.0 / math.sqrt(D), True, out=out.t.transpose(1, 2))
+        if T == 1:  # one new token: the decode kernel (reads the cache once)
+            K.attn_decode(qh, kh, vh, 1.0 / math.sqrt(D), out=out.t.transpose(1, 2))
+        else:
+            K.attn_fwd(qh, kh, vh, 1.0 / math.sqrt(D), True, out=out.t.transpose(1, 2))
         return self.out_proj(Tensor(out.reshape(B, T, C)))
+
+
+    def forward_step(self, x, cache, lengths):
+        """One-token decode step whose positions live in device memory, so a
+        recorded step replays unchanged: x (B, 1, C); this token's key/value
+        go to cache row lengths[b] - 1 (mtx_kv_append_f32) and attention runs
+        over each sequence's first lengths[b] cached keys (mtx_attn_decode)."""
+        from . import kernels as K
+
+        B, T, C = x.shape
+        assert T == 1, "forward_step takes one token per sequence"
+        H, D = self.n_head, self.head_dim
+        if self._qkv is None:
+            self.fuse_qkv()
+        qkv = F.linear(x, *self._qkv).data.t  # (B, 1, 3C): [q | k | v]
+        q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
+        kc, vc = cache
+        K.kv_append(k, kc.t, lengths)
+        K.kv_append(v, vc.t, lengths)
+        heads = lambda t: t.view(t.shape[0], t.shape[1], H, D).transpose(1, 2) if t.is_contiguous() \
+            else t.unflatten(2, (H, D)).transpose(1, 2)
+        out = dev.empty((B, 1, H, D))
+        K.attn_decode(heads(q), heads(kc.t), heads(vc.t), 1.0 / math.sqrt(D),
+                      out=out.t.transpose(1, 2), lengths=lengths)
+        return self.out_proj(Tensor(out.reshape(B, 1, C)))
+
+    def fuse_qkv(self):
+        """Concatenate the q/k/v projections into one (C, 3C) weight and (3C,)
+        bias for decode steps (one GEMM instead of three).  A snapshot: call
+        again after the weights change (generate_greedy does, per call)."""
+        W = torch.cat([p.weight.data.t for p in (self.q_proj, self.k_proj, self.v_proj)], dim=1)
+        b = torch.cat([p.bias.data.t for p in (self.q_proj, self.k_proj, self.v_proj)], dim=0)
+        self._qkv = (Tensor(DeviceArray(W.contiguous())), Tensor(DeviceArray(b.contiguous())))
 
 
 class TransformerBlock(Module):
@@ -95,6 +133,11 @@ class TransformerBlock(Module):
 
     def forward_cached(self, x, cache, t0):
         x = x + self.attn.forward_cached(self.ln1(x), cache, t0)
+        x = x + self.mlp(self.ln2(x))
+        return x
+
+    def forward_step(self, x, cache, lengths):
+        x = x + self.attn.forward_step(self.ln1(x), cache, lengths)
         x = x + self.mlp(self.ln2(x))
         return x
 
@@ -146,42 +189,83 @@ class GPT(Module):
         x = self.ln_f(x)
         return self.lm_head(x)
 
-    def generate_greedy(self, idx, max_new_tokens, return_margins=False):
+    def generate_greedy(self, idx, max_new_tokens, return_margins=False, graph=True):
         """Greedy decoding: argmax (first maximum, as np.argmax) of the last
         position's logits -- the C4 harness over transformer.py:93-104 -- with
         a KV cache: one prefill over the prompt, then one-token steps whose
-        attention runs on the device against the cached keys and values
-        (1 query vs the growing prefix).  Needs T0 + max_new_tokens <=
+        attention is the decode kernel against the cached keys and values.
+        The loop stays on the device: each step's pick (mtx_argmax_f32) lands
+        in the id buffer the next step's embedding reads, and the step's
+        positions (cache row, key count, position id) are device counters
+        advanced by mtx_decode_advance.  A step therefore replays unchanged:
+        with graph=True the first one-token step runs eagerly, the second is
+        recorded as a HIP graph and replayed for the rest.  The host
+        synchronises once, at the end.  Needs T0 + max_new_tokens <=
         block_size (beyond it the reference crops the context and recomputes
         positions, which a cache cannot reuse; use generate() then).
         Returns ids (B, T0 + n) and, if asked, the top-2 logit margins (B, n)."""
+        from . import kernels as K
+
         idx = np.asarray(idx)
         B, T0 = idx.shape
-        Tmax = T0 + max_new_tokens
+        n = int(max_new_tokens)
+        Tmax = T0 + n
         if Tmax > self.block_size:
             raise ValueError(f"prompt + new tokens = {Tmax} exceeds block_size {self.block_size}")
+        if n < 1:
+            return (idx.copy(), np.empty((B, 0))) if return_margins else idx.copy()
         C = self.tok_emb.weight.shape[1]
         caches = [(dev.empty((B, Tmax, C)), dev.empty((B, Tmax, C))) for _ in self.blocks]
-        out = np.empty((B, Tmax), dtype=np.int64)
-        out[:, :T0] = idx
-        margins = np.empty((B, max_new_tokens), dtype=np.float64)
+        ids = dev.empty((Tmax, B), dtype=torch.int64)  # time-major: a step's ids are contiguous
+        margins = dev.empty((n, B))
+        pos = self._positions(Tmax)
+
         with no_grad():
-            t0, cur = 0, idx
-            for step in range(max_new_tokens):
-                T = cur.shape[1]
-                x = self.tok_emb(cur) + self.pos_emb(np.arange(t0, t0 + T))
-                for block, cache in zip(self.blocks, caches):
-                    x = block.forward_cached(x, cache, t0)
-                x = self.ln_f(x)
-                last = Tensor(x.data.t[:, T - 1:T, :])
-                logits = self.lm_head(last).data.numpy()[:, 0, :]
-                nxt = np.argmax(logits, axis=-1)
-                top2 = np.sort(logits, axis=-1)[:, -2:]
-                margins[:, step] = top2[:, 1] - top2[:, 0]
-                out[:, T0 + step] = nxt
-                t0 += T
-                cur = nxt[:, None]
-        return (out, margins) if return_margins else out
+            # prefill over the prompt
+            prompt = dev.index_array(idx)
+            x = self.tok_emb(prompt) + self.pos_emb(DeviceArray(pos.t[:T0]))
+            for block, cache in zip(self.blocks, caches):
+                x = block.forward_cached(x, cache, 0)
+            x = self.ln_f(Tensor(x.data.t[:, T0 - 1:T0, :]))
+            K.argmax_rows(self.lm_head(x).data.t.view(B, -1), idx=ids.t[T0], margin=margins.t[0])
+            if n > 1:
+                for block in self.blocks:
+                    block.attn.fuse_qkv()
+                cur = ids.t[T0].clone()              # ids fed to the next step, then overwritten
+                mcur = torch.empty((B,), dtype=torch.float32, device=cur.device)
+                lengths = torch.full((B,), T0 + 1, dtype=torch.int32, device=cur.device)
+                posd = torch.full((1,), T0, dtype=torch.int64, device=cur.device)
+
+                def step():
+                    x = self.tok_emb(DeviceArray(cur.view(B, 1))) + self.pos_emb(DeviceArray(posd))
+                    for block, cache in zip(self.blocks, caches):
+                        x = block.forward_step(x, cache, lengths)
+                    logits = self.lm_head(self.ln_f(x)).data.t.view(B, -1)
+                    K.argmax_rows(logits, idx=cur, margin=mcur)
+                    K.decode_advance(lengths, posd)
+
+                def record(s):
+                    ids.t[T0 + s].copy_(cur)
+                    margins.t[s].copy_(mcur)
+
+                step()
+                record(1)
+                if graph and n > 2:
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g):
+                        step()
+                    for s in range(2, n):
+                        g.replay()
+                        record(s)
+                else:
+                    for s in range(2, n):
+                        step()
+                        record(s)
+        out = ids.t.t().cpu().numpy()
+        out[:, :T0] = idx
+        if return_margins:
+            return out, margins.t.t().cpu().numpy().astype(np.float64)
+        return out
 
     def generate(self, idx, max_new_tokens, temperature=1.0):
         """Sample tokens as the reference does (transformer.py:93-104): full

@@ -99,3 +99,40 @@ def test_python_wrapper_raises_value_error():
     with pytest.raises(ValueError, match="phase"):
         L.call("mtx_attn_bwd_phase", 0, L.MTX_F32, 1, 1, 8, 8, 64, p, s, p, s, p, s, p, s, p, s, p,
                p, s, p, s, p, s, p, 1 << 20, 0.125, 1, 0, None)
+
+
+def _dec(**over):
+    args = dict(dtype=L.MTX_F32, B=2, H=3, Lk=40, D=64, q=16, qs=(192, 64, 0, 1), k=16,
+                ks=(7680, 64, 192, 1), v=16, vs=(7680, 64, 192, 1), o=16, os=(192, 64, 0, 1))
+    args.update(over)
+    a = args
+    p = lambda x: C.c_void_p(x) if x else None
+    return L.lib().mtx_attn_decode(a["dtype"], a["B"], a["H"], a["Lk"], a["D"],
+                                   p(a["q"]), _strides(*a["qs"]), p(a["k"]), _strides(*a["ks"]),
+                                   p(a["v"]), _strides(*a["vs"]), p(a["o"]), _strides(*a["os"]),
+                                   None, None, 0.125, None)
+
+
+@pytest.mark.parametrize("over,code,frag", [
+    (dict(dtype=5), L.MTX_ERR_DTYPE, "dtype"),
+    (dict(Lk=8193), L.MTX_ERR_SHAPE, "8192"),
+    (dict(Lk=-1), L.MTX_ERR_SHAPE, "cached keys"),
+    (dict(D=24), L.MTX_ERR_SHAPE, "head dim"),
+    (dict(B=0), L.MTX_ERR_SHAPE, "B,H"),
+    (dict(k=0), L.MTX_ERR_ARG, "null"),
+    (dict(vs=(7680, 64, 192, 2)), L.MTX_ERR_ARG, "d stride"),
+    (dict(ks=(7680, 64, 190, 1)), L.MTX_ERR_ARG, "multiple"),
+    (dict(o=8), L.MTX_ERR_ARG, "aligned"),
+])
+def test_attn_decode_rejects_bad_arguments(over, code, frag):
+    rc = _dec(**over)
+    assert rc == code
+    assert frag in L.lib().mtx_last_error().decode()
+
+
+def test_argmax_rejects_bad_arguments():
+    p = C.c_void_p(16)
+    assert L.lib().mtx_argmax_f32(4, 65, p, 64, p, 1, None, 0, None) == L.MTX_ERR_ARG
+    assert "ld" in L.lib().mtx_last_error().decode()
+    assert L.lib().mtx_argmax_f32(0, 65, p, 65, p, 1, None, 0, None) == L.MTX_ERR_SHAPE
+    assert L.lib().mtx_argmax_f32(4, 65, None, 65, p, 1, None, 0, None) == L.MTX_ERR_ARG

@@ -1,0 +1,136 @@
+"""GPU parity of the decode-step attention (mtx_attn_decode) and the device
+greedy pick (mtx_argmax_f32).
+
+Decode attention is the reference's attention sub-graph (transformer.py:36-44)
+at one query position against L cached keys; the oracle is
+oracle.attention.flash_forward (float64 softmax(scale q k^T) v and its
+log-sum-exp) on the same keys.  Bars as for the fused kernels: fp32
+|gpu - ref| <= 1e-5 + 1e-4 |ref|; bf16 inputs max err <= 2e-2 max|ref| and
+relative Frobenius error <= 2e-2.  The greedy pick must equal np.argmax (first
+maximum) exactly, and the margin the top-2 difference of np.sort.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle.attention import bf16_round, flash_forward
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _cache(rng, B, H, Lmax, D, dtype):
+    """q (B,H,1,D) and (B,Lmax,H*D) key/value caches with their head views."""
+    import torch
+
+    q = rng.standard_normal((B, H, 1, D), dtype=np.float32)
+    kc = rng.standard_normal((B, Lmax, H * D), dtype=np.float32)
+    vc = rng.standard_normal((B, Lmax, H * D), dtype=np.float32)
+    if dtype == torch.bfloat16:
+        q, kc, vc = (bf16_round(0.5 * x) for x in (q, kc, vc))
+    heads = lambda t: t.view(B, Lmax, H, D).transpose(1, 2)
+    tq, tk, tv = (torch.from_numpy(x).cuda().to(dtype) for x in (q, kc, vc))
+    host = lambda x: x.reshape(B, Lmax, H, D).transpose(0, 2, 1, 3)
+    return (tq, heads(tk), heads(tv)), (q, host(kc), host(vc))
+
+
+def _check(got, ref, dtype, name):
+    import torch
+
+    got = got.astype(np.float64)
+    if dtype == torch.float32:
+        err = np.abs(got - ref)
+        assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), (name, float(err.max()))
+    else:
+        amax = np.abs(ref).max()
+        assert np.abs(got - ref).max() <= 2e-2 * amax, (name, float(np.abs(got - ref).max()), amax)
+        assert np.linalg.norm(got - ref) <= 2e-2 * np.linalg.norm(ref), name
+
+
+@pytest.mark.parametrize("dtype_name", ["float32", "bfloat16"])
+@pytest.mark.parametrize("D", [16, 64, 128])
+def test_decode_matches_oracle_ragged(dev, dtype_name, D):
+    import torch
+    from minitorch_amd import kernels as K
+
+    dtype = getattr(torch, dtype_name)
+    B, H, Lmax = 4, 3, 300
+    lengths = [1, 137, 256, 300]
+    _say(f"[decode] {dtype_name} D={D} B={B} H={H} lengths={lengths}")
+    rng = np.random.default_rng(40 + D)
+    (tq, tk, tv), (q, k, v) = _cache(rng, B, H, Lmax, D, dtype)
+    lens = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    lse = torch.empty((B, H), dtype=torch.float32, device="cuda")
+    o, _ = K.attn_decode(tq, tk, tv, D ** -0.5, lse=lse, lengths=lens)
+    torch.cuda.synchronize()
+    o = o.float().cpu().numpy()
+    lse = lse.cpu().numpy()
+    for b, Lb in enumerate(lengths):
+        ro, rl = flash_forward(q[b:b + 1], k[b:b + 1, :, :Lb], v[b:b + 1, :, :Lb], D ** -0.5, causal=False)
+        _check(o[b:b + 1], ro, dtype, f"o b={b}")
+        np.testing.assert_allclose(lse[b], rl[0, :, 0], rtol=1e-4 if dtype == torch.float32 else 2e-2,
+                                   atol=1e-5 if dtype == torch.float32 else 2e-2)
+
+
+def test_decode_full_cache_and_empty(dev):
+    """No lengths: every sequence uses all L keys (L = 8192, the maximum);
+    length 0 gives o = 0 and lse = -inf."""
+    import torch
+    from minitorch_amd import kernels as K
+
+    _say("[decode] L=8192 fp32, and a zero length")
+    rng = np.random.default_rng(7)
+    (tq, tk, tv), (q, k, v) = _cache(rng, 1, 2, 8192, 64, torch.float32)
+    lse = torch.empty((1, 2), dtype=torch.float32, device="cuda")
+    o, _ = K.attn_decode(tq, tk, tv, 0.125, lse=lse)
+    ro, rl = flash_forward(q, k, v, 0.125, causal=False)
+    torch.cuda.synchronize()
+    _check(o.cpu().numpy(), ro, torch.float32, "o")
+    np.testing.assert_allclose(lse.cpu().numpy(), rl[..., 0], rtol=1e-5, atol=1e-5)
+    zero = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    o, _ = K.attn_decode(tq, tk, tv, 0.125, lse=lse, lengths=zero)
+    torch.cuda.synchronize()
+    assert np.all(o.cpu().numpy() == 0) and np.all(np.isneginf(lse.cpu().numpy()))
+
+
+def test_decode_matches_fused_forward_at_last_position(dev):
+    """A decode step equals the fused causal forward's last query row."""
+    import torch
+    from minitorch_amd import kernels as K
+
+    _say("[decode] vs fused forward, last row")
+    rng = np.random.default_rng(11)
+    B, H, T, D = 2, 6, 97, 64
+    q, k, v = (torch.from_numpy(rng.standard_normal((B, H, T, D), dtype=np.float32)).cuda() for _ in range(3))
+    o_full, lse_full = K.attn_fwd(q, k, v, 0.125, True)
+    lse = torch.empty((B, H), dtype=torch.float32, device="cuda")
+    o, _ = K.attn_decode(q[:, :, T - 1:T], k, v, 0.125, lse=lse)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(o.cpu().numpy(), o_full[:, :, T - 1:T].cpu().numpy(), rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(lse.cpu().numpy(), lse_full[:, :, T - 1].cpu().numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_argmax_matches_numpy(dev):
+    import torch
+    from minitorch_amd import kernels as K
+
+    _say("[argmax] rows of 65 and 200 columns, with ties")
+    rng = np.random.default_rng(5)
+    for cols in (65, 200):
+        x = rng.standard_normal((70, cols)).astype(np.float32)
+        x[0, 3] = x[0, 40] = 9.0          # tie: first index wins, margin 0
+        x[1, -1] = 50.0                   # maximum in the last column
+        x[2, :] = 1.0                     # all equal
+        x[3, 64 % cols] = x[3, 0] = 7.0   # tie across lanes
+        t = torch.from_numpy(x).cuda()
+        margin = torch.empty((70,), dtype=torch.float32, device="cuda")
+        idx, _ = K.argmax_rows(t, margin=margin)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(idx.cpu().numpy(), np.argmax(x, axis=1))
+        top2 = np.sort(x, axis=1)[:, -2:]
+        np.testing.assert_array_equal(margin.cpu().numpy(), top2[:, 1] - top2[:, 0])

@@ -193,6 +193,24 @@ def test_kv_cache_greedy_matches_recompute_and_oracle(dev):
     np.testing.assert_array_equal(toks, idx)
 
 
+def test_greedy_graph_replay_matches_eager(dev):
+    """The decode step recorded as a HIP graph and replayed (38 replays, with
+    the loop's own eager copies between them) gives bit-identical tokens and
+    margins to running every step eagerly."""
+    from oracle.gpt import GPTConfig, init_params
+
+    _say("[gpt] greedy: graph replay vs eager steps")
+    cfg = GPTConfig(vocab=65, block=64, n_embd=96, n_head=6, n_layer=3)
+    P = init_params(cfg, np.random.default_rng(33))
+    prompts = np.random.default_rng(34).integers(0, cfg.vocab, (5, 24))
+    model = gpu_gpt(cfg, P)
+    model.eval()
+    t_eager, m_eager = model.generate_greedy(prompts, 40, return_margins=True, graph=False)
+    t_graph, m_graph = model.generate_greedy(prompts, 40, return_margins=True, graph=True)
+    np.testing.assert_array_equal(t_graph, t_eager)
+    np.testing.assert_array_equal(m_graph, m_eager)
+
+
 def test_c4_greedy_full_config(dev):
     """Config C4 at full size: 64 prompts x 32 tokens, +224 greedy tokens with
     the C2 model, tokens identical to the oracle's (fixture
