@@ -144,6 +144,54 @@ def gpt_flops_per_step(c):
     return 6 * n_mm * B * T + 3 * L * (2 * B * T * T * C)
 
 
+def bench_c4(n_new=224):
+    """Config C4: greedy decoding with the C2 model (weights N(0, 0.02) from
+    default_rng(2), biases 0, eval mode) of 64 prompts of 32 ids drawn from
+    default_rng(4), + n_new tokens each: prefill, then one-token steps with the
+    KV cache (GPT.generate_greedy: decode kernel, device-side pick, one step
+    recorded as a HIP graph and replayed).  The timed region is the whole
+    generate call, ids on the host at the end.  Also times the decode
+    attention kernel alone at the longest step (L = 256, fp32 cache) with HIP
+    events and reports its read bandwidth (K and V once)."""
+    import torch
+
+    import minitorch_amd as mt
+    from minitorch_amd import kernels as K
+
+    c = C2_CFG
+    model = mt.GPT(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"], dropout=0.0)
+    model.init_weights(np.random.default_rng(2))
+    model.eval()
+    prompts = np.random.default_rng(4).integers(0, c["vocab"], (64, 32))
+    model.generate_greedy(prompts, 8)  # warm-up (library load, allocator)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(2):
+        t0 = time.perf_counter()
+        toks = model.generate_greedy(prompts, n_new)
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    assert toks.shape == (64, 32 + n_new)
+    # decode kernel alone, L = 256
+    B, H, L, D = 64, c["n_head"], 256, c["n_embd"] // c["n_head"]
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q = torch.randn((B, H, 1, D), device="cuda", generator=g)
+    kc = torch.randn((B, L, H * D), device="cuda", generator=g)
+    vc = torch.randn((B, L, H * D), device="cuda", generator=g)
+    heads = lambda t: t.view(B, L, H, D).transpose(1, 2)
+    out = torch.empty_like(q)
+    ms = time_loop(lambda: K.attn_decode(q, heads(kc), heads(vc), D ** -0.5, out=out), 200, 10)
+    nbytes = 2 * B * H * L * D * 4
+    return {"tokens_per_s": round(64 * n_new / best, 1), "ms_total": round(best * 1e3, 2),
+            "ms_per_token_step": round(best * 1e3 / n_new, 4),
+            "decode_kernel": {"L": L, "us_per_launch": round(ms * 1e3, 3),
+                              "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                              "frac_of_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4),
+                              "bytes_per_launch": nbytes,
+                              "note": "K+V (50 MB) fit the 256 MB MALL, so repeated launches read it from there"},
+            "config": "C2 model (6x384, 6 heads), 64 prompts x 32 ids, +224 greedy tokens, fp32, KV cache"}
+
+
 def bench_gpt(c, seed, steps, warmup):
     """Training steps (forward, cross-entropy, zero_grad, backward, Adam
     lr 3e-4) on seeded synthetic token batches already resident on the GPU.
@@ -211,6 +259,26 @@ def cpu_baseline_gpt(c, budget_s, B_sample):
     return n * B_sample * cfg.block / dt, n, dt
 
 
+def cpu_baseline_c4(budget_s):
+    """The reference's generation loop restated in NumPy (oracle/gpt.py
+    greedy_generate: full forward over the context per token, as
+    transformer.py:93-104 does) for the C4 model and prompts, one new token at
+    a time for all 64 prompts until budget_s.  Returns tokens/s."""
+    from oracle.gpt import GPTConfig, greedy_generate, init_params
+
+    c = C2_CFG
+    cfg = GPTConfig(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"])
+    P = init_params(cfg, np.random.default_rng(2))
+    idx = np.random.default_rng(4).integers(0, c["vocab"], (64, 32))
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n < 224:
+        idx, _ = greedy_generate(P, cfg, idx, 1)
+        n += 1
+    dt = time.perf_counter() - t0
+    return 64 * n / dt, n, dt
+
+
 def pmc_traffic(kernel):
     """HBM bytes per launch of `kernel` at C3 from the committed rocprofv3 PMC
     summary (profiles/pmc_traffic.json), or None."""
@@ -240,7 +308,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=("all", "c3", "c1", "gpt2", "gpt0"), default="all",
+    ap.add_argument("--only", choices=("all", "c3", "c1", "c4", "gpt2", "gpt0"), default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run 5 device copies of MIB MiB (a kernel of known HBM "
@@ -272,6 +340,9 @@ def main():
         ms, losses = bench_gpt(c, 2, args.steps, args.warmup)
         print(f"[bench] {args.only}: {ms:.3f} ms/step, {c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, "
               f"losses {losses}", file=sys.stderr)
+        return
+    if args.only == "c4":
+        print(f"[bench] C4 {bench_c4()}", file=sys.stderr)
         return
     if args.only == "c1":
         r1, _ = bench_attention(32, 8, 256, 64, torch.float32, 1, 1.0, args.steps, args.warmup)
@@ -316,6 +387,10 @@ def main():
     ms_c0, _ = bench_gpt(C0_CFG, 0, args.steps, 3)
     tok_c0 = C0_CFG["B"] * C0_CFG["block"] / (ms_c0 * 1e-3)
 
+    print("[bench] C4 greedy decoding (64 x (32 + 224) tokens)", file=sys.stderr, flush=True)
+    c4 = bench_c4()
+    print(f"[bench] C4 {c4['tokens_per_s']:.0f} tokens/s", file=sys.stderr, flush=True)
+
     cpu = None
     cpu_gpt = None
     if not args.no_cpu:
@@ -330,6 +405,11 @@ def main():
         print("[bench] CPU baseline, GPT C2 step on 1 sequence (NumPy restatement)", file=sys.stderr, flush=True)
         tps2, n2, dt2 = cpu_baseline_gpt(C2_CFG, args.cpu_budget / 2, 1)
         tps0, n0, dt0 = cpu_baseline_gpt(C0_CFG, 3.0, C0_CFG["B"])
+        tps4, n4, dt4 = cpu_baseline_c4(args.cpu_budget / 3)
+        c4["cpu_baseline"] = {"value": round(tps4, 2), "unit": "tokens/s", "cores": blas_threads(), "kind": "port",
+                              "sample": f"first {n4} of the 224 greedy steps for all 64 prompts ({dt4:.1f}s), "
+                                        f"full-recompute NumPy restatement of GPT.generate (oracle/gpt.py); "
+                                        f"later steps have longer contexts, so this overstates the full run"}
         cpu_gpt = {"C2_tokens_per_s": round(tps2, 2), "C0_tokens_per_s": round(tps0, 1),
                    "cores": blas_threads(), "kind": "port",
                    "sample": f"C2 model, {n2} training steps on 1 sequence of 256 tokens ({dt2:.1f}s); "
@@ -372,6 +452,7 @@ def main():
                        "config": "vocab 65, n_embd 64, 4 heads, 2 layers, T=32, B=16, fp32"},
                 "cpu_baseline": cpu_gpt,
             },
+            "C4_greedy_decode": c4,
         },
     }
     print(json.dumps(line), flush=True)

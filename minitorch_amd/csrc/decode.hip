@@ -13,9 +13,10 @@
 //            contiguous elements) and forms s = (c q).k in registers, where
 //            c = scale*log2(e); scores go to LDS, the max and the sum of
 //            exp2(s - max) are reduced over the workgroup;
-//   phase 2: thread t owns output element d = t % D for the key group
-//            t / D; each wave reads a value row per key (coalesced) and
-//            accumulates p_j v[j][d]; the key groups are summed through LDS.
+//   phase 2: thread t owns output elements 4*(t % (D/4)) .. +3 for the key
+//            group t / (D/4); a value row per key is read by D/4 adjacent
+//            threads (coalesced), several keys in flight per thread, and the
+//            key groups are summed through LDS.
 // mtx_argmax_f32 is np.argmax over rows (first maximum) plus the top-2 margin,
 // the greedy harness's pick, so decoding needs no host round trip per token.
 // mtx_kv_append_f32 and mtx_decode_advance keep a decode step's positions in
@@ -68,9 +69,14 @@ __device__ __forceinline__ void load_row(const T* __restrict__ p, float* out) {
 }
 
 template <typename T>
-__device__ __forceinline__ float load1(const T* p) {
-  if constexpr (sizeof(T) == 4) return *p;
-  else return bf2f(*p);
+__device__ __forceinline__ f32x4 load4(const T* p) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const f32x4*>(p);
+  } else {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                 __uint_as_float(u.y & 0xffff0000u)};
+  }
 }
 
 template <typename T>
@@ -94,7 +100,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecArgs a) {
   extern __shared__ float smem[];  // [L] scores, then reduction scratch
   __shared__ float red[kDecThreads / 64];
-  __shared__ float part[kDecThreads];
+  __shared__ __attribute__((aligned(16))) float part[kDecThreads * 4];
 
   const int bh = blockIdx.x;
   const int b = bh / a.H, h = bh % a.H;
@@ -143,11 +149,13 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecArgs 
   const float l = (red[0] + red[1]) + (red[2] + red[3]);
 
   // ---- phase 2: o[d] = sum_j p_j v[j][d] / l ----
-  constexpr int NG = kDecThreads / D;  // key groups
-  const int d = tid % D, kg = tid / D;
-  float acc = 0.f;
-  for (int j = kg; j < L; j += NG) acc = fmaf(smem[j], load1<T>(vp + (int64_t)j * a.sv.t + d), acc);
-  part[tid] = acc;
+  constexpr int DV = D / 4;             // 4-element slices per row
+  constexpr int NG = kDecThreads / DV;  // key groups
+  const int dv = tid % DV, kg = tid / DV;
+  f32x4 acc = zero4();
+#pragma unroll 4
+  for (int j = kg; j < L; j += NG) acc += smem[j] * load4<T>(vp + (int64_t)j * a.sv.t + 4 * dv);
+  *reinterpret_cast<f32x4*>(part + kg * D + 4 * dv) = acc;
   __syncthreads();
   if (tid < D) {
     float o = 0.f;

@@ -20,6 +20,14 @@ from .module import Module, Sequential
 from .tensor import Tensor, no_grad
 
 
+def _linear_into(x, lin, out):
+    """out += x @ W + b, in place (inference only: no graph node)."""
+    from .linalg import bmm
+
+    bmm(x.data.t, lin.weight.data.t, out.data.t, beta=1.0, bias=lin.bias.data.t)
+    return out
+
+
 class MultiHeadAttention(Module):
     def __init__(self, n_embd, n_head, dropout=0.0):
         super().__init__()
@@ -78,11 +86,14 @@ class MultiHeadAttention(Module):
         return self.out_proj(Tensor(out.reshape(B, T, C)))
 
 
-    def forward_step(self, x, cache, lengths):
+    def forward_step(self, x, cache, lengths, residual=None):
         """One-token decode step whose positions live in device memory, so a
         recorded step replays unchanged: x (B, 1, C); this token's key/value
         go to cache row lengths[b] - 1 (mtx_kv_append_f32) and attention runs
-        over each sequence's first lengths[b] cached keys (mtx_attn_decode)."""
+        over each sequence's first lengths[b] cached keys (mtx_attn_decode).
+        With `residual` (B, 1, C) the output projection is accumulated into it
+        in place (the block's residual add folded into the GEMM) and it is
+        returned."""
         from . import kernels as K
 
         B, T, C = x.shape
@@ -100,6 +111,8 @@ class MultiHeadAttention(Module):
         out = dev.empty((B, 1, H, D))
         K.attn_decode(heads(q), heads(kc.t), heads(vc.t), 1.0 / math.sqrt(D),
                       out=out.t.transpose(1, 2), lengths=lengths)
+        if residual is not None:
+            return _linear_into(Tensor(out.reshape(B, 1, C)), self.out_proj, residual)
         return self.out_proj(Tensor(out.reshape(B, 1, C)))
 
     def fuse_qkv(self):
@@ -137,9 +150,13 @@ class TransformerBlock(Module):
         return x
 
     def forward_step(self, x, cache, lengths):
-        x = x + self.attn.forward_step(self.ln1(x), cache, lengths)
-        x = x + self.mlp(self.ln2(x))
-        return x
+        """Decode step (no autograd): x is updated in place, both residual
+        adds folded into the out_proj / second MLP GEMMs (beta = 1)."""
+        fc1, act, fc2, drop = self.mlp.layers
+        if drop._training and drop.p > 0.0:
+            raise NotImplementedError("decode steps run without dropout (use model.eval() or p = 0)")
+        self.attn.forward_step(self.ln1(x), cache, lengths, residual=x)
+        return _linear_into(act(fc1(self.ln2(x))), fc2, x)
 
 
 class GPT(Module):
