@@ -65,6 +65,7 @@ const char* mtx_version(void);
  * this is exactly the reference's triu(k=1) mask (the -1e9 entries give exact
  * zeros in the reference, so skipping them is equivalent).
  * D must be one of 16, 32, 64, 128.  Tq, Tk >= 1, Tq <= Tk when causal.
+ * The t (row) stride of every tensor must be < 2^24 elements.
  */
 int mtx_attn_fwd(int dtype, int B, int H, int Tq, int Tk, int D,
                  const void* q, const int64_t* q_strides,

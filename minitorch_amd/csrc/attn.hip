@@ -108,20 +108,31 @@ struct TileRegs {
   static constexpr int PER = (NCH + kThreads - 1) / kThreads;  // chunks per thread
   uint4 r[PER];
 
-  // rows >= nrows read as zero; `full` (wave-uniform): every row of the tile is
-  // < nrows, so loads need no guard
+  // Rows >= nrows read as zero.  The tile's first row is a wave-uniform
+  // pointer and each lane adds a 32-bit offset (row strides are < 2^24
+  // elements, checked on the host); whole tiles take a branch without guards.
   __device__ __forceinline__ void fetch(const T* __restrict__ g, int64_t ts, int r0, int nrows, int tid) {
-    const bool full = r0 + R <= nrows;
+    const T* __restrict__ base = g + (int64_t)r0 * ts;
+    const int its = (int)ts;
+    if (r0 + R <= nrows) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = tid + i * kThreads;
-      uint4 v0 = make_uint4(0u, 0u, 0u, 0u);
-      if (NCH % kThreads == 0 || c < NCH) {
+      for (int i = 0; i < PER; ++i) {
+        const int c = tid + i * kThreads;
+        if (NCH % kThreads != 0 && c >= NCH) continue;
         const int rr = c / CPR, cc = c % CPR;
-        const int row = r0 + rr;
-        if (full || row < nrows) v0 = *reinterpret_cast<const uint4*>(g + (int64_t)row * ts + cc * V);
+        r[i] = *reinterpret_cast<const uint4*>(base + rr * its + cc * V);
       }
-      r[i] = v0;
+    } else {
+      const int nrel = nrows - r0;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int c = tid + i * kThreads;
+        const int rr = c / CPR, cc = c % CPR;
+        uint4 v0 = make_uint4(0u, 0u, 0u, 0u);
+        if ((NCH % kThreads == 0 || c < NCH) && rr < nrel)
+          v0 = *reinterpret_cast<const uint4*>(base + rr * its + cc * V);
+        r[i] = v0;
+      }
     }
   }
 
@@ -141,11 +152,18 @@ struct TileRegs {
 // (resp. l^32) in the two results, in some order, on every lane, so a
 // commutative op of the two needs no lane select.  Every lane of the group
 // gets the same bits.
+// v_max_f32 without the NaN-quieting copies fmaxf adds for operands that come
+// from lane moves (the scores are never NaN for valid inputs)
+__device__ __forceinline__ float vmax(float x, float y) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(y));
+  return r;
+}
 __device__ __forceinline__ float max4l(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  v = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float sum4l(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -344,11 +362,12 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
   constexpr float kTau = 8.f;
   f32x4 acc[NQ][DT];
   f32x4 cin[NQ];
-  float m[NQ], l[NQ];
+  float m[NQ], l[NQ], lim[NQ];  // lim: -inf before the row's first key, kTau after
 #pragma unroll
   for (int qs = 0; qs < NQ; ++qs) {
     m[qs] = -INFINITY;
     l[qs] = 0.f;
+    lim[qs] = -INFINITY;
     cin[qs] = zero4();
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[qs][dt] = zero4();
@@ -412,14 +431,15 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[qs][kt][r]);
       mx = max4l(mx);
-      const bool keep = m[qs] != -INFINITY && mx <= kTau;
-      if (__builtin_amdgcn_ballot_w64(!keep) != 0ull) {
+      if (__builtin_amdgcn_ballot_w64(mx > lim[qs]) != 0ull) {
         // move this lane's reference up by d (0 for lanes that keep theirs);
         // everything is updated in place
-        const float d = (keep || mx == -INFINITY) ? 0.f : mx;
+        const bool move = mx > lim[qs];
+        const float d = move ? mx : 0.f;
         const bool fresh = m[qs] == -INFINITY;
         const float alpha = fresh ? 0.f : __builtin_amdgcn_exp2f(-d);
-        m[qs] = fresh ? (mx == -INFINITY ? -INFINITY : d) : m[qs] + d;
+        m[qs] = fresh ? (move ? d : -INFINITY) : m[qs] + d;
+        lim[qs] = m[qs] == -INFINITY ? -INFINITY : kTau;
         const float cm = m[qs] == -INFINITY ? 0.f : -m[qs];
         cin[qs] = f32x4{cm, cm, cm, cm};
 #pragma unroll
@@ -896,6 +916,8 @@ int check_bhtd(const char* name, const void* p, const int64_t* s, int esize) {
                   "%s: stride[%d]=%lld must be a non-negative multiple of %d elements", name, i,
                   (long long)s[i], vec);
   MTX_CHECK_ARG(((uintptr_t)p & 15u) == 0, "%s: pointer must be 16-byte aligned", name);
+  // tile loads use 32-bit offsets from a tile's first row
+  MTX_CHECK_SHAPE(s[2] < (1 << 24), "%s: the t stride (%lld elements) must be < 2^24", name, (long long)s[2]);
   return MTX_OK;
 }
 

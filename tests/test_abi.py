@@ -64,6 +64,7 @@ def _fwd(**over):
     (dict(vs=(512, 512, 66, 1)), L.MTX_ERR_ARG, "multiple"),
     (dict(o=24), L.MTX_ERR_ARG, "aligned"),
     (dict(scale=-1.0), L.MTX_ERR_ARG, "scale"),
+    (dict(ks=(1 << 30, 512, 1 << 24, 1)), L.MTX_ERR_SHAPE, "t stride"),
 ])
 def test_attn_fwd_rejects_bad_arguments(over, code, frag):
     rc = _fwd(**over)
