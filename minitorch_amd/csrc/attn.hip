@@ -147,6 +147,74 @@ struct TileRegs {
   }
 };
 
+// LDS tile layout.  bf16 tiles have unpadded rows whose 16-byte chunks are
+// permuted per row (chunk c of row r at chunk c ^ swz(r)), so that the two
+// fragment read patterns (16-byte reads of 16 consecutive rows at one column;
+// 8-byte transposing reads of 4-row x 16-column blocks) spread over the LDS
+// banks and a wave's 1 KiB direct load (TileDma) is one contiguous run of
+// rows.  swz has period 16 in r, so a fragment's offset inside a 16-row block
+// is a per-lane constant.  fp32 tiles use padded rows (register staging).
+template <typename T, int D>
+struct Lay {
+  static constexpr bool DIRECT = sizeof(T) == 2;  // global -> LDS loads
+  static constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  static constexpr int CPR = D / EPC;              // chunks per row
+  static constexpr int LD = DIRECT ? D : D + 4;    // row stride (elements)
+  __host__ __device__ static constexpr int swz(int r) {
+    return ((((r >> 1) << 1) + ((r >> 3) & 1)) & 7) & (CPR - 1);
+  }
+  // element offset of (r, col); an access must not cross a 16-byte chunk
+  __host__ __device__ static constexpr int at(int r, int col) {
+    if constexpr (DIRECT) return r * LD + ((((col / EPC) ^ swz(r)) * EPC) | (col % EPC));
+    else return r * LD + col;
+  }
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+
+// bf16 tile of R rows staged by direct global -> LDS loads
+// (global_load_lds_dwordx4: lane i of a wave writes bytes [16i, 16i+16) of
+// the wave's 1 KiB destination), so no registers hold the next tile.  Each
+// lane loads the global chunk that belongs at its LDS position.  Rows >=
+// nrows repeat row nrows-1 (finite data the kernels mask or weight by 0).
+// Completion: s_waitcnt vmcnt(0) by every wave, then a barrier.
+template <typename T, int R, int D>
+struct TileDma {
+  using LY = Lay<T, D>;
+  static constexpr int NI = R * LY::CPR / 64;           // wave-loads per tile
+  static constexpr int PW = (NI + kWaves - 1) / kWaves;  // per wave
+  int off[PW];                                          // lane offsets for whole tiles
+
+  __device__ __forceinline__ void init(int64_t ts, int wid, int lane) {
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+      const int c = (wid + j * kWaves) * 64 + lane;
+      const int row = c / LY::CPR, pch = c % LY::CPR;
+      off[j] = row * (int)ts + (pch ^ LY::swz(row)) * LY::EPC;
+    }
+  }
+  __device__ __forceinline__ void issue(const T* __restrict__ g, int64_t ts, int r0, int nrows, T* buf, int wid,
+                                        int lane) const {
+    const T* base = g + (int64_t)r0 * ts;
+    const bool full = r0 + R <= nrows;
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+      const int ins = wid + j * kWaves;
+      if (NI % kWaves != 0 && ins >= NI) continue;
+      int o = off[j];
+      if (!full) {
+        const int c = ins * 64 + lane;
+        const int row = c / LY::CPR, pch = c % LY::CPR;
+        o = min(row, nrows - r0 - 1) * (int)ts + (pch ^ LY::swz(row)) * LY::EPC;
+      }
+      __builtin_amdgcn_global_load_lds((glb_void*)(base + o), (lds_void*)(buf + ins * 64 * LY::EPC), 16, 0, 0);
+    }
+  }
+};
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Reductions over the 4 lanes l, l^16, l^32, l^48 of a wave64 with the gfx950
 // lane swaps: v_permlane16_swap / v_permlane32_swap leave {v[l], v[l^16]}
 // (resp. l^32) in the two results, in some order, on every lane, so a
@@ -200,9 +268,10 @@ __device__ __forceinline__ typename Mfma<T>::frag dfrag(const T* __restrict__ p,
   }
 }
 
-// A operand X^T[d][j] for k-step s over the j (key or query) dimension of a
-// row-major LDS tile X[j][d] (row stride rld), for d = 16*dt + n, where the
-// matching B operand comes from C-layout accumulators (see pfrag).
+// Transposed operand (ltfrag below): A operand X^T[d][j] for k-step s over the
+// j (key or query) dimension of a row-major LDS tile X[j][d], for
+// d = 16*dt + n, where the matching B operand comes from C-layout
+// accumulators (see pfrag).
 //   fp32: step s covers j = 16*(s/4) + 4g + (s%4): one scalar read.
 //   bf16: step s covers j = 32s + 16*(e/4) + 4g + (e%4), e = 0..7, read with
 //   two gfx950 transposing LDS loads (ds_read_b64_tr_b16).  Within each
@@ -213,15 +282,53 @@ __device__ __forceinline__ typename Mfma<T>::frag dfrag(const T* __restrict__ p,
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-template <typename T>
-__device__ __forceinline__ typename Mfma<T>::frag tfrag(const T* __restrict__ rowbuf, int rld, int dt, int n,
-                                                        int g, int s) {
+// Fragment reads from an LDS tile in the Lay<T, D> layout.  LaneOffs::d(kc):
+// the lane's offset of the "quarter map" fragment kc inside a 16-row block
+// (row n); LaneOffs::t(dt): the lane's offset of the transposed operand for
+// d-block dt.  With the swizzle the offsets for other kc / dt differ from the
+// first only in bits below the row base, by xor.
+template <typename T, int D>
+struct LaneOffs {
+  using LY = Lay<T, D>;
+  static constexpr int QPL = D / 4;
+  int d0, t0;
+  __device__ __forceinline__ LaneOffs(int n, int g) {
+    d0 = LY::at(n, g * QPL);
+    if constexpr (sizeof(T) == 4) t0 = LY::at(4 * g, n);
+    else t0 = LY::at(4 * g + (n >> 2), 4 * (n & 3));
+  }
+  __device__ __forceinline__ int d(int kc) const {
+    if constexpr (LY::DIRECT) return d0 ^ (kc * (sizeof(T) == 4 ? 1 : 8));
+    else return d0 + kc * (sizeof(T) == 4 ? 1 : 8);
+  }
+  __device__ __forceinline__ int t(int dt) const {
+    if constexpr (LY::DIRECT) return t0 ^ (16 * dt);
+    else return t0 + 16 * dt;
+  }
+};
+
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::frag lfrag(const T* __restrict__ p) {
   if constexpr (sizeof(T) == 4) {
-    return rowbuf[(16 * (s >> 2) + 4 * g + (s & 3)) * rld + 16 * dt + n];
+    return *p;
+  } else if constexpr (D / 4 >= 8) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+  } else {  // D == 16: 4 real elements, 4 zeros
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return __builtin_bit_cast(bf16x8, make_uint4(u.x, u.y, 0u, 0u));
+  }
+}
+
+// transposed operand for k-step s; `to` = LaneOffs::t(dt)
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::frag ltfrag(const T* __restrict__ buf, int s, int to) {
+  constexpr int LD = Lay<T, D>::LD;
+  if constexpr (sizeof(T) == 4) {
+    return buf[(16 * (s >> 2) + (s & 3)) * LD + to];
   } else {
-    const T* p = rowbuf + (32 * s + 4 * g + (n >> 2)) * rld + 16 * dt + 4 * (n & 3);
+    const T* p = buf + 32 * s * LD + to;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 16 * rld));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 16 * LD));
     const uint2 ul = __builtin_bit_cast(uint2, lo), uh = __builtin_bit_cast(uint2, hi);
     return __builtin_bit_cast(bf16x8, make_uint4(ul.x, ul.y, uh.x, uh.y));
   }
@@ -289,15 +396,6 @@ __device__ __forceinline__ void store_grad4(float* __restrict__ p, f32x4 v, bool
   *reinterpret_cast<f32x4*>(p) = v;
 }
 
-// Row padding (elements) of LDS tiles: keeps 16-byte row alignment and
-// spreads rows over the LDS banks.
-#ifndef MTX_BF16_LDS_PAD
-#define MTX_BF16_LDS_PAD 8
-#endif
-template <typename T>
-__host__ __device__ constexpr int lds_pad() {
-  return sizeof(T) == 2 ? MTX_BF16_LDS_PAD : 4;
-}
 
 // ---------------------------------------------------------------------------
 // forward
@@ -313,11 +411,16 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
   constexpr int BQ = kWaves * NQ * 16;
   constexpr int BK = 64;
   constexpr int NS = BK / MF::KI;             // k-steps of the PV product per tile
-  constexpr int LDR = D + lds_pad<T>();  // row-major LDS stride
-  constexpr int KSZ = BK * LDR, VSZ = BK * LDR;
-  constexpr int NBUF = (KSZ + VSZ) * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) T Ks[NBUF * KSZ];
-  __shared__ __attribute__((aligned(16))) T Vs[NBUF * VSZ];
+  using LY = Lay<T, D>;
+  constexpr int LD = LY::LD;  // LDS row stride
+  constexpr int KSZ = BK * LD;
+  constexpr int NBUF = 2 * KSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
+  // separate arrays per buffer, picked with compile-time parities: the
+  // compiler then sees the direct loads into one buffer and the reads of the
+  // other as disjoint and does not wait for the loads before the reads
+  __shared__ __attribute__((aligned(16))) T K0[KSZ], V0[KSZ];
+  __shared__ __attribute__((aligned(16))) T K1[NBUF == 2 ? KSZ : 1], V1[NBUF == 2 ? KSZ : 1];
 
   const int BH = a.B * a.H;
   const int nqb = (a.Tq + BQ - 1) / BQ;
@@ -375,25 +478,47 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
 
   const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
   const int ntile = (kend + BK - 1) / BK;
-  TileRegs<T, BK, D> kreg, vreg;
-  if (ntile > 0) {
+  const LaneOffs<T, D> lo(n, g);
+  TileDma<T, BK, D> kdma, vdma;  // bf16: direct global -> LDS
+  TileRegs<T, BK, D> kreg, vreg;  // fp32: through registers
+  if constexpr (LY::DIRECT) {
+    kdma.init(a.sk.t, wid, lane);
+    vdma.init(a.sv.t, wid, lane);
+    if (ntile > 0) {
+      kdma.issue(kp, a.sk.t, 0, a.Tk, K0, wid, lane);
+      vdma.issue(vp, a.sv.t, 0, a.Tk, V0, wid, lane);
+    }
+  } else if (ntile > 0) {
     kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
     vreg.fetch(vp, a.sv.t, 0, a.Tk, tid);
   }
-  for (int it = 0; it < ntile; ++it) {
+  // one key tile; P = buffer parity (for direct loads the loop below is
+  // unrolled by two so that P is a compile-time constant)
+  auto step = [&](auto par, const int it) {
+    const int P = int(par) % NBUF;  // a constant for the unrolled (direct-load) loop
+    const int PN = (P + 1) % NBUF;
     const int kb = it * BK;
-    T* __restrict__ Kb = Ks + (NBUF == 2 ? (it & 1) : 0) * KSZ;
-    T* __restrict__ Vb = Vs + (NBUF == 2 ? (it & 1) : 0) * VSZ;
-    if constexpr (NBUF == 1) __syncthreads();
-    kreg.put(Kb, LDR, tid);
-    vreg.put(Vb, LDR, tid);
+    T* __restrict__ Kb = P ? K1 : K0;
+    T* __restrict__ Vb = P ? V1 : V0;
+    if constexpr (LY::DIRECT) {
+      wait_dma();
+    } else {
+      if constexpr (NBUF == 1) __syncthreads();
+      kreg.put(Kb, LD, tid);
+      vreg.put(Vb, LD, tid);
+    }
     __syncthreads();
     if (it + 1 < ntile) {
-      kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
-      vreg.fetch(vp, a.sv.t, kb + BK, a.Tk, tid);
+      if constexpr (LY::DIRECT) {
+        kdma.issue(kp, a.sk.t, kb + BK, a.Tk, PN ? K1 : K0, wid, lane);
+        vdma.issue(vp, a.sv.t, kb + BK, a.Tk, PN ? V1 : V0, wid, lane);
+      } else {
+        kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
+        vreg.fetch(vp, a.sv.t, kb + BK, a.Tk, tid);
+      }
     }
 
-    if (a.causal && kb > qw0 + NQ * 16 - 1 + off) continue;  // nothing visible for this wave
+    if (a.causal && kb > qw0 + NQ * 16 - 1 + off) return;  // nothing visible for this wave
     const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
 
     f32x4 s[NQ][4];
@@ -401,7 +526,7 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
     for (int kt = 0; kt < 4; ++kt) {
       frag kf[KC];
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) kf[kc] = dfrag<T, D>(Kb + (16 * kt + n) * LDR, g, kc);
+      for (int kc = 0; kc < KC; ++kc) kf[kc] = lfrag<T, D>(Kb + 16 * kt * LD + lo.d(kc));
 #pragma unroll
       for (int qs = 0; qs < NQ; ++qs) {
         f32x4 t = cin[qs];
@@ -463,10 +588,18 @@ __global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
-        const frag vf = tfrag<T>(Vb, LDR, dt, n, g, st);
+        const frag vf = ltfrag<T, D>(Vb, st, lo.t(dt));
 #pragma unroll
         for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(vf, pf[qs][st], acc[qs][dt]);
       }
+  };
+  if constexpr (LY::DIRECT) {
+    for (int it = 0; it < ntile; it += 2) {
+      step(std::integral_constant<int, 0>{}, it);
+      if (it + 1 < ntile) step(std::integral_constant<int, 1>{}, it + 1);
+    }
+  } else {
+    for (int it = 0; it < ntile; ++it) step(it & 1, it);
   }
 
   // finalize: O = acc / l, lse = (m + log2 l) * ln2
@@ -526,15 +659,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   constexpr int BKV = kWaves * NK * 16;
   constexpr int BQ = 64;
   constexpr int NS = BQ / MF::KI;
-  constexpr int LDR = D + lds_pad<T>();
-  constexpr int RSZ = BQ * LDR;
+  using LY = Lay<T, D>;
+  constexpr int LD = LY::LD;
+  constexpr int RSZ = BQ * LD;
   constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) T Qs[NBUF * RSZ];
-  __shared__ __attribute__((aligned(16))) T Ds[NBUF * RSZ];
+  static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
+  // separate arrays per buffer, picked with compile-time parities (see the
+  // forward kernel)
+  __shared__ __attribute__((aligned(16))) T Q0[RSZ], D0[RSZ];
+  __shared__ __attribute__((aligned(16))) T Q1[NBUF == 2 ? RSZ : 1], D1[NBUF == 2 ? RSZ : 1];
   // per query of the tile: -lse*log2(e) and -delta, the starting accumulators
   // of the S and dP MFMAs, so they yield log2(P) and dP - delta directly
-  __shared__ __attribute__((aligned(16))) float lse_s[NBUF * BQ];
-  __shared__ __attribute__((aligned(16))) float del_s[NBUF * BQ];
+  __shared__ __attribute__((aligned(16))) float L0[BQ], E0[BQ], L1[BQ], E1[BQ];
 
   const int BH = a.B * a.H;
   const int nkb = (a.Tk + BKV - 1) / BKV;
@@ -583,37 +719,59 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
   int qstart = a.causal ? max(0, k0 - off) : 0;
   qstart = (qstart / BQ) * BQ;
   const int ntile = qstart < a.Tq ? (a.Tq - qstart + BQ - 1) / BQ : 0;
-  TileRegs<T, BQ, D> qreg, dreg;
+  const LaneOffs<T, D> lo(n, g);
+  TileDma<T, BQ, D> qdma, ddma;  // bf16: direct global -> LDS
+  TileRegs<T, BQ, D> qreg, dreg;  // fp32: through registers
+  if constexpr (LY::DIRECT) {
+    qdma.init(a.sq.t, wid, lane);
+    ddma.init(a.sdo.t, wid, lane);
+  }
   float lse_r = 0.f, del_r = 0.f;
-  auto fetch = [&](int qt) {
-    qreg.fetch(qp, a.sq.t, qt, a.Tq, tid);
-    dreg.fetch(dop, a.sdo.t, qt, a.Tq, tid);
+  // the next tile's loads: lse / delta (through registers, raw; converted
+  // when stored, so the loads are not waited for here) first, so that waiting
+  // for them never waits for the direct tile loads issued after them
+  auto fetch = [&](int qt, T* qdst, T* ddst) {
     if (tid < BQ) {
-      const int qi = qt + tid;
-      lse_r = qi < a.Tq ? -lsep[qi] * kLog2e : -INFINITY;
-      del_r = qi < a.Tq ? -delp[qi] : 0.f;
+      const int qi = min(qt + tid, a.Tq - 1);
+      lse_r = lsep[qi];
+      del_r = delp[qi];
+    }
+    if constexpr (LY::DIRECT) {
+      qdma.issue(qp, a.sq.t, qt, a.Tq, qdst, wid, lane);
+      ddma.issue(dop, a.sdo.t, qt, a.Tq, ddst, wid, lane);
+    } else {
+      qreg.fetch(qp, a.sq.t, qt, a.Tq, tid);
+      dreg.fetch(dop, a.sdo.t, qt, a.Tq, tid);
     }
   };
-  if (ntile > 0) fetch(qstart);
-  for (int it = 0; it < ntile; ++it) {
+  if (ntile > 0) fetch(qstart, Q0, D0);
+  // one query tile; P = buffer parity (for direct loads the loop below is
+  // unrolled by two so that P is a compile-time constant)
+  auto step = [&](auto par, const int it) {
+    const int P = int(par) % NBUF;
+    const int PN = (P + 1) % NBUF;
     const int qt = qstart + it * BQ;
-    const int bsel = NBUF == 2 ? (it & 1) : 0;
-    T* __restrict__ Qb = Qs + bsel * RSZ;
-    T* __restrict__ Db = Ds + bsel * RSZ;
-    float* __restrict__ lse_b = lse_s + bsel * BQ;
-    float* __restrict__ del_b = del_s + bsel * BQ;
-    if constexpr (NBUF == 1) __syncthreads();
-    qreg.put(Qb, LDR, tid);
-    dreg.put(Db, LDR, tid);
+    T* __restrict__ Qb = P ? Q1 : Q0;
+    T* __restrict__ Db = P ? D1 : D0;
+    float* __restrict__ lse_b = P ? L1 : L0;
+    float* __restrict__ del_b = P ? E1 : E0;
+    if constexpr (LY::DIRECT) {
+      wait_dma();
+    } else {
+      if constexpr (NBUF == 1) __syncthreads();
+      qreg.put(Qb, LD, tid);
+      dreg.put(Db, LD, tid);
+    }
     if (tid < BQ) {
-      lse_b[tid] = lse_r;
-      del_b[tid] = del_r;
+      const bool ok = qt + tid < a.Tq;
+      lse_b[tid] = ok ? -lse_r * kLog2e : -INFINITY;
+      del_b[tid] = ok ? -del_r : 0.f;
     }
     __syncthreads();
-    if (it + 1 < ntile) fetch(qt + BQ);
+    if (it + 1 < ntile) fetch(qt + BQ, PN ? Q1 : Q0, PN ? D1 : D0);
 
     // wave-level causal skip: every key of the wave is after every query of the tile
-    if (a.causal && kw0 > qt + BQ - 1 + off) continue;
+    if (a.causal && kw0 > qt + BQ - 1 + off) return;
     const bool need_mask = a.causal && (kw0 + NK * 16 - 1 > qt + off);
     auto tile = [&](auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
@@ -634,8 +792,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
         frag qa[KC], da[KC];
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
-          qa[kc] = dfrag<T, D>(Qb + (16 * qs + n) * LDR, g, kc);
-          da[kc] = dfrag<T, D>(Db + (16 * qs + n) * LDR, g, kc);
+          qa[kc] = lfrag<T, D>(Qb + 16 * qs * LD + lo.d(kc));
+          da[kc] = lfrag<T, D>(Db + 16 * qs * LD + lo.d(kc));
         }
         const f32x4 nlse = *reinterpret_cast<const f32x4*>(lse_b + 16 * qs + 4 * g);
         const f32x4 ndel = *reinterpret_cast<const f32x4*>(del_b + 16 * qs + 4 * g);
@@ -669,8 +827,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const frag dof = tfrag<T>(Db, LDR, dt, n, g, st);
-          const frag qf2 = tfrag<T>(Qb, LDR, dt, n, g, st);
+          const frag dof = ltfrag<T, D>(Db, st, lo.t(dt));
+          const frag qf2 = ltfrag<T, D>(Qb, st, lo.t(dt));
 #pragma unroll
           for (int ks = 0; ks < NK; ++ks) {
             dva[ks][dt] = MF::mma(dof, pb[ks], dva[ks][dt]);
@@ -686,6 +844,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
 #else
     tile(std::true_type{});
 #endif
+  };
+  if constexpr (LY::DIRECT) {
+    for (int it = 0; it < ntile; it += 2) {
+      step(std::integral_constant<int, 0>{}, it);
+      if (it + 1 < ntile) step(std::integral_constant<int, 1>{}, it + 1);
+    }
+  } else {
+    for (int it = 0; it < ntile; ++it) step(it & 1, it);
   }
 
   float* __restrict__ dkp = a.dk + b * a.sdk.b + h * a.sdk.h;
@@ -720,11 +886,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
   constexpr int BQ = kWaves * NQ * 16;
   constexpr int BK = 64;
   constexpr int NS = BK / MF::KI;
-  constexpr int LDR = D + lds_pad<T>();
-  constexpr int RSZ = BK * LDR;
+  using LY = Lay<T, D>;
+  constexpr int LD = LY::LD;
+  constexpr int RSZ = BK * LD;
   constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) T Ks[NBUF * RSZ];
-  __shared__ __attribute__((aligned(16))) T Vs[NBUF * RSZ];
+  static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
+  // separate arrays per buffer, picked with compile-time parities (see the
+  // forward kernel)
+  __shared__ __attribute__((aligned(16))) T K0[RSZ], V0[RSZ];
+  __shared__ __attribute__((aligned(16))) T K1[NBUF == 2 ? RSZ : 1], V1[NBUF == 2 ? RSZ : 1];
 
   const int BH = a.B * a.H;
   const int nqb = (a.Tq + BQ - 1) / BQ;
@@ -796,26 +966,47 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
 
   const int kend = a.causal ? min(a.Tk, q0 + BQ + off) : a.Tk;
   const int ntile = (kend + BK - 1) / BK;
-  TileRegs<T, BK, D> kreg, vreg;
-  if (ntile > 0) {
+  const LaneOffs<T, D> lo(n, g);
+  TileDma<T, BK, D> kdma, vdma;  // bf16: direct global -> LDS
+  TileRegs<T, BK, D> kreg, vreg;  // fp32: through registers
+  if constexpr (LY::DIRECT) {
+    kdma.init(a.sk.t, wid, lane);
+    vdma.init(a.sv.t, wid, lane);
+    if (ntile > 0) {
+      kdma.issue(kp, a.sk.t, 0, a.Tk, K0, wid, lane);
+      vdma.issue(vp, a.sv.t, 0, a.Tk, V0, wid, lane);
+    }
+  } else if (ntile > 0) {
     kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
     vreg.fetch(vp, a.sv.t, 0, a.Tk, tid);
   }
-  for (int it = 0; it < ntile; ++it) {
+  // one key tile; P = buffer parity (for direct loads the loop below is
+  // unrolled by two so that P is a compile-time constant)
+  auto step = [&](auto par, const int it) {
+    const int P = int(par) % NBUF;  // a constant for the unrolled (direct-load) loop
+    const int PN = (P + 1) % NBUF;
     const int kb = it * BK;
-    const int bsel = NBUF == 2 ? (it & 1) : 0;
-    T* __restrict__ Kb = Ks + bsel * RSZ;
-    T* __restrict__ Vb = Vs + bsel * RSZ;
-    if constexpr (NBUF == 1) __syncthreads();
-    kreg.put(Kb, LDR, tid);
-    vreg.put(Vb, LDR, tid);
+    T* __restrict__ Kb = P ? K1 : K0;
+    T* __restrict__ Vb = P ? V1 : V0;
+    if constexpr (LY::DIRECT) {
+      wait_dma();
+    } else {
+      if constexpr (NBUF == 1) __syncthreads();
+      kreg.put(Kb, LD, tid);
+      vreg.put(Vb, LD, tid);
+    }
     __syncthreads();
     if (it + 1 < ntile) {
-      kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
-      vreg.fetch(vp, a.sv.t, kb + BK, a.Tk, tid);
+      if constexpr (LY::DIRECT) {
+        kdma.issue(kp, a.sk.t, kb + BK, a.Tk, PN ? K1 : K0, wid, lane);
+        vdma.issue(vp, a.sv.t, kb + BK, a.Tk, PN ? V1 : V0, wid, lane);
+      } else {
+        kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
+        vreg.fetch(vp, a.sv.t, kb + BK, a.Tk, tid);
+      }
     }
 
-    if (a.causal && kb > qw0 + NQ * 16 - 1 + off) continue;
+    if (a.causal && kb > qw0 + NQ * 16 - 1 + off) return;
     const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
     auto tile = [&](auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
@@ -826,8 +1017,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
       frag kfr[KC], vfr[KC];
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        kfr[kc] = dfrag<T, D>(Kb + (16 * kt + n) * LDR, g, kc);
-        vfr[kc] = dfrag<T, D>(Vb + (16 * kt + n) * LDR, g, kc);
+        kfr[kc] = lfrag<T, D>(Kb + 16 * kt * LD + lo.d(kc));
+        vfr[kc] = lfrag<T, D>(Vb + 16 * kt * LD + lo.d(kc));
       }
 #pragma unroll
       for (int qs = 0; qs < NQ; ++qs) {
@@ -858,7 +1049,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
       for (int qs = 0; qs < NQ; ++qs) db[qs] = pfrag<T, 4>(ds[qs], st);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const frag kt_f = tfrag<T>(Kb, LDR, dt, n, g, st);
+        const frag kt_f = ltfrag<T, D>(Kb, st, lo.t(dt));
 #pragma unroll
         for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(kt_f, db[qs], acc[qs][dt]);
       }
@@ -866,6 +1057,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
       };
     if (need_mask) tile(std::true_type{});
     else tile(std::false_type{});
+  };
+  if constexpr (LY::DIRECT) {
+    for (int it = 0; it < ntile; it += 2) {
+      step(std::integral_constant<int, 0>{}, it);
+      if (it + 1 < ntile) step(std::integral_constant<int, 1>{}, it + 1);
+    }
+  } else {
+    for (int it = 0; it < ntile; ++it) step(it & 1, it);
   }
 
   float* __restrict__ dqp = a.dq + b * a.sdq.b + h * a.sdq.h;
