@@ -32,9 +32,9 @@
 
 // 1: the dK/dV tile body is instantiated twice (masked diagonal tiles,
 // unmasked interior tiles); 0: one body with a run-time mask test
-// waves per SIMD the forward kernel is compiled for
+// waves per SIMD the forward kernel is compiled for (bf16, D <= 64; others 2)
 #ifndef MTX_FWD_WAVES
-#define MTX_FWD_WAVES 2
+#define MTX_FWD_WAVES 4
 #endif
 #ifndef MTX_DKDV_SPLIT
 #define MTX_DKDV_SPLIT 1
@@ -401,7 +401,8 @@ __device__ __forceinline__ void store_grad4(float* __restrict__ p, f32x4 v, bool
 // forward
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NQ>
-__global__ __launch_bounds__(kThreads, MTX_FWD_WAVES) void attn_fwd_kernel(const FwdArgs a) {
+__global__ __launch_bounds__(kThreads, (sizeof(T) == 2 && D <= 64) ? MTX_FWD_WAVES : 2) void attn_fwd_kernel(
+    const FwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
