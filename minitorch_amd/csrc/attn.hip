@@ -32,7 +32,13 @@
 
 // 1: the dK/dV tile body is instantiated twice (masked diagonal tiles,
 // unmasked interior tiles); 0: one body with a run-time mask test
-// waves per SIMD the forward kernel is compiled for (bf16, D <= 64; others 2)
+// waves per SIMD the dQ kernel is compiled for (bf16, D <= 64; fp32 D = 128:
+// 1, for its accumulators; others 2)
+#ifndef MTX_DQ_WAVES
+#define MTX_DQ_WAVES 3
+#endif
+// waves per SIMD the forward kernel is compiled for (bf16, D <= 64; fp32
+// D = 128: 1; others 2)
 #ifndef MTX_FWD_WAVES
 #define MTX_FWD_WAVES 4
 #endif
@@ -401,8 +407,8 @@ __device__ __forceinline__ void store_grad4(float* __restrict__ p, f32x4 v, bool
 // forward
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NQ>
-__global__ __launch_bounds__(kThreads, (sizeof(T) == 2 && D <= 64) ? MTX_FWD_WAVES : 2) void attn_fwd_kernel(
-    const FwdArgs a) {
+__global__ __launch_bounds__(kThreads, (sizeof(T) == 2 && D <= 64) ? MTX_FWD_WAVES : (D == 128 && sizeof(T) == 4 ? 1 : 2))
+void attn_fwd_kernel(const FwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
@@ -650,7 +656,7 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const BwdArgs a) {
 // backward, pass 1: dK, dV (key-outer).  Each wave owns NK*16 keys.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NK>
-__global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void attn_dkdv_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
@@ -877,7 +883,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dkdv_kernel(const BwdArgs a)
 // FD: also computes delta[i] = sum_d dO[i,d] O[i,d] for its rows (from the
 // same fragments it loads anyway) and writes it for the dK/dV pass.
 template <typename T, int D, int NQ, bool FD>
-__global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(kThreads, (sizeof(T) == 2 && D <= 64) ? MTX_DQ_WAVES : (D == 128 && sizeof(T) == 4 ? 1 : 2))
+void attn_dq_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
@@ -1012,9 +1019,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
     auto tile = [&](auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
 
-    f32x4 ds[NQ][4];
+    // two 32-key halves: dS of a half, then its dQ products (only one
+    // half's dS is live)
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int hf = 0; hf < 2; ++hf) {
+    f32x4 ds[NQ][2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int kt = 2 * hf + kk;
       frag kfr[KC], vfr[KC];
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
@@ -1038,22 +1050,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_dq_kernel(const BwdArgs a) {
             if (a.causal) lim = min(lim, qw0 + 16 * qs + n + off - kb - 16 * kt - 4 * g);
             if (r > lim) pv = 0.f;
           }
-          ds[qs][kt][r] = pv * dpv[r];
+          ds[qs][kk][r] = pv * dpv[r];
         }
       }
     }
 
 #pragma unroll
-    for (int st = 0; st < NS; ++st) {
+    for (int st = hf * NS / 2; st < (hf + 1) * NS / 2; ++st) {
       frag db[NQ];
 #pragma unroll
-      for (int qs = 0; qs < NQ; ++qs) db[qs] = pfrag<T, 4>(ds[qs], st);
+      for (int qs = 0; qs < NQ; ++qs) db[qs] = pfrag<T, 2>(ds[qs], st - hf * NS / 2);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const frag kt_f = ltfrag<T, D>(Kb, st, lo.t(dt));
 #pragma unroll
         for (int qs = 0; qs < NQ; ++qs) acc[qs][dt] = MF::mma(kt_f, db[qs], acc[qs][dt]);
       }
+    }
     }
       };
     if (need_mask) tile(std::true_type{});
