@@ -17,7 +17,7 @@ import numpy as np
 from . import device as dev
 from . import kernels as K
 from .device import DeviceArray
-from .tensor import Tensor, _accum_grad, _grad_target, grad_enabled
+from .tensor import Tensor, _accum_grad, _grad_target, _parents, grad_enabled
 
 
 def _track(*ts):
@@ -28,7 +28,7 @@ def _node(data, prev, op, backward, track):
     out = Tensor(data, requires_grad=track)
     if track:
         out._backward = backward
-        out._prev = set(prev)
+        out._prev = _parents(prev)
         out._op = op
     return out
 

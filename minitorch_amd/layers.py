@@ -15,7 +15,7 @@ from . import functional as F
 from . import kernels as K
 from .device import DeviceArray
 from .module import Module
-from .tensor import Tensor, _grad_target, grad_enabled
+from .tensor import Tensor, _grad_target, grad_enabled, _parents
 
 
 class Linear(Module):
@@ -113,7 +113,7 @@ class LayerNorm(Module):
                                     dbeta=dbet, accumulate=acc_p)
 
             out._backward = _backward
-            out._prev = {x, gamma, beta}
+            out._prev = _parents((x, gamma, beta))
             out._op = "layernorm"
         return out
 

@@ -5,6 +5,8 @@ of (param, grad, m, v) pointers), with the reference's float32 arithmetic.
 """
 from __future__ import annotations
 
+import numpy as np
+
 from . import device as dev
 from . import kernels as K
 
@@ -52,6 +54,35 @@ class Adam(Optimizer):
                                       [self.m[i].t for i in live], [self.v[i].t for i in live])
             self._key = key
         K.adam_step(self._table, self.lr, self.beta1, self.beta2, self.eps, self.weight_decay, self.t)
+
+    def state_dict(self):
+        """Host copy of the optimizer state for checkpoint / resume: the step
+        count `t` and the moment estimates `m.<i>`, `v.<i>` in parameter order.
+        (The reference keeps this state in memory only, optim.py:43-45.)"""
+        state = {"t": np.asarray(self.t, dtype=np.int64)}
+        for i in range(len(self.params)):
+            state[f"m.{i}"] = self.m[i].numpy().copy()
+            state[f"v.{i}"] = self.v[i].numpy().copy()
+        return state
+
+    def load_state_dict(self, state):
+        """Restore a state_dict() (same parameter list, same shapes); the
+        moment buffers are overwritten in place."""
+        for i, p in enumerate(self.params):
+            for name, buf in (("m", self.m[i]), ("v", self.v[i])):
+                arr = np.asarray(state[f"{name}.{i}"], dtype=np.float32)
+                if arr.shape != tuple(p.shape):
+                    raise ValueError(f"{name}.{i}: shape {arr.shape} does not match parameter {tuple(p.shape)}")
+                buf.t.copy_(dev.from_host(arr).t)
+        self.t = int(state["t"])
+
+    def save(self, path):
+        np.savez(path, **self.state_dict())
+
+    def load(self, path):
+        with np.load(path) as data:
+            self.load_state_dict({k: data[k] for k in data.files})
+        return self
 
 
 class SGD(Optimizer):

@@ -14,6 +14,11 @@ Differences, all on purpose:
   * A gradient that is written for the first time goes straight into a new
     buffer (the reference zero-fills, then adds: same values).
   * Python scalars in arithmetic become cached device constants.
+  * ``_prev`` is a tuple of the distinct inputs in argument order, not a set:
+    the backward walk, and so the order in which a tensor's consumers add
+    into its gradient, is the same on every run (the reference's order
+    follows set iteration, i.e. object addresses), which makes training
+    bit-reproducible.
 """
 from __future__ import annotations
 
@@ -24,6 +29,11 @@ import numpy as np
 from . import device as dev
 from . import kernels as K
 from .device import DeviceArray
+
+
+def _parents(inputs):
+    """Distinct inputs in first-occurrence order (an op's ``_prev``)."""
+    return tuple(dict.fromkeys(inputs))
 
 _grad_enabled = True
 
@@ -110,7 +120,7 @@ class Tensor:
         self.requires_grad = requires_grad and _grad_enabled
         self.grad = None
         self._backward = lambda: None
-        self._prev = set()
+        self._prev = ()
         self._op = ""
 
     # ---------------------------------------------------------------- props
@@ -160,7 +170,7 @@ class Tensor:
         out = Tensor(data, requires_grad=track)
         if track:
             out._backward = backward
-            out._prev = set(prev)
+            out._prev = _parents(prev)
             out._op = op
         return out
 
@@ -601,7 +611,7 @@ def cat(tensors, axis=0):
 
     if track:
         out._backward = _backward
-        out._prev = set(tensors)
+        out._prev = _parents(tensors)
         out._op = "cat"
     return out
 
