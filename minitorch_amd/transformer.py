@@ -285,16 +285,73 @@ class GPT(Module):
         return out
 
     def generate(self, idx, max_new_tokens, temperature=1.0):
-        """Sample tokens as the reference does (transformer.py:93-104): full
-        forward over the cropped context, host softmax over the last logits,
-        np.random.choice per row."""
+        """Sample tokens as the reference does (transformer.py:93-104): each
+        step takes the last position's logits / temperature, a softmax, and
+        one np.random.choice per row from NumPy's global RNG, rows in order.
+        The logits come from one-token KV-cache steps while the context fits
+        block_size; once the reference would crop it (positions shift) they
+        come from a full forward over the cropped context.  The softmax runs
+        on the device; the host draws.  With active dropout (training mode,
+        p > 0) every step is a full forward, as in the reference."""
+        from . import kernels as K
+
         idx = np.asarray(idx)
-        for _ in range(max_new_tokens):
-            idx_cond = idx[:, -self.block_size:]
-            logits = self.forward(idx_cond).data[:, -1, :] / temperature
-            logits = logits - logits.max(axis=-1, keepdims=True)
-            probs = np.exp(logits)
-            probs = probs / probs.sum(axis=-1, keepdims=True)
-            next_ids = np.array([np.random.choice(probs.shape[-1], p=p) for p in probs])
-            idx = np.concatenate([idx, next_ids[:, None]], axis=1)
-        return idx
+        B, T0 = idx.shape
+        n = int(max_new_tokens)
+        blk = self.block_size
+        out = np.empty((B, T0 + n), dtype=np.int64)
+        out[:, :T0] = idx
+        if n < 1:
+            return out
+        V = self.lm_head.weight.shape[1]
+        C = self.tok_emb.weight.shape[1]
+        temp = dev.const(float(temperature))
+        def walk(m):
+            yield m
+            for _, c in m._children():
+                if isinstance(c, Module):
+                    yield from walk(c)
+
+        dropout_on = any(isinstance(m, Dropout) and m._training and m.p > 0.0 for m in walk(self))
+
+        def sample(logits2d):
+            scaled = dev.empty((B, V))
+            K.ewise("DIV", scaled.t, logits2d, temp.t)
+            probs = dev.empty((B, V))
+            K.softmax_fwd(scaled.t, probs.t)
+            p = probs.numpy().astype(np.float64)
+            p /= p.sum(axis=-1, keepdims=True)
+            return np.array([np.random.choice(V, p=pr) for pr in p])
+
+        def last_logits(x):
+            x = self.ln_f(Tensor(x.data.t[:, -1:, :]))
+            return self.lm_head(x).data.t.view(B, V)
+
+        with no_grad():
+            ctx = T0
+            caches = None
+            if T0 <= blk and not dropout_on:
+                caches = [(dev.empty((B, blk, C)), dev.empty((B, blk, C))) for _ in self.blocks]
+                pos = self._positions(blk)
+                x = self.tok_emb(dev.index_array(idx)) + self.pos_emb(DeviceArray(pos.t[:T0]))
+                for block, cache in zip(self.blocks, caches):
+                    x = block.forward_cached(x, cache, 0)
+                logits = last_logits(x)
+            else:
+                logits = self.forward(out[:, max(0, ctx - blk):ctx]).data.t[:, -1, :]
+            for i in range(n):
+                out[:, ctx] = sample(logits)
+                ctx += 1
+                if i == n - 1:
+                    break
+                if caches is not None and ctx <= blk:
+                    # the new token sits at position ctx - 1 of an uncropped context
+                    t = ctx - 1
+                    x = self.tok_emb(dev.index_array(out[:, t:t + 1])) + self.pos_emb(DeviceArray(pos.t[t:t + 1]))
+                    for block, cache in zip(self.blocks, caches):
+                        x = block.forward_cached(x, cache, t)
+                    logits = last_logits(x)
+                else:
+                    caches = None
+                    logits = self.forward(out[:, max(0, ctx - blk):ctx]).data.t[:, -1, :]
+        return out

@@ -18,6 +18,7 @@ state_dict keys are checked against oracle.gpt.param_spec first.
 from __future__ import annotations
 
 import argparse
+import gc
 import sys
 import time
 from pathlib import Path
@@ -125,6 +126,12 @@ def train_curve(cfg: GPTConfig, seed: int, B: int, steps: int, path, full_grads_
             extra["grad_norms"] = np.array(norms)
         opt.step()
         losses.append(float(loss.data))
+        # drop this step's graph before the next forward builds one (at C2 the
+        # reference's float64 graph is ~30 GB)
+        del logits, loss
+        for p in model.parameters():
+            p.grad = None
+        gc.collect()
         print(f"  step {it:2d} loss {losses[-1]:.10f}  ({time.time() - t0:.1f}s)", flush=True)
         # saved after every step (write + rename) so a long run leaves a usable prefix
         tmp = path.with_name(path.stem + ".part.npz")
@@ -155,17 +162,40 @@ def greedy(path, seed=100, B=4, T0=8, n_new=24):
     print(f"wrote {path.name}: min top-2 margin {np.min(margins):.3e}")
 
 
+def sampling(path, seed=300, B=4, T0=8, temperature=0.8):
+    """The reference's sampling GPT.generate (transformer.py:93-104) on a
+    C0-size model, NumPy's global RNG seeded with np.random.seed: 16 new
+    tokens (the context stays within block_size = 32) and, from the same
+    state, 40 more from a fresh prompt (the context outgrows block_size, so
+    the reference crops it)."""
+    rng = np.random.default_rng(seed)
+    model = ref_model(C0, rng)
+    model.eval()
+    prompts = rng.integers(0, C0.vocab, (B, T0))
+    np.random.seed(seed)
+    with mt.no_grad():
+        short = model.generate(prompts, 16, temperature=temperature)
+        long = model.generate(prompts[:, :4], 40, temperature=temperature)
+    np.savez(path, prompts=prompts, short=short, long=long, seed=seed, temperature=temperature)
+    print(f"wrote {path.name}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--c2", action="store_true", help="also run the C2 20-step curve (slow)")
     ap.add_argument("--only-c2", action="store_true")
+    ap.add_argument("--only-sampling", action="store_true")
     args = ap.parse_args()
+    if args.only_sampling:
+        sampling(HERE / "sampling_c0.npz")
+        return
     if not args.only_c2:
         attention_subgraph(HERE / "attn_subgraph.npz")
         mha_module(HERE / "mha_module.npz")
         print("C0 training, 20 steps")
         train_curve(C0, 0, 16, 20, HERE / "c0_train.npz")
         greedy(HERE / "greedy_c0.npz")
+        sampling(HERE / "sampling_c0.npz")
     if args.c2 or args.only_c2:
         print("C2 training, 20 steps")
         train_curve(C2, 2, 64, 20, HERE / "c2_train.npz")

@@ -280,3 +280,30 @@ def test_checkpoint_resume_matches_uninterrupted(dev, tmp_path):
     assert first + rest == ref, (first + rest, ref)
     for (k, a), (_, b) in zip(m1.state_dict().items(), m3.state_dict().items()):
         assert np.array_equal(a, b), k
+
+
+def test_sampling_generate_matches_reference(dev):
+    """Sampling GPT.generate (transformer.py:93-104) vs the reference's own
+    tokens (tests/golden/sampling_c0.npz): same weights, NumPy's global RNG
+    seeded alike, temperature 0.8; 16 tokens within block_size (KV-cache
+    steps) and 40 tokens that outgrow it (cropped full forwards).  The
+    probabilities differ from the reference's float64 ones by float32
+    rounding, so a draw could only differ when the uniform lands within ~1e-7
+    of a CDF step; the fixture's draws do not."""
+    from oracle.gpt import C0, init_params
+
+    _say("[gpt] sampling generate vs reference golden")
+    g = load("sampling_c0.npz")
+    seed = int(g["seed"])
+    rng = np.random.default_rng(seed)
+    model = gpu_gpt(C0, init_params(C0, rng))
+    model.eval()
+    prompts = rng.integers(0, C0.vocab, (4, 8))
+    np.testing.assert_array_equal(prompts, g["prompts"])
+    np.random.seed(seed)
+    short = model.generate(prompts, 16, temperature=float(g["temperature"]))
+    long = model.generate(prompts[:, :4], 40, temperature=float(g["temperature"]))
+    for name, got in (("short", short), ("long", long)):
+        ref = g[name]
+        bad = np.argwhere(got != ref)
+        assert bad.size == 0, f"{name}: first mismatch at {tuple(bad[0])} ({got[tuple(bad[0])]} vs {ref[tuple(bad[0])]})"
