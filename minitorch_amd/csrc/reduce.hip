@@ -72,6 +72,7 @@ __global__ __launch_bounds__(256) void reduce_kernel(const RedArgs g) {
     const int64_t r1 = min(g.nred, r0 + g.chunk);
     if (g.nr == 1) {
       const int64_t st = g.rstr[0];
+#pragma unroll 8
       for (int64_t r = r0 + ty; r < r1; r += 4) {
         const float v = base[r * st];
         acc = is_max ? fmaxf(acc, v) : acc + v;
@@ -105,6 +106,7 @@ __global__ __launch_bounds__(256) void reduce_combine_kernel(const RedArgs g) {
   const bool is_max = g.op == MTX_RED_MAX;
   float acc = is_max ? -INFINITY : 0.f;
   if (o < g.nout) {
+#pragma unroll 8
     for (int s = ty; s < g.nsplit; s += 4) {
       const float v = g.ws[(int64_t)s * g.nout + o];
       acc = is_max ? fmaxf(acc, v) : acc + v;
@@ -119,6 +121,23 @@ __global__ __launch_bounds__(256) void reduce_combine_kernel(const RedArgs g) {
   float v = g.alpha * t;
   if (g.accumulate) v += g.out[o];
   g.out[o] = v;
+}
+
+void merge_dims(int64_t* shp, int64_t* str, int& n) {
+  int m = 0;
+  for (int d = 0; d < n; ++d) {
+    if (shp[d] == 1 && n > 1) continue;  // extent 1: contributes no offset
+    if (m > 0 && str[m - 1] == str[d] * shp[d]) {
+      shp[m - 1] *= shp[d];
+      str[m - 1] = str[d];
+    } else {
+      shp[m] = shp[d];
+      str[m] = str[d];
+      ++m;
+    }
+  }
+  if (m == 0) { shp[0] = 1; str[0] = 0; m = 1; }
+  n = m;
 }
 
 int plan_splits(int64_t nout, int64_t nred) {
@@ -161,6 +180,12 @@ extern "C" int mtx_reduce_f32(int op, int ndim, const int64_t* shape, const floa
     }
   }
   if (g.nr == 0) { g.rshape[0] = 1; g.rstr[0] = 0; g.nr = 1; }
+  // merge neighbouring dims whose strides chain (stride[i] == stride[i+1] *
+  // extent[i+1]): the row-major index order, and so the summation order, is
+  // unchanged, and a contiguous (B, T, C) -> (C) reduction takes the
+  // single-dim path without per-element index division
+  merge_dims(g.rshape, g.rstr, g.nr);
+  merge_dims(g.kshape, g.kstr, g.nk);
   g.nout = nout;
   g.nred = nred;
   int s = plan_splits(nout, nred);

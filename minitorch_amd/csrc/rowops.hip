@@ -188,6 +188,7 @@ __global__ __launch_bounds__(256) void layernorm_param_partial(const float* __re
   const int64_t r0 = (int64_t)s * chunk, r1 = min(rows, r0 + chunk);
   float ag = 0.f, ab = 0.f;
   if (c < C) {
+#pragma unroll 4
     for (int64_t r = r0 + ty; r < r1; r += 4) {
       const float g = dy[r * lddy + c];
       ag += g * ((x[r * ldx + c] - mean_in[r]) / std_in[r]);
@@ -211,6 +212,7 @@ __global__ __launch_bounds__(256) void layernorm_param_combine(const float* __re
   const int c = blockIdx.x * 64 + tx;
   float ag = 0.f, ab = 0.f;
   if (c < C) {
+#pragma unroll 8
     for (int s = ty; s < nsplit; s += 4) {
       ag += ws[((int64_t)s * 2 + 0) * C + c];
       ab += ws[((int64_t)s * 2 + 1) * C + c];

@@ -103,7 +103,9 @@ def test_ewise_broadcast_and_accumulate(dev):
 
 
 @pytest.mark.parametrize("shape,axes", [((5, 7), [0]), ((5, 7), [1]), ((3, 4, 5), [0, 1]),
-                                        ((16384, 384), [0]), ((2, 3, 4, 5), [1, 3]), ((7,), [0])])
+                                        ((16384, 384), [0]), ((2, 3, 4, 5), [1, 3]), ((7,), [0]),
+                                        ((64, 256, 384), [0, 1]), ((1, 5, 1, 7), [0, 2]),
+                                        ((3, 1, 4, 5), [0, 1, 2]), ((4, 6, 8), [0, 2])])
 def test_reduce_sum(dev, shape, axes):
     import torch
     from minitorch_amd import kernels as Kn
@@ -117,6 +119,27 @@ def test_reduce_sum(dev, shape, axes):
     ref = 0.5 * a.astype(np.float64).sum(axis=tuple(axes))
     R = int(np.prod([shape[i] for i in axes]))
     close(H(out).reshape(np.shape(ref)), ref, atol=dot_tol(R), name="reduce")
+
+
+def test_reduce_merged_dims_bit_identical(dev):
+    """Reducing (B, T, C) over (B, T) merges the two reduced dims into one of
+    B*T rows; the result must be bit-identical to reducing the (B*T, C) view,
+    and a transposed (non-mergeable) input must still match float64."""
+    from minitorch_amd import kernels as Kn
+    import torch
+
+    rng = np.random.default_rng(9)
+    a = rng.standard_normal((64, 256, 384), dtype=np.float32)
+    ta = T(a)
+    o3 = torch.empty(384, device="cuda")
+    o2 = torch.empty(384, device="cuda")
+    Kn.reduce(ta, [0, 1], o3)
+    Kn.reduce(ta.reshape(64 * 256, 384), [0], o2)
+    assert np.array_equal(H(o3), H(o2))
+    tt = ta.transpose(0, 2)  # (384, 256, 64), strides (1, 384, 98304)
+    ot = torch.empty(256, device="cuda")
+    Kn.reduce(tt, [0, 2], ot)
+    close(H(ot), a.astype(np.float64).sum(axis=(0, 2)), atol=dot_tol(64 * 384), name="reduce-strided")
 
 
 @pytest.mark.parametrize("rows,L,causal", [(3, 5, 0), (64, 65, 0), (40, 256, 256), (8, 1000, 0)])
