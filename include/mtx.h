@@ -199,6 +199,24 @@ int mtx_gemm_f32(int M, int N, int K, int batch,
                  float beta, float* c, int64_t sc_m, int64_t sc_n, int64_t sc_b,
                  const float* bias, void* workspace, size_t workspace_bytes, void* stream);
 
+/* One decode-step projection in a single launch (no workspace):
+ *   P = A @ B + bias, A (M, K) row stride lda (unit k stride), B (K, N) row
+ *   stride ldb (unit n stride), M <= 64 rows, K <= 512;
+ *   columns [0, ncols_c) of P:  C = act(P + beta * C), act 0 = none,
+ *                               1 = GELU (tanh form, functional.py:54-59);
+ *   columns [ncols_c, N):       the first half to kcache, the second to
+ *                               vcache, at row lengths[m] - 1 of sequence m
+ *                               (rows outside [0, T) are skipped).
+ * Replaces, in GPT.generate's per-token forward (transformer.py:93-104), the
+ * fused q/k/v projection (transformer.py:32-34, layers.py:31-37) plus the
+ * two cache writes, and Linear + GELU of the MLP (transformer.py:56-58).
+ * MTX_ERR_SHAPE outside the size limits (callers then use mtx_gemm_f32,
+ * mtx_kv_append_f32 and mtx_gelu_fwd_f32). */
+int mtx_gemm_step_f32(int M, int N, int K, const float* a, int64_t lda, const float* b, int64_t ldb,
+                      float beta, float* c, int64_t ldc, const float* bias, int act, int ncols_c,
+                      float* kcache, float* vcache, int64_t cache_stride_b, int64_t cache_stride_t,
+                      int T, const int* lengths, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Elementwise and reductions                                               */
 /* ------------------------------------------------------------------------ */

@@ -61,6 +61,8 @@ SIGNATURES = {
     "mtx_kv_append_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _P]),
     "mtx_decode_advance": (_I, [_I, _P, _P, _P]),
     "mtx_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "mtx_gemm_step_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _F, _P, _I64, _P, _I, _I,
+                               _P, _P, _I64, _I64, _I, _P, _P]),
     "mtx_gemm_f32": (_I, [_I, _I, _I, _I,
                           _F, _P, _I64, _I64, _I64,
                           _P, _I64, _I64, _I64,

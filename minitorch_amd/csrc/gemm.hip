@@ -35,6 +35,16 @@ struct GemmArgs {
   int M, N, K, batch;
   int ksplit, kchunk; // K range of split s: [s*kchunk, min(K, (s+1)*kchunk))
   float alpha, beta;
+  // decode-step epilogue (skinny kernel only): act 1 = GELU (tanh form) on
+  // the C columns; product columns [nc, N) go to the KV caches instead of C:
+  // the first half to kc, the second to vc, at row lengths[m] - 1 of
+  // sequence m (row stride cst, sequence stride csb, T rows)
+  int act, nc;
+  float* kc;
+  float* vc;
+  int64_t csb, cst;
+  int cT;
+  const int* lengths;
 };
 
 template <int BM, int BN, bool AK, bool BN1>
@@ -250,6 +260,128 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny products: M <= 64 rows (a decode step's sequences), K <= 512.
+// One workgroup of 16 waves owns 16 output columns for every row; the waves
+// split K into 16-wide slices dealt round-robin, and their partial tiles are
+// summed through LDS in wave order (deterministic, one launch, no split-K
+// workspace).  Within a slice the lane of group grp supplies, to the four
+// MFMA steps s = 0..3, k = 4*grp + s for both A and B (the same k on both
+// sides, so each MFMA contracts over four distinct k and the four steps
+// cover the slice); A's four values are then one 16-byte load when A is
+// contiguous along k.  Each wave loads kSkG slices before multiplying them
+// (one when A needs scalar loads).
+// ---------------------------------------------------------------------------
+#ifndef MTX_SKINNY_WAVES
+#define MTX_SKINNY_WAVES 16
+#endif
+#ifndef MTX_SKINNY_INFLIGHT
+#define MTX_SKINNY_INFLIGHT 1
+#endif
+constexpr int kSkW = MTX_SKINNY_WAVES;     // waves per workgroup
+constexpr int kSkT = kSkW * 64;            // threads per workgroup
+constexpr int kSkG = MTX_SKINNY_INFLIGHT;  // slices in flight per wave
+// every workgroup reads all of A (M x K) through its CU, so long K is left to
+// split-K over more workgroups (measured at M = 64: K = 384 5.9 us against
+// 8.9 us for split-K + reduce; K = 1536 16 us either way)
+constexpr int kSkMaxM = 64, kSkMaxK = 512;
+
+// four values at k..k+3 along a dimension of stride sk; V: the host has
+// checked that the operand is contiguous along k, 16-byte aligned at every
+// k multiple of 4, and K % 4 == 0, so a k group is either whole or past K
+template <bool V>
+__device__ __forceinline__ f32x4 load4_k(const float* __restrict__ p, int64_t sk, int k, int K, bool ok) {
+  f32x4 x = zero4();
+  if constexpr (V) {
+    if (ok && k < K) x = *reinterpret_cast<const f32x4*>(p);
+  } else {
+    if (ok) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (k + j < K) x[j] = p[(int64_t)j * sk];
+    }
+  }
+  return x;
+}
+
+template <bool AV, bool BV>
+__global__ __launch_bounds__(kSkT) void gemm_skinny_kernel(const GemmArgs g) {
+  __shared__ float red[kSkW][kSkMaxM * 16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int n16 = lane & 15, grp = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int bidx = blockIdx.y;
+  const int n = n0 + n16;
+  const bool nok = n < g.N;
+  const int nsl = (g.K + 15) / 16;
+  // lane bases: row 16i + n16 of A (i = 0..3 by a row offset of 16 rows),
+  // column n of B, both at k = 4 * grp
+  const float* __restrict__ Ab = g.a + (int64_t)bidx * g.sab + (int64_t)n16 * g.sam + (int64_t)(4 * grp) * g.sak;
+  const float* __restrict__ Bb = g.b + (int64_t)bidx * g.sbb + (int64_t)n * g.sbn + (int64_t)(4 * grp) * g.sbk;
+  const int64_t a16 = 16 * g.sam;
+  // slices in flight: A with four scalar loads per group needs the registers
+  constexpr int G = AV ? kSkG : 1;
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = zero4();
+  for (int s0 = wid; s0 < nsl; s0 += G * kSkW) {
+    f32x4 af[G][4], bf[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const int kb = (s0 + j * kSkW) * 16;  // past K after the last slice: zeros
+      const int k = kb + 4 * grp;
+      const float* pa = Ab + (int64_t)kb * g.sak;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[j][i] = load4_k<AV>(pa + i * a16, g.sak, k, g.K, 16 * i + n16 < g.M);
+      bf[j] = load4_k<BV>(Bb + (int64_t)kb * g.sbk, g.sbk, k, g.K, nok);
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[j][i][s], bf[j][s], acc[i], 0, 0, 0);
+  }
+  // acc[i][r] = partial C[16i + 4grp + r][n16]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wid][(16 * i + 4 * grp + r) * 16 + n16] = acc[i][r];
+  __syncthreads();
+#pragma unroll
+  for (int e = tid; e < kSkMaxM * 16; e += kSkT) {
+    const int row = e >> 4, col = n0 + (e & 15);
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSkW; ++w) v += red[w][e];
+    if (row < g.M && col < g.N) {
+      float o = g.alpha * v + (g.bias ? g.bias[col] : 0.f);
+      if (col < g.nc) {
+        float* p = g.c + (int64_t)bidx * g.scb + (int64_t)row * g.scm + (int64_t)col * g.scn;
+        if (g.beta != 0.f) o += g.beta * *p;
+        if (g.act == 1) o = gelu_tanh(o);
+        *p = o;
+      } else {
+        const int half = (g.N - g.nc) >> 1;
+        const int j = col - g.nc;
+        float* cache = j < half ? g.kc : g.vc;
+        const int jj = j < half ? j : j - half;
+        const int t = g.lengths[row] - 1;
+        if (t >= 0 && t < g.cT) cache[(int64_t)row * g.csb + (int64_t)t * g.cst + jj] = o;
+      }
+    }
+  }
+}
+
+// operand contiguous along k with every 4-aligned k group 16-byte aligned
+bool k_vec(const float* p, int64_t s_row, int64_t s_k, int64_t s_batch, int K) {
+  return s_k == 1 && K % 4 == 0 && (((uintptr_t)p) & 15u) == 0 && s_row % 4 == 0 && s_batch % 4 == 0;
+}
+
+bool use_skinny(int M, int K) { return M <= kSkMaxM && K <= kSkMaxK; }
+
 // Sum the split-K partials in split order; apply alpha, beta, bias.
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const GemmArgs g) {
   const int64_t MN = (int64_t)g.M * g.N;
@@ -322,6 +454,7 @@ using namespace mtx;
 
 extern "C" size_t mtx_gemm_workspace_bytes(int M, int N, int K, int batch) {
   if (M < 1 || N < 1 || K < 1 || batch < 1) return 0;
+  if (use_skinny(M, K)) return 0;
   Plan p = plan_gemm(M, N, K, batch, (size_t)-1);
   return p.ksplit > 1 ? (size_t)p.ksplit * batch * (size_t)M * N * sizeof(float) : 0;
 }
@@ -342,11 +475,23 @@ extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
   MTX_CHECK_SHAPE((int64_t)batch * cdiv(M, 64) < 65535 * 64, "gemm: too many tiles");
   GemmArgs g{a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, c, sc_m, sc_n, sc_b, bias,
              static_cast<float*>(workspace), M, N, K, batch, 1, K, alpha, beta};
+  g.nc = N;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (K == 0) {  // C = beta*C + bias
     g.ksplit = 1;
     g.kchunk = 0;
     return launch_tile<64, 64>(g, true, true, st);
+  }
+  if (use_skinny(M, K)) {
+    MTX_CHECK_SHAPE(batch < 65536, "gemm: batch too large");
+    const bool av = k_vec(a, sa_m, sa_k, sa_b, K), bv = k_vec(b, sb_n, sb_k, sb_b, K);
+    const dim3 grid(cdiv(N, 16), batch);
+    if (av && bv) hipLaunchKernelGGL((gemm_skinny_kernel<true, true>), grid, dim3(kSkT), 0, st, g);
+    else if (av) hipLaunchKernelGGL((gemm_skinny_kernel<true, false>), grid, dim3(kSkT), 0, st, g);
+    else if (bv) hipLaunchKernelGGL((gemm_skinny_kernel<false, true>), grid, dim3(kSkT), 0, st, g);
+    else hipLaunchKernelGGL((gemm_skinny_kernel<false, false>), grid, dim3(kSkT), 0, st, g);
+    MTX_LAUNCHED();
+    return MTX_OK;
   }
   Plan p = plan_gemm(M, N, K, batch, workspace ? workspace_bytes : 0);
   g.ksplit = p.ksplit;
@@ -360,5 +505,40 @@ extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
     hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(256), 0, st, g);
     MTX_LAUNCHED();
   }
+  return MTX_OK;
+}
+
+extern "C" int mtx_gemm_step_f32(int M, int N, int K, const float* a, int64_t lda, const float* b, int64_t ldb,
+                                 float beta, float* c, int64_t ldc, const float* bias, int act, int ncols_c,
+                                 float* kcache, float* vcache, int64_t cache_stride_b, int64_t cache_stride_t,
+                                 int T, const int* lengths, void* stream) {
+  MTX_CHECK_SHAPE(M >= 1 && N >= 1 && K >= 1, "gemm_step: sizes must be >= 1");
+  MTX_CHECK_SHAPE(use_skinny(M, K), "gemm_step: needs M <= %d and K <= %d (got M=%d, K=%d)", kSkMaxM, kSkMaxK,
+                  M, K);
+  MTX_CHECK_ARG(a && b && (ncols_c == 0 || c), "gemm_step: null operand");
+  MTX_CHECK_ARG(act == 0 || act == 1, "gemm_step: act must be 0 (none) or 1 (gelu)");
+  MTX_CHECK_ARG(ncols_c >= 0 && ncols_c <= N, "gemm_step: ncols_c %d not in [0, N=%d]", ncols_c, N);
+  MTX_CHECK_ARG(lda >= K && ldb >= N && (ncols_c == 0 || ldc >= ncols_c), "gemm_step: row strides too small");
+  if (ncols_c < N) {
+    MTX_CHECK_ARG((N - ncols_c) % 2 == 0, "gemm_step: the cache columns must split evenly into k and v");
+    MTX_CHECK_ARG(kcache && vcache && lengths, "gemm_step: null cache or lengths");
+    MTX_CHECK_ARG(T >= 1 && cache_stride_t >= (N - ncols_c) / 2 && cache_stride_b >= (int64_t)T * cache_stride_t,
+                  "gemm_step: cache strides do not hold (B, T, C) rows");
+  }
+  GemmArgs g{a, lda, 1, 0, b, ldb, 1, 0, c, ldc, 1, 0, bias, nullptr, M, N, K, 1, 1, K, 1.f, beta};
+  g.act = act;
+  g.nc = ncols_c;
+  g.kc = kcache;
+  g.vc = vcache;
+  g.csb = cache_stride_b;
+  g.cst = cache_stride_t;
+  g.cT = T;
+  g.lengths = lengths;
+  const bool av = k_vec(a, lda, 1, 0, K);
+  const dim3 grid(cdiv(N, 16), 1);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (av) hipLaunchKernelGGL((gemm_skinny_kernel<true, false>), grid, dim3(kSkT), 0, st, g);
+  else hipLaunchKernelGGL((gemm_skinny_kernel<false, false>), grid, dim3(kSkT), 0, st, g);
+  MTX_LAUNCHED();
   return MTX_OK;
 }

@@ -42,6 +42,19 @@ int fail(int code, const char* fmt, ...);
   } while (0)
 
 // ---------------------------------------------------------------------------
+// GELU, tanh form with the reference's float32 constants
+// (functional.py:54-59: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))));
+// shared by the elementwise kernel and the GEMM epilogue so both compute the
+// same expression
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float gelu_c0() { return 0.7978845834732056f; }  // float32(sqrt(2/pi))
+__device__ __forceinline__ float gelu_c1() { return 0.044714998453855515f; }  // float32(0.044715)
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
+  return v * 0.5f * (tanhf(inner) + 1.0f);
+}
+
+// ---------------------------------------------------------------------------
 // vector types
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));

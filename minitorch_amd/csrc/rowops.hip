@@ -230,15 +230,10 @@ __global__ __launch_bounds__(256) void layernorm_param_combine(const float* __re
   }
 }
 
-// GELU, tanh form with the reference's float32 constants
-__device__ __forceinline__ float gelu_c0() { return 0.7978845834732056f; }  // float32(sqrt(2/pi))
-__device__ __forceinline__ float gelu_c1() { return 0.044714998453855515f; }  // float32(0.044715)
 
 __global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const float v = x[i];
-    const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
-    y[i] = v * 0.5f * (tanhf(inner) + 1.0f);
+    y[i] = gelu_tanh(x[i]);
   }
 }
 

@@ -264,6 +264,50 @@ def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=
     return c
 
 
+# size limits of mtx_gemm_step_f32 (one-launch decode-step projections)
+STEP_MAX_M, STEP_MAX_K = 64, 512
+ACT_NONE, ACT_GELU = 0, 1
+
+
+def step_fits(M, K):
+    """True when mtx_gemm_step_f32 takes an (M, K) activation."""
+    return 1 <= M <= STEP_MAX_M and 1 <= K <= STEP_MAX_K
+
+
+def gemm_step(a, b, bias=None, c=None, beta=0.0, act=ACT_NONE, kv=None):
+    """One decode-step projection: P = a @ b + bias, a (M, K) with unit k
+    stride, b (K, N) with unit n stride.  Columns of P go to c (M, Nc) as
+    act(P + beta*c); with kv = (kcache, vcache, lengths) the last 2*Ck columns
+    go to the caches (B, T, Ck) at row lengths[m] - 1 instead (Nc = N - 2*Ck)."""
+    M, Kd = a.shape
+    N = b.shape[1]
+    if a.stride(1) != 1 or b.stride(1) != 1 or b.shape[0] != Kd:
+        raise ValueError("gemm_step: a (M, K) and b (K, N) need unit inner strides")
+    if kv is not None:
+        kc, vc, lengths = kv
+        _need_cuda(kc, vc, lengths)
+        Bc, T, Ck = kc.shape
+        if vc.shape != kc.shape or vc.stride() != kc.stride() or kc.stride(2) != 1 or Bc < M:
+            raise ValueError("gemm_step: k/v caches must be (B >= M, T, C) with equal strides")
+        if lengths.dtype != torch.int32 or lengths.numel() < M:
+            raise ValueError("gemm_step: lengths must be int32 with >= M entries")
+        nc = N - 2 * Ck
+        cache_args = (L.ptr(kc), L.ptr(vc), kc.stride(0), kc.stride(1), T, L.ptr(lengths))
+    else:
+        nc = N
+        cache_args = (None, None, 0, 0, 0, None)
+    if nc < 0:
+        raise ValueError("gemm_step: N too small for the cache columns")
+    if nc > 0:
+        if c is None or c.shape != (M, nc) or c.stride(1) != 1:
+            raise ValueError(f"gemm_step: c must be ({M}, {nc}) with unit column stride")
+    L.call("mtx_gemm_step_f32", int(M), int(N), int(Kd), L.ptr(a), a.stride(0), L.ptr(b), b.stride(0),
+           float(beta), L.ptr(c) if nc > 0 else None, c.stride(0) if nc > 0 else 0,
+           L.ptr(bias) if bias is not None else None, int(act), int(nc), *cache_args,
+           L.stream_handle(a.device))
+    return c
+
+
 # ---------------------------------------------------------------------------
 # row kernels
 # ---------------------------------------------------------------------------

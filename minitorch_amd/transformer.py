@@ -89,7 +89,8 @@ class MultiHeadAttention(Module):
     def forward_step(self, x, cache, lengths, residual=None):
         """One-token decode step whose positions live in device memory, so a
         recorded step replays unchanged: x (B, 1, C); this token's key/value
-        go to cache row lengths[b] - 1 (mtx_kv_append_f32) and attention runs
+        go to cache row lengths[b] - 1 (written by the q/k/v GEMM itself,
+        mtx_gemm_step_f32, or by mtx_kv_append_f32 past its size limits) and attention runs
         over each sequence's first lengths[b] cached keys (mtx_attn_decode).
         With `residual` (B, 1, C) the output projection is accumulated into it
         in place (the block's residual add folded into the GEMM) and it is
@@ -101,11 +102,18 @@ class MultiHeadAttention(Module):
         H, D = self.n_head, self.head_dim
         if self._qkv is None:
             self.fuse_qkv()
-        qkv = F.linear(x, *self._qkv).data.t  # (B, 1, 3C): [q | k | v]
-        q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
         kc, vc = cache
-        K.kv_append(k, kc.t, lengths)
-        K.kv_append(v, vc.t, lengths)
+        if K.step_fits(B, C):
+            # one launch: q to its buffer, k and v straight into the caches
+            q = dev.empty((B, 1, C)).t
+            W, b = self._qkv
+            K.gemm_step(x.data.t.reshape(B, C), W.data.t, bias=b.data.t, c=q.view(B, C),
+                        kv=(kc.t, vc.t, lengths))
+        else:
+            qkv = F.linear(x, *self._qkv).data.t  # (B, 1, 3C): [q | k | v]
+            q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
+            K.kv_append(k, kc.t, lengths)
+            K.kv_append(v, vc.t, lengths)
         heads = lambda t: t.view(t.shape[0], t.shape[1], H, D).transpose(1, 2) if t.is_contiguous() \
             else t.unflatten(2, (H, D)).transpose(1, 2)
         out = dev.empty((B, 1, H, D))
@@ -155,8 +163,18 @@ class TransformerBlock(Module):
         fc1, act, fc2, drop = self.mlp.layers
         if drop._training and drop.p > 0.0:
             raise NotImplementedError("decode steps run without dropout (use model.eval() or p = 0)")
+        from . import kernels as K
+
         self.attn.forward_step(self.ln1(x), cache, lengths, residual=x)
-        return _linear_into(act(fc1(self.ln2(x))), fc2, x)
+        B, _, C = x.shape
+        h_in = self.ln2(x)
+        if K.step_fits(B, C) and isinstance(act, GELU):
+            # fc1 with its GELU in one launch
+            h = dev.empty((B, 1, fc1.weight.shape[1]))
+            K.gemm_step(h_in.data.t.reshape(B, C), fc1.weight.data.t, bias=fc1.bias.data.t,
+                        c=h.t.view(B, -1), act=K.ACT_GELU)
+            return _linear_into(Tensor(h), fc2, x)
+        return _linear_into(act(fc1(h_in)), fc2, x)
 
 
 class GPT(Module):

@@ -137,3 +137,33 @@ def test_argmax_rejects_bad_arguments():
     assert "ld" in L.lib().mtx_last_error().decode()
     assert L.lib().mtx_argmax_f32(0, 65, p, 65, p, 1, None, 0, None) == L.MTX_ERR_SHAPE
     assert L.lib().mtx_argmax_f32(4, 65, None, 65, p, 1, None, 0, None) == L.MTX_ERR_ARG
+
+
+def _step(**over):
+    a = dict(M=64, N=1152, K=384, a=16, lda=384, b=16, ldb=1152, c=16, ldc=384, act=0, nc=384,
+             kc=16, vc=16, sb=256 * 384, st=384, T=256, lengths=16)
+    a.update(over)
+    p = lambda x: C.c_void_p(x) if x else None
+    return L.lib().mtx_gemm_step_f32(a["M"], a["N"], a["K"], p(a["a"]), a["lda"], p(a["b"]), a["ldb"], 0.0,
+                                     p(a["c"]), a["ldc"], None, a["act"], a["nc"], p(a["kc"]), p(a["vc"]),
+                                     a["sb"], a["st"], a["T"], p(a["lengths"]), None)
+
+
+@pytest.mark.parametrize("over,code,frag", [
+    (dict(M=65), L.MTX_ERR_SHAPE, "M <= 64"),
+    (dict(K=513, lda=513), L.MTX_ERR_SHAPE, "K <= 512"),
+    (dict(M=0), L.MTX_ERR_SHAPE, ">= 1"),
+    (dict(act=2), L.MTX_ERR_ARG, "act"),
+    (dict(nc=1153), L.MTX_ERR_ARG, "ncols_c"),
+    (dict(nc=385, ldc=385), L.MTX_ERR_ARG, "evenly"),
+    (dict(kc=0), L.MTX_ERR_ARG, "null cache"),
+    (dict(lengths=0), L.MTX_ERR_ARG, "null cache"),
+    (dict(st=100), L.MTX_ERR_ARG, "cache strides"),
+    (dict(lda=100), L.MTX_ERR_ARG, "row strides"),
+    (dict(a=0), L.MTX_ERR_ARG, "null operand"),
+])
+def test_gemm_step_rejects_bad_arguments(over, code, frag):
+    """Every rejection returns before any launch (no GPU needed)."""
+    rc = _step(**over)
+    assert rc == code
+    assert frag in L.lib().mtx_last_error().decode()

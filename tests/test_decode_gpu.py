@@ -134,3 +134,65 @@ def test_argmax_matches_numpy(dev):
         np.testing.assert_array_equal(idx.cpu().numpy(), np.argmax(x, axis=1))
         top2 = np.sort(x, axis=1)[:, -2:]
         np.testing.assert_array_equal(margin.cpu().numpy(), top2[:, 1] - top2[:, 0])
+
+
+def _gelu64(x):
+    c0, c1 = np.float64(np.float32(np.sqrt(2 / np.pi))), np.float64(np.float32(0.044715))
+    return 0.5 * x * (1.0 + np.tanh(c0 * (x + c1 * x ** 3)))
+
+
+@pytest.mark.parametrize("M,K,N,act,beta", [(64, 384, 1536, 1, 0.0), (37, 384, 384, 0, 1.0),
+                                            (5, 100, 70, 1, 0.5), (64, 512, 16, 0, 0.0)])
+def test_gemm_step_matches_float64(dev, M, K, N, act, beta):
+    """mtx_gemm_step_f32 without cache columns: C = act(A @ B + bias + beta*C)."""
+    import torch
+    from minitorch_amd import kernels as Kn
+
+    _say(f"[gemm_step] M={M} K={K} N={N} act={act} beta={beta}")
+    rng = np.random.default_rng(M + K + N)
+    a = rng.standard_normal((M, K), dtype=np.float32)
+    b = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    bias = rng.standard_normal(N, dtype=np.float32)
+    c0 = rng.standard_normal((M, N), dtype=np.float32)
+    ta, tb, tbias, tc = (torch.from_numpy(x).cuda() for x in (a, b, bias, c0))
+    Kn.gemm_step(ta, tb, bias=tbias, c=tc, beta=beta, act=act)
+    ref = a.astype(np.float64) @ b + bias + beta * c0
+    if act:
+        ref = _gelu64(ref)
+    got = tc.cpu().numpy()
+    err = np.abs(got - ref)
+    assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), f"max err {err.max():.3e}"
+
+
+def test_gemm_step_writes_kv_cache_rows(dev):
+    """The q/k/v step projection: q columns to c, k and v columns to cache row
+    lengths[m] - 1; rows of sequences with lengths 0 or past T untouched."""
+    import torch
+    from minitorch_amd import kernels as Kn
+
+    _say("[gemm_step] kv scatter")
+    rng = np.random.default_rng(77)
+    B, C, T = 64, 384, 40
+    a = rng.standard_normal((B, C), dtype=np.float32)
+    w = (0.05 * rng.standard_normal((C, 3 * C))).astype(np.float32)
+    bias = rng.standard_normal(3 * C, dtype=np.float32)
+    lengths = rng.integers(1, T + 1, B).astype(np.int32)
+    lengths[3], lengths[10] = 0, T + 1  # skipped
+    kc0 = rng.standard_normal((B, T, C), dtype=np.float32)
+    vc0 = rng.standard_normal((B, T, C), dtype=np.float32)
+    ta, tw, tb = (torch.from_numpy(x).cuda() for x in (a, w, bias))
+    tk, tv, tl = torch.from_numpy(kc0.copy()).cuda(), torch.from_numpy(vc0.copy()).cuda(), torch.from_numpy(lengths).cuda()
+    q = torch.empty(B, C, device="cuda")
+    Kn.gemm_step(ta, tw, bias=tb, c=q, kv=(tk, tv, tl))
+    P = a.astype(np.float64) @ w + bias
+    tol = lambda r: 1e-5 + 1e-4 * np.abs(r)
+    assert np.all(np.abs(q.cpu().numpy() - P[:, :C]) <= tol(P[:, :C]))
+    kg, vg = tk.cpu().numpy(), tv.cpu().numpy()
+    kref, vref = kc0.copy(), vc0.copy()
+    for m in range(B):
+        t = lengths[m] - 1
+        if 0 <= t < T:
+            assert np.all(np.abs(kg[m, t] - P[m, C:2 * C]) <= tol(P[m, C:2 * C])), m
+            assert np.all(np.abs(vg[m, t] - P[m, 2 * C:]) <= tol(P[m, 2 * C:])), m
+            kref[m, t], vref[m, t] = kg[m, t], vg[m, t]
+    assert np.array_equal(kg, kref) and np.array_equal(vg, vref), "rows other than lengths-1 changed"

@@ -54,6 +54,12 @@ def dot_tol(K):
     (256, 65, 384, False, False, 1, True),
     (384, 1536, 4096, True, False, 1, False),   # weight-gradient shape: split-K path
     (33, 17, 2000, True, True, 2, False),
+    # M <= 64 rows (decode steps): the one-launch skinny kernel
+    (64, 1152, 384, False, False, 1, True),
+    (64, 384, 512, False, False, 1, True),
+    (64, 65, 384, False, False, 1, True),
+    (50, 100, 500, True, True, 2, False),
+    (64, 384, 1536, False, False, 1, True),     # K past the skinny limit: split-K
 ])
 def test_gemm(dev, M, N, K, ta, tb, batch, bias):
     import torch
