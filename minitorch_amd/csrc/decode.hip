@@ -85,17 +85,6 @@ __device__ __forceinline__ void store1(T* p, float x) {
   else *p = f2bf(x);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-
 template <typename T, int D>
 __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecArgs a) {
   extern __shared__ float smem[];  // [L] scores, then reduction scratch

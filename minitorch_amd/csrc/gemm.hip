@@ -261,7 +261,8 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// Skinny products: M <= 64 rows (a decode step's sequences), K <= 512.
+// Skinny products: M <= 64 rows (a decode step's sequences), K <= 4096 (in
+// up to 8 ranges of 512, one workgroup each, when longer than 512).
 // One workgroup of 16 waves owns 16 output columns for every row; the waves
 // split K into 16-wide slices dealt round-robin, and their partial tiles are
 // summed through LDS in wave order (deterministic, one launch, no split-K
@@ -281,10 +282,12 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
 constexpr int kSkW = MTX_SKINNY_WAVES;     // waves per workgroup
 constexpr int kSkT = kSkW * 64;            // threads per workgroup
 constexpr int kSkG = MTX_SKINNY_INFLIGHT;  // slices in flight per wave
-// every workgroup reads all of A (M x K) through its CU, so long K is left to
-// split-K over more workgroups (measured at M = 64: K = 384 5.9 us against
-// 8.9 us for split-K + reduce; K = 1536 16 us either way)
-constexpr int kSkMaxM = 64, kSkMaxK = 512;
+// every workgroup reads all of its K range of A (M x K) through its CU, so a
+// longer K is split over workgroups of at most kSkMaxK each (grid.z), whose
+// partial tiles gemm_splitk_reduce sums in split order (measured at M = 64:
+// K = 384 one launch 5.9 us against 8.9 us for tiled split-K + reduce;
+// K = 1536 unsplit 16 us)
+constexpr int kSkMaxM = 64, kSkMaxK = 512, kSkMaxSplit = 8;
 
 // four values at k..k+3 along a dimension of stride sk; V: the host has
 // checked that the operand is contiguous along k, 16-byte aligned at every
@@ -312,9 +315,12 @@ __global__ __launch_bounds__(kSkT) void gemm_skinny_kernel(const GemmArgs g) {
   const int n16 = lane & 15, grp = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int bidx = blockIdx.y;
+  const int split = blockIdx.z;
   const int n = n0 + n16;
   const bool nok = n < g.N;
-  const int nsl = (g.K + 15) / 16;
+  // this workgroup's 16-wide k slices (kchunk is a multiple of 16)
+  const int sbeg = split * (g.kchunk / 16);
+  const int nsl = min((g.K + 15) / 16, sbeg + g.kchunk / 16);
   // lane bases: row 16i + n16 of A (i = 0..3 by a row offset of 16 rows),
   // column n of B, both at k = 4 * grp
   const float* __restrict__ Ab = g.a + (int64_t)bidx * g.sab + (int64_t)n16 * g.sam + (int64_t)(4 * grp) * g.sak;
@@ -326,11 +332,15 @@ __global__ __launch_bounds__(kSkT) void gemm_skinny_kernel(const GemmArgs g) {
   f32x4 acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = zero4();
-  for (int s0 = wid; s0 < nsl; s0 += G * kSkW) {
+  for (int s0 = sbeg + wid; s0 < nsl; s0 += G * kSkW) {
     f32x4 af[G][4], bf[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       const int kb = (s0 + j * kSkW) * 16;  // past K after the last slice: zeros
+      if (G > 1 && s0 + j * kSkW >= nsl) {       // past this split's range
+        af[j][0] = af[j][1] = af[j][2] = af[j][3] = bf[j] = zero4();
+        continue;
+      }
       const int k = kb + 4 * grp;
       const float* pa = Ab + (int64_t)kb * g.sak;
 #pragma unroll
@@ -356,7 +366,9 @@ __global__ __launch_bounds__(kSkT) void gemm_skinny_kernel(const GemmArgs g) {
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < kSkW; ++w) v += red[w][e];
-    if (row < g.M && col < g.N) {
+    if (row < g.M && col < g.N && g.ksplit > 1) {
+      g.ws[((int64_t)split * g.batch + bidx) * g.M * g.N + (int64_t)row * g.N + col] = v;
+    } else if (row < g.M && col < g.N) {
       float o = g.alpha * v + (g.bias ? g.bias[col] : 0.f);
       if (col < g.nc) {
         float* p = g.c + (int64_t)bidx * g.scb + (int64_t)row * g.scm + (int64_t)col * g.scn;
@@ -381,6 +393,11 @@ bool k_vec(const float* p, int64_t s_row, int64_t s_k, int64_t s_batch, int K) {
 }
 
 bool use_skinny(int M, int K) { return M <= kSkMaxM && K <= kSkMaxK; }
+// K splits of the skinny kernel for an M x K activation, 0 when it does not apply
+int skinny_splits(int M, int K) {
+  if (M > kSkMaxM || K > kSkMaxK * kSkMaxSplit) return 0;
+  return cdiv(K, kSkMaxK);
+}
 
 // Sum the split-K partials in split order; apply alpha, beta, bias.
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const GemmArgs g) {
@@ -454,7 +471,7 @@ using namespace mtx;
 
 extern "C" size_t mtx_gemm_workspace_bytes(int M, int N, int K, int batch) {
   if (M < 1 || N < 1 || K < 1 || batch < 1) return 0;
-  if (use_skinny(M, K)) return 0;
+  if (const int sp = skinny_splits(M, K)) return sp > 1 ? (size_t)sp * batch * (size_t)M * N * sizeof(float) : 0;
   Plan p = plan_gemm(M, N, K, batch, (size_t)-1);
   return p.ksplit > 1 ? (size_t)p.ksplit * batch * (size_t)M * N * sizeof(float) : 0;
 }
@@ -482,15 +499,25 @@ extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
     g.kchunk = 0;
     return launch_tile<64, 64>(g, true, true, st);
   }
-  if (use_skinny(M, K)) {
+  if (int sp = skinny_splits(M, K)) {
     MTX_CHECK_SHAPE(batch < 65536, "gemm: batch too large");
+    // without room for the partials, one workgroup covers all of K
+    if (sp > 1 && (!workspace || workspace_bytes < (size_t)sp * batch * (size_t)M * N * sizeof(float))) sp = 1;
+    g.ksplit = sp;
+    g.kchunk = sp > 1 ? kSkMaxK : cdiv(K, 16) * 16;
     const bool av = k_vec(a, sa_m, sa_k, sa_b, K), bv = k_vec(b, sb_n, sb_k, sb_b, K);
-    const dim3 grid(cdiv(N, 16), batch);
+    const dim3 grid(cdiv(N, 16), batch, sp);
     if (av && bv) hipLaunchKernelGGL((gemm_skinny_kernel<true, true>), grid, dim3(kSkT), 0, st, g);
     else if (av) hipLaunchKernelGGL((gemm_skinny_kernel<true, false>), grid, dim3(kSkT), 0, st, g);
     else if (bv) hipLaunchKernelGGL((gemm_skinny_kernel<false, true>), grid, dim3(kSkT), 0, st, g);
     else hipLaunchKernelGGL((gemm_skinny_kernel<false, false>), grid, dim3(kSkT), 0, st, g);
     MTX_LAUNCHED();
+    if (sp > 1) {
+      const int64_t total = (int64_t)M * N * batch;
+      const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
+      hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(256), 0, st, g);
+      MTX_LAUNCHED();
+    }
     return MTX_OK;
   }
   Plan p = plan_gemm(M, N, K, batch, workspace ? workspace_bytes : 0);
@@ -525,7 +552,7 @@ extern "C" int mtx_gemm_step_f32(int M, int N, int K, const float* a, int64_t ld
     MTX_CHECK_ARG(T >= 1 && cache_stride_t >= (N - ncols_c) / 2 && cache_stride_b >= (int64_t)T * cache_stride_t,
                   "gemm_step: cache strides do not hold (B, T, C) rows");
   }
-  GemmArgs g{a, lda, 1, 0, b, ldb, 1, 0, c, ldc, 1, 0, bias, nullptr, M, N, K, 1, 1, K, 1.f, beta};
+  GemmArgs g{a, lda, 1, 0, b, ldb, 1, 0, c, ldc, 1, 0, bias, nullptr, M, N, K, 1, 1, cdiv(K, 16) * 16, 1.f, beta};
   g.act = act;
   g.nc = ncols_c;
   g.kc = kcache;

@@ -55,6 +55,21 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 }
 
 // ---------------------------------------------------------------------------
+// wave64 reductions (butterfly over lane xor 32, 16, ..., 1: every lane gets
+// the same bits)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
 // vector types
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));

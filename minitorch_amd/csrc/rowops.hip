@@ -16,17 +16,6 @@
 namespace mtx {
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
-}
-
 // visible(j) for causal rows: row r of a stack of (Tq, L) matrices
 __device__ __forceinline__ int causal_limit(int64_t row, int causal_tq, int L) {
   if (causal_tq <= 0) return L;
@@ -83,6 +72,31 @@ __global__ __launch_bounds__(256) void softmax_bwd_kernel(const float* __restric
   }
 }
 
+// LayerNorm statistics of one row held by a wave, lane-strided
+// (v[i] = x[lane + 64 i], 0 past C): mean, then v[i] <- x - mean (0 past C)
+// and sd = sqrt(biased variance + eps) (layers.py:82-86).
+template <int VPL>
+__device__ __forceinline__ void ln_stats(float (&v)[VPL], int lane, int C, float eps, float& mean, float& sd) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) s += v[i];
+  mean = wave_sum(s) / (float)C;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int j = lane + 64 * i;
+    const float d = j < C ? v[i] - mean : 0.f;
+    v[i] = d;
+    q += d * d;
+  }
+  const float var = wave_sum(q) / (float)C;
+  sd = sqrtf(var + eps);
+}
+// normalised, scaled and shifted value of d = x - mean (layers.py:85-86)
+__device__ __forceinline__ float ln_apply(float d, float sd, float gamma, float beta) {
+  return (d / sd) * gamma + beta;
+}
+
 // LayerNorm forward: y = (x - mean) / sqrt(var + eps) * gamma + beta.
 // Saves mean and std per row for the backward.
 template <int VPL>  // values per lane held in registers (C <= 64 * VPL)
@@ -98,29 +112,18 @@ __global__ __launch_bounds__(256) void layernorm_fwd_kernel(const float* __restr
   if (row >= rows) return;
   const float* xr = x + row * ldx;
   float v[VPL];
-  float s = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int j = lane + 64 * i;
     v[i] = j < C ? xr[j] : 0.f;
-    s += v[i];
   }
-  const float mean = wave_sum(s) / (float)C;
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int j = lane + 64 * i;
-    const float d = j < C ? v[i] - mean : 0.f;
-    v[i] = d;
-    q += d * d;
-  }
-  const float var = wave_sum(q) / (float)C;
-  const float sd = sqrtf(var + eps);
+  float mean, sd;
+  ln_stats<VPL>(v, lane, C, eps, mean, sd);
   float* yr = y + row * ldy;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int j = lane + 64 * i;
-    if (j < C) yr[j] = (v[i] / sd) * gamma[j] + beta[j];
+    if (j < C) yr[j] = ln_apply(v[i], sd, gamma[j], beta[j]);
   }
   if (lane == 0) {
     mean_out[row] = mean;

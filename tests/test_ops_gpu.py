@@ -59,7 +59,9 @@ def dot_tol(K):
     (64, 384, 512, False, False, 1, True),
     (64, 65, 384, False, False, 1, True),
     (50, 100, 500, True, True, 2, False),
-    (64, 384, 1536, False, False, 1, True),     # K past the skinny limit: split-K
+    (64, 384, 1536, False, False, 1, True),     # skinny, K split over 3 workgroups
+    (17, 40, 1000, True, False, 2, True),       # skinny split, scalar A loads, batched
+    (64, 64, 4100, False, False, 1, False),     # K past the skinny range: tiled split-K
 ])
 def test_gemm(dev, M, N, K, ta, tb, batch, bias):
     import torch
