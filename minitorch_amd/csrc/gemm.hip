@@ -24,7 +24,10 @@ namespace mtx {
 namespace {
 
 constexpr int kGT = 256;  // threads per GEMM workgroup
-constexpr int BK = 16;
+#ifndef MTX_GEMM_BK
+#define MTX_GEMM_BK 16
+#endif
+constexpr int BK = MTX_GEMM_BK;  // k-tile depth of the tiled kernel
 
 struct GemmArgs {
   const float* a; int64_t sam, sak, sab;
@@ -35,6 +38,10 @@ struct GemmArgs {
   int M, N, K, batch;
   int ksplit, kchunk; // K range of split s: [s*kchunk, min(K, (s+1)*kchunk))
   float alpha, beta;
+  // A and B give 16-byte-aligned vectors along their unit-stride dimension
+  // at every multiple of 4 (base, other strides and batch strides: set by
+  // the host; enables the interior-tile loads)
+  int vec_ok;
   // decode-step epilogue (skinny kernel only): act 1 = GELU (tanh form) on
   // the C columns; product columns [nc, N) go to the KV caches instead of C:
   // the first half to kc, the second to vc, at row lengths[m] - 1 of
@@ -194,20 +201,45 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = zero4();
 
-  f32x4 ra[BM * BK / 4 / kGT], rb[BN * BK / 4 / kGT];
-  if (kbeg < kend) {
-    load_a<BM, AK>(g, A, m0, kbeg, kend, ra, tid);
-    load_b<BN, BN1>(g, Bp, n0, kbeg, kend, rb, tid);
+  constexpr int AV = BM * BK / 4 / kGT, BV = BN * BK / 4 / kGT;
+  f32x4 ra[AV], rb[BV];
+  // Interior tiles (every row and column in range, 16-byte aligned vectors
+  // checked on the host) load whole k tiles without per-element checks,
+  // from per-thread offsets computed once; other tiles and the last partial
+  // k tile take the checked loaders.
+  const bool interior = g.vec_ok && m0 + BM <= g.M && n0 + BN <= g.N;
+  int64_t aoff[AV], boff[BV];
+#pragma unroll
+  for (int i = 0; i < AV; ++i) {
+    const int idx = tid + i * kGT;
+    aoff[i] = AK ? (int64_t)(m0 + idx / (BK / 4)) * g.sam + (idx % (BK / 4)) * 4
+                 : (int64_t)(idx / (BM / 4)) * g.sak + m0 + (idx % (BM / 4)) * 4;
   }
+#pragma unroll
+  for (int i = 0; i < BV; ++i) {
+    const int idx = tid + i * kGT;
+    boff[i] = BN1 ? (int64_t)(idx / (BN / 4)) * g.sbk + n0 + (idx % (BN / 4)) * 4
+                  : (int64_t)(n0 + idx / (BK / 4)) * g.sbn + (idx % (BK / 4)) * 4;
+  }
+  const int64_t ak = AK ? 1 : g.sak, bk = BN1 ? g.sbk : 1;  // k stride of the offsets
+  auto fetch = [&](int k0) {
+    if (interior && k0 + BK <= kend) {
+#pragma unroll
+      for (int i = 0; i < AV; ++i) ra[i] = *reinterpret_cast<const f32x4*>(A + aoff[i] + (int64_t)k0 * ak);
+#pragma unroll
+      for (int i = 0; i < BV; ++i) rb[i] = *reinterpret_cast<const f32x4*>(Bp + boff[i] + (int64_t)k0 * bk);
+    } else {
+      load_a<BM, AK>(g, A, m0, k0, kend, ra, tid);
+      load_b<BN, BN1>(g, Bp, n0, k0, kend, rb, tid);
+    }
+  };
+  if (kbeg < kend) fetch(kbeg);
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     __syncthreads();
     store_a<BM, AK>(As, ra, tid);
     store_b<BN, BN1>(Bs, rb, tid);
     __syncthreads();
-    if (k0 + BK < kend) {
-      load_a<BM, AK>(g, A, m0, k0 + BK, kend, ra, tid);
-      load_b<BN, BN1>(g, Bp, n0, k0 + BK, kend, rb, tid);
-    }
+    if (k0 + BK < kend) fetch(k0 + BK);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 4) {
       float af[TM], bf[TN];
@@ -493,6 +525,11 @@ extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
   GemmArgs g{a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, c, sc_m, sc_n, sc_b, bias,
              static_cast<float*>(workspace), M, N, K, batch, 1, K, alpha, beta};
   g.nc = N;
+  {
+    const bool a_ok = (((uintptr_t)a) & 15u) == 0 && (sa_k == 1 ? sa_m % 4 == 0 : sa_k % 4 == 0) && sa_b % 4 == 0;
+    const bool b_ok = (((uintptr_t)b) & 15u) == 0 && (sb_n == 1 ? sb_k % 4 == 0 : sb_n % 4 == 0) && sb_b % 4 == 0;
+    g.vec_ok = a_ok && b_ok;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (K == 0) {  // C = beta*C + bias
     g.ksplit = 1;
