@@ -441,6 +441,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const GemmArgs g) {
     const int64_t e = i % MN;
     const int m = (int)(e / g.N), n = (int)(e % g.N);
     float s = 0.f;
+#pragma unroll 8
     for (int sp = 0; sp < g.ksplit; ++sp) s += g.ws[((int64_t)sp * g.batch + bidx) * MN + e];
     float* p = g.c + (int64_t)bidx * g.scb + (int64_t)m * g.scm + (int64_t)n * g.scn;
     float v = g.alpha * s + (g.bias ? g.bias[n] : 0.f);
@@ -458,10 +459,15 @@ struct Plan {
 Plan plan_gemm(int M, int N, int K, int batch, size_t ws_bytes) {
   Plan p{128, 128, 1, K};
   auto tiles = [&](int bm, int bn) { return (int64_t)cdiv(M, bm) * cdiv(N, bn) * batch; };
-  if (tiles(128, 128) < 512) { p.bm = 64; p.bn = 64; }
+  // Long-K products with both sides >= 128 (weight gradients, K = B*T) keep
+  // 128x128 tiles and split K further: with 64x64 tiles every tile row and
+  // column re-reads its operand panel from beyond L2, twice the traffic.
+  const bool longk = K >= 4096 && M >= 128 && N >= 128;
+  if (tiles(128, 128) < 512 && !longk) { p.bm = 64; p.bn = 64; }
   const int64_t t = tiles(p.bm, p.bn);
   if (t < 256 && K >= 1024) {
-    int want = (int)std::min<int64_t>(16, (512 + t - 1) / t);
+    // up to 64 splits of >= 256 each for K >= 4096 (partials: want x M x N floats)
+    int want = (int)std::min<int64_t>(K >= 4096 ? 64 : 16, (512 + t - 1) / t);
     // each split keeps >= 256 of K
     want = std::min(want, std::max(1, K / 256));
     const size_t need = (size_t)want * batch * (size_t)M * N * sizeof(float);
