@@ -17,7 +17,7 @@ import numpy as np
 from . import device as dev
 from . import kernels as K
 from .device import DeviceArray
-from .tensor import Tensor, _accum_grad, _grad_target, _parents, grad_enabled
+from .tensor import Tensor, _accum_grad, _grad_target, _own_grad, _parents, grad_enabled
 
 
 def _track(*ts):
@@ -189,17 +189,23 @@ def causal_attention(q, k, v, scale=None):
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     qt, kt, vt = q.data.t, k.data.t, v.data.t
-    o, lse = K.attn_fwd(qt, kt, vt, scale, True)
+    B, H, Tq, _ = qt.shape
+    # the output is stored as (B, T, H, D), so merging the heads back to
+    # (B, T, C) (transformer.py:45) is a view, not a copy
+    o = torch_empty((B, Tq, H, D), qt.dtype).transpose(1, 2)
+    o, lse = K.attn_fwd(qt, kt, vt, scale, True, out=o)
     out = None
 
     def _backward():
-        do = out.grad.contiguous().t
+        g = out.grad.t
+        do = g if _kernel_layout(g) else out.grad.contiguous().t
         need = [t.requires_grad for t in (q, k, v)]
         if not any(need):
             return
         tgt = []
         for t in (q, k, v):
             if t.requires_grad and t.grad is not None:
+                _own_grad(t)
                 tgt.append((t.grad.t, True))
             else:
                 buf = dev.DeviceArray(torch_empty_like(t.data.t))
@@ -220,6 +226,20 @@ def causal_attention(q, k, v, scale=None):
 
     out = _node(DeviceArray(o), (q, k, v), "causal_attention", _backward, _track(q, k, v))
     return out
+
+
+def torch_empty(shape, dtype):
+    import torch
+
+    return torch.empty(shape, dtype=dtype, device=dev.device())
+
+
+def _kernel_layout(t):
+    """A (B, H, T, D) view the attention kernels take as it is: unit d stride,
+    16-byte aligned base and other strides."""
+    vec = 16 // t.element_size()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all(s % vec == 0 for s in t.stride()[:-1]))
 
 
 def torch_empty_like(t):

@@ -74,18 +74,44 @@ def _sum_to_shape(g: DeviceArray, shape) -> DeviceArray:
     return out
 
 
+# ids of the non-leaf tensors that have exactly one consumer in the graph the
+# running backward() walks (set by Tensor.backward)
+_single_consumer: set = set()
+
+
 def _accum_grad(tensor: "Tensor", grad: DeviceArray, owned: bool = False):
     """tensor.py:29-33.  `owned` marks a freshly computed buffer with
     tensor's shape that nobody else references: it becomes the gradient
-    without a copy."""
+    without a copy.  A non-leaf tensor with a single consumer receives exactly
+    one gradient per backward pass, which is final (its producer ran first),
+    so it takes that buffer (or view, e.g. through reshape / transpose) as its
+    gradient without a copy; such an alias is copied into a buffer of its own
+    before anything accumulates into it."""
     if tensor.grad is None:
         if owned and grad.shape == tensor.shape and grad.t.is_contiguous():
             tensor.grad = grad
+            tensor._grad_alias = False
+            return
+        if id(tensor) in _single_consumer and grad.shape == tensor.shape:
+            tensor.grad = grad
+            tensor._grad_alias = True
             return
         tensor.grad = dev.empty(tensor.shape)
+        tensor._grad_alias = False
         K.ewise("COPY", tensor.grad.t, grad.t)
     else:
+        _own_grad(tensor)
         K.ewise("COPY", tensor.grad.t, grad.t, accumulate=True)
+
+
+def _own_grad(tensor: "Tensor"):
+    """Give tensor a gradient buffer of its own (copy an alias) before it is
+    written in place."""
+    if tensor.grad is not None and getattr(tensor, "_grad_alias", False):
+        own = dev.empty(tensor.shape)
+        K.ewise("COPY", own.t, tensor.grad.t)
+        tensor.grad = own
+        tensor._grad_alias = False
 
 
 def _grad_target(tensor: "Tensor"):
@@ -94,7 +120,9 @@ def _grad_target(tensor: "Tensor"):
     accumulate mode."""
     if tensor.grad is None:
         tensor.grad = dev.empty(tensor.shape)
+        tensor._grad_alias = False
         return tensor.grad, False
+    _own_grad(tensor)
     return tensor.grad, True
 
 
@@ -564,8 +592,20 @@ class Tensor:
             for child in node._prev:
                 if child not in visited:
                     stack.append((child, False))
-        for node in reversed(topo):
-            node._backward()
+        # consumers per tensor; gradients aliased in an earlier pass get
+        # buffers of their own first (their sources may be accumulated into)
+        counts: dict = {}
+        for node in topo:
+            _own_grad(node)
+            for child in node._prev:
+                counts[id(child)] = counts.get(id(child), 0) + 1
+        global _single_consumer
+        _single_consumer = {id(n) for n in topo if n._prev and counts.get(id(n), 0) == 1}
+        try:
+            for node in reversed(topo):
+                node._backward()
+        finally:
+            _single_consumer = set()
 
     def zero_grad(self):
         self.grad = None

@@ -340,3 +340,60 @@ def test_embedding_backward_both_paths(dev):
         ref = base.astype(np.float64).copy()
         np.add.at(ref, ids, g)
         close(H(dw), ref, atol=dot_tol(n), name=f"embedding_bwd V={V}")
+
+
+def test_view_gradients_alias_and_accumulate_like_reference(dev):
+    """Gradients through reshape / transpose views reach a single-consumer
+    tensor without a copy; the values, a second backward pass without
+    zero_grad (which accumulates, as the reference's _accum_grad does), a
+    tensor used twice by one node and the attention output's strided
+    gradient all match NumPy."""
+    import minitorch_amd as mt
+    import minitorch_amd.functional as F
+
+    _say("[autograd] view aliasing")
+    rng = np.random.default_rng(12)
+    xa = rng.standard_normal((2, 6, 8), dtype=np.float32)
+    wa = rng.standard_normal((2, 2, 6, 4), dtype=np.float32)
+    x = mt.Tensor(xa, requires_grad=True)
+    w = mt.Tensor(wa)
+    h = x * 2.0                                   # non-leaf, one consumer (the reshape)
+    v = h.reshape(2, 6, 2, 4).transpose(1, 2)     # (2, 2, 6, 4) view of h
+    loss = (v * w).sum()
+    loss.backward()
+    gx = 2.0 * wa.transpose(0, 2, 1, 3).reshape(2, 6, 8)
+    close(x.grad.numpy(), gx, name="x.grad")
+    close(h.grad.numpy(), wa.transpose(0, 2, 1, 3).reshape(2, 6, 8), name="h.grad")
+    # second pass without zero_grad: every gradient (intermediate ones
+    # included) accumulates once more, as in the reference
+    loss.backward()
+    # the reference's semantics: loss.grad stays 1, and every intermediate
+    # gradient accumulates its upstream's already accumulated one, so after
+    # two passes (v*w).grad = 2, v.grad = w + 2w = 3w, the reshape's input
+    # w' + 3w' = 4w', h.grad = w' + 4w' = 5w' and x.grad = 2w' + 2*5w' = 12w'
+    Wt = wa.transpose(0, 2, 1, 3).reshape(2, 6, 8)
+    close(v.grad.numpy(), 3 * wa, name="v.grad after two passes")
+    close(h.grad.numpy(), 5 * Wt, name="h.grad after two passes")
+    close(x.grad.numpy(), 12 * Wt, name="x.grad after two passes")
+    # a tensor used twice by one node (x * x through a view)
+    y = mt.Tensor(xa, requires_grad=True)
+    r = y.reshape(2, 48)
+    (r * r).sum().backward()
+    close(y.grad.numpy(), 2 * xa, name="x*x")
+    # attention output: gradient arriving through transpose / reshape (strided)
+    B, H, T, D = 2, 3, 17, 16
+    q, k, vv = (mt.Tensor(rng.standard_normal((B, T, H * D), dtype=np.float32), requires_grad=True)
+                for _ in range(3))
+    heads = lambda t: t.reshape(B, T, H, D).transpose(1, 2)
+    o = F.causal_attention(heads(q), heads(k), heads(vv))
+    m = o.transpose(1, 2).reshape(B, T, H * D)
+    dy = rng.standard_normal((B, T, H * D), dtype=np.float32)
+    (m * mt.Tensor(dy)).sum().backward()
+    from oracle.attention import reference_attention
+    sp = lambda a: a.reshape(B, T, H, D).transpose(0, 2, 1, 3)
+    ro, rdq, rdk, rdv = reference_attention(sp(q.data.numpy()), sp(k.data.numpy()), sp(vv.data.numpy()),
+                                            sp(dy), 1.0 / np.sqrt(D), True)
+    mg = lambda a: a.transpose(0, 2, 1, 3).reshape(B, T, H * D)
+    close(m.numpy(), mg(ro), name="attn out")
+    for t, r_ in ((q, rdq), (k, rdk), (vv, rdv)):
+        close(t.grad.numpy(), mg(r_), name="attn grad")
