@@ -34,6 +34,12 @@
 // unmasked interior tiles); 0: one body with a run-time mask test
 // waves per SIMD the dQ kernel is compiled for (bf16, D <= 64; fp32 D = 128:
 // 1, for its accumulators; others 2)
+// fp32, D <= 64: one tile buffer (staged through registers, two barriers
+// per tile) halves the LDS per workgroup (35 KB), so twice as many
+// workgroups share a CU; measured 9% faster than two buffers at C1
+#ifndef MTX_F32_NBUF1
+#define MTX_F32_NBUF1 1
+#endif
 #ifndef MTX_DQ_WAVES
 #define MTX_DQ_WAVES 3
 #endif
@@ -421,7 +427,7 @@ void attn_fwd_kernel(const FwdArgs a) {
   using LY = Lay<T, D>;
   constexpr int LD = LY::LD;  // LDS row stride
   constexpr int KSZ = BK * LD;
-  constexpr int NBUF = 2 * KSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  constexpr int NBUF = (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * KSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
   static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
   // separate arrays per buffer, picked with compile-time parities: the
   // compiler then sees the direct loads into one buffer and the reads of the
@@ -669,7 +675,7 @@ __global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void 
   using LY = Lay<T, D>;
   constexpr int LD = LY::LD;
   constexpr int RSZ = BQ * LD;
-  constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  constexpr int NBUF = (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
   static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
   // separate arrays per buffer, picked with compile-time parities (see the
   // forward kernel)
@@ -897,7 +903,7 @@ void attn_dq_kernel(const BwdArgs a) {
   using LY = Lay<T, D>;
   constexpr int LD = LY::LD;
   constexpr int RSZ = BK * LD;
-  constexpr int NBUF = 2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1;
+  constexpr int NBUF = (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
   static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
   // separate arrays per buffer, picked with compile-time parities (see the
   // forward kernel)
