@@ -706,22 +706,6 @@ __global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void 
   const int off = a.Tk - a.Tq;
   const float c = a.scale * kLog2e;
 
-  // K and V fragments of this wave's keys (B operands of S = Q K^T, dP = dO V^T);
-  // K pre-multiplied by c = scale*log2(e), so S comes out in log2 units
-  frag kf[NK][KC], vf[NK][KC];
-#pragma unroll
-  for (int ks = 0; ks < NK; ++ks) {
-    const int row = kw0 + 16 * ks + n;
-    const int rr = row < a.Tk ? row : a.Tk - 1;
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc) {
-      frag fk = scale_frag<T>(dfrag<T, D>(kp + (int64_t)rr * a.sk.t, g, kc), c);
-      frag fv = dfrag<T, D>(vp + (int64_t)rr * a.sv.t, g, kc);
-      if (row >= a.Tk) { fk = frag{}; fv = frag{}; }
-      kf[ks][kc] = fk;
-      vf[ks][kc] = fv;
-    }
-  }
 
   f32x4 dka[NK][DT], dva[NK][DT];
 #pragma unroll
@@ -758,6 +742,24 @@ __global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void 
     }
   };
   if (ntile > 0) fetch(qstart, Q0, D0);
+  // the K/V fragments are loaded after the first tile is requested, so both
+  // latencies overlap (measured 1.5% faster at C3)
+  // K and V fragments of this wave's keys (B operands of S = Q K^T, dP = dO V^T);
+  // K pre-multiplied by c = scale*log2(e), so S comes out in log2 units
+  frag kf[NK][KC], vf[NK][KC];
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks) {
+    const int row = kw0 + 16 * ks + n;
+    const int rr = row < a.Tk ? row : a.Tk - 1;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      frag fk = scale_frag<T>(dfrag<T, D>(kp + (int64_t)rr * a.sk.t, g, kc), c);
+      frag fv = dfrag<T, D>(vp + (int64_t)rr * a.sv.t, g, kc);
+      if (row >= a.Tk) { fk = frag{}; fv = frag{}; }
+      kf[ks][kc] = fk;
+      vf[ks][kc] = fv;
+    }
+  }
   // one query tile; P = buffer parity (for direct loads the loop below is
   // unrolled by two so that P is a compile-time constant)
   auto step = [&](auto par, const int it) {
