@@ -207,10 +207,14 @@ def bench_c4(n_new=224):
             "config": "C2 model (6x384, 6 heads), 64 prompts x 32 ids, +224 greedy tokens, fp32, KV cache"}
 
 
-def bench_gpt(c, seed, steps, warmup):
+def bench_gpt(c, seed, steps, warmup, graph=False):
     """Training steps (forward, cross-entropy, zero_grad, backward, Adam
     lr 3e-4) on seeded synthetic token batches already resident on the GPU.
-    Returns ms per step and the losses of the timed steps."""
+    With graph=True the step runs through minitorch_amd.CapturedStep (Adam in
+    capturable mode): two eager calls, the third recorded as a HIP graph and
+    replayed from then on (each call copies its batch into the recorded
+    step's input buffers), so the host's per-kernel dispatch leaves the
+    timed loop.  Returns ms per step and the losses of the timed steps."""
     import torch
 
     import minitorch_amd as mt
@@ -222,20 +226,28 @@ def bench_gpt(c, seed, steps, warmup):
     opt = mt.Adam(model.parameters(), lr=3e-4)
     model.train()
     B, T, V = c["B"], c["block"], c["vocab"]
+    if graph:
+        warmup = max(warmup, 3)  # two eager calls, then the recorded one
     batches = []
     for _ in range(warmup + steps):
         ids = rng.integers(0, V, (B, T + 1))
         batches.append((D.index_array(ids[:, :-1]), D.index_array(ids[:, 1:].reshape(-1))))
     losses = []
 
-    def step(i):
-        x, y = batches[i]
+    def train_step(x, y):
         logits = model(x)
         loss = mt.cross_entropy_loss(logits.reshape(B * T, V), mt.Tensor(y))
         opt.zero_grad()
         loss.backward()
         opt.step()
         return loss
+
+    if graph:
+        opt.capturable()
+        captured = mt.CapturedStep(train_step, opt, warmup=2)
+
+    def step(i):
+        return captured(*batches[i]) if graph else train_step(*batches[i])
 
     for i in range(warmup):
         step(i)
@@ -244,10 +256,12 @@ def bench_gpt(c, seed, steps, warmup):
     e0.record()
     last = []
     for i in range(warmup, warmup + steps):
-        last.append(step(i))
+        loss = step(i)
+        # a replayed step overwrites the recorded loss buffer: keep a copy
+        last.append(loss.data.t.clone() if graph else loss)
     e1.record()
     torch.cuda.synchronize()
-    losses = [float(l_) for l_ in last]
+    losses = [float(l_.cpu()) if isinstance(l_, torch.Tensor) else float(l_) for l_ in last]
     return e0.elapsed_time(e1) / steps, losses
 
 
@@ -352,9 +366,10 @@ def main():
         return
     if args.only in ("gpt2", "gpt0"):
         c = C2_CFG if args.only == "gpt2" else C0_CFG
-        ms, losses = bench_gpt(c, 2, args.steps, args.warmup)
-        print(f"[bench] {args.only}: {ms:.3f} ms/step, {c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, "
-              f"losses {losses}", file=sys.stderr)
+        for graph in (True, False):
+            ms, losses = bench_gpt(c, 2, args.steps, args.warmup, graph=graph)
+            print(f"[bench] {args.only} ({'graph' if graph else 'eager'}): {ms:.3f} ms/step, "
+                  f"{c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, losses {losses}", file=sys.stderr)
         return
     if args.only == "c4":
         print(f"[bench] C4 {bench_c4()}", file=sys.stderr)
@@ -393,13 +408,15 @@ def main():
 
     # ---- GPT training: C2 (GPT-small char model) and C0 (tiny) ----
     print("[bench] GPT C2 training (B=64, T=256, 6x384)", file=sys.stderr, flush=True)
-    ms_c2, losses_c2 = bench_gpt(C2_CFG, 2, max(3, args.steps // 4), 2)
+    ms_c2, losses_c2 = bench_gpt(C2_CFG, 2, max(3, args.steps // 4), 3, graph=True)
+    ms_c2_eager, _ = bench_gpt(C2_CFG, 2, max(3, args.steps // 4), 2)
     tok_c2 = C2_CFG["B"] * C2_CFG["block"] / (ms_c2 * 1e-3)
     fl_c2 = gpt_flops_per_step(C2_CFG)
     print(f"[bench] C2 {ms_c2:.2f} ms/step = {tok_c2:.0f} tokens/s, losses {losses_c2}", file=sys.stderr,
           flush=True)
     print("[bench] GPT C0 training (B=16, T=32, 2x64)", file=sys.stderr, flush=True)
-    ms_c0, _ = bench_gpt(C0_CFG, 0, args.steps, 3)
+    ms_c0, _ = bench_gpt(C0_CFG, 0, args.steps, 3, graph=True)
+    ms_c0_eager, _ = bench_gpt(C0_CFG, 0, args.steps, 3)
     tok_c0 = C0_CFG["B"] * C0_CFG["block"] / (ms_c0 * 1e-3)
 
     print("[bench] C4 greedy decoding (64 x (32 + 224) tokens)", file=sys.stderr, flush=True)
@@ -462,9 +479,13 @@ def main():
                        "model_tflops": round(fl_c2 / (ms_c2 * 1e-3) / 1e12, 2),
                        "pct_of_fp32_peak": round(100 * fl_c2 / (ms_c2 * 1e-3) / 1e12 / PEAK_FP32, 2),
                        "config": "vocab 65, n_embd 384, 6 heads, 6 layers, T=256, B=64, fp32, Adam 3e-4",
-                       "losses": [round(x, 5) for x in losses_c2]},
+                       "losses": [round(x, 5) for x in losses_c2],
+                       "mode": "step replayed from a HIP graph (CapturedStep)",
+                       "ms_per_step_eager": round(ms_c2_eager, 3)},
                 "C0": {"tokens_per_s": round(tok_c0, 1), "ms_per_step": round(ms_c0, 3),
-                       "config": "vocab 65, n_embd 64, 4 heads, 2 layers, T=32, B=16, fp32"},
+                       "config": "vocab 65, n_embd 64, 4 heads, 2 layers, T=32, B=16, fp32",
+                       "mode": "step replayed from a HIP graph (CapturedStep)",
+                       "ms_per_step_eager": round(ms_c0_eager, 3)},
                 "cpu_baseline": cpu_gpt,
             },
             "C4_greedy_decode": c4,

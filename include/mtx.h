@@ -337,6 +337,21 @@ int mtx_adam_blocks(const int64_t* sizes, int ntensors, int64_t* block0_out);
 int mtx_adam_f32(const void* table, int ntensors, int64_t total_blocks, double lr, double beta1,
                  double beta2, double eps, double weight_decay, int step, void* stream);
 
+/*
+ * The same update with the step count t in device memory (*step, int32: the
+ * launch increments it, then updates with the new t), so a training step
+ * recorded as a HIP graph replays unchanged.  The bias corrections are read
+ * from bias_table (2 * table_len floats: entry (t - 1) % table_len holds
+ * 1 - beta1^t, 1 - beta2^t, the float32 values mtx_adam_f32 computes),
+ * filled on the host by mtx_adam_bias_table for the steps about to run.
+ * (No counterpart in the reference, whose Adam keeps t on the host,
+ * optim.py:43-59; for callers that replay recorded steps.)
+ */
+int mtx_adam_bias_table(double beta1, double beta2, int first_step, int len, float* out);
+int mtx_adam_dev_f32(const void* table, int ntensors, int64_t total_blocks, double lr, double beta1,
+                     double beta2, double eps, double weight_decay, int* step, const float* bias_table,
+                     int table_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

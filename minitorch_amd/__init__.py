@@ -9,6 +9,7 @@ include/mtx.h; torch is used only for device memory and streams.
 __version__ = "0.1.0"
 
 from . import functional as F  # noqa: E402
+from .graphs import CapturedStep  # noqa: E402
 from .layers import GELU, Dropout, Embedding, LayerNorm, Linear, ReLU, Sigmoid, Softmax, Tanh  # noqa: E402
 from .loss import cross_entropy_loss, mse_loss  # noqa: E402
 from .module import Module, Sequential  # noqa: E402
@@ -23,5 +24,6 @@ __all__ = [
     "GPT", "TransformerBlock", "MultiHeadAttention",
     "mse_loss", "cross_entropy_loss",
     "SGD", "Adam",
+    "CapturedStep",
     "F",
 ]

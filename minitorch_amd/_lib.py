@@ -86,6 +86,8 @@ SIGNATURES = {
     "mtx_adam_blocks": (_I, [_I64P, _I, _I64P]),
     "mtx_onehot_f32": (_I, [_P, _I64, _I64, _P, _P]),
     "mtx_adam_f32": (_I, [_P, _I, _I64, _D, _D, _D, _D, _D, _I, _P]),
+    "mtx_adam_bias_table": (_I, [_D, _D, _I, _I, _P]),
+    "mtx_adam_dev_f32": (_I, [_P, _I, _I64, _D, _D, _D, _D, _D, _P, _P, _I, _P]),
 }
 
 

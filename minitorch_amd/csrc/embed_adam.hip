@@ -13,6 +13,8 @@
 //   p -= (lr * (m / (1-b1^t))) / (sqrt(v / (1-b2^t)) + eps)
 #include "mtx_common.h"
 
+#include <cmath>
+
 namespace mtx {
 namespace {
 
@@ -77,9 +79,9 @@ struct AdamEntry {
   int64_t block0;  // first block of this tensor
 };
 
-__global__ __launch_bounds__(256) void adam_kernel(const AdamEntry* __restrict__ tab, int ntab, float lr, float b1,
-                                                   float b2, float c1, float c2, float bc1, float bc2, float eps,
-                                                   float wd) {
+// one element's update; bc1, bc2 = the step's bias corrections 1 - b^t
+__device__ __forceinline__ void adam_update(const AdamEntry* __restrict__ tab, int ntab, float lr, float b1, float b2,
+                                            float c1, float c2, float bc1, float bc2, float eps, float wd) {
   // locate this block's tensor (tables are short: linear scan)
   int t = 0;
   while (t + 1 < ntab && tab[t + 1].block0 <= (int64_t)blockIdx.x) ++t;
@@ -97,10 +99,57 @@ __global__ __launch_bounds__(256) void adam_kernel(const AdamEntry* __restrict__
   e.p[i] = e.p[i] - (lr * mh) / (sqrtf(vh) + eps);
 }
 
+__global__ __launch_bounds__(256) void adam_kernel(const AdamEntry* __restrict__ tab, int ntab, float lr, float b1,
+                                                   float b2, float c1, float c2, float bc1, float bc2, float eps,
+                                                   float wd) {
+  adam_update(tab, ntab, lr, b1, b2, c1, c2, bc1, bc2, eps, wd);
+}
+
+// Graph-replayable Adam: the step count lives in device memory (incremented
+// by the one-thread kernel below, launched just before the update), and the
+// bias corrections come from a table the host fills with the same float32
+// values mtx_adam_f32 computes, entry (t - 1) % len for step t.
+__global__ void adam_count_kernel(int* __restrict__ step) { step[0] += 1; }
+
+__global__ __launch_bounds__(256) void adam_dev_kernel(const AdamEntry* __restrict__ tab, int ntab, float lr, float b1,
+                                                       float b2, float c1, float c2, const int* __restrict__ step,
+                                                       const float* __restrict__ bc, int bc_len, float eps,
+                                                       float wd) {
+  const int j = (step[0] - 1) % bc_len;
+  adam_update(tab, ntab, lr, b1, b2, c1, c2, bc[2 * j], bc[2 * j + 1], eps, wd);
+}
+
 }  // namespace
 }  // namespace mtx
 
 using namespace mtx;
+
+extern "C" int mtx_adam_bias_table(double beta1, double beta2, int first_step, int len, float* out) {
+  MTX_CHECK_ARG(out != nullptr && len >= 1 && first_step >= 1, "adam_bias_table: bad argument");
+  for (int s = first_step; s < first_step + len; ++s) {
+    const int j = (s - 1) % len;
+    out[2 * j] = (float)(1.0 - std::pow(beta1, (double)s));
+    out[2 * j + 1] = (float)(1.0 - std::pow(beta2, (double)s));
+  }
+  return MTX_OK;
+}
+
+extern "C" int mtx_adam_dev_f32(const void* table, int ntensors, int64_t total_blocks, double lr, double beta1,
+                                double beta2, double eps, double weight_decay, int* step, const float* bias_table,
+                                int table_len, void* stream) {
+  MTX_CHECK_ARG(table && ntensors >= 1 && step && bias_table && table_len >= 1, "adam_dev: null or empty argument");
+  MTX_CHECK_SHAPE(total_blocks >= 0 && total_blocks < (1LL << 31), "adam_dev: bad block count");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(adam_count_kernel, dim3(1), dim3(1), 0, st, step);
+  MTX_LAUNCHED();
+  if (total_blocks == 0) return MTX_OK;
+  const float c1 = (float)(1.0 - beta1), c2 = (float)(1.0 - beta2);
+  hipLaunchKernelGGL(adam_dev_kernel, dim3((unsigned)total_blocks), dim3(256), 0, st,
+                     static_cast<const AdamEntry*>(table), ntensors, (float)lr, (float)beta1, (float)beta2, c1, c2,
+                     step, bias_table, table_len, (float)eps, (float)weight_decay);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
 
 extern "C" int mtx_embedding_fwd_f32(const float* weight, int64_t ldw, int64_t V, const int64_t* idx, int64_t n,
                                      float* out, int64_t ldo, int C, void* stream) {

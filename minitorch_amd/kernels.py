@@ -445,6 +445,26 @@ class AdamTable:
         self.total_blocks = int(b0[n - 1] + (params[n - 1].numel() + 255) // 256) if n else 0
 
 
+def adam_bias_table(beta1, beta2, first_step, length):
+    """Host float32 table of the bias corrections (1 - beta1^t, 1 - beta2^t)
+    for steps first_step .. first_step + length - 1, entry (t - 1) % length."""
+    import numpy as np
+
+    out = np.empty(2 * length, dtype=np.float32)
+    L.call("mtx_adam_bias_table", float(beta1), float(beta2), int(first_step), int(length),
+           out.ctypes.data_as(L.C.c_void_p))
+    return out
+
+
+def adam_step_dev(table: AdamTable, lr, beta1, beta2, eps, weight_decay, step_dev, bias_dev):
+    """Adam with the step count in device memory (step_dev int32 (1,),
+    incremented by the launch) and bias corrections from bias_dev (2*len
+    float32, adam_bias_table): a launch that replays unchanged in a graph."""
+    L.call("mtx_adam_dev_f32", L.ptr(table.table), table.n, table.total_blocks, float(lr), float(beta1),
+           float(beta2), float(eps), float(weight_decay), L.ptr(step_dev), L.ptr(bias_dev),
+           bias_dev.numel() // 2, L.stream_handle())
+
+
 def adam_step(table: AdamTable, lr, beta1, beta2, eps, weight_decay, step):
     L.call("mtx_adam_f32", L.ptr(table.table), table.n, table.total_blocks, float(lr), float(beta1),
            float(beta2), float(eps), float(weight_decay), int(step), L.stream_handle())

@@ -16,10 +16,17 @@ class Optimizer:
         self.params = list(params)
         self.lr = lr
         self.weight_decay = weight_decay
+        self._capturable = False
 
     def zero_grad(self):
+        """Drop the gradients (optim.py:11-13); in capturable mode the
+        persistent buffers are refilled with zeros instead, so their addresses
+        stay the ones a recorded step uses."""
         for p in self.params:
-            p.grad = None
+            if self._capturable and p.grad is not None:
+                K.fill(p.grad.t, 0.0)
+            else:
+                p.grad = None
 
     def step(self):
         raise NotImplementedError
@@ -38,11 +45,60 @@ class Adam(Optimizer):
         self._table = None
         self._key = None
 
+    def capturable(self, window: int = 4096):
+        """Make step() replayable as part of a recorded HIP graph: every
+        trainable parameter keeps a persistent gradient buffer (zero-filled by
+        zero_grad; accumulating into zeros gives the same bits as a first
+        write), and the step count lives in device memory, the bias
+        corrections coming from a host-filled table that covers `window`
+        steps at a time (refilled between steps by prepare()).  Returns self."""
+        import torch
+
+        for p in self.params:
+            if p.requires_grad and p.grad is None:
+                p.grad = dev.zeros(p.shape)
+        self._step_dev = torch.full((1,), self.t, dtype=torch.int32, device=dev.device())
+        self._bias_dev = torch.empty(2 * window, dtype=torch.float32, device=dev.device())
+        self._bias_first = None
+        self._capturable = True
+        self.prepare()
+        return self
+
+    def prepare(self):
+        """Host work before the next step (eager, recorded or replayed): make
+        the bias table cover step t + 1.  A no-op unless capturable."""
+        if not self._capturable:
+            return
+        import torch
+
+        t_next = self.t + 1
+        n = self._bias_dev.numel() // 2
+        f = self._bias_first
+        if f is None or not (f <= t_next < f + n):
+            host = K.adam_bias_table(self.beta1, self.beta2, t_next, n)
+            self._bias_dev.copy_(torch.from_numpy(host))
+            self._bias_first = t_next
+
     def step(self):
+        if self._capturable:
+            self.prepare()
+            self.t += 1
+            live = [i for i, p in enumerate(self.params) if p.requires_grad and p.grad is not None]
+            if live:
+                self._adam_table(live)
+                K.adam_step_dev(self._table, self.lr, self.beta1, self.beta2, self.eps, self.weight_decay,
+                                self._step_dev, self._bias_dev)
+            return
         self.t += 1
         live = [i for i, p in enumerate(self.params) if p.requires_grad and p.grad is not None]
         if not live:
             return
+        self._adam_table(live)
+        K.adam_step(self._table, self.lr, self.beta1, self.beta2, self.eps, self.weight_decay, self.t)
+
+    def _adam_table(self, live):
+        """The device table of (param, grad, m, v) pointers, rebuilt only when
+        a pointer changed."""
         for i in live:
             p = self.params[i]
             if not p.grad.t.is_contiguous():
@@ -53,7 +109,6 @@ class Adam(Optimizer):
                                       [self.params[i].grad.t for i in live],
                                       [self.m[i].t for i in live], [self.v[i].t for i in live])
             self._key = key
-        K.adam_step(self._table, self.lr, self.beta1, self.beta2, self.eps, self.weight_decay, self.t)
 
     def state_dict(self):
         """Host copy of the optimizer state for checkpoint / resume: the step
@@ -75,6 +130,10 @@ class Adam(Optimizer):
                     raise ValueError(f"{name}.{i}: shape {arr.shape} does not match parameter {tuple(p.shape)}")
                 buf.t.copy_(dev.from_host(arr).t)
         self.t = int(state["t"])
+        if self._capturable:
+            self._step_dev.fill_(self.t)
+            self._bias_first = None
+            self.prepare()
 
     def save(self, path):
         np.savez(path, **self.state_dict())

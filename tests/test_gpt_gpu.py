@@ -307,3 +307,47 @@ def test_sampling_generate_matches_reference(dev):
         ref = g[name]
         bad = np.argwhere(got != ref)
         assert bad.size == 0, f"{name}: first mismatch at {tuple(bad[0])} ({got[tuple(bad[0])]} vs {ref[tuple(bad[0])]})"
+
+
+def test_captured_training_step_matches_eager(dev):
+    """A C0 training step recorded as a HIP graph (graphs.CapturedStep, Adam
+    in capturable mode) and replayed gives the eager run's losses and
+    parameters bit for bit, across a bias-table window boundary."""
+    import minitorch_amd as mt
+    from minitorch_amd import device as D
+    from oracle.gpt import C0, draw_batch, init_params
+
+    _say("[gpt] captured training step vs eager")
+    B, T, V = 16, C0.block, C0.vocab
+
+    def run(captured, steps=8):
+        rng = np.random.default_rng(0)
+        model = gpu_gpt(C0, init_params(C0, rng))
+        opt = mt.Adam(model.parameters(), lr=3e-4)
+        model.train()
+        batches = []
+        for _ in range(steps):
+            x, y = draw_batch(rng, V, B, T)
+            batches.append((D.index_array(x), D.index_array(y.reshape(-1))))
+
+        def step(x, y):
+            logits = model(x)
+            loss = mt.cross_entropy_loss(logits.reshape(B * T, V), mt.Tensor(y))
+            opt.zero_grad()
+            loss.backward()
+            opt.step()
+            return loss
+
+        if captured:
+            opt.capturable(window=3)  # small table: refilled while replaying
+            step = mt.CapturedStep(step, opt, warmup=2)
+        losses = [float(step(x, y)) for x, y in batches]
+        return np.array(losses), [p.data.numpy().copy() for p in model.parameters()], opt.t
+
+    le, pe, te = run(False)
+    lc, pc, tc = run(True)
+    _say(f"  eager {le[-1]:.7f} captured {lc[-1]:.7f}")
+    assert te == tc == 8
+    np.testing.assert_array_equal(lc, le)
+    for a, b in zip(pc, pe):
+        np.testing.assert_array_equal(a, b)
