@@ -42,6 +42,10 @@ class CapturedStep:
         self._static = None
         if optimizer is not None and not optimizer._capturable:
             raise ValueError("the optimizer must be in capturable mode (optimizer.capturable())")
+        if warmup < 1:
+            # first calls create cached device constants (host -> device
+            # copies), which a recording cannot contain
+            raise ValueError("a captured step needs at least one eager warm-up call")
 
     def _stage(self, inputs):
         tens = [x.t if isinstance(x, DeviceArray) else x for x in inputs]

@@ -62,6 +62,9 @@ class Adam(Optimizer):
         self._bias_first = None
         self._capturable = True
         self.prepare()
+        live = [i for i, p in enumerate(self.params) if p.requires_grad and p.grad is not None]
+        if live:
+            self._adam_table(live)  # built now: a recording cannot upload it
         return self
 
     def prepare(self):

@@ -167,3 +167,11 @@ def test_gemm_step_rejects_bad_arguments(over, code, frag):
     rc = _step(**over)
     assert rc == code
     assert frag in L.lib().mtx_last_error().decode()
+
+
+def test_captured_step_needs_an_eager_warmup():
+    """A recording cannot contain the first call's host -> device uploads."""
+    from minitorch_amd.graphs import CapturedStep
+
+    with pytest.raises(ValueError, match="warm-up"):
+        CapturedStep(lambda: None, warmup=0)
