@@ -131,6 +131,61 @@ int mtx_attn_bwd_phase(int phases, int dtype, int B, int H, int Tq, int Tk, int 
                        float scale, int causal, int accumulate, void* stream);
 
 /*
+ * Attention with dropout on the softmax output: the reference's
+ * MultiHeadAttention applies attn_drop (Dropout, layers.py:115-122) to
+ * softmax(scores) before attn @ v (transformer.py:42-44), i.e.
+ *   out = (P * keep * keep_scale) @ v,  keep_scale = 1/(1-p).
+ * keep is a uint8 mask (nonzero = kept) laid out as (B, H, Tq, keep_ld):
+ * element (b, h, i, j) at keep[((b*H + h)*Tq + i)*keep_ld + j]; keep_ld >= Tk,
+ * keep_ld % 4 == 0, keep 4-byte aligned.  lse stays the log-sum-exp of the
+ * undropped scores.  Other arguments as mtx_attn_fwd.
+ */
+int mtx_attn_fwd_dropout(int dtype, int B, int H, int Tq, int Tk, int D,
+                         const void* q, const int64_t* q_strides,
+                         const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides,
+                         void* o, const int64_t* o_strides,
+                         float* lse, float scale, int causal,
+                         const uint8_t* keep, int64_t keep_ld, float keep_scale,
+                         void* stream);
+
+/*
+ * Backward of mtx_attn_fwd_dropout, with the same keep mask: the reference's
+ * dropout closure (layers.py:124-126, grad * mask * scale) composed with the
+ * closures listed at mtx_attn_bwd.  With Z = keep * keep_scale and
+ * dP' = dO V^T:  dV = (P*Z)^T dO;  dS = P*(Z*dP' - rowsum(dO*O));  dQ, dK as
+ * in mtx_attn_bwd (rowsum(P*Z*dP') = rowsum(dO*O) still holds).  Other
+ * arguments as mtx_attn_bwd.
+ */
+int mtx_attn_bwd_dropout(int dtype, int B, int H, int Tq, int Tk, int D,
+                         const void* q, const int64_t* q_strides,
+                         const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides,
+                         const void* o, const int64_t* o_strides,
+                         const void* dout, const int64_t* do_strides,
+                         const float* lse,
+                         float* dq, const int64_t* dq_strides,
+                         float* dk, const int64_t* dk_strides,
+                         float* dv, const int64_t* dv_strides,
+                         void* workspace, size_t workspace_bytes,
+                         float scale, int causal, int accumulate,
+                         const uint8_t* keep, int64_t keep_ld, float keep_scale,
+                         void* stream);
+
+/*
+ * Dropout keep-mask drawn on the device, replacing the host draw
+ * np.random.rand(*shape) > p of Dropout.forward (layers.py:120) where the
+ * mask feeds a fused kernel.  Philox4x32-10 keyed by seed; the 32-bit output
+ * word (e % 4) of counter offset + e/4 gives element e (row-major index over
+ * rows x cols) the uniform u = (word >> 8) * 2^-24, and keep = (u > p).
+ * Element (i, j) is written to keep[i*ld + j]; bytes j >= cols of a row are
+ * left untouched.  A later call with offset += ceil(rows*cols/4) draws fresh
+ * numbers.  0 <= p < 1.
+ */
+int mtx_dropout_keep_philox(uint8_t* keep, int64_t rows, int cols, int64_t ld, float p,
+                            uint64_t seed, uint64_t offset, void* stream);
+
+/*
  * Decode-step attention: one query per (b, h) against its L cached keys,
  * o = softmax(scale * q k^T) v, lse = log sum_j exp(scale * q.k_j).  This is
  * the reference's attention sub-graph (transformer.py:36-44) at the last

@@ -54,6 +54,15 @@ SIGNATURES = {
                                 _P,
                                 _P, _I64P, _P, _I64P, _P, _I64P,
                                 _P, _SZ, _F, _I, _I, _P]),
+    "mtx_attn_fwd_dropout": (_I, [_I, _I, _I, _I, _I, _I,
+                                  _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
+                                  _P, _F, _I, _P, _I64, _F, _P]),
+    "mtx_attn_bwd_dropout": (_I, [_I, _I, _I, _I, _I, _I,
+                                  _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
+                                  _P,
+                                  _P, _I64P, _P, _I64P, _P, _I64P,
+                                  _P, _SZ, _F, _I, _I, _P, _I64, _F, _P]),
+    "mtx_dropout_keep_philox": (_I, [_P, _I64, _I, _I64, _F, C.c_uint64, C.c_uint64, _P]),
     "mtx_attn_decode": (_I, [_I, _I, _I, _I, _I,
                              _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
                              _P, _P, _F, _P]),

@@ -71,6 +71,11 @@ struct FwdArgs {
   int B, H, Tq, Tk;
   float scale;
   int causal;
+  // attention dropout (keep == nullptr: none): keep[(bh*Tq + i)*kld + j] != 0
+  // keeps P[i][j], scaled by kscale = 1/(1-p); kld is a multiple of 4
+  const uint8_t* keep;
+  int64_t kld;
+  float kscale;
 };
 
 struct BwdArgs {
@@ -88,6 +93,9 @@ struct BwdArgs {
   float scale;
   int causal;
   int accumulate;
+  const uint8_t* keep;  // attention dropout, as in FwdArgs
+  int64_t kld;
+  float kscale;
 };
 
 // Work mapping: block id -> (tile index, bh).  Blocks of one bh share an XCD
@@ -226,6 +234,16 @@ struct TileDma {
 };
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Attention dropout (the reference's Dropout on the softmax output,
+// layers.py:115-122 applied at transformer.py:43): P[i][j] is multiplied by
+// keep[i][j] * kscale.  keep4: the keep bytes of keys j0 .. j0+3 of one
+// query row as one dword (j0 % 4 == 0 and kld % 4 == 0 keep it aligned and
+// inside the row); zf: the factor for byte r of such a word.
+__device__ __forceinline__ uint32_t keep4(const uint8_t* __restrict__ keep, int64_t row_off, int j0, int64_t kld) {
+  return j0 < kld ? *reinterpret_cast<const uint32_t*>(keep + row_off + j0) : 0u;
+}
+__device__ __forceinline__ float zf(uint32_t w, int r, float ks) { return ((w >> (8 * r)) & 0xffu) ? ks : 0.f; }
 
 // Reductions over the 4 lanes l, l^16, l^32, l^48 of a wave64 with the gfx950
 // lane swaps: v_permlane16_swap / v_permlane32_swap leave {v[l], v[l^16]}
@@ -412,7 +430,7 @@ __device__ __forceinline__ void store_grad4(float* __restrict__ p, f32x4 v, bool
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NQ>
+template <typename T, int D, int NQ, bool DROP>
 __global__ __launch_bounds__(kThreads, (sizeof(T) == 2 && D <= 64) ? MTX_FWD_WAVES : (D == 128 && sizeof(T) == 4 ? 1 : 2))
 void attn_fwd_kernel(const FwdArgs a) {
   using MF = Mfma<T>;
@@ -534,6 +552,18 @@ void attn_fwd_kernel(const FwdArgs a) {
     if (a.causal && kb > qw0 + NQ * 16 - 1 + off) return;  // nothing visible for this wave
     const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
 
+    // dropout keep bytes of this lane's query and keys kb + 16kt + 4g + 0..3,
+    // requested before the score products so their latency overlaps them
+    uint32_t kwd[NQ][4];
+    if constexpr (DROP) {
+#pragma unroll
+      for (int qs = 0; qs < NQ; ++qs) {
+        const int64_t ro = ((int64_t)bh * a.Tq + min(qw0 + 16 * qs + n, a.Tq - 1)) * a.kld;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) kwd[qs][kt] = keep4(a.keep, ro, kb + 16 * kt + 4 * g, a.kld);
+      }
+    }
+
     f32x4 s[NQ][4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -586,14 +616,29 @@ void attn_fwd_kernel(const FwdArgs a) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[qs][dt] *= alpha;
       }
+      if constexpr (DROP) {
+        // the row sum normalises the softmax before dropout; P V uses the
+        // kept, rescaled probabilities
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s[qs][kt][r] = __builtin_amdgcn_exp2f(s[qs][kt][r]);
+          for (int r = 0; r < 4; ++r) {
+            const float pv = __builtin_amdgcn_exp2f(s[qs][kt][r]);
+            l[qs] += pv;
+            s[qs][kt][r] = pv * zf(kwd[qs][kt], r, a.kscale);
+          }
 #pragma unroll
-      for (int st = 0; st < NS; ++st) {
-        pf[qs][st] = pfrag<T, 4>(s[qs], st);
-        l[qs] = frag_sum<T>(pf[qs][st], l[qs]);
+        for (int st = 0; st < NS; ++st) pf[qs][st] = pfrag<T, 4>(s[qs], st);
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[qs][kt][r] = __builtin_amdgcn_exp2f(s[qs][kt][r]);
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+          pf[qs][st] = pfrag<T, 4>(s[qs], st);
+          l[qs] = frag_sum<T>(pf[qs][st], l[qs]);
+        }
       }
     }
 
@@ -661,7 +706,7 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const BwdArgs a) {
 // ---------------------------------------------------------------------------
 // backward, pass 1: dK, dV (key-outer).  Each wave owns NK*16 keys.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NK>
+template <typename T, int D, int NK, bool DROP>
 __global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void attn_dkdv_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
@@ -788,6 +833,24 @@ __global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void 
     // wave-level causal skip: every key of the wave is after every query of the tile
     if (a.causal && kw0 > qt + BQ - 1 + off) return;
     const bool need_mask = a.causal && (kw0 + NK * 16 - 1 > qt + off);
+    // dropout keep bytes of this lane's keys for queries qt + 16qs + 4g + r,
+    // packed one query quad per word
+    uint32_t kwd[BQ / 16][NK];
+    if constexpr (DROP) {
+#pragma unroll
+      for (int qs = 0; qs < BQ / 16; ++qs)
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) {
+          const int kj = min(kw0 + 16 * ks + n, a.Tk - 1);
+          uint32_t w = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int qi = min(qt + 16 * qs + 4 * g + r, a.Tq - 1);
+            w |= (uint32_t)(a.keep[((int64_t)bh * a.Tq + qi) * a.kld + kj] != 0) << (8 * r);
+          }
+          kwd[qs][ks] = w;
+        }
+    }
     auto tile = [&](auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
 
@@ -826,8 +889,17 @@ __global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void 
           for (int r = 0; r < 4; ++r) {
             float pv = __builtin_amdgcn_exp2f(sv[r]);
             if (MASKED && need_mask && r < hid) pv = 0.f;
-            p[ks][j][r] = pv;
-            ds[ks][j][r] = pv * dpv[r];
+            if constexpr (DROP) {
+              // dV takes the kept P; dS = P (z dP' - delta) with z = keep*kscale
+              // and dP' = dO V^T (the product with the kept P); the MFMA gave
+              // dpv = dP' - delta and ndel = -delta
+              const float z = zf(kwd[qs][ks], r, a.kscale);
+              p[ks][j][r] = pv * z;
+              ds[ks][j][r] = pv * (z * (dpv[r] - ndel[r]) + ndel[r]);
+            } else {
+              p[ks][j][r] = pv;
+              ds[ks][j][r] = pv * dpv[r];
+            }
           }
         }
       }
@@ -890,7 +962,7 @@ __global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void 
 // ---------------------------------------------------------------------------
 // FD: also computes delta[i] = sum_d dO[i,d] O[i,d] for its rows (from the
 // same fragments it loads anyway) and writes it for the dK/dV pass.
-template <typename T, int D, int NQ, bool FD>
+template <typename T, int D, int NQ, bool FD, bool DROP>
 __global__ __launch_bounds__(kThreads, (sizeof(T) == 2 && D <= 64) ? MTX_DQ_WAVES : (D == 128 && sizeof(T) == 4 ? 1 : 2))
 void attn_dq_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
@@ -1024,6 +1096,16 @@ void attn_dq_kernel(const BwdArgs a) {
 
     if (a.causal && kb > qw0 + NQ * 16 - 1 + off) return;
     const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
+    // dropout keep bytes of this lane's query, keys kb + 16kt + 4g + 0..3
+    uint32_t kwd[NQ][4];
+    if constexpr (DROP) {
+#pragma unroll
+      for (int qs = 0; qs < NQ; ++qs) {
+        const int64_t ro = ((int64_t)bh * a.Tq + min(qw0 + 16 * qs + n, a.Tq - 1)) * a.kld;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) kwd[qs][kt] = keep4(a.keep, ro, kb + 16 * kt + 4 * g, a.kld);
+      }
+    }
     auto tile = [&](auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
 
@@ -1058,7 +1140,13 @@ void attn_dq_kernel(const BwdArgs a) {
             if (a.causal) lim = min(lim, qw0 + 16 * qs + n + off - kb - 16 * kt - 4 * g);
             if (r > lim) pv = 0.f;
           }
-          ds[qs][kk][r] = pv * dpv[r];
+          if constexpr (DROP) {
+            // dS = P (z dP' - delta), dpv = dP' - delta (see the dK/dV pass)
+            const float z = zf(kwd[qs][kt], r, a.kscale);
+            ds[qs][kk][r] = pv * (z * (dpv[r] - ndel[qs][r]) + ndel[qs][r]);
+          } else {
+            ds[qs][kk][r] = pv * dpv[r];
+          }
         }
       }
     }
@@ -1159,7 +1247,10 @@ int launch_fwd(const FwdArgs& a, hipStream_t st) {
   constexpr int NQ = Cfg<T, D>::NQF;
   constexpr int BQ = kWaves * NQ * 16;
   const int grid = cdiv(a.Tq, BQ) * a.B * a.H;
-  hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQ>), dim3(grid), dim3(kThreads), 0, st, a);
+  if (a.keep)
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQ, true>), dim3(grid), dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NQ, false>), dim3(grid), dim3(kThreads), 0, st, a);
   MTX_LAUNCHED();
   return MTX_OK;
 }
@@ -1179,15 +1270,25 @@ int launch_bwd(const BwdArgs& a, int phases, hipStream_t st) {
   }
   if (phases & MTX_ATTN_BWD_DQ) {
     const int gq = cdiv(a.Tq, kWaves * NQ * 16) * a.B * a.H;
-    if (fuse)
-      hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ, true>), dim3(gq), dim3(kThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ, false>), dim3(gq), dim3(kThreads), 0, st, a);
+    if (a.keep) {
+      if (fuse)
+        hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ, true, true>), dim3(gq), dim3(kThreads), 0, st, a);
+      else
+        hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ, false, true>), dim3(gq), dim3(kThreads), 0, st, a);
+    } else {
+      if (fuse)
+        hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ, true, false>), dim3(gq), dim3(kThreads), 0, st, a);
+      else
+        hipLaunchKernelGGL((attn_dq_kernel<T, D, NQ, false, false>), dim3(gq), dim3(kThreads), 0, st, a);
+    }
     MTX_LAUNCHED();
   }
   if (phases & MTX_ATTN_BWD_DKDV) {
     const int gk = cdiv(a.Tk, kWaves * NK * 16) * a.B * a.H;
-    hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK>), dim3(gk), dim3(kThreads), 0, st, a);
+    if (a.keep)
+      hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, true>), dim3(gk), dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, false>), dim3(gk), dim3(kThreads), 0, st, a);
     MTX_LAUNCHED();
   }
   return MTX_OK;
@@ -1218,12 +1319,21 @@ int dispatch_bwd(int D, const BwdArgs& a, int phases, hipStream_t st) {
 
 using namespace mtx;
 
-extern "C" int mtx_attn_fwd(int dtype, int B, int H, int Tq, int Tk, int D,
-                            const void* q, const int64_t* q_strides,
-                            const void* k, const int64_t* k_strides,
-                            const void* v, const int64_t* v_strides,
-                            void* o, const int64_t* o_strides,
-                            float* lse, float scale, int causal, void* stream) {
+namespace {
+int check_keep(const uint8_t* keep, int64_t keep_ld, float keep_scale, int Tk) {
+  if (!keep) return MTX_OK;
+  MTX_CHECK_ARG(((uintptr_t)keep & 3u) == 0, "keep: pointer must be 4-byte aligned");
+  MTX_CHECK_ARG(keep_ld >= Tk && keep_ld % 4 == 0,
+                "keep_ld=%lld must be >= Tk=%d and a multiple of 4", (long long)keep_ld, Tk);
+  MTX_CHECK_ARG(std::isfinite(keep_scale) && keep_scale > 0.f, "keep_scale must be finite and > 0");
+  return MTX_OK;
+}
+
+int attn_fwd_impl(int dtype, int B, int H, int Tq, int Tk, int D,
+                  const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                  const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides,
+                  float* lse, float scale, int causal, const uint8_t* keep, int64_t keep_ld,
+                  float keep_scale, void* stream) {
   int rc = check_dims(dtype, B, H, Tq, Tk, D, causal);
   if (rc) return rc;
   const int es = dtype == MTX_F32 ? 4 : 2;
@@ -1231,12 +1341,37 @@ extern "C" int mtx_attn_fwd(int dtype, int B, int H, int Tq, int Tk, int D,
   if ((rc = check_bhtd("k", k, k_strides, es))) return rc;
   if ((rc = check_bhtd("v", v, v_strides, es))) return rc;
   if ((rc = check_bhtd("o", o, o_strides, es))) return rc;
+  if ((rc = check_keep(keep, keep_ld, keep_scale, Tk))) return rc;
   MTX_CHECK_ARG(lse != nullptr, "lse: null pointer");
   MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
   FwdArgs a{q, s3(q_strides), k, s3(k_strides), v, s3(v_strides), o, s3(o_strides),
-            lse, B, H, Tq, Tk, scale, causal ? 1 : 0};
+            lse, B, H, Tq, Tk, scale, causal ? 1 : 0, keep, keep_ld, keep_scale};
   hipStream_t st = static_cast<hipStream_t>(stream);
   return dtype == MTX_F32 ? dispatch_fwd<float>(D, a, st) : dispatch_fwd<bf16_t>(D, a, st);
+}
+}  // namespace
+
+extern "C" int mtx_attn_fwd(int dtype, int B, int H, int Tq, int Tk, int D,
+                            const void* q, const int64_t* q_strides,
+                            const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides,
+                            void* o, const int64_t* o_strides,
+                            float* lse, float scale, int causal, void* stream) {
+  return attn_fwd_impl(dtype, B, H, Tq, Tk, D, q, q_strides, k, k_strides, v, v_strides, o, o_strides,
+                       lse, scale, causal, nullptr, 0, 1.f, stream);
+}
+
+extern "C" int mtx_attn_fwd_dropout(int dtype, int B, int H, int Tq, int Tk, int D,
+                                    const void* q, const int64_t* q_strides,
+                                    const void* k, const int64_t* k_strides,
+                                    const void* v, const int64_t* v_strides,
+                                    void* o, const int64_t* o_strides,
+                                    float* lse, float scale, int causal,
+                                    const uint8_t* keep, int64_t keep_ld, float keep_scale,
+                                    void* stream) {
+  MTX_CHECK_ARG(keep != nullptr, "keep: null pointer");
+  return attn_fwd_impl(dtype, B, H, Tq, Tk, D, q, q_strides, k, k_strides, v, v_strides, o, o_strides,
+                       lse, scale, causal, keep, keep_ld, keep_scale, stream);
 }
 
 extern "C" size_t mtx_attn_bwd_workspace_bytes(int B, int H, int Tq) {
@@ -1244,7 +1379,8 @@ extern "C" size_t mtx_attn_bwd_workspace_bytes(int B, int H, int Tq) {
   return (size_t)B * H * Tq * sizeof(float);
 }
 
-extern "C" int mtx_attn_bwd_phase(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
+namespace {
+int attn_bwd_impl(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
                             const void* q, const int64_t* q_strides,
                             const void* k, const int64_t* k_strides,
                             const void* v, const int64_t* v_strides,
@@ -1255,7 +1391,8 @@ extern "C" int mtx_attn_bwd_phase(int phases, int dtype, int B, int H, int Tq, i
                             float* dk, const int64_t* dk_strides,
                             float* dv, const int64_t* dv_strides,
                             void* workspace, size_t workspace_bytes,
-                            float scale, int causal, int accumulate, void* stream) {
+                            float scale, int causal, int accumulate,
+                            const uint8_t* keep, int64_t keep_ld, float keep_scale, void* stream) {
   MTX_CHECK_ARG(phases > 0 && (phases & ~MTX_ATTN_BWD_ALL) == 0, "bad phase mask %d", phases);
   int rc = check_dims(dtype, B, H, Tq, Tk, D, causal);
   if (rc) return rc;
@@ -1274,13 +1411,54 @@ extern "C" int mtx_attn_bwd_phase(int phases, int dtype, int B, int H, int Tq, i
                 "workspace too small: %zu < %zu bytes", workspace_bytes,
                 mtx_attn_bwd_workspace_bytes(B, H, Tq));
   MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
+  if ((rc = check_keep(keep, keep_ld, keep_scale, Tk))) return rc;
   BwdArgs a{q, s3(q_strides), k, s3(k_strides), v, s3(v_strides), o, s3(o_strides),
             dout, s3(do_strides), lse, static_cast<float*>(workspace),
             dq, s3(dq_strides), dk, s3(dk_strides), dv, s3(dv_strides),
-            B, H, Tq, Tk, scale, causal ? 1 : 0, accumulate ? 1 : 0};
+            B, H, Tq, Tk, scale, causal ? 1 : 0, accumulate ? 1 : 0, keep, keep_ld, keep_scale};
   hipStream_t st = static_cast<hipStream_t>(stream);
   return dtype == MTX_F32 ? dispatch_bwd<float>(D, a, phases, st)
                           : dispatch_bwd<bf16_t>(D, a, phases, st);
+}
+
+}  // namespace
+
+extern "C" int mtx_attn_bwd_phase(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
+                            const void* q, const int64_t* q_strides,
+                            const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides,
+                            const void* o, const int64_t* o_strides,
+                            const void* dout, const int64_t* do_strides,
+                            const float* lse,
+                            float* dq, const int64_t* dq_strides,
+                            float* dk, const int64_t* dk_strides,
+                            float* dv, const int64_t* dv_strides,
+                            void* workspace, size_t workspace_bytes,
+                            float scale, int causal, int accumulate, void* stream) {
+  return attn_bwd_impl(phases, dtype, B, H, Tq, Tk, D, q, q_strides, k, k_strides, v, v_strides, o,
+                       o_strides, dout, do_strides, lse, dq, dq_strides, dk, dk_strides, dv, dv_strides,
+                       workspace, workspace_bytes, scale, causal, accumulate, nullptr, 0, 1.f, stream);
+}
+
+extern "C" int mtx_attn_bwd_dropout(int dtype, int B, int H, int Tq, int Tk, int D,
+                                    const void* q, const int64_t* q_strides,
+                                    const void* k, const int64_t* k_strides,
+                                    const void* v, const int64_t* v_strides,
+                                    const void* o, const int64_t* o_strides,
+                                    const void* dout, const int64_t* do_strides,
+                                    const float* lse,
+                                    float* dq, const int64_t* dq_strides,
+                                    float* dk, const int64_t* dk_strides,
+                                    float* dv, const int64_t* dv_strides,
+                                    void* workspace, size_t workspace_bytes,
+                                    float scale, int causal, int accumulate,
+                                    const uint8_t* keep, int64_t keep_ld, float keep_scale,
+                                    void* stream) {
+  MTX_CHECK_ARG(keep != nullptr, "keep: null pointer");
+  return attn_bwd_impl(MTX_ATTN_BWD_ALL, dtype, B, H, Tq, Tk, D, q, q_strides, k, k_strides, v,
+                       v_strides, o, o_strides, dout, do_strides, lse, dq, dq_strides, dk, dk_strides,
+                       dv, dv_strides, workspace, workspace_bytes, scale, causal, accumulate, keep,
+                       keep_ld, keep_scale, stream);
 }
 
 extern "C" int mtx_attn_bwd(int dtype, int B, int H, int Tq, int Tk, int D,

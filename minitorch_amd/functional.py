@@ -180,11 +180,15 @@ def linear(x, weight, bias=None):
     return out
 
 
-def causal_attention(q, k, v, scale=None):
+def causal_attention(q, k, v, scale=None, keep=None, keep_scale=1.0):
     """softmax(q k^T * scale + causal mask) @ v for (B, H, T, D) tensors --
     exactly transformer.py:36-44 -- as one fused flash kernel (libmtx_hip
     mtx_attn_fwd / mtx_attn_bwd).  q, k, v may be the strided views that
-    _split_heads makes (no copies); gradients come back in the same layout."""
+    _split_heads makes (no copies); gradients come back in the same layout.
+    keep: optional dropout keep-mask (a uint8 (B, H, T, ld) device tensor,
+    see attention_keep_mask) applied to the softmax output with keep_scale =
+    1/(1-p), the reference's attn_drop (transformer.py:43, layers.py:115-126);
+    forward and backward use the same mask (mtx_attn_*_dropout)."""
     D = q.shape[-1]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
@@ -193,7 +197,8 @@ def causal_attention(q, k, v, scale=None):
     # the output is stored as (B, T, H, D), so merging the heads back to
     # (B, T, C) (transformer.py:45) is a view, not a copy
     o = torch_empty((B, Tq, H, D), qt.dtype).transpose(1, 2)
-    o, lse = K.attn_fwd(qt, kt, vt, scale, True, out=o)
+    drop = {} if keep is None else {"keep": keep, "keep_scale": float(keep_scale)}
+    o, lse = K.attn_fwd(qt, kt, vt, scale, True, out=o, **drop)
     out = None
 
     def _backward():
@@ -214,18 +219,56 @@ def causal_attention(q, k, v, scale=None):
         none_acc = not any(a for _, a in tgt)
         if acc_all or none_acc:
             K.attn_bwd(qt, kt, vt, o, do, lse, scale, True, dq=tgt[0][0], dk=tgt[1][0], dv=tgt[2][0],
-                       accumulate=acc_all)
+                       accumulate=acc_all, **drop)
             for t, (buf, acc) in zip((q, k, v), tgt):
                 if t.requires_grad and not acc:
                     t.grad = DeviceArray(buf)
         else:
-            dq, dk, dv = K.attn_bwd(qt, kt, vt, o, do, lse, scale, True)
+            dq, dk, dv = K.attn_bwd(qt, kt, vt, o, do, lse, scale, True, **drop)
             for t, gbuf in zip((q, k, v), (dq, dk, dv)):
                 if t.requires_grad:
                     _accum_grad(t, DeviceArray(gbuf), owned=True)
 
     out = _node(DeviceArray(o), (q, k, v), "causal_attention", _backward, _track(q, k, v))
     return out
+
+
+# Source of attention dropout masks.  "host": np.random.rand(B, H, Tq, Tk) > p
+# from NumPy's global RNG, the reference's draw (layers.py:120) at the same
+# point of the forward, so a seeded run reproduces the reference's masks;
+# "device": the Philox4x32-10 generator on the GPU (mtx_dropout_keep_philox),
+# with a counter offset that advances per mask.
+_DROPOUT_RNG = {"mode": "host", "seed": 0, "offset": 0}
+
+
+def set_attention_dropout_rng(mode: str = "host", seed: int = 0) -> None:
+    """Choose where attention dropout masks come from ("host" or "device");
+    "device" restarts the Philox stream at (seed, offset 0)."""
+    if mode not in ("host", "device"):
+        raise ValueError(f"unknown dropout RNG mode {mode!r}")
+    _DROPOUT_RNG.update(mode=mode, seed=int(seed), offset=0)
+
+
+def attention_keep_mask(shape, p: float):
+    """Keep-mask of a (B, H, Tq, Tk) attention matrix for drop probability p,
+    as the fused kernels take it (uint8 (B, H, Tq, ld), ld = Tk rounded up to
+    a multiple of 4).  Returns (mask, keep_scale)."""
+    import torch
+
+    if torch.cuda.is_current_stream_capturing():
+        # a recorded step would replay this draw (host mask or Philox
+        # offset) unchanged on every call
+        raise RuntimeError("attention dropout masks cannot be drawn inside a recorded (captured) step")
+    B, H, Tq, Tk = (int(x) for x in shape)
+    keep_scale = float(np.float32(1.0 / (1.0 - p)))
+    if _DROPOUT_RNG["mode"] == "device":
+        mask, _DROPOUT_RNG["offset"] = K.dropout_keep_philox(
+            (B, H, Tq, Tk), p, _DROPOUT_RNG["seed"], _DROPOUT_RNG["offset"], device=dev.device())
+        return mask, keep_scale
+    ld = K.keep_ld(Tk)
+    host = np.zeros((B, H, Tq, ld), dtype=np.uint8)
+    host[..., :Tk] = np.random.rand(B, H, Tq, Tk) > p
+    return dev.from_host(host, dtype=np.uint8).t, keep_scale
 
 
 def torch_empty(shape, dtype):

@@ -25,10 +25,44 @@ def _bhtd(name, t):
         raise ValueError(f"{name}: the last (d) dimension must be contiguous")
 
 
-def attn_fwd(q, k, v, scale: float, causal: bool = True, out=None, lse=None):
+def _check_keep(keep, B, H, Tq, Tk):
+    """A dropout keep-mask as the kernels take it: contiguous uint8
+    (B, H, Tq, ld) with ld >= Tk, ld % 4 == 0 (nonzero = kept)."""
+    if keep.dtype != torch.uint8 or not keep.is_contiguous() or keep.dim() != 4:
+        raise ValueError("keep must be a contiguous uint8 (B,H,Tq,ld) tensor")
+    if tuple(keep.shape[:3]) != (B, H, Tq) or keep.shape[3] < Tk or keep.shape[3] % 4:
+        raise ValueError(f"keep shape {tuple(keep.shape)} does not fit (B,H,Tq)={(B, H, Tq)}, Tk={Tk}")
+    if keep.device.type != "cuda":
+        raise ValueError("keep must be a device tensor")
+    return keep.shape[3]
+
+
+def keep_ld(Tk: int) -> int:
+    """Row stride (bytes) of a keep-mask for Tk keys."""
+    return (Tk + 3) // 4 * 4
+
+
+def dropout_keep_philox(shape, p: float, seed: int, offset: int, out=None, device=None):
+    """Keep-mask (B, H, Tq, keep_ld(Tk)) uint8 for dropout probability p, from
+    the device Philox4x32-10 generator (mtx_dropout_keep_philox): element
+    e of the logical (B*H*Tq, Tk) array uses output word e % 4 of counter
+    offset + e // 4.  Returns (mask, next offset)."""
+    B, H, Tq, Tk = (int(x) for x in shape)
+    ld = keep_ld(Tk)
+    if out is None:
+        out = torch.zeros((B, H, Tq, ld), dtype=torch.uint8, device=device if device is not None else "cuda")
+    rows = B * H * Tq
+    L.call("mtx_dropout_keep_philox", L.ptr(out), rows, Tk, ld, float(p), int(seed) & (2**64 - 1),
+           int(offset) & (2**64 - 1), L.stream_handle(out.device))
+    return out, offset + (rows * Tk + 3) // 4
+
+
+def attn_fwd(q, k, v, scale: float, causal: bool = True, out=None, lse=None, keep=None,
+             keep_scale: float = 1.0):
     """Fused attention forward.  q: (B,H,Tq,D), k/v: (B,H,Tk,D), fp32 or bf16,
     any strides with a contiguous last dim.  Returns (out, lse) with out like q
-    and lse fp32 (B,H,Tq)."""
+    and lse fp32 (B,H,Tq).  keep: optional dropout keep-mask (see
+    _check_keep); then out = (P * keep * keep_scale) @ v."""
     _need_cuda(q, k, v)
     for name, t in (("q", q), ("k", k), ("v", v)):
         _bhtd(name, t)
@@ -45,6 +79,13 @@ def attn_fwd(q, k, v, scale: float, causal: bool = True, out=None, lse=None):
     _bhtd("out", out)
     if not lse.is_contiguous() or lse.shape != (B, H, Tq) or lse.dtype != torch.float32:
         raise ValueError("lse must be a contiguous fp32 (B,H,Tq) tensor")
+    if keep is not None:
+        ld = _check_keep(keep, B, H, Tq, Tk)
+        L.call("mtx_attn_fwd_dropout", L.dtype_code(q), B, H, Tq, Tk, D,
+               L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
+               L.ptr(out), L.strides(out), L.ptr(lse), float(scale), int(bool(causal)),
+               L.ptr(keep), ld, float(keep_scale), L.stream_handle(q.device))
+        return out, lse
     L.call("mtx_attn_fwd", L.dtype_code(q), B, H, Tq, Tk, D,
            L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
            L.ptr(out), L.strides(out), L.ptr(lse), float(scale), int(bool(causal)),
@@ -128,9 +169,10 @@ def decode_advance(lengths, pos=None):
 
 def attn_bwd(q, k, v, out, dout, lse, scale: float, causal: bool = True,
              dq=None, dk=None, dv=None, accumulate: bool = False, workspace=None,
-             phases: int = L.ATTN_BWD_ALL):
+             phases: int = L.ATTN_BWD_ALL, keep=None, keep_scale: float = 1.0):
     """Fused attention backward.  Returns fp32 (dq, dk, dv).  With
-    accumulate=True the given dq/dk/dv are added to instead of overwritten."""
+    accumulate=True the given dq/dk/dv are added to instead of overwritten.
+    keep/keep_scale: the forward's dropout mask (all phases only)."""
     _need_cuda(q, k, v, out, dout, lse)
     for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout)):
         _bhtd(name, t)
@@ -154,6 +196,18 @@ def attn_bwd(q, k, v, out, dout, lse, scale: float, causal: bool = True,
     nbytes = L.lib().mtx_attn_bwd_workspace_bytes(B, H, Tq)
     if workspace is None:
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    if keep is not None:
+        if int(phases) != L.ATTN_BWD_ALL:
+            raise ValueError("the dropout backward runs all phases")
+        ld = _check_keep(keep, B, H, Tq, Tk)
+        L.call("mtx_attn_bwd_dropout", L.dtype_code(q), B, H, Tq, Tk, D,
+               L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
+               L.ptr(out), L.strides(out), L.ptr(dout), L.strides(dout), L.ptr(lse),
+               L.ptr(dq), L.strides(dq), L.ptr(dk), L.strides(dk), L.ptr(dv), L.strides(dv),
+               L.ptr(workspace), workspace.numel() * workspace.element_size(),
+               float(scale), int(bool(causal)), int(bool(accumulate)), L.ptr(keep), ld,
+               float(keep_scale), L.stream_handle(q.device))
+        return dq, dk, dv
     L.call("mtx_attn_bwd_phase", int(phases), L.dtype_code(q), B, H, Tq, Tk, D,
            L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
            L.ptr(out), L.strides(out), L.ptr(dout), L.strides(dout), L.ptr(lse),

@@ -50,10 +50,13 @@ class MultiHeadAttention(Module):
         q = self._split_heads(self.q_proj(x), B, T)
         k = self._split_heads(self.k_proj(x), B, T)
         v = self._split_heads(self.v_proj(x), B, T)
+        drop = {}
         if self.attn_drop.p > 0.0 and self.attn_drop._training:
-            raise NotImplementedError("attention dropout inside the fused kernel is not implemented; "
-                                      "use dropout=0.0 (the benchmark configurations do)")
-        out = F.causal_attention(q, k, v, scale=1.0 / math.sqrt(self.head_dim))
+            # attn_drop (transformer.py:43) inside the fused kernel: the mask
+            # is drawn here, where the reference draws it
+            keep, ks = F.attention_keep_mask((B, self.n_head, T, T), self.attn_drop.p)
+            drop = {"keep": keep, "keep_scale": ks}
+        out = F.causal_attention(q, k, v, scale=1.0 / math.sqrt(self.head_dim), **drop)
         out = out.transpose(1, 2).reshape(B, T, C)
         return self.out_proj(out)
 

@@ -57,11 +57,15 @@ def _softmax_backward(p: np.ndarray, gout: np.ndarray) -> np.ndarray:
     return g - p * g.sum(axis=-1, keepdims=True)
 
 
-def reference_attention(q, k, v, dout=None, scale=None, causal=True):
+def reference_attention(q, k, v, dout=None, scale=None, causal=True, keep=None, p=0.0):
     """The reference's attention sub-graph with its exact dtype flow.
 
     q, k, v: (..., T, D) float32 (the _split_heads views, transformer.py:26-28).
     dout: upstream gradient of ``out`` or None (forward only).
+    keep: optional dropout keep mask (..., Tq, Tk) (nonzero = kept) with drop
+    probability p: attn_drop (Dropout.forward, layers.py:115-122) between the
+    softmax and attn @ v, ``attn * mask.astype(float32) * (1.0 / (1.0 - p))``,
+    and its closure ``grad * mask * scale`` (layers.py:124-126).
     Returns (out, dq, dk, dv); grads are None when dout is None.
 
     Forward: transformer.py:36-44, with matmul tensor.py:207-208, the scalar
@@ -88,13 +92,21 @@ def reference_attention(q, k, v, dout=None, scale=None, causal=True):
         mask = (causal_mask(Tq, Tk).astype(F32) * F32(-1e9)).astype(F32)
         scores = scores + mask
     attn = _softmax_lastdim(scores)  # float64
-    out = attn @ v  # float64 @ float32 -> float64
+    if keep is not None:
+        dmask = (np.asarray(keep) != 0).astype(F32)
+        dscale = 1.0 / (1.0 - p)
+        attn_d = attn * dmask * dscale  # float64
+    else:
+        attn_d = attn
+    out = attn_d @ v  # float64 @ float32 -> float64
     if dout is None:
         return out, None, None, None
     gout = np.asarray(dout, dtype=F64)
     # attn @ v backward (tensor.py:213-218); v's grad holder is fp32
     d_attn = gout @ np.swapaxes(v, -1, -2)
-    dv = (np.swapaxes(attn, -1, -2) @ gout).astype(F32)
+    dv = (np.swapaxes(attn_d, -1, -2) @ gout).astype(F32)
+    if keep is not None:
+        d_attn = d_attn * dmask * dscale  # dropout closure
     # softmax backward -> grad of scores (float64 node)
     d_scores = _softmax_backward(attn, d_attn)
     # mask add: identity; mul by scale: grad flows into the fp32 q@k^T node
@@ -106,8 +118,9 @@ def reference_attention(q, k, v, dout=None, scale=None, causal=True):
     return out, dq, dk, dv
 
 
-def attention_f64(q, k, v, dout=None, scale=None, causal=True):
-    """Same mathematics as reference_attention, entirely in float64.
+def attention_f64(q, k, v, dout=None, scale=None, causal=True, keep=None, p_drop=0.0):
+    """Same mathematics as reference_attention, entirely in float64 (with the
+    same optional dropout keep mask / probability).
 
     Returns (out, p, dq, dk, dv, ds) where p is the probability matrix and ds
     the score gradient (grad w.r.t. scale * q k^T + mask), for invariant checks.
@@ -123,12 +136,13 @@ def attention_f64(q, k, v, dout=None, scale=None, causal=True):
     if causal:
         s = np.where(causal_mask(Tq, Tk), -np.inf, s)
     p = _softmax_lastdim(s)
-    out = p @ v
+    z = 1.0 if keep is None else (np.asarray(keep) != 0) / (1.0 - p_drop)
+    out = (p * z) @ v
     if dout is None:
         return out, p, None, None, None, None
     g = np.asarray(dout, dtype=F64)
-    dv = np.swapaxes(p, -1, -2) @ g
-    dp = g @ np.swapaxes(v, -1, -2)
+    dv = np.swapaxes(p * z, -1, -2) @ g
+    dp = (g @ np.swapaxes(v, -1, -2)) * z
     ds = _softmax_backward(p, dp)
     dq = scale * (ds @ k)
     dk = scale * (np.swapaxes(ds, -1, -2) @ q)

@@ -4,7 +4,7 @@
 Run in the build container only (the reference is mounted at
 /root/reference; it never travels to the GPU box and nothing else imports it):
 
-    python tests/golden/make_golden.py            # attention, MHA, C0 train, greedy
+    python tests/golden/make_golden.py            # attention, MHA, C0 train (+ dropout), greedy
     python tests/golden/make_golden.py --c2       # also the C2 20-step loss curve (slow)
 
 These are the functions no closed form, finite difference or library
@@ -141,6 +141,33 @@ def train_curve(cfg: GPTConfig, seed: int, B: int, steps: int, path, full_grads_
     print(f"wrote {path.name}")
 
 
+def train_curve_dropout(cfg: GPTConfig, seed: int, B: int, steps: int, p: float, dseed: int, path):
+    """The harness loop with dropout p in every Dropout of the model (the
+    embedding dropout, each block's attn_drop and MLP dropout, transformer.py:
+    75-76, 24, 60), the reference's demo setting (char_transformer.py:62).
+    Masks come from NumPy's global RNG seeded with np.random.seed(dseed) after
+    the model is built, in the reference's draw order.  Loss per step."""
+    rng = np.random.default_rng(seed)
+    model = mt.GPT(cfg.vocab, cfg.block, cfg.n_embd, cfg.n_head, cfg.n_layer, dropout=p)
+    model.load_state_dict(init_params(cfg, rng))
+    opt = mt.Adam(model.parameters(), lr=3e-4)
+    model.train()
+    np.random.seed(dseed)
+    losses = []
+    for it in range(steps):
+        x, y = draw_batch(rng, cfg.vocab, B, cfg.block)
+        logits = model(x)
+        Bb, T, V = logits.shape
+        loss = mt.cross_entropy_loss(logits.reshape(Bb * T, V), mt.Tensor(y.reshape(-1)))
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        losses.append(float(loss.data))
+        print(f"  step {it:2d} loss {losses[-1]:.10f}", flush=True)
+    np.savez(path, losses=np.array(losses), seed=seed, B=B, steps=steps, p=p, dseed=dseed)
+    print(f"wrote {path.name}")
+
+
 def greedy(path, seed=100, B=4, T0=8, n_new=24):
     """Greedy decoding harness over the reference forward: argmax of
     model(idx[:, -block:]).data[:, -1, :] (transformer.py:97-98), eval mode,
@@ -185,9 +212,13 @@ def main():
     ap.add_argument("--c2", action="store_true", help="also run the C2 20-step curve (slow)")
     ap.add_argument("--only-c2", action="store_true")
     ap.add_argument("--only-sampling", action="store_true")
+    ap.add_argument("--only-dropout", action="store_true")
     args = ap.parse_args()
     if args.only_sampling:
         sampling(HERE / "sampling_c0.npz")
+        return
+    if args.only_dropout:
+        train_curve_dropout(C0, 0, 16, 10, 0.1, 1234, HERE / "c0_train_dropout.npz")
         return
     if not args.only_c2:
         attention_subgraph(HERE / "attn_subgraph.npz")
@@ -196,6 +227,7 @@ def main():
         train_curve(C0, 0, 16, 20, HERE / "c0_train.npz")
         greedy(HERE / "greedy_c0.npz")
         sampling(HERE / "sampling_c0.npz")
+        train_curve_dropout(C0, 0, 16, 10, 0.1, 1234, HERE / "c0_train_dropout.npz")
     if args.c2 or args.only_c2:
         print("C2 training, 20 steps")
         train_curve(C2, 2, 64, 20, HERE / "c2_train.npz")
