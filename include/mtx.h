@@ -186,6 +186,22 @@ int mtx_dropout_keep_philox(uint8_t* keep, int64_t rows, int cols, int64_t ld, f
                             uint64_t seed, uint64_t offset, void* stream);
 
 /*
+ * Packed q/k/v projection support.  MultiHeadAttention's q_proj, k_proj and
+ * v_proj (transformer.py:32-34, three Linear(C, C) on the same input) run as
+ * one GEMM over the concatenated (C_in, 3C) weight; the reference has no
+ * packed layout (it runs three matmuls, tensor.py:207-223).
+ * mtx_pack3_f32:   dst (rows, 3*cols) = [s0 | s1 | s2], each (rows, cols).
+ * mtx_unpack3_f32: d_b (rows, cols) = src[:, b*cols:(b+1)*cols], added to d_b
+ *                  when bit b of accumulate_mask is set (the reference's
+ *                  _accum_grad, tensor.py:29-33).
+ * All operands contiguous fp32.
+ */
+int mtx_pack3_f32(const float* s0, const float* s1, const float* s2, int64_t rows, int64_t cols,
+                  float* dst, void* stream);
+int mtx_unpack3_f32(const float* src, int64_t rows, int64_t cols, float* d0, float* d1, float* d2,
+                    int accumulate_mask, void* stream);
+
+/*
  * Decode-step attention: one query per (b, h) against its L cached keys,
  * o = softmax(scale * q k^T) v, lse = log sum_j exp(scale * q.k_j).  This is
  * the reference's attention sub-graph (transformer.py:36-44) at the last

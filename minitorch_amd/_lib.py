@@ -63,6 +63,8 @@ SIGNATURES = {
                                   _P, _I64P, _P, _I64P, _P, _I64P,
                                   _P, _SZ, _F, _I, _I, _P, _I64, _F, _P]),
     "mtx_dropout_keep_philox": (_I, [_P, _I64, _I, _I64, _F, C.c_uint64, C.c_uint64, _P]),
+    "mtx_pack3_f32": (_I, [_P, _P, _P, _I64, _I64, _P, _P]),
+    "mtx_unpack3_f32": (_I, [_P, _I64, _I64, _P, _P, _P, _I, _P]),
     "mtx_attn_decode": (_I, [_I, _I, _I, _I, _I,
                              _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
                              _P, _P, _F, _P]),

@@ -6,7 +6,9 @@ softmax, log_softmax (functional.py:9-97).  Added fused ops, each one autograd
 node with a hand-written backward (the precedent is the reference's Conv2d,
 conv.py:66-95):
   linear(x, W, b)              x @ W + b with the bias in the GEMM epilogue
+  linear_qkv(x, lq, lk, lv)    the three q/k/v projections as one packed GEMM
   causal_attention(q, k, v)    transformer.py:36-44 as one flash kernel
+  causal_attention_packed      the same over a packed [q | k | v] tensor
 """
 from __future__ import annotations
 
@@ -177,6 +179,101 @@ def linear(x, weight, bias=None):
             K.reduce(g.t, list(range(g.ndim - 1)), target.t, accumulate=acc)
 
     out = _node(data, prev, "linear", _backward, _track(*prev))
+    return out
+
+
+def linear_qkv(x, lq, lk, lv):
+    """q_proj(x), k_proj(x), v_proj(x) (transformer.py:32-34) as one node whose
+    output is the packed (..., 3C) tensor [q | k | v]: one GEMM over the
+    concatenated (C_in, 3C) weight with the concatenated bias in its epilogue.
+    Backward: dX = dQKV W^T as one GEMM with K = 3C, dW = X^T dQKV as one
+    (C_in, 3C) GEMM and db as one column reduction, each split back into the
+    three Linears' gradients (mtx_unpack3_f32, accumulating like _accum_grad).
+    The three layers keep their own parameters and state_dict keys."""
+    from .linalg import bmm
+
+    Ws = (lq.weight, lk.weight, lv.weight)
+    bs = (lq.bias, lk.bias, lv.bias)
+    Cin, C = Ws[0].shape
+    if x.shape[-1] != Cin:
+        raise AssertionError(f"Linear expects last dim {Cin}, got {x.shape[-1]}")
+    wcat = dev.empty((Cin, 3 * C))
+    K.pack3([w.data.t for w in Ws], wcat.t)
+    bcat = dev.empty((1, 3 * C))
+    K.pack3([b.data.t.view(1, C) for b in bs], bcat.t)
+    data = dev.empty(tuple(x.shape[:-1]) + (3 * C,))
+    xt = x.data.t if x.ndim >= 2 else x.data.t.unsqueeze(0)
+    ot = data.t if x.ndim >= 2 else data.t.unsqueeze(0)
+    bmm(xt, wcat.t, ot, bias=bcat.t.view(-1))
+    prev = (x,) + Ws + bs
+    out = None
+
+    def _backward():
+        g = out.grad
+        g2 = g.t.reshape(-1, 3 * C)
+        if x.requires_grad:
+            target, acc = _grad_target(x)
+            gt = g.t if x.ndim >= 2 else g.t.unsqueeze(0)
+            tt = target.t if x.ndim >= 2 else target.t.unsqueeze(0)
+            bmm(gt, wcat.t.transpose(0, 1), tt, beta=1.0 if acc else 0.0)
+        if any(w.requires_grad for w in Ws):
+            x2 = x.data.t.reshape(-1, Cin)
+            dw = dev.empty((Cin, 3 * C))
+            K.gemm(x2.transpose(0, 1), g2, dw.t, 1.0, 0.0, None, M=Cin, N=3 * C, K=x2.shape[0])
+            _unpack_grads(dw.t, Ws)
+        if any(b.requires_grad for b in bs):
+            db = dev.empty((1, 3 * C))
+            K.reduce(g2, [0], db.t.view(-1))
+            _unpack_grads(db.t, bs, rows_view=(1, C))
+
+    out = _node(data, prev, "linear_qkv", _backward, _track(*prev))
+    return out
+
+
+def _unpack_grads(src, params, rows_view=None):
+    """Split a packed (rows, 3C) gradient into the three parameters' gradients
+    (fresh buffers, or added to existing ones)."""
+    targets, acc = [], []
+    for p in params:
+        if p.requires_grad:
+            t, a = _grad_target(p)
+        else:
+            t, a = dev.empty(p.shape), False  # computed and discarded
+        targets.append(t.t if rows_view is None else t.t.view(*rows_view))
+        acc.append(a)
+    K.unpack3(src, targets, acc)
+
+
+def causal_attention_packed(qkv, n_head, scale=None, keep=None, keep_scale=1.0):
+    """causal_attention (transformer.py:36-44) over the q, k, v column blocks
+    of one packed (B, T, 3C) tensor (linear_qkv's output).  The heads are
+    strided views of it (strides (T*3C, D, 3C, 1), no copies), and the
+    backward writes dq, dk, dv straight into the column blocks of qkv's
+    gradient, so the packed projection's backward reads a single buffer.
+    Returns the (B, H, T, D) output as causal_attention does."""
+    t = qkv.data.t
+    B, T, C3 = t.shape
+    C = C3 // 3
+    D = C // n_head
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    heads = lambda a: [a.view(B, T, 3, n_head, D)[:, :, i].transpose(1, 2) for i in range(3)]
+    qt, kt, vt = heads(t)
+    o = torch_empty((B, T, n_head, D), t.dtype).transpose(1, 2)
+    drop = {} if keep is None else {"keep": keep, "keep_scale": float(keep_scale)}
+    o, lse = K.attn_fwd(qt, kt, vt, scale, True, out=o, **drop)
+    out = None
+
+    def _backward():
+        if not qkv.requires_grad:
+            return
+        g = out.grad.t
+        do = g if _kernel_layout(g) else out.grad.contiguous().t
+        target, acc = _grad_target(qkv)
+        dq, dk, dv = heads(target.t)
+        K.attn_bwd(qt, kt, vt, o, do, lse, scale, True, dq=dq, dk=dk, dv=dv, accumulate=acc, **drop)
+
+    out = _node(DeviceArray(o), (qkv,), "causal_attention", _backward, _track(qkv))
     return out
 
 

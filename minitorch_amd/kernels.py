@@ -25,6 +25,37 @@ def _bhtd(name, t):
         raise ValueError(f"{name}: the last (d) dimension must be contiguous")
 
 
+def pack3(srcs, dst):
+    """dst (rows, 3*cols) = [s0 | s1 | s2] for three contiguous fp32 (rows,
+    cols) tensors (mtx_pack3_f32)."""
+    s0, s1, s2 = srcs
+    rows, cols = s0.shape
+    _need_cuda(s0, s1, s2, dst)
+    for t in (s0, s1, s2):
+        if tuple(t.shape) != (rows, cols) or not t.is_contiguous() or t.dtype != torch.float32:
+            raise ValueError("pack3: sources must be contiguous fp32 tensors of one shape")
+    if tuple(dst.shape) != (rows, 3 * cols) or not dst.is_contiguous() or dst.dtype != torch.float32:
+        raise ValueError(f"pack3: dst must be contiguous fp32 ({rows}, {3 * cols})")
+    L.call("mtx_pack3_f32", L.ptr(s0), L.ptr(s1), L.ptr(s2), rows, cols, L.ptr(dst),
+           L.stream_handle(dst.device))
+    return dst
+
+
+def unpack3(src, dsts, accumulate=(False, False, False)):
+    """d_b (rows, cols) (+)= src[:, b*cols:(b+1)*cols] (mtx_unpack3_f32)."""
+    d0, d1, d2 = dsts
+    rows, cols = d0.shape
+    _need_cuda(src, d0, d1, d2)
+    for t in (d0, d1, d2):
+        if tuple(t.shape) != (rows, cols) or not t.is_contiguous() or t.dtype != torch.float32:
+            raise ValueError("unpack3: targets must be contiguous fp32 tensors of one shape")
+    if tuple(src.shape) != (rows, 3 * cols) or not src.is_contiguous() or src.dtype != torch.float32:
+        raise ValueError(f"unpack3: src must be contiguous fp32 ({rows}, {3 * cols})")
+    mask = sum(1 << i for i, a in enumerate(accumulate) if a)
+    L.call("mtx_unpack3_f32", L.ptr(src), rows, cols, L.ptr(d0), L.ptr(d1), L.ptr(d2), mask,
+           L.stream_handle(src.device))
+
+
 def _check_keep(keep, B, H, Tq, Tk):
     """A dropout keep-mask as the kernels take it: contiguous uint8
     (B, H, Tq, ld) with ld >= Tk, ld % 4 == 0 (nonzero = kept)."""

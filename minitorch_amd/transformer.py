@@ -47,16 +47,23 @@ class MultiHeadAttention(Module):
 
     def forward(self, x):
         B, T, C = x.shape
-        q = self._split_heads(self.q_proj(x), B, T)
-        k = self._split_heads(self.k_proj(x), B, T)
-        v = self._split_heads(self.v_proj(x), B, T)
         drop = {}
         if self.attn_drop.p > 0.0 and self.attn_drop._training:
             # attn_drop (transformer.py:43) inside the fused kernel: the mask
-            # is drawn here, where the reference draws it
+            # is drawn where the reference draws it (no other draw happens
+            # between the projections and the softmax)
             keep, ks = F.attention_keep_mask((B, self.n_head, T, T), self.attn_drop.p)
             drop = {"keep": keep, "keep_scale": ks}
-        out = F.causal_attention(q, k, v, scale=1.0 / math.sqrt(self.head_dim), **drop)
+        scale = 1.0 / math.sqrt(self.head_dim)
+        projs = (self.q_proj, self.k_proj, self.v_proj)
+        if all(p.bias is not None for p in projs):
+            # the three projections as one packed GEMM; attention reads the
+            # heads from the packed tensor and writes its gradient there
+            qkv = F.linear_qkv(x, *projs)
+            out = F.causal_attention_packed(qkv, self.n_head, scale=scale, **drop)
+        else:
+            q, k, v = (self._split_heads(p(x), B, T) for p in projs)
+            out = F.causal_attention(q, k, v, scale=scale, **drop)
         out = out.transpose(1, 2).reshape(B, T, C)
         return self.out_proj(out)
 

@@ -397,3 +397,27 @@ def test_view_gradients_alias_and_accumulate_like_reference(dev):
     close(m.numpy(), mg(ro), name="attn out")
     for t, r_ in ((q, rdq), (k, rdk), (vv, rdv)):
         close(t.grad.numpy(), mg(r_), name="attn grad")
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 5), (7, 384), (384, 384), (3, 6)])
+def test_pack3_unpack3(dev, rows, cols):
+    """mtx_pack3_f32 / mtx_unpack3_f32 against NumPy concatenation and
+    slicing, with every accumulate-mask bit (vector and scalar paths)."""
+    import torch
+
+    from minitorch_amd import kernels as K
+
+    rng = np.random.default_rng(rows * 1000 + cols)
+    src = [rng.standard_normal((rows, cols), dtype=np.float32) for _ in range(3)]
+    ts = [torch.from_numpy(a).to(dev) for a in src]
+    packed = torch.empty((rows, 3 * cols), dtype=torch.float32, device=dev)
+    K.pack3(ts, packed)
+    np.testing.assert_array_equal(packed.cpu().numpy(), np.concatenate(src, axis=1))
+    base = [rng.standard_normal((rows, cols), dtype=np.float32) for _ in range(3)]
+    for mask in range(8):
+        acc = [bool(mask >> i & 1) for i in range(3)]
+        outs = [torch.from_numpy(b.copy()).to(dev) for b in base]
+        K.unpack3(packed, outs, acc)
+        for i in range(3):
+            expect = src[i] + base[i] if acc[i] else src[i]
+            np.testing.assert_array_equal(outs[i].cpu().numpy(), expect)
