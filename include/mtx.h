@@ -270,6 +270,25 @@ int mtx_gemm_f32(int M, int N, int K, int batch,
                  float beta, float* c, int64_t sc_m, int64_t sc_n, int64_t sc_b,
                  const float* bias, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * mtx_gemm_f32 with an activation epilogue, for Linear followed by GELU
+ * (the MLP of TransformerBlock, transformer.py:56-58; F.gelu
+ * functional.py:54-59) and its backward:
+ *   act 0: as mtx_gemm_f32 (aux unused);
+ *   act 1: C = gelu(V) with V = alpha*A@B + beta*C + bias; when aux is not
+ *          NULL, V (the pre-activation the backward needs) is stored to aux;
+ *   act 2: C = V * gelu'(aux), aux the pre-activation (the GELU closure's
+ *          grad * gelu'(x) applied to the product that yields grad).
+ * aux is M x N per batch with strides (sx_m, sx_n, sx_b).  gelu is the tanh
+ * form with the reference's float32 constants.
+ */
+int mtx_gemm_act_f32(int M, int N, int K, int batch,
+                     float alpha, const float* a, int64_t sa_m, int64_t sa_k, int64_t sa_b,
+                     const float* b, int64_t sb_k, int64_t sb_n, int64_t sb_b,
+                     float beta, float* c, int64_t sc_m, int64_t sc_n, int64_t sc_b,
+                     const float* bias, int act, float* aux, int64_t sx_m, int64_t sx_n,
+                     int64_t sx_b, void* workspace, size_t workspace_bytes, void* stream);
+
 /* One decode-step projection in a single launch (no workspace):
  *   P = A @ B + bias, A (M, K) row stride lda (unit k stride), B (K, N) row
  *   stride ldb (unit n stride), M <= 64 rows, K <= 512;

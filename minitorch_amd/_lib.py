@@ -79,6 +79,11 @@ SIGNATURES = {
                           _P, _I64, _I64, _I64,
                           _F, _P, _I64, _I64, _I64,
                           _P, _P, _SZ, _P]),
+    "mtx_gemm_act_f32": (_I, [_I, _I, _I, _I,
+                              _F, _P, _I64, _I64, _I64,
+                              _P, _I64, _I64, _I64,
+                              _F, _P, _I64, _I64, _I64,
+                              _P, _I, _P, _I64, _I64, _I64, _P, _SZ, _P]),
     "mtx_ewise_f32": (_I, [_I, _I, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _F, _F, _I, _P]),
     "mtx_reduce_workspace_bytes": (_SZ, [_I, _I64P, _IP]),
     "mtx_reduce_f32": (_I, [_I, _I, _I64P, _P, _I64P, _IP, _P, _F, _I, _P, _SZ, _P]),

@@ -52,7 +52,22 @@ struct GemmArgs {
   int64_t csb, cst;
   int cT;
   const int* lengths;
+  // tiled-kernel activation epilogue (mtx_gemm_act_f32): act 1 = GELU, with
+  // the pre-activation value also stored to aux when aux != null; act 2 =
+  // multiply by GELU'(aux) (aux = the pre-activation read back)
+  float* aux;
+  int64_t sxm, sxn, sxb;
 };
+
+// the value stored at C[m][n] of batch b from the product's value v
+__device__ __forceinline__ float epilogue(const GemmArgs& g, float v, int bidx, int m, int n) {
+  if (g.act == 1) {
+    if (g.aux) g.aux[(int64_t)bidx * g.sxb + (int64_t)m * g.sxm + (int64_t)n * g.sxn] = v;
+    return gelu_tanh_fast(v);
+  }
+  if (g.act == 2) return v * gelu_grad_fast(g.aux[(int64_t)bidx * g.sxb + (int64_t)m * g.sxm + (int64_t)n * g.sxn]);
+  return v;
+}
 
 template <int BM, int BN, bool AK, bool BN1>
 struct Tiles {
@@ -286,7 +301,7 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
           float* p = Cp + (int64_t)m * g.scm + (int64_t)n * g.scn;
           float v = g.alpha * acc[i][j][r] + bv;
           if (g.beta != 0.f) v += g.beta * *p;
-          *p = v;
+          *p = epilogue(g, v, bidx, m, n);
         }
       }
     }
@@ -446,7 +461,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const GemmArgs g) {
     float* p = g.c + (int64_t)bidx * g.scb + (int64_t)m * g.scm + (int64_t)n * g.scn;
     float v = g.alpha * s + (g.bias ? g.bias[n] : 0.f);
     if (g.beta != 0.f) v += g.beta * *p;
-    *p = v;
+    *p = epilogue(g, v, bidx, m, n);
   }
 }
 
@@ -463,7 +478,12 @@ Plan plan_gemm(int M, int N, int K, int batch, size_t ws_bytes) {
   // 128x128 tiles and split K further: with 64x64 tiles every tile row and
   // column re-reads its operand panel from beyond L2, twice the traffic.
   const bool longk = K >= 4096 && M >= 128 && N >= 128;
-  if (tiles(128, 128) < 512 && !longk) { p.bm = 64; p.bn = 64; }
+  // 128x128 tiles only when they fill whole rounds of the 256 CUs: a last,
+  // partly filled round of these long-running tiles costs more than the
+  // smaller tiles' extra operand traffic (16384 x 1152, K = 384: 179 us with
+  // 1152 = 4.5 x 256 tiles of 128x128)
+  const int64_t t128 = tiles(128, 128);
+  if (!longk && (t128 < 512 || t128 % 256 != 0)) { p.bm = 64; p.bn = 64; }
   const int64_t t = tiles(p.bm, p.bn);
   if (t < 256 && K >= 1024) {
     // up to 64 splits of >= 256 each for K >= 4096 (partials: want x M x N floats)
@@ -514,12 +534,11 @@ extern "C" size_t mtx_gemm_workspace_bytes(int M, int N, int K, int batch) {
   return p.ksplit > 1 ? (size_t)p.ksplit * batch * (size_t)M * N * sizeof(float) : 0;
 }
 
-extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
-                            float alpha, const float* a, int64_t sa_m, int64_t sa_k, int64_t sa_b,
-                            const float* b, int64_t sb_k, int64_t sb_n, int64_t sb_b,
-                            float beta, float* c, int64_t sc_m, int64_t sc_n, int64_t sc_b,
-                            const float* bias, void* workspace, size_t workspace_bytes,
-                            void* stream) {
+namespace {
+int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64_t sa_m, int64_t sa_k,
+              int64_t sa_b, const float* b, int64_t sb_k, int64_t sb_n, int64_t sb_b, float beta, float* c,
+              int64_t sc_m, int64_t sc_n, int64_t sc_b, const float* bias, int act, float* aux, int64_t sx_m,
+              int64_t sx_n, int64_t sx_b, void* workspace, size_t workspace_bytes, void* stream) {
   MTX_CHECK_SHAPE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "negative GEMM size");
   if (M == 0 || N == 0 || batch == 0) return MTX_OK;
   MTX_CHECK_ARG(c != nullptr, "gemm: null C");
@@ -531,18 +550,25 @@ extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
   GemmArgs g{a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, c, sc_m, sc_n, sc_b, bias,
              static_cast<float*>(workspace), M, N, K, batch, 1, K, alpha, beta};
   g.nc = N;
+  g.aux = aux;
+  g.sxm = sx_m;
+  g.sxn = sx_n;
+  g.sxb = sx_b;
   {
     const bool a_ok = (((uintptr_t)a) & 15u) == 0 && (sa_k == 1 ? sa_m % 4 == 0 : sa_k % 4 == 0) && sa_b % 4 == 0;
     const bool b_ok = (((uintptr_t)b) & 15u) == 0 && (sb_n == 1 ? sb_k % 4 == 0 : sb_n % 4 == 0) && sb_b % 4 == 0;
     g.vec_ok = a_ok && b_ok;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (K == 0) {  // C = beta*C + bias
+  // the activation epilogue runs in the tiled kernel and the split-K reduce
+  // (the skinny kernel's act field is the decode step's own)
+  g.act = act;
+  if (K == 0) {  // C = act(beta*C + bias)
     g.ksplit = 1;
     g.kchunk = 0;
     return launch_tile<64, 64>(g, true, true, st);
   }
-  if (int sp = skinny_splits(M, K)) {
+  if (int sp = act ? 0 : skinny_splits(M, K)) {
     MTX_CHECK_SHAPE(batch < 65536, "gemm: batch too large");
     // without room for the partials, one workgroup covers all of K
     if (sp > 1 && (!workspace || workspace_bytes < (size_t)sp * batch * (size_t)M * N * sizeof(float))) sp = 1;
@@ -576,6 +602,30 @@ extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
     MTX_LAUNCHED();
   }
   return MTX_OK;
+}
+}  // namespace
+
+extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
+                            float alpha, const float* a, int64_t sa_m, int64_t sa_k, int64_t sa_b,
+                            const float* b, int64_t sb_k, int64_t sb_n, int64_t sb_b,
+                            float beta, float* c, int64_t sc_m, int64_t sc_n, int64_t sc_b,
+                            const float* bias, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return gemm_impl(M, N, K, batch, alpha, a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, beta, c, sc_m, sc_n, sc_b,
+                   bias, 0, nullptr, 0, 0, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mtx_gemm_act_f32(int M, int N, int K, int batch,
+                                float alpha, const float* a, int64_t sa_m, int64_t sa_k, int64_t sa_b,
+                                const float* b, int64_t sb_k, int64_t sb_n, int64_t sb_b,
+                                float beta, float* c, int64_t sc_m, int64_t sc_n, int64_t sc_b,
+                                const float* bias, int act, float* aux, int64_t sx_m, int64_t sx_n,
+                                int64_t sx_b, void* workspace, size_t workspace_bytes, void* stream) {
+  MTX_CHECK_ARG(act >= 0 && act <= 2, "gemm_act: act=%d must be 0 (none), 1 (GELU) or 2 (GELU backward)", act);
+  MTX_CHECK_ARG(act != 2 || aux != nullptr, "gemm_act: act 2 needs the pre-activation aux");
+  MTX_CHECK_ARG(sx_m >= 0 && sx_n >= 0 && sx_b >= 0, "gemm_act: negative aux stride");
+  return gemm_impl(M, N, K, batch, alpha, a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, beta, c, sc_m, sc_n, sc_b,
+                   bias, act, act ? aux : nullptr, sx_m, sx_n, sx_b, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mtx_gemm_step_f32(int M, int N, int K, const float* a, int64_t lda, const float* b, int64_t ldb,

@@ -53,6 +53,30 @@ __device__ __forceinline__ float gelu_tanh(float v) {
   const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
   return v * 0.5f * (tanhf(inner) + 1.0f);
 }
+// The same two functions with tanh(u) = 1 - 2 / (exp(2u) + 1) (one exp and
+// one reciprocal instead of tanhf's range reduction: absolute error of tanh
+// about 2e-7), for GEMM epilogues where tanhf's cost would stall the tile's
+// stores.  exp overflowing to +inf gives tanh = 1, underflowing to 0 gives -1.
+__device__ __forceinline__ float tanh_fast(float u) {
+  return 1.0f - 2.0f * __frcp_rn(__expf(2.0f * u) + 1.0f);
+}
+__device__ __forceinline__ float gelu_tanh_fast(float v) {
+  const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
+  return v * 0.5f * (tanh_fast(inner) + 1.0f);
+}
+__device__ __forceinline__ float gelu_grad_fast(float v) {
+  const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
+  const float t = tanh_fast(inner);
+  return 0.5f * (t + 1.0f) + 0.5f * v * (1.0f - t * t) * gelu_c0() * (1.0f + 3.0f * gelu_c1() * v * v);
+}
+// d gelu_tanh / dv: the product rule through 0.5 v (1 + tanh(u)),
+// u = c0 (v + c1 v^3) (the reference's gelu backward, functional.py:54-59
+// composed with tanh's, functional.py:39-51)
+__device__ __forceinline__ float gelu_grad(float v) {
+  const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
+  const float t = tanhf(inner);
+  return 0.5f * (t + 1.0f) + 0.5f * v * (1.0f - t * t) * gelu_c0() * (1.0f + 3.0f * gelu_c1() * v * v);
+}
 
 // ---------------------------------------------------------------------------
 // wave64 reductions (butterfly over lane xor 32, 16, ..., 1: every lane gets

@@ -243,11 +243,7 @@ __global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__
 __global__ __launch_bounds__(256) void gelu_bwd_kernel(const float* __restrict__ x, const float* __restrict__ dy,
                                                        float* __restrict__ dx, int64_t n, int accumulate) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const float v = x[i];
-    const float inner = (v + v * v * v * gelu_c1()) * gelu_c0();
-    const float t = tanhf(inner);
-    const float d = 0.5f * (t + 1.0f) + 0.5f * v * (1.0f - t * t) * gelu_c0() * (1.0f + 3.0f * gelu_c1() * v * v);
-    float r = d * dy[i];
+    float r = gelu_grad(x[i]) * dy[i];
     if (accumulate) r += dx[i];
     dx[i] = r;
   }

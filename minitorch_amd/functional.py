@@ -7,6 +7,7 @@ node with a hand-written backward (the precedent is the reference's Conv2d,
 conv.py:66-95):
   linear(x, W, b)              x @ W + b with the bias in the GEMM epilogue
   linear_qkv(x, lq, lk, lv)    the three q/k/v projections as one packed GEMM
+  mlp_gelu(x, fc1, fc2)        Linear -> GELU -> Linear, GELU in the GEMM epilogues
   causal_attention(q, k, v)    transformer.py:36-44 as one flash kernel
   causal_attention_packed      the same over a packed [q | k | v] tensor
 """
@@ -227,6 +228,58 @@ def linear_qkv(x, lq, lk, lv):
             _unpack_grads(db.t, bs, rows_view=(1, C))
 
     out = _node(data, prev, "linear_qkv", _backward, _track(*prev))
+    return out
+
+
+def mlp_gelu(x, fc1, fc2):
+    """fc2(gelu(fc1(x))) -- the MLP of TransformerBlock (transformer.py:56-59:
+    Linear, GELU, Linear; Linear layers.py:31-37, F.gelu functional.py:54-59)
+    -- as one node.  Forward: the fc1 GEMM applies GELU in its epilogue and
+    also stores the pre-activation h the backward needs; then the fc2 GEMM.
+    Backward: dW2, db2 from dY; dh = (dY W2^T) * gelu'(h) as one GEMM whose
+    epilogue applies the GELU derivative; then dW1, db1 and dX from dh.  The
+    two Linears keep their own parameters and state_dict keys."""
+    W1, b1, W2, b2 = fc1.weight, fc1.bias, fc2.weight, fc2.bias
+    Cin, Hd = W1.shape
+    Cout = W2.shape[1]
+    if x.shape[-1] != Cin or W2.shape[0] != Hd:
+        raise AssertionError(f"MLP shapes do not chain: x {tuple(x.shape)}, fc1 {tuple(W1.shape)}, "
+                             f"fc2 {tuple(W2.shape)}")
+    lead = tuple(x.shape[:-1])
+    rows = int(np.prod(lead)) if lead else 1
+    x2 = x.data.t.reshape(rows, Cin)
+    h = torch_empty((rows, Hd), x2.dtype)
+    a = torch_empty((rows, Hd), x2.dtype)
+    K.gemm(x2, W1.data.t, a, bias=b1.data.t, act=K.GEMM_ACT_GELU, aux=h)
+    data = dev.empty(lead + (Cout,))
+    K.gemm(a, W2.data.t, data.t.view(rows, Cout), bias=b2.data.t)
+    prev = (x, W1, b1, W2, b2)
+    out = None
+
+    def _backward():
+        g2 = out.grad.t.reshape(rows, Cout)
+        if W2.requires_grad:
+            t, acc = _grad_target(W2)
+            K.gemm(a.transpose(0, 1), g2, t.t, 1.0, 1.0 if acc else 0.0, None, M=Hd, N=Cout, K=rows)
+        if b2.requires_grad:
+            t, acc = _grad_target(b2)
+            K.reduce(g2, [0], t.t, accumulate=acc)
+        need_h = x.requires_grad or W1.requires_grad or b1.requires_grad
+        if not need_h:
+            return
+        dh = torch_empty((rows, Hd), g2.dtype)
+        K.gemm(g2, W2.data.t.transpose(0, 1), dh, act=K.GEMM_ACT_GELU_BWD, aux=h)
+        if W1.requires_grad:
+            t, acc = _grad_target(W1)
+            K.gemm(x2.transpose(0, 1), dh, t.t, 1.0, 1.0 if acc else 0.0, None, M=Cin, N=Hd, K=rows)
+        if b1.requires_grad:
+            t, acc = _grad_target(b1)
+            K.reduce(dh, [0], t.t, accumulate=acc)
+        if x.requires_grad:
+            t, acc = _grad_target(x)
+            K.gemm(dh, W1.data.t.transpose(0, 1), t.t.view(rows, Cin), 1.0, 1.0 if acc else 0.0, None)
+
+    out = _node(data, prev, "mlp_gelu", _backward, _track(*prev))
     return out
 
 

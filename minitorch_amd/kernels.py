@@ -324,10 +324,15 @@ def reduce(a, axes, out, op=L.RED_SUM, alpha: float = 1.0, accumulate=False):
 # GEMM
 # ---------------------------------------------------------------------------
 
+GEMM_ACT_NONE, GEMM_ACT_GELU, GEMM_ACT_GELU_BWD = 0, 1, 2
+
+
 def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=1,
-         sa=None, sb=None, sc=None):
+         sa=None, sb=None, sc=None, act=GEMM_ACT_NONE, aux=None):
     """C = alpha*A@B + beta*C (+bias) with explicit (row, col, batch) strides
-    for each operand; defaults take them from 2-D/3-D tensors."""
+    for each operand; defaults take them from 2-D/3-D tensors.  act/aux: the
+    GELU epilogues of mtx_gemm_act_f32 (aux shaped like C: the pre-activation
+    written by act 1, read by act 2)."""
     if sa is None:
         sa = (a.stride(-2), a.stride(-1), a.stride(0) if a.dim() == 3 else 0)
     if sb is None:
@@ -337,9 +342,29 @@ def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=
     M = a.shape[-2] if M is None else M
     K = a.shape[-1] if K is None else K
     N = b.shape[-1] if N is None else N
+    for name, t in (("A", a), ("B", b), ("C", c), ("bias", bias), ("aux", aux)):
+        if t is not None and t.dtype != torch.float32:
+            raise ValueError(f"gemm: {name} must be fp32 (got {t.dtype})")
     # one operand stride must be unit; otherwise the caller passes a copy
     ws_bytes = L.lib().mtx_gemm_workspace_bytes(M, N, K, batch)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=c.device) if ws_bytes else None
+    if act != GEMM_ACT_NONE:
+        if aux is not None:
+            if tuple(aux.shape[-2:]) != (M, N) or aux.dtype != torch.float32:
+                raise ValueError(f"gemm: aux must be fp32 with C's shape ({M}, {N})")
+            sx = (aux.stride(-2), aux.stride(-1), aux.stride(0) if aux.dim() == 3 else 0)
+        elif act == GEMM_ACT_GELU_BWD:
+            raise ValueError("gemm: the GELU backward epilogue needs aux")
+        else:
+            sx = (0, 0, 0)
+        L.call("mtx_gemm_act_f32", int(M), int(N), int(K), int(batch),
+               float(alpha), L.ptr(a), int(sa[0]), int(sa[1]), int(sa[2]),
+               L.ptr(b), int(sb[0]), int(sb[1]), int(sb[2]),
+               float(beta), L.ptr(c), int(sc[0]), int(sc[1]), int(sc[2]),
+               L.ptr(bias) if bias is not None else None, int(act),
+               L.ptr(aux) if aux is not None else None, int(sx[0]), int(sx[1]), int(sx[2]),
+               L.ptr(ws) if ws is not None else None, ws_bytes, L.stream_handle())
+        return c
     L.call("mtx_gemm_f32", int(M), int(N), int(K), int(batch),
            float(alpha), L.ptr(a), int(sa[0]), int(sa[1]), int(sa[2]),
            L.ptr(b), int(sb[0]), int(sb[1]), int(sb[2]),

@@ -159,7 +159,13 @@ class TransformerBlock(Module):
 
     def forward(self, x):
         x = x + self.attn(self.ln1(x))
-        x = x + self.mlp(self.ln2(x))
+        fc1, act, fc2, drop = self.mlp.layers
+        if (isinstance(fc1, Linear) and isinstance(act, GELU) and isinstance(fc2, Linear)
+                and fc1.bias is not None and fc2.bias is not None):
+            # Linear -> GELU -> Linear as one node (GELU in the GEMM epilogues)
+            x = x + drop(F.mlp_gelu(self.ln2(x), fc1, fc2))
+        else:
+            x = x + self.mlp(self.ln2(x))
         return x
 
     def forward_cached(self, x, cache, t0):

@@ -421,3 +421,34 @@ def test_pack3_unpack3(dev, rows, cols):
         for i in range(3):
             expect = src[i] + base[i] if acc[i] else src[i]
             np.testing.assert_array_equal(outs[i].cpu().numpy(), expect)
+
+
+@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (512, 1536, 384), (96, 80, 8192)])
+def test_gemm_gelu_epilogues(dev, M, N, K):
+    """mtx_gemm_act_f32: act 1 = gelu(A@B + bias) with the pre-activation in
+    aux, act 2 = (A@B) * gelu'(aux), against NumPy float64 (the K = 8192 case
+    takes the split-K path, whose reduce applies the epilogue)."""
+    import torch
+
+    from minitorch_amd import kernels as K_
+
+    rng = np.random.default_rng(M + N + K)
+    a = (rng.standard_normal((M, K), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
+    b = rng.standard_normal((K, N), dtype=np.float32)
+    bias = rng.standard_normal(N, dtype=np.float32)
+    ta, tb, tbias = (torch.from_numpy(x).to(dev) for x in (a, b, bias))
+    c = torch.empty((M, N), dtype=torch.float32, device=dev)
+    h = torch.empty((M, N), dtype=torch.float32, device=dev)
+    K_.gemm(ta, tb, c, bias=tbias, act=K_.GEMM_ACT_GELU, aux=h)
+    v = a.astype(np.float64) @ b.astype(np.float64) + bias
+    c0, c1 = 0.7978845834732056, 0.044714998453855515
+    t = np.tanh(c0 * (v + c1 * v ** 3))
+    gelu = 0.5 * v * (1 + t)
+    dgelu = 0.5 * (1 + t) + 0.5 * v * (1 - t * t) * c0 * (1 + 3 * c1 * v * v)
+    tol = lambda r: 1e-5 + 1e-4 * np.abs(r)
+    assert np.all(np.abs(h.cpu().numpy() - v) <= tol(v))
+    assert np.all(np.abs(c.cpu().numpy() - gelu) <= tol(gelu))
+    d = torch.empty((M, N), dtype=torch.float32, device=dev)
+    K_.gemm(ta, tb, d, act=K_.GEMM_ACT_GELU_BWD, aux=h)
+    ref = (a.astype(np.float64) @ b.astype(np.float64)) * dgelu
+    assert np.all(np.abs(d.cpu().numpy() - ref) <= tol(ref) + 1e-5 * np.abs(ref).max())
