@@ -20,6 +20,8 @@
 // alpha, beta and bias.
 #include "mtx_common.h"
 
+#include <type_traits>
+
 namespace mtx {
 namespace {
 
@@ -189,7 +191,7 @@ __device__ __forceinline__ void store_b(float* __restrict__ Bs, const f32x4 (&r)
   }
 }
 
-template <int BM, int BN, bool AK, bool BN1>
+template <int BM, int BN, bool AK, bool BN1, int ACT>
 __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
   constexpr int WM = BM / 2, WN = BN / 2;  // wave tile
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -287,8 +289,24 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
     return;
   }
   float* __restrict__ Cp = g.c + (int64_t)bidx * g.scb;
+  // the activation is a template parameter, so the plain GEMMs keep their
+  // register budget; the GELU-backward reads one tile row's pre-activations
+  // (16 values) ahead of their use
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
+    float xa[TN][4];
+    if constexpr (ACT == 2) {
+      const float* __restrict__ X = g.aux + (int64_t)bidx * g.sxb;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = min(n0 + wn + 16 * j + n16, g.N - 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = min(m0 + wm + 16 * i + 4 * grp + r, g.M - 1);
+          xa[j][r] = X[(int64_t)m * g.sxm + (int64_t)n * g.sxn];
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + wn + 16 * j + n16;
@@ -301,10 +319,17 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
           float* p = Cp + (int64_t)m * g.scm + (int64_t)n * g.scn;
           float v = g.alpha * acc[i][j][r] + bv;
           if (g.beta != 0.f) v += g.beta * *p;
-          *p = epilogue(g, v, bidx, m, n);
+          if constexpr (ACT == 1) {
+            if (g.aux) g.aux[(int64_t)bidx * g.sxb + (int64_t)m * g.sxm + (int64_t)n * g.sxn] = v;
+            v = gelu_tanh_fast(v);
+          } else if constexpr (ACT == 2) {
+            v *= gelu_grad_fast(xa[j][r]);
+          }
+          *p = v;
         }
       }
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -511,13 +536,23 @@ Plan plan_gemm(int M, int N, int K, int batch, size_t ws_bytes) {
   return p;
 }
 
+template <int BM, int BN, int ACT>
+void launch_tile_act(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
+  dim3 grid(cdiv(g.N, BN), cdiv(g.M, BM), g.batch * g.ksplit);
+  if (ak && bn1) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, true, true, ACT>), grid, dim3(kGT), 0, st, g);
+  else if (ak) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, true, false, ACT>), grid, dim3(kGT), 0, st, g);
+  else if (bn1) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, false, true, ACT>), grid, dim3(kGT), 0, st, g);
+  else hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, false, false, ACT>), grid, dim3(kGT), 0, st, g);
+}
+
+// the activation epilogue applies only when the tile kernel writes C itself
+// (unsplit K); with split K the reduce kernel applies it
 template <int BM, int BN>
 int launch_tile(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
-  dim3 grid(cdiv(g.N, BN), cdiv(g.M, BM), g.batch * g.ksplit);
-  if (ak && bn1) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, true, true>), grid, dim3(kGT), 0, st, g);
-  else if (ak) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, true, false>), grid, dim3(kGT), 0, st, g);
-  else if (bn1) hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, false, true>), grid, dim3(kGT), 0, st, g);
-  else hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, false, false>), grid, dim3(kGT), 0, st, g);
+  const int act = g.ksplit > 1 ? 0 : g.act;
+  if (act == 1) launch_tile_act<BM, BN, 1>(g, ak, bn1, st);
+  else if (act == 2) launch_tile_act<BM, BN, 2>(g, ak, bn1, st);
+  else launch_tile_act<BM, BN, 0>(g, ak, bn1, st);
   MTX_LAUNCHED();
   return MTX_OK;
 }
