@@ -30,6 +30,16 @@ constexpr int kGT = 256;  // threads per GEMM workgroup
 #define MTX_GEMM_BK 16
 #endif
 constexpr int BK = MTX_GEMM_BK;  // k-tile depth of the tiled kernel
+// split-K planning of long-K products: aim at about MTX_SPLIT_TARGET
+// workgroups, each with at least MTX_SPLIT_MINK of K (C2 weight gradients,
+// K = 16384, summed over the four shapes of a layer: target 256 5.23 ms,
+// 512 4.21, 768 3.98, 1024 4.04-4.08 per step)
+#ifndef MTX_SPLIT_TARGET
+#define MTX_SPLIT_TARGET 768
+#endif
+#ifndef MTX_SPLIT_MINK
+#define MTX_SPLIT_MINK 256
+#endif
 
 struct GemmArgs {
   const float* a; int64_t sam, sak, sab;
@@ -511,10 +521,10 @@ Plan plan_gemm(int M, int N, int K, int batch, size_t ws_bytes) {
   if (!longk && (t128 < 512 || t128 % 256 != 0)) { p.bm = 64; p.bn = 64; }
   const int64_t t = tiles(p.bm, p.bn);
   if (t < 256 && K >= 1024) {
-    // up to 64 splits of >= 256 each for K >= 4096 (partials: want x M x N floats)
-    int want = (int)std::min<int64_t>(K >= 4096 ? 64 : 16, (512 + t - 1) / t);
-    // each split keeps >= 256 of K
-    want = std::min(want, std::max(1, K / 256));
+    // up to 64 splits for K >= 4096 (partials: want x M x N floats)
+    int want = (int)std::min<int64_t>(K >= 4096 ? 64 : 16, (MTX_SPLIT_TARGET + t - 1) / t);
+    // each split keeps >= MTX_SPLIT_MINK of K
+    want = std::min(want, std::max(1, K / MTX_SPLIT_MINK));
     const size_t need = (size_t)want * batch * (size_t)M * N * sizeof(float);
     if (want > 1 && need <= ws_bytes) {
       p.ksplit = want;
