@@ -379,7 +379,10 @@ int mtx_layernorm_fwd_f32(const float* x, int64_t ldx, const float* gamma, const
                           float* y, int64_t ldy, float* mean, float* std_, int64_t rows, int C,
                           float eps, void* stream);
 size_t mtx_layernorm_bwd_workspace_bytes(int64_t rows, int C);
-/* LayerNorm backward: dx (if non-NULL) and dgamma/dbeta (if non-NULL). */
+/* LayerNorm backward: dx (if non-NULL) and dgamma/dbeta (if non-NULL), in one
+ * pass over x and dy when both are asked for.  accumulate: bit 0 adds into dx,
+ * bit 1 adds into dgamma and dbeta.  workspace: at least
+ * mtx_layernorm_bwd_workspace_bytes(rows, C) when dgamma is given. */
 int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* gamma, const float* mean,
                           const float* std_, const float* dy, int64_t lddy, float* dx, int64_t lddx,
                           float* dgamma, float* dbeta, int64_t rows, int C, int accumulate,

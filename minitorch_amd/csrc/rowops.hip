@@ -175,64 +175,174 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(const float* __restr
   }
 }
 
-// dgamma[c] = sum_r dy[r,c] * xh[r,c], dbeta[c] = sum_r dy[r,c].  Block = 64
-// columns x 4 row lanes over one chunk of rows; partials [split][2][C] go to
-// the workspace and are combined in split order (deterministic).
-__global__ __launch_bounds__(256) void layernorm_param_partial(const float* __restrict__ x, int64_t ldx,
-                                                               const float* __restrict__ mean_in,
-                                                               const float* __restrict__ std_in,
-                                                               const float* __restrict__ dy, int64_t lddy,
-                                                               float* __restrict__ ws, int64_t rows, int C,
-                                                               int64_t chunk) {
-  __shared__ float pg[4][64], pb[4][64];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + tx;
-  const int s = blockIdx.y;
-  const int64_t r0 = (int64_t)s * chunk, r1 = min(rows, r0 + chunk);
-  float ag = 0.f, ab = 0.f;
-  if (c < C) {
-#pragma unroll 4
-    for (int64_t r = r0 + ty; r < r1; r += 4) {
-      const float g = dy[r * lddy + c];
-      ag += g * ((x[r * ldx + c] - mean_in[r]) / std_in[r]);
-      ab += g;
+// LayerNorm backward with the parameter gradients in the same pass over x and
+// dy: block b (8 waves) owns rows [b*chunk, (b+1)*chunk); wave w takes rows
+// w, w+8, ... of them, writes dx (if asked) as layernorm_bwd_kernel does, and
+// keeps per-column sums of dy * xh (dgamma) and dy (dbeta) in registers.  The
+// next row's x, dy (and dx when accumulating) are loaded while the current
+// row is reduced.  The eight waves' sums are added pairwise through LDS in a
+// fixed order and the block's partials [b][2][C] go to the workspace;
+// layernorm_param_combine adds them in block order (deterministic).
+// Dynamic LDS: 4 * 2 * C floats.
+constexpr int LNP_WAVES = 8;
+template <int VPL>
+__global__ __launch_bounds__(64 * LNP_WAVES) void layernorm_bwd_param_kernel(
+    const float* __restrict__ x, int64_t ldx, const float* __restrict__ gamma, const float* __restrict__ mean_in,
+    const float* __restrict__ std_in, const float* __restrict__ dy, int64_t lddy, float* __restrict__ dx,
+    int64_t lddx, float* __restrict__ ws, int64_t rows, int C, int64_t chunk, int acc_dx) {
+  extern __shared__ float red[];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t r0 = (int64_t)blockIdx.x * chunk, r1 = min(rows, r0 + chunk);
+  const bool rd_dx = dx != nullptr && acc_dx != 0;
+  // rows of up to 768 columns keep gamma in registers and prefetch the next
+  // row (x, dy and the dx being added to); wider rows would spill
+  constexpr bool PF = VPL <= 12;
+  float gm[VPL], ag[VPL], ab[VPL], cx[VPL], cg[VPL], cd[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int j = lane + 64 * i;
+    gm[i] = PF && j < C ? gamma[j] : 0.f;
+    ag[i] = 0.f;
+    ab[i] = 0.f;
+  }
+  auto load_row = [&](int64_t rr, float (&px)[VPL], float (&pg)[VPL], float (&pd)[VPL]) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int j = lane + 64 * i;
+      const bool ok = rr < r1 && j < C;
+      px[i] = ok ? x[rr * ldx + j] : 0.f;
+      pg[i] = ok ? dy[rr * lddy + j] : 0.f;
+      pd[i] = PF && ok && rd_dx ? dx[rr * lddx + j] : 0.f;
+    }
+  };
+  int64_t r = r0 + w;
+  if constexpr (PF) load_row(r, cx, cg, cd);
+  for (; r < r1; r += LNP_WAVES) {
+    const float mean = mean_in[r], sd = std_in[r];
+    const int64_t rn = r + LNP_WAVES;
+    float nx[PF ? VPL : 1], ng[PF ? VPL : 1], nd[PF ? VPL : 1];
+    if constexpr (PF) load_row(rn, nx, ng, nd);
+    else load_row(r, cx, cg, cd);
+    // in place: cx becomes xh = (x - mean) / sd, cg becomes g = dy * gamma
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int j = lane + 64 * i;
+      const float xh = j < C ? (cx[i] - mean) / sd : 0.f;
+      const float g = cg[i] * (PF ? gm[i] : (j < C ? gamma[j] : 0.f));
+      s1 += g;
+      s2 += g * xh;
+      ag[i] += cg[i] * xh;
+      ab[i] += cg[i];
+      cx[i] = xh;
+      cg[i] = g;
+    }
+    if (dx) {
+      s1 = wave_sum(s1) / (float)C;
+      s2 = wave_sum(s2) / (float)C;
+      float* dr = dx + r * lddx;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int j = lane + 64 * i;
+        if (j < C) {
+          float v = (cg[i] - s1 - cx[i] * s2) / sd;
+          if (acc_dx) v += PF ? cd[i] : dr[j];
+          dr[j] = v;
+        }
+      }
+    }
+    if constexpr (PF) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        cx[i] = nx[i];
+        cg[i] = ng[i];
+        cd[i] = nd[i];
+      }
     }
   }
-  pg[ty][tx] = ag;
-  pb[ty][tx] = ab;
+  // waves 4..7 hand their sums to waves 0..3, then waves 1..3 to wave 0
+  if (w >= 4) {
+    float* rw = red + (int64_t)(w - 4) * 2 * C;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int j = lane + 64 * i;
+      if (j < C) {
+        rw[j] = ag[i];
+        rw[C + j] = ab[i];
+      }
+    }
+  }
   __syncthreads();
-  if (ty == 0 && c < C) {
-    ws[((int64_t)s * 2 + 0) * C + c] = pg[0][tx] + pg[1][tx] + pg[2][tx] + pg[3][tx];
-    ws[((int64_t)s * 2 + 1) * C + c] = pb[0][tx] + pb[1][tx] + pb[2][tx] + pb[3][tx];
+  if (w < 4) {
+    const float* rw = red + (int64_t)w * 2 * C;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int j = lane + 64 * i;
+      if (j < C) {
+        ag[i] += rw[j];
+        ab[i] += rw[C + j];
+      }
+    }
+  }
+  __syncthreads();
+  if (w >= 1 && w < 4) {
+    float* rw = red + (int64_t)(w - 1) * 2 * C;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int j = lane + 64 * i;
+      if (j < C) {
+        rw[j] = ag[i];
+        rw[C + j] = ab[i];
+      }
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    float* out = ws + (int64_t)blockIdx.x * 2 * C;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int j = lane + 64 * i;
+      if (j < C) {
+        out[j] = ((ag[i] + red[j]) + red[2 * C + j]) + red[4 * C + j];
+        out[C + j] = ((ab[i] + red[C + j]) + red[3 * C + j]) + red[5 * C + j];
+      }
+    }
   }
 }
 
+// dgamma / dbeta = sums of the nsplit block partials [s][2][C], in block
+// order.  Block = 16 columns x 16 partial lanes; blockIdx.y picks dgamma (0)
+// or dbeta (1).
 __global__ __launch_bounds__(256) void layernorm_param_combine(const float* __restrict__ ws, int nsplit, int C,
                                                                float* __restrict__ dgamma,
                                                                float* __restrict__ dbeta, int accumulate) {
-  __shared__ float pg[4][64], pb[4][64];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + tx;
-  float ag = 0.f, ab = 0.f;
+  __shared__ float part[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int c = blockIdx.x * 16 + tx;
+  const int which = blockIdx.y;
+  float a = 0.f;
   if (c < C) {
 #pragma unroll 8
-    for (int s = ty; s < nsplit; s += 4) {
-      ag += ws[((int64_t)s * 2 + 0) * C + c];
-      ab += ws[((int64_t)s * 2 + 1) * C + c];
-    }
+    for (int s = ty; s < nsplit; s += 16) a += ws[((int64_t)s * 2 + which) * C + c];
   }
-  pg[ty][tx] = ag;
-  pb[ty][tx] = ab;
+  part[ty][tx] = a;
   __syncthreads();
   if (ty == 0 && c < C) {
-    ag = pg[0][tx] + pg[1][tx] + pg[2][tx] + pg[3][tx];
-    ab = pb[0][tx] + pb[1][tx] + pb[2][tx] + pb[3][tx];
-    if (accumulate) { ag += dgamma[c]; ab += dbeta[c]; }
-    dgamma[c] = ag;
-    dbeta[c] = ab;
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += part[k][tx];
+    float* o = which ? dbeta : dgamma;
+    if (accumulate) t += o[c];
+    o[c] = t;
   }
 }
 
+// Row blocks of the fused backward: about 32 rows each (4 per wave), at most
+// 1024 blocks (eight waves per SIMD on 256 CUs).
+static int64_t ln_param_blocks(int64_t rows) {
+  int64_t nb = (rows + 31) / 32;
+  return nb < 1 ? 1 : (nb > 1024 ? 1024 : nb);
+}
 
 __global__ __launch_bounds__(256) void gelu_fwd_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
@@ -353,11 +463,7 @@ extern "C" int mtx_layernorm_fwd_f32(const float* x, int64_t ldx, const float* g
 
 extern "C" size_t mtx_layernorm_bwd_workspace_bytes(int64_t rows, int C) {
   if (rows < 1 || C < 1) return 0;
-  // enough (64-column x split) blocks to fill the GPU, >= 64 rows per split
-  const int64_t bx = (C + 63) / 64;
-  int64_t nsplit = 1;
-  while (bx * nsplit < 1024 && rows / (nsplit * 2) >= 64 && nsplit < 512) nsplit *= 2;
-  return (size_t)nsplit * 2 * C * sizeof(float);
+  return (size_t)ln_param_blocks(rows) * 2 * C * sizeof(float);
 }
 
 extern "C" int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* gamma, const float* mean,
@@ -368,33 +474,45 @@ extern "C" int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* g
   MTX_CHECK_SHAPE(rows >= 0 && C >= 1 && C <= 2048 && ldx >= C && lddy >= C, "layernorm_bwd: bad shape");
   MTX_CHECK_ARG(!dx || lddx >= C, "layernorm_bwd: bad lddx");
   MTX_CHECK_ARG((dgamma == nullptr) == (dbeta == nullptr), "layernorm_bwd: dgamma and dbeta go together");
+  MTX_CHECK_ARG(accumulate >= 0 && accumulate <= 3, "layernorm_bwd: accumulate takes bits 0 (dx) and 1 (params)");
   if (rows == 0) return MTX_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dx) {
-    const int vpl = (C + 63) / 64;
-    dim3 gr(rows_grid(rows)), bl(256);
-#define LN_B(V) hipLaunchKernelGGL(layernorm_bwd_kernel<V>, gr, bl, 0, st, x, ldx, gamma, mean, std_, dy, lddy, dx, lddx, rows, C, accumulate ? 1 : 0)
-    if (vpl <= 1) LN_B(1);
-    else if (vpl <= 2) LN_B(2);
-    else if (vpl <= 4) LN_B(4);
-    else if (vpl <= 8) LN_B(8);
-    else if (vpl <= 16) LN_B(16);
-    else LN_B(32);
-#undef LN_B
-    MTX_LAUNCHED();
-  }
+  const int vpl = (C + 63) / 64;
+  const int acc_dx = accumulate & 1, acc_p = (accumulate >> 1) & 1;
   if (dgamma) {
     const size_t need = mtx_layernorm_bwd_workspace_bytes(rows, C);
     MTX_CHECK_ARG(workspace && workspace_bytes >= need, "layernorm_bwd: workspace too small (%zu < %zu)",
                   workspace_bytes, need);
-    const int nsplit = (int)(need / (2 * C * sizeof(float)));
+    const int nsplit = (int)ln_param_blocks(rows);
     const int64_t chunk = (rows + nsplit - 1) / nsplit;
     float* ws = static_cast<float*>(workspace);
-    hipLaunchKernelGGL(layernorm_param_partial, dim3((C + 63) / 64, nsplit), dim3(256), 0, st, x, ldx, mean,
-                       std_, dy, lddy, ws, rows, C, chunk);
+    const size_t lds = (size_t)8 * C * sizeof(float);
+#define LN_P(V) hipLaunchKernelGGL(layernorm_bwd_param_kernel<V>, dim3(nsplit), dim3(64 * LNP_WAVES), lds, st, x, ldx, gamma, mean, std_, dy, lddy, dx, lddx, ws, rows, C, chunk, acc_dx)
+    if (vpl <= 1) LN_P(1);
+    else if (vpl <= 2) LN_P(2);
+    else if (vpl <= 4) LN_P(4);
+    else if (vpl <= 6) LN_P(6);
+    else if (vpl <= 8) LN_P(8);
+    else if (vpl <= 12) LN_P(12);
+    else if (vpl <= 16) LN_P(16);
+    else LN_P(32);
+#undef LN_P
     MTX_LAUNCHED();
-    hipLaunchKernelGGL(layernorm_param_combine, dim3((C + 63) / 64), dim3(256), 0, st, ws, nsplit, C, dgamma,
-                       dbeta, accumulate ? 1 : 0);
+    hipLaunchKernelGGL(layernorm_param_combine, dim3((C + 15) / 16, 2), dim3(256), 0, st, ws, nsplit, C, dgamma,
+                       dbeta, acc_p);
+    MTX_LAUNCHED();
+  } else if (dx) {
+    dim3 gr(rows_grid(rows)), bl(256);
+#define LN_B(V) hipLaunchKernelGGL(layernorm_bwd_kernel<V>, gr, bl, 0, st, x, ldx, gamma, mean, std_, dy, lddy, dx, lddx, rows, C, acc_dx)
+    if (vpl <= 1) LN_B(1);
+    else if (vpl <= 2) LN_B(2);
+    else if (vpl <= 4) LN_B(4);
+    else if (vpl <= 6) LN_B(6);
+    else if (vpl <= 8) LN_B(8);
+    else if (vpl <= 12) LN_B(12);
+    else if (vpl <= 16) LN_B(16);
+    else LN_B(32);
+#undef LN_B
     MTX_LAUNCHED();
   }
   return MTX_OK;

@@ -466,7 +466,14 @@ def layernorm_fwd(x, gamma, beta, y, mean, std, eps):
     return y
 
 
-def layernorm_bwd(x, gamma, mean, std, dy, dx=None, dgamma=None, dbeta=None, accumulate=False):
+def layernorm_bwd(x, gamma, mean, std, dy, dx=None, dgamma=None, dbeta=None, accumulate=False,
+                  accumulate_params=None):
+    """dx and/or dgamma, dbeta in one pass over x and dy.  `accumulate` adds
+    into dx; `accumulate_params` (default: same as `accumulate`) adds into
+    dgamma and dbeta."""
+    if accumulate_params is None:
+        accumulate_params = accumulate
+    flags = (1 if accumulate else 0) | (2 if accumulate_params else 0)
     r, C, ldx = _rows(x)
     _, _, lddy = _rows(dy)
     lddx = _rows(dx)[2] if dx is not None else C
@@ -478,7 +485,7 @@ def layernorm_bwd(x, gamma, mean, std, dy, dx=None, dgamma=None, dbeta=None, acc
     L.call("mtx_layernorm_bwd_f32", L.ptr(x), ldx, L.ptr(gamma), L.ptr(mean), L.ptr(std),
            L.ptr(dy), lddy, L.ptr(dx) if dx is not None else None, lddx,
            L.ptr(dgamma) if dgamma is not None else None, L.ptr(dbeta) if dbeta is not None else None,
-           r, C, int(bool(accumulate)), L.ptr(ws) if ws is not None else None, ws_bytes,
+           r, C, flags, L.ptr(ws) if ws is not None else None, ws_bytes,
            L.stream_handle())
 
 

@@ -105,12 +105,9 @@ class LayerNorm(Module):
                     if ag != ab:  # one of them already held a gradient: keep it simple
                         raise RuntimeError("LayerNorm parameters with mismatched grad state")
                     dgam, dbet, acc_p = tg.t, tb.t, ag
-                if dx is not None:
+                if dx is not None or dgam is not None:
                     K.layernorm_bwd(xc.t.view(rows, C), gamma.data.t, mean.t, std.t, g, dx=dx,
-                                    accumulate=acc_x)
-                if dgam is not None:
-                    K.layernorm_bwd(xc.t.view(rows, C), gamma.data.t, mean.t, std.t, g, dgamma=dgam,
-                                    dbeta=dbet, accumulate=acc_p)
+                                    dgamma=dgam, dbeta=dbet, accumulate=acc_x, accumulate_params=acc_p)
 
             out._backward = _backward
             out._prev = _parents((x, gamma, beta))

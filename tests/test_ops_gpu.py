@@ -182,7 +182,7 @@ def test_softmax_and_log_softmax(dev, rows, L, causal):
         close(H(dx), dy - p * dy.sum(-1, keepdims=True), name="log_softmax_bwd")
 
 
-@pytest.mark.parametrize("rows,C", [(5, 64), (300, 384), (17, 1536), (3, 33)])
+@pytest.mark.parametrize("rows,C", [(5, 64), (300, 384), (17, 1536), (3, 33), (4099, 384), (1000, 2048)])
 def test_layernorm(dev, rows, C):
     import torch
     from minitorch_amd import kernels as Kn
@@ -211,6 +211,21 @@ def test_layernorm(dev, rows, C):
     close(H(dx), hx.g, atol=1e-4 * np.sqrt(C) / 10, name="ln_dx")
     close(H(dg), hg.g, atol=dot_tol(rows), name="ln_dgamma")
     close(H(db), hb.g, atol=dot_tol(rows), name="ln_dbeta")
+    # one fused call: dx added into a held gradient, dgamma / dbeta overwritten
+    base = rng.standard_normal((rows, C), dtype=np.float32)
+    dx2 = T(base)
+    dg2 = T(np.full(C, 7.0, np.float32))
+    db2 = T(np.full(C, -3.0, np.float32))
+    Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dx=dx2, dgamma=dg2, dbeta=db2, accumulate=True,
+                     accumulate_params=False)
+    close(H(dx2), hx.g + base, atol=1e-4 * np.sqrt(C) / 10, name="ln_dx_fused_acc")
+    assert np.array_equal(H(dg2), H(dg)) and np.array_equal(H(db2), H(db))
+    # and the other way round: parameters accumulate, dx overwritten
+    Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dx=dx2, dgamma=dg2, dbeta=db2, accumulate=False,
+                     accumulate_params=True)
+    close(H(dx2), hx.g, atol=1e-4 * np.sqrt(C) / 10, name="ln_dx_fused")
+    close(H(dg2), 2 * hg.g, atol=2 * dot_tol(rows), name="ln_dgamma_acc")
+    close(H(db2), 2 * hb.g, atol=2 * dot_tol(rows), name="ln_dbeta_acc")
 
 
 def test_gelu(dev):
