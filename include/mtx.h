@@ -289,6 +289,22 @@ int mtx_gemm_act_f32(int M, int N, int K, int batch,
                      const float* bias, int act, float* aux, int64_t sx_m, int64_t sx_n,
                      int64_t sx_b, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Weight and bias gradients of a Linear layer in one pass over dY:
+ *   C = A @ B + beta * C            (dW = X^T dY: tensor.py:216-218 through
+ *                                    Linear.forward's x @ W, layers.py:31-37)
+ *   dbias[n] = sum_k B[k][n]        (+ dbias[n] when dbias_accumulate; the
+ *                                    add's _sum_to_shape of b, tensor.py:20-30,
+ *                                    111-119)
+ * batch 1; strides as mtx_gemm_f32.  The column sums come from the B values
+ * the MFMA tiles already load; with split K they are reduced with the C
+ * partials (workspace: mtx_gemm_workspace_bytes(M, N, K, 1)).
+ */
+int mtx_gemm_wgrad_f32(int M, int N, int K, const float* a, int64_t sa_m, int64_t sa_k,
+                       const float* b, int64_t sb_k, int64_t sb_n, float beta, float* c, int64_t sc_m,
+                       int64_t sc_n, float* dbias, int dbias_accumulate, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* One decode-step projection in a single launch (no workspace):
  *   P = A @ B + bias, A (M, K) row stride lda (unit k stride), B (K, N) row
  *   stride ldb (unit n stride), M <= 64 rows, K <= 512;

@@ -69,6 +69,12 @@ struct GemmArgs {
   // multiply by GELU'(aux) (aux = the pre-activation read back)
   float* aux;
   int64_t sxm, sxn, sxb;
+  // weight-gradient variant (mtx_gemm_wgrad_f32, batch 1): colsum[n] =
+  // sum over k of B[k][n] (the bias gradient), added to colsum when
+  // colsum_acc; with split K the per-split sums go to the workspace after the
+  // C partials, [split][N], and the reduce adds them in split order
+  float* colsum;
+  int colsum_acc;
 };
 
 // the value stored at C[m][n] of batch b from the product's value v
@@ -227,6 +233,11 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = zero4();
+  // ACT 3: column sums of B from the values each lane feeds the MFMAs (lane
+  // (grp, n16) sees B[k][wn + 16j + n16] for every k = grp mod 4)
+  float csum[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) csum[j] = 0.f;
 
   constexpr int AV = BM * BK / 4 / kGT, BV = BN * BK / 4 / kGT;
   f32x4 ra[AV], rb[BV];
@@ -279,6 +290,31 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+      if constexpr (ACT == 3) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) csum[j] += bf[j];
+      }
+    }
+  }
+
+  // ACT 3: the first row of tiles (its waves 0 and 1, which together cover
+  // the BN columns) adds the four lane groups' sums and stores them
+  if constexpr (ACT == 3) {
+    if (blockIdx.y == 0 && wm == 0) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float v = csum[j];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        const int n = n0 + wn + 16 * j + n16;
+        if (grp == 0 && n < g.N) {
+          if (g.ksplit > 1) {
+            g.ws[(int64_t)g.ksplit * g.M * g.N + (int64_t)split * g.N + n] = v;
+          } else {
+            g.colsum[n] = g.colsum_acc ? g.colsum[n] + v : v;
+          }
+        }
+      }
     }
   }
 
@@ -485,6 +521,14 @@ int skinny_splits(int M, int K) {
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const GemmArgs g) {
   const int64_t MN = (int64_t)g.M * g.N;
   const int64_t total = MN * g.batch;
+  if (g.colsum) {  // the weight-gradient variant's column sums (batch 1)
+    for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < g.N; n += (int64_t)gridDim.x * blockDim.x) {
+      float s = 0.f;
+#pragma unroll 8
+      for (int sp = 0; sp < g.ksplit; ++sp) s += g.ws[(int64_t)g.ksplit * MN + (int64_t)sp * g.N + n];
+      g.colsum[n] = g.colsum_acc ? g.colsum[n] + s : s;
+    }
+  }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int bidx = (int)(i / MN);
@@ -525,7 +569,7 @@ Plan plan_gemm(int M, int N, int K, int batch, size_t ws_bytes) {
     int want = (int)std::min<int64_t>(K >= 4096 ? 64 : 16, (MTX_SPLIT_TARGET + t - 1) / t);
     // each split keeps >= MTX_SPLIT_MINK of K
     want = std::min(want, std::max(1, K / MTX_SPLIT_MINK));
-    const size_t need = (size_t)want * batch * (size_t)M * N * sizeof(float);
+    const size_t need = (size_t)want * batch * (size_t)(M + 1) * N * sizeof(float);
     if (want > 1 && need <= ws_bytes) {
       p.ksplit = want;
       p.kchunk = cdiv(cdiv(K, want), BK) * BK;
@@ -560,7 +604,8 @@ void launch_tile_act(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
 template <int BM, int BN>
 int launch_tile(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
   const int act = g.ksplit > 1 ? 0 : g.act;
-  if (act == 1) launch_tile_act<BM, BN, 1>(g, ak, bn1, st);
+  if (g.colsum) launch_tile_act<BM, BN, 3>(g, ak, bn1, st);
+  else if (act == 1) launch_tile_act<BM, BN, 1>(g, ak, bn1, st);
   else if (act == 2) launch_tile_act<BM, BN, 2>(g, ak, bn1, st);
   else launch_tile_act<BM, BN, 0>(g, ak, bn1, st);
   MTX_LAUNCHED();
@@ -576,20 +621,24 @@ extern "C" size_t mtx_gemm_workspace_bytes(int M, int N, int K, int batch) {
   if (M < 1 || N < 1 || K < 1 || batch < 1) return 0;
   if (const int sp = skinny_splits(M, K)) return sp > 1 ? (size_t)sp * batch * (size_t)M * N * sizeof(float) : 0;
   Plan p = plan_gemm(M, N, K, batch, (size_t)-1);
-  return p.ksplit > 1 ? (size_t)p.ksplit * batch * (size_t)M * N * sizeof(float) : 0;
+  // split partials [split][batch][M][N], then the weight-gradient variant's
+  // column sums [split][N]
+  return p.ksplit > 1 ? (size_t)p.ksplit * batch * (size_t)(M + 1) * N * sizeof(float) : 0;
 }
 
 namespace {
 int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64_t sa_m, int64_t sa_k,
               int64_t sa_b, const float* b, int64_t sb_k, int64_t sb_n, int64_t sb_b, float beta, float* c,
               int64_t sc_m, int64_t sc_n, int64_t sc_b, const float* bias, int act, float* aux, int64_t sx_m,
-              int64_t sx_n, int64_t sx_b, void* workspace, size_t workspace_bytes, void* stream) {
+              int64_t sx_n, int64_t sx_b, void* workspace, size_t workspace_bytes, void* stream,
+              float* colsum = nullptr, int colsum_acc = 0) {
   MTX_CHECK_SHAPE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "negative GEMM size");
   if (M == 0 || N == 0 || batch == 0) return MTX_OK;
   MTX_CHECK_ARG(c != nullptr, "gemm: null C");
   MTX_CHECK_ARG(K == 0 || (a != nullptr && b != nullptr), "gemm: null A or B");
-  MTX_CHECK_ARG(sa_k == 1 || sa_m == 1, "gemm: A needs a unit stride along m or k");
-  MTX_CHECK_ARG(sb_n == 1 || sb_k == 1, "gemm: B needs a unit stride along k or n");
+  // (an empty K leaves A and B unread, whatever their strides)
+  MTX_CHECK_ARG(K == 0 || sa_k == 1 || sa_m == 1, "gemm: A needs a unit stride along m or k");
+  MTX_CHECK_ARG(K == 0 || sb_n == 1 || sb_k == 1, "gemm: B needs a unit stride along k or n");
   MTX_CHECK_ARG(sc_m >= 0 && sc_n >= 0 && sa_b >= 0 && sb_b >= 0 && sc_b >= 0, "gemm: negative stride");
   MTX_CHECK_SHAPE((int64_t)batch * cdiv(M, 64) < 65535 * 64, "gemm: too many tiles");
   GemmArgs g{a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, c, sc_m, sc_n, sc_b, bias,
@@ -599,6 +648,8 @@ int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64
   g.sxm = sx_m;
   g.sxn = sx_n;
   g.sxb = sx_b;
+  g.colsum = colsum;
+  g.colsum_acc = colsum_acc;
   {
     const bool a_ok = (((uintptr_t)a) & 15u) == 0 && (sa_k == 1 ? sa_m % 4 == 0 : sa_k % 4 == 0) && sa_b % 4 == 0;
     const bool b_ok = (((uintptr_t)b) & 15u) == 0 && (sb_n == 1 ? sb_k % 4 == 0 : sb_n % 4 == 0) && sb_b % 4 == 0;
@@ -613,7 +664,7 @@ int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64
     g.kchunk = 0;
     return launch_tile<64, 64>(g, true, true, st);
   }
-  if (int sp = act ? 0 : skinny_splits(M, K)) {
+  if (int sp = (act || colsum) ? 0 : skinny_splits(M, K)) {
     MTX_CHECK_SHAPE(batch < 65536, "gemm: batch too large");
     // without room for the partials, one workgroup covers all of K
     if (sp > 1 && (!workspace || workspace_bytes < (size_t)sp * batch * (size_t)M * N * sizeof(float))) sp = 1;
@@ -671,6 +722,16 @@ extern "C" int mtx_gemm_act_f32(int M, int N, int K, int batch,
   MTX_CHECK_ARG(sx_m >= 0 && sx_n >= 0 && sx_b >= 0, "gemm_act: negative aux stride");
   return gemm_impl(M, N, K, batch, alpha, a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, beta, c, sc_m, sc_n, sc_b,
                    bias, act, act ? aux : nullptr, sx_m, sx_n, sx_b, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mtx_gemm_wgrad_f32(int M, int N, int K, const float* a, int64_t sa_m, int64_t sa_k,
+                                  const float* b, int64_t sb_k, int64_t sb_n, float beta, float* c, int64_t sc_m,
+                                  int64_t sc_n, float* dbias, int dbias_accumulate, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  MTX_CHECK_ARG(dbias != nullptr, "gemm_wgrad: null dbias (use mtx_gemm_f32 without a bias gradient)");
+  MTX_CHECK_SHAPE(M >= 1 && N >= 1 && K >= 0, "gemm_wgrad: sizes must be M, N >= 1, K >= 0");
+  return gemm_impl(M, N, K, 1, 1.f, a, sa_m, sa_k, 0, b, sb_k, sb_n, 0, beta, c, sc_m, sc_n, 0, nullptr, 0,
+                   nullptr, 0, 0, 0, workspace, workspace_bytes, stream, dbias, dbias_accumulate ? 1 : 0);
 }
 
 extern "C" int mtx_gemm_step_f32(int M, int N, int K, const float* a, int64_t lda, const float* b, int64_t ldb,

@@ -173,9 +173,11 @@ def linear(x, weight, bias=None):
             gt = g.t if x.ndim >= 2 else g.t.unsqueeze(0)
             tt = target.t if x.ndim >= 2 else target.t.unsqueeze(0)
             bmm(gt, weight.data.t.transpose(0, 1), tt, beta=1.0 if acc else 0.0)
+        db_done = False
         if weight.requires_grad:
-            matmul_grad_b(x.data, g, weight)
-        if bias is not None and bias.requires_grad:
+            db_done = matmul_grad_b(x.data, g, weight,
+                                    bias=bias if bias is not None and bias.requires_grad else None)
+        if bias is not None and bias.requires_grad and not db_done:
             target, acc = _grad_target(bias)
             K.reduce(g.t, list(range(g.ndim - 1)), target.t, accumulate=acc)
 
@@ -217,14 +219,18 @@ def linear_qkv(x, lq, lk, lv):
             gt = g.t if x.ndim >= 2 else g.t.unsqueeze(0)
             tt = target.t if x.ndim >= 2 else target.t.unsqueeze(0)
             bmm(gt, wcat.t.transpose(0, 1), tt, beta=1.0 if acc else 0.0)
+        need_db = any(b.requires_grad for b in bs)
+        db = dev.empty((1, 3 * C)) if need_db else None
         if any(w.requires_grad for w in Ws):
+            # dW and db (the column sums of dQKV) in one GEMM
             x2 = x.data.t.reshape(-1, Cin)
             dw = dev.empty((Cin, 3 * C))
-            K.gemm(x2.transpose(0, 1), g2, dw.t, 1.0, 0.0, None, M=Cin, N=3 * C, K=x2.shape[0])
+            K.gemm(x2.transpose(0, 1), g2, dw.t, 1.0, 0.0, None, M=Cin, N=3 * C, K=x2.shape[0],
+                   colsum=db.t.view(-1) if need_db else None)
             _unpack_grads(dw.t, Ws)
-        if any(b.requires_grad for b in bs):
-            db = dev.empty((1, 3 * C))
+        elif need_db:
             K.reduce(g2, [0], db.t.view(-1))
+        if need_db:
             _unpack_grads(db.t, bs, rows_view=(1, C))
 
     out = _node(data, prev, "linear_qkv", _backward, _track(*prev))
@@ -258,29 +264,34 @@ def mlp_gelu(x, fc1, fc2):
 
     def _backward():
         g2 = out.grad.t.reshape(rows, Cout)
-        if W2.requires_grad:
-            t, acc = _grad_target(W2)
-            K.gemm(a.transpose(0, 1), g2, t.t, 1.0, 1.0 if acc else 0.0, None, M=Hd, N=Cout, K=rows)
-        if b2.requires_grad:
-            t, acc = _grad_target(b2)
-            K.reduce(g2, [0], t.t, accumulate=acc)
+        _wgrad(a.transpose(0, 1), g2, W2, b2, Hd, Cout, rows)
         need_h = x.requires_grad or W1.requires_grad or b1.requires_grad
         if not need_h:
             return
         dh = torch_empty((rows, Hd), g2.dtype)
         K.gemm(g2, W2.data.t.transpose(0, 1), dh, act=K.GEMM_ACT_GELU_BWD, aux=h)
-        if W1.requires_grad:
-            t, acc = _grad_target(W1)
-            K.gemm(x2.transpose(0, 1), dh, t.t, 1.0, 1.0 if acc else 0.0, None, M=Cin, N=Hd, K=rows)
-        if b1.requires_grad:
-            t, acc = _grad_target(b1)
-            K.reduce(dh, [0], t.t, accumulate=acc)
+        _wgrad(x2.transpose(0, 1), dh, W1, b1, Cin, Hd, rows)
         if x.requires_grad:
             t, acc = _grad_target(x)
             K.gemm(dh, W1.data.t.transpose(0, 1), t.t.view(rows, Cin), 1.0, 1.0 if acc else 0.0, None)
 
     out = _node(data, prev, "mlp_gelu", _backward, _track(*prev))
     return out
+
+
+def _wgrad(at, g, W, b, M, N, rows):
+    """W.grad (+)= at @ g (at: (M, rows), g: (rows, N)) and b.grad (+)= the
+    column sums of g, in one GEMM when both are wanted."""
+    tw = tb = None
+    if W.requires_grad:
+        tw, accw = _grad_target(W)
+    if b.requires_grad:
+        tb, accb = _grad_target(b)
+    if tw is not None:
+        K.gemm(at, g, tw.t, 1.0, 1.0 if accw else 0.0, None, M=M, N=N, K=rows,
+               colsum=tb.t if tb is not None else None, colsum_accumulate=tb is not None and accb)
+    elif tb is not None:
+        K.reduce(g, [0], tb.t, accumulate=accb)
 
 
 def _unpack_grads(src, params, rows_view=None):

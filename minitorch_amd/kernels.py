@@ -328,11 +328,14 @@ GEMM_ACT_NONE, GEMM_ACT_GELU, GEMM_ACT_GELU_BWD = 0, 1, 2
 
 
 def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=1,
-         sa=None, sb=None, sc=None, act=GEMM_ACT_NONE, aux=None):
+         sa=None, sb=None, sc=None, act=GEMM_ACT_NONE, aux=None, colsum=None, colsum_accumulate=False):
     """C = alpha*A@B + beta*C (+bias) with explicit (row, col, batch) strides
     for each operand; defaults take them from 2-D/3-D tensors.  act/aux: the
     GELU epilogues of mtx_gemm_act_f32 (aux shaped like C: the pre-activation
-    written by act 1, read by act 2)."""
+    written by act 1, read by act 2).  colsum: a contiguous (N,) tensor that
+    receives (or, with colsum_accumulate, adds) the column sums of B -- a
+    Linear layer's bias gradient next to its weight gradient
+    (mtx_gemm_wgrad_f32: batch 1, alpha 1, no bias or activation)."""
     if sa is None:
         sa = (a.stride(-2), a.stride(-1), a.stride(0) if a.dim() == 3 else 0)
     if sb is None:
@@ -348,6 +351,16 @@ def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=
     # one operand stride must be unit; otherwise the caller passes a copy
     ws_bytes = L.lib().mtx_gemm_workspace_bytes(M, N, K, batch)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=c.device) if ws_bytes else None
+    if colsum is not None:
+        if batch != 1 or alpha != 1.0 or bias is not None or act != GEMM_ACT_NONE:
+            raise ValueError("gemm: colsum needs batch 1, alpha 1 and no bias or activation")
+        if colsum.dtype != torch.float32 or colsum.numel() != N or not colsum.is_contiguous():
+            raise ValueError(f"gemm: colsum must be a contiguous fp32 tensor of N={N} elements")
+        L.call("mtx_gemm_wgrad_f32", int(M), int(N), int(K), L.ptr(a), int(sa[0]), int(sa[1]),
+               L.ptr(b), int(sb[0]), int(sb[1]), float(beta), L.ptr(c), int(sc[0]), int(sc[1]),
+               L.ptr(colsum), int(bool(colsum_accumulate)),
+               L.ptr(ws) if ws is not None else None, ws_bytes, L.stream_handle())
+        return c
     if act != GEMM_ACT_NONE:
         if aux is not None:
             if tuple(aux.shape[-2:]) != (M, N) or aux.dtype != torch.float32:

@@ -113,9 +113,11 @@ def matmul_data(a: DeviceArray, b: DeviceArray) -> DeviceArray:
     return DeviceArray(out)
 
 
-def matmul_grad_b(a: DeviceArray, g: DeviceArray, other):
+def matmul_grad_b(a: DeviceArray, g: DeviceArray, other, bias=None):
     """Accumulate dB = A^T @ G, summed to B's shape, into other.grad
-    (tensor.py:216-218)."""
+    (tensor.py:216-218).  With `bias` (a Linear's bias, x @ W + b), its
+    gradient -- the column sums of G -- comes out of the same GEMM where the
+    2-D weight path applies; returns True when it did."""
     from .tensor import _accum_grad, _grad_target, _sum_to_shape
 
     at, gt = a.t, g.t
@@ -133,13 +135,18 @@ def matmul_grad_b(a: DeviceArray, g: DeviceArray, other):
             rows = int(np.prod(batch)) * ae.shape[-2]
             target, acc = _grad_target(other)
             tt = target.t if other.ndim == 2 else target.t.view(-1, 1)
+            tb, accb = (None, False)
+            if bias is not None and other.ndim == 2 and bias.ndim == 1 and bias.shape[0] == gt.shape[-1]:
+                tb, accb = _grad_target(bias)
             K.gemm(ae, gt, tt, 1.0, 1.0 if acc else 0.0, None,
                    M=ae.shape[-1], N=gt.shape[-1], K=rows, batch=1,
-                   sa=(ae.stride(-1), ra, 0), sb=(rg, gt.stride(-1), 0), sc=(tt.stride(0), tt.stride(1), 0))
-            return
+                   sa=(ae.stride(-1), ra, 0), sb=(rg, gt.stride(-1), 0), sc=(tt.stride(0), tt.stride(1), 0),
+                   colsum=tb.t if tb is not None else None, colsum_accumulate=accb)
+            return tb is not None
     res = DeviceArray(torch.empty(batch + (at.shape[-1], gt.shape[-1]), dtype=torch.float32,
                                   device=gt.device))
     bmm(at.transpose(-1, -2), gt, res.t)
     if other.ndim == 1:
         res = res.reshape(*res.shape[:-1])
     _accum_grad(other, _sum_to_shape(res, other.shape), owned=True)
+    return False

@@ -467,3 +467,41 @@ def test_gemm_gelu_epilogues(dev, M, N, K):
     K_.gemm(ta, tb, d, act=K_.GEMM_ACT_GELU_BWD, aux=h)
     ref = (a.astype(np.float64) @ b.astype(np.float64)) * dgelu
     assert np.all(np.abs(d.cpu().numpy() - ref) <= tol(ref) + 1e-5 * np.abs(ref).max())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,acc", [(384, 1152, 16384, False), (384, 65, 4096, True), (200, 130, 777, False),
+                                       (64, 48, 300, True), (7, 5, 3, False), (384, 384, 0, True)])
+def test_gemm_wgrad_colsum(dev, M, N, K, acc):
+    """mtx_gemm_wgrad_f32: dW = A @ B (+ beta C) and the column sums of B (a
+    Linear's bias gradient) from one launch, against NumPy float64.  The
+    first case takes the split-K path (the sums go through the reduce), the
+    odd shapes the edge-tile loaders, K = 0 gives C = beta C and sums of 0."""
+    import torch
+
+    from minitorch_amd import kernels as K_
+
+    _say(f"[gemm_wgrad] M={M} N={N} K={K} acc={acc}")
+    rng = np.random.default_rng(M * 7 + N + K)
+    # A as the transposed view of a (K, M) activation, as the weight gradient uses it
+    x = rng.standard_normal((K, M), dtype=np.float32)
+    g = rng.standard_normal((K, N), dtype=np.float32)
+    c0 = rng.standard_normal((M, N), dtype=np.float32)
+    s0 = rng.standard_normal(N, dtype=np.float32)
+    tx, tg = T(x), T(g)
+    c = T(c0)
+    s = T(s0)
+    beta = 1.0 if acc else 0.0
+    K_.gemm(tx.transpose(0, 1), tg, c, 1.0, beta, None, M=M, N=N, K=K, colsum=s, colsum_accumulate=acc)
+    ref_c = x.astype(np.float64).T @ g.astype(np.float64) + (c0 if acc else 0)
+    ref_s = g.astype(np.float64).sum(0) + (s0 if acc else 0)
+    close(H(c), ref_c, atol=dot_tol(max(K, 1)) * 2, name="wgrad_c")
+    close(H(s), ref_s, atol=dot_tol(max(K, 1)) * 2, name="wgrad_colsum")
+    # the same tiled product without the column sums gives the same C (M <= 64
+    # products without them take the skinny kernel instead)
+    c2 = T(c0)
+    K_.gemm(tx.transpose(0, 1), tg, c2, 1.0, beta, None, M=M, N=N, K=K)
+    if M > 64:
+        assert np.array_equal(H(c2), H(c))
+    else:
+        close(H(c2), H(c), atol=dot_tol(max(K, 1)) * 2, name="wgrad_vs_plain")
