@@ -238,6 +238,8 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
   float csum[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) csum[j] = 0.f;
+  // only the waves whose sums are stored (below) add them (wave-uniform)
+  const bool cs_wave = blockIdx.y == 0 && __builtin_amdgcn_readfirstlane(wm) == 0;
 
   constexpr int AV = BM * BK / 4 / kGT, BV = BN * BK / 4 / kGT;
   f32x4 ra[AV], rb[BV];
@@ -291,8 +293,10 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
       if constexpr (ACT == 3) {
+        if (cs_wave) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) csum[j] += bf[j];
+          for (int j = 0; j < TN; ++j) csum[j] += bf[j];
+        }
       }
     }
   }
@@ -300,7 +304,7 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
   // ACT 3: the first row of tiles (its waves 0 and 1, which together cover
   // the BN columns) adds the four lane groups' sums and stores them
   if constexpr (ACT == 3) {
-    if (blockIdx.y == 0 && wm == 0) {
+    if (cs_wave) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         float v = csum[j];
@@ -521,16 +525,19 @@ int skinny_splits(int M, int K) {
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const GemmArgs g) {
   const int64_t MN = (int64_t)g.M * g.N;
   const int64_t total = MN * g.batch;
-  if (g.colsum) {  // the weight-gradient variant's column sums (batch 1)
-    for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < g.N; n += (int64_t)gridDim.x * blockDim.x) {
+  // indices past the C elements are the weight-gradient variant's column
+  // sums (batch 1), on threads of their own
+  const int64_t extra = g.colsum ? g.N : 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total + extra;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (i >= total) {
+      const int64_t n = i - total;
       float s = 0.f;
 #pragma unroll 8
       for (int sp = 0; sp < g.ksplit; ++sp) s += g.ws[(int64_t)g.ksplit * MN + (int64_t)sp * g.N + n];
       g.colsum[n] = g.colsum_acc ? g.colsum[n] + s : s;
+      continue;
     }
-  }
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
     const int bidx = (int)(i / MN);
     const int64_t e = i % MN;
     const int m = (int)(e / g.N), n = (int)(e % g.N);
@@ -692,7 +699,7 @@ int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64
   int rc = (p.bm == 128) ? launch_tile<128, 128>(g, ak, bn1, st) : launch_tile<64, 64>(g, ak, bn1, st);
   if (rc) return rc;
   if (p.ksplit > 1) {
-    const int64_t total = (int64_t)M * N * batch;
+    const int64_t total = (int64_t)M * N * batch + (colsum ? N : 0);
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 4096);
     hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(256), 0, st, g);
     MTX_LAUNCHED();
