@@ -521,6 +521,29 @@ int skinny_splits(int M, int K) {
   return cdiv(K, kSkMaxK);
 }
 
+// Column sums of B (batch 1) for the weight-gradient entry point when its
+// product takes the skinny kernel (M <= 64): 16 columns x 16 k lanes per
+// workgroup, the lanes' sums added in lane order.
+__global__ __launch_bounds__(256) void gemm_colsum_kernel(const GemmArgs g) {
+  __shared__ float part[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int n = blockIdx.x * 16 + tx;
+  float s = 0.f;
+  if (n < g.N) {
+    const float* __restrict__ col = g.b + (int64_t)n * g.sbn;
+#pragma unroll 8
+    for (int k = ty; k < g.K; k += 16) s += col[(int64_t)k * g.sbk];
+  }
+  part[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0 && n < g.N) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += part[k][tx];
+    g.colsum[n] = g.colsum_acc ? g.colsum[n] + t : t;
+  }
+}
+
 // Sum the split-K partials in split order; apply alpha, beta, bias.
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const GemmArgs g) {
   const int64_t MN = (int64_t)g.M * g.N;
@@ -671,8 +694,13 @@ int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64
     g.kchunk = 0;
     return launch_tile<64, 64>(g, true, true, st);
   }
-  if (int sp = (act || colsum) ? 0 : skinny_splits(M, K)) {
+  if (int sp = act ? 0 : skinny_splits(M, K)) {
     MTX_CHECK_SHAPE(batch < 65536, "gemm: batch too large");
+    if (colsum) {  // the skinny kernel and its reduce leave the sums to their own kernel
+      hipLaunchKernelGGL(gemm_colsum_kernel, dim3(cdiv(N, 16)), dim3(256), 0, st, g);
+      MTX_LAUNCHED();
+      g.colsum = nullptr;
+    }
     // without room for the partials, one workgroup covers all of K
     if (sp > 1 && (!workspace || workspace_bytes < (size_t)sp * batch * (size_t)M * N * sizeof(float))) sp = 1;
     g.ksplit = sp;
