@@ -453,7 +453,9 @@ extern "C" int mtx_layernorm_fwd_f32(const float* x, int64_t ldx, const float* g
   if (vpl <= 1) LN_F(1);
   else if (vpl <= 2) LN_F(2);
   else if (vpl <= 4) LN_F(4);
+  else if (vpl <= 6) LN_F(6);
   else if (vpl <= 8) LN_F(8);
+  else if (vpl <= 12) LN_F(12);
   else if (vpl <= 16) LN_F(16);
   else LN_F(32);
 #undef LN_F
