@@ -278,7 +278,10 @@ int mtx_gemm_f32(int M, int N, int K, int batch,
  *   act 1: C = gelu(V) with V = alpha*A@B + beta*C + bias; when aux is not
  *          NULL, V (the pre-activation the backward needs) is stored to aux;
  *   act 2: C = V * gelu'(aux), aux the pre-activation (the GELU closure's
- *          grad * gelu'(x) applied to the product that yields grad).
+ *          grad * gelu'(x) applied to the product that yields grad);
+ *   act 4: C = V + aux, aux a residual stream other than C (the block's
+ *          x + attn(...) and x + mlp(...), transformer.py:64-65, as the
+ *          output projection's epilogue).
  * aux is M x N per batch with strides (sx_m, sx_n, sx_b).  gelu is the tanh
  * form with the reference's float32 constants.
  */

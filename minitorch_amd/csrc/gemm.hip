@@ -66,7 +66,8 @@ struct GemmArgs {
   const int* lengths;
   // tiled-kernel activation epilogue (mtx_gemm_act_f32): act 1 = GELU, with
   // the pre-activation value also stored to aux when aux != null; act 2 =
-  // multiply by GELU'(aux) (aux = the pre-activation read back)
+  // multiply by GELU'(aux) (aux = the pre-activation read back); act 4 = add
+  // aux (a residual stream)
   float* aux;
   int64_t sxm, sxn, sxb;
   // weight-gradient variant (mtx_gemm_wgrad_f32, batch 1): colsum[n] =
@@ -84,6 +85,7 @@ __device__ __forceinline__ float epilogue(const GemmArgs& g, float v, int bidx, 
     return gelu_tanh_fast(v);
   }
   if (g.act == 2) return v * gelu_grad_fast(g.aux[(int64_t)bidx * g.sxb + (int64_t)m * g.sxm + (int64_t)n * g.sxn]);
+  if (g.act == 4) return v + g.aux[(int64_t)bidx * g.sxb + (int64_t)m * g.sxm + (int64_t)n * g.sxn];
   return v;
 }
 
@@ -374,6 +376,8 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
             v = gelu_tanh_fast(v);
           } else if constexpr (ACT == 2) {
             v *= gelu_grad_fast(xa[j][r]);
+          } else if constexpr (ACT == 4) {
+            v += g.aux[(int64_t)bidx * g.sxb + (int64_t)m * g.sxm + (int64_t)n * g.sxn];
           }
           *p = v;
         }
@@ -637,6 +641,7 @@ int launch_tile(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
   if (g.colsum) launch_tile_act<BM, BN, 3>(g, ak, bn1, st);
   else if (act == 1) launch_tile_act<BM, BN, 1>(g, ak, bn1, st);
   else if (act == 2) launch_tile_act<BM, BN, 2>(g, ak, bn1, st);
+  else if (act == 4) launch_tile_act<BM, BN, 4>(g, ak, bn1, st);
   else launch_tile_act<BM, BN, 0>(g, ak, bn1, st);
   MTX_LAUNCHED();
   return MTX_OK;
@@ -752,8 +757,10 @@ extern "C" int mtx_gemm_act_f32(int M, int N, int K, int batch,
                                 float beta, float* c, int64_t sc_m, int64_t sc_n, int64_t sc_b,
                                 const float* bias, int act, float* aux, int64_t sx_m, int64_t sx_n,
                                 int64_t sx_b, void* workspace, size_t workspace_bytes, void* stream) {
-  MTX_CHECK_ARG(act >= 0 && act <= 2, "gemm_act: act=%d must be 0 (none), 1 (GELU) or 2 (GELU backward)", act);
+  MTX_CHECK_ARG(act == 0 || act == 1 || act == 2 || act == 4,
+                "gemm_act: act=%d must be 0 (none), 1 (GELU), 2 (GELU backward) or 4 (add aux)", act);
   MTX_CHECK_ARG(act != 2 || aux != nullptr, "gemm_act: act 2 needs the pre-activation aux");
+  MTX_CHECK_ARG(act != 4 || (aux != nullptr && aux != c), "gemm_act: act 4 needs a residual aux other than C");
   MTX_CHECK_ARG(sx_m >= 0 && sx_n >= 0 && sx_b >= 0, "gemm_act: negative aux stride");
   return gemm_impl(M, N, K, batch, alpha, a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, beta, c, sc_m, sc_n, sc_b,
                    bias, act, act ? aux : nullptr, sx_m, sx_n, sx_b, workspace, workspace_bytes, stream);

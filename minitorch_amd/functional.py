@@ -149,10 +149,13 @@ def log_softmax(x, axis=-1):
     return out
 
 
-def linear(x, weight, bias=None):
+def linear(x, weight, bias=None, residual=None):
     """x @ W + b (layers.py:31-37) as one node: bias fused into the GEMM
     epilogue; backward dX = dY W^T, dW = X^T dY (batch folded into the
-    contraction), db = column sums of dY."""
+    contraction), db = column sums of dY.  With `residual` (a tensor of the
+    output's shape) the node is residual + (x @ W + b) -- the block's
+    x + attn(...) (transformer.py:64) -- with the add in the same GEMM
+    epilogue; the residual's gradient is dY."""
     from .linalg import bmm, matmul_data, matmul_grad_b
 
     if x.shape[-1] != weight.shape[0]:
@@ -160,14 +163,24 @@ def linear(x, weight, bias=None):
     N = weight.shape[1]
     out_shape = tuple(x.shape[:-1]) + (N,)
     data = dev.empty(out_shape)
-    xt = x.data.t if x.ndim >= 2 else x.data.t.unsqueeze(0)
-    ot = data.t if x.ndim >= 2 else data.t.unsqueeze(0)
-    bmm(xt, weight.data.t, ot, bias=bias.data.t if bias is not None else None)
-    prev = (x, weight) + ((bias,) if bias is not None else ())
+    if residual is not None:
+        if tuple(residual.shape) != out_shape or x.ndim < 2:
+            raise AssertionError(f"linear: residual {tuple(residual.shape)} does not match output {out_shape}")
+        rows = int(np.prod(out_shape[:-1]))
+        x2 = x.data.t.reshape(rows, x.shape[-1])
+        K.gemm(x2, weight.data.t, data.t.view(rows, N), bias=bias.data.t if bias is not None else None,
+               act=K.GEMM_ACT_ADD, aux=residual.data.t.reshape(rows, N))
+    else:
+        xt = x.data.t if x.ndim >= 2 else x.data.t.unsqueeze(0)
+        ot = data.t if x.ndim >= 2 else data.t.unsqueeze(0)
+        bmm(xt, weight.data.t, ot, bias=bias.data.t if bias is not None else None)
+    prev = (x, weight) + ((bias,) if bias is not None else ()) + ((residual,) if residual is not None else ())
     out = None
 
     def _backward():
         g = out.grad
+        if residual is not None and residual.requires_grad:
+            _accum_grad(residual, g)
         if x.requires_grad:
             target, acc = _grad_target(x)
             gt = g.t if x.ndim >= 2 else g.t.unsqueeze(0)
@@ -237,14 +250,17 @@ def linear_qkv(x, lq, lk, lv):
     return out
 
 
-def mlp_gelu(x, fc1, fc2):
+def mlp_gelu(x, fc1, fc2, residual=None):
     """fc2(gelu(fc1(x))) -- the MLP of TransformerBlock (transformer.py:56-59:
     Linear, GELU, Linear; Linear layers.py:31-37, F.gelu functional.py:54-59)
     -- as one node.  Forward: the fc1 GEMM applies GELU in its epilogue and
     also stores the pre-activation h the backward needs; then the fc2 GEMM.
     Backward: dW2, db2 from dY; dh = (dY W2^T) * gelu'(h) as one GEMM whose
     epilogue applies the GELU derivative; then dW1, db1 and dX from dh.  The
-    two Linears keep their own parameters and state_dict keys."""
+    two Linears keep their own parameters and state_dict keys.  With
+    `residual` (shaped like the output) the node is residual + mlp(x) -- the
+    block's x + mlp(...) (transformer.py:65) -- with the add in the fc2 GEMM's
+    epilogue; the residual's gradient is dY."""
     W1, b1, W2, b2 = fc1.weight, fc1.bias, fc2.weight, fc2.bias
     Cin, Hd = W1.shape
     Cout = W2.shape[1]
@@ -258,11 +274,19 @@ def mlp_gelu(x, fc1, fc2):
     a = torch_empty((rows, Hd), x2.dtype)
     K.gemm(x2, W1.data.t, a, bias=b1.data.t, act=K.GEMM_ACT_GELU, aux=h)
     data = dev.empty(lead + (Cout,))
-    K.gemm(a, W2.data.t, data.t.view(rows, Cout), bias=b2.data.t)
-    prev = (x, W1, b1, W2, b2)
+    if residual is not None:
+        if tuple(residual.shape) != lead + (Cout,):
+            raise AssertionError(f"mlp_gelu: residual {tuple(residual.shape)} does not match output")
+        K.gemm(a, W2.data.t, data.t.view(rows, Cout), bias=b2.data.t, act=K.GEMM_ACT_ADD,
+               aux=residual.data.t.reshape(rows, Cout))
+    else:
+        K.gemm(a, W2.data.t, data.t.view(rows, Cout), bias=b2.data.t)
+    prev = (x, W1, b1, W2, b2) + ((residual,) if residual is not None else ())
     out = None
 
     def _backward():
+        if residual is not None and residual.requires_grad:
+            _accum_grad(residual, out.grad)
         g2 = out.grad.t.reshape(rows, Cout)
         _wgrad(a.transpose(0, 1), g2, W2, b2, Hd, Cout, rows)
         need_h = x.requires_grad or W1.requires_grad or b1.requires_grad

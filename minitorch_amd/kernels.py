@@ -324,7 +324,7 @@ def reduce(a, axes, out, op=L.RED_SUM, alpha: float = 1.0, accumulate=False):
 # GEMM
 # ---------------------------------------------------------------------------
 
-GEMM_ACT_NONE, GEMM_ACT_GELU, GEMM_ACT_GELU_BWD = 0, 1, 2
+GEMM_ACT_NONE, GEMM_ACT_GELU, GEMM_ACT_GELU_BWD, GEMM_ACT_ADD = 0, 1, 2, 4
 
 
 def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=1,
@@ -332,7 +332,8 @@ def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=
     """C = alpha*A@B + beta*C (+bias) with explicit (row, col, batch) strides
     for each operand; defaults take them from 2-D/3-D tensors.  act/aux: the
     GELU epilogues of mtx_gemm_act_f32 (aux shaped like C: the pre-activation
-    written by act 1, read by act 2).  colsum: a contiguous (N,) tensor that
+    written by act 1, read by act 2), or GEMM_ACT_ADD: C = ... + aux (a
+    residual stream, not C itself).  colsum: a contiguous (N,) tensor that
     receives (or, with colsum_accumulate, adds) the column sums of B -- a
     Linear layer's bias gradient next to its weight gradient
     (mtx_gemm_wgrad_f32: batch 1, alpha 1, no bias or activation)."""
@@ -366,8 +367,8 @@ def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=
             if tuple(aux.shape[-2:]) != (M, N) or aux.dtype != torch.float32:
                 raise ValueError(f"gemm: aux must be fp32 with C's shape ({M}, {N})")
             sx = (aux.stride(-2), aux.stride(-1), aux.stride(0) if aux.dim() == 3 else 0)
-        elif act == GEMM_ACT_GELU_BWD:
-            raise ValueError("gemm: the GELU backward epilogue needs aux")
+        elif act in (GEMM_ACT_GELU_BWD, GEMM_ACT_ADD):
+            raise ValueError("gemm: this epilogue needs aux")
         else:
             sx = (0, 0, 0)
         L.call("mtx_gemm_act_f32", int(M), int(N), int(K), int(batch),

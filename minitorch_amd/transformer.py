@@ -45,7 +45,10 @@ class MultiHeadAttention(Module):
         # (B, T, C) -> (B, n_head, T, head_dim), a strided view
         return x.reshape(B, T, self.n_head, self.head_dim).transpose(1, 2)
 
-    def forward(self, x):
+    def forward(self, x, residual=None):
+        """Causal self-attention of x (transformer.py:36-44).  With `residual`
+        (shaped like x) the result is residual + attention(x), the add done in
+        the output projection's GEMM epilogue."""
         B, T, C = x.shape
         drop = {}
         if self.attn_drop.p > 0.0 and self.attn_drop._training:
@@ -65,6 +68,8 @@ class MultiHeadAttention(Module):
             q, k, v = (self._split_heads(p(x), B, T) for p in projs)
             out = F.causal_attention(q, k, v, scale=scale, **drop)
         out = out.transpose(1, 2).reshape(B, T, C)
+        if residual is not None:
+            return F.linear(out, self.out_proj.weight, self.out_proj.bias, residual=residual)
         return self.out_proj(out)
 
 
@@ -158,12 +163,17 @@ class TransformerBlock(Module):
         )
 
     def forward(self, x):
-        x = x + self.attn(self.ln1(x))
+        # the residual adds (transformer.py:64-65) happen in the epilogues of
+        # the output projection and of fc2 (when the MLP's dropout is off)
+        x = self.attn(self.ln1(x), residual=x)
         fc1, act, fc2, drop = self.mlp.layers
         if (isinstance(fc1, Linear) and isinstance(act, GELU) and isinstance(fc2, Linear)
                 and fc1.bias is not None and fc2.bias is not None):
             # Linear -> GELU -> Linear as one node (GELU in the GEMM epilogues)
-            x = x + drop(F.mlp_gelu(self.ln2(x), fc1, fc2))
+            if isinstance(drop, Dropout) and (not drop._training or drop.p == 0.0):
+                x = F.mlp_gelu(self.ln2(x), fc1, fc2, residual=x)
+            else:
+                x = x + drop(F.mlp_gelu(self.ln2(x), fc1, fc2))
         else:
             x = x + self.mlp(self.ln2(x))
         return x

@@ -505,3 +505,26 @@ def test_gemm_wgrad_colsum(dev, M, N, K, acc):
         assert np.array_equal(H(c2), H(c))
     else:
         close(H(c2), H(c), atol=dot_tol(max(K, 1)) * 2, name="wgrad_vs_plain")
+
+
+@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (16384, 384, 384), (96, 80, 8192)])
+def test_gemm_residual_epilogue(dev, M, N, K):
+    """mtx_gemm_act_f32 act 4: C = A@B + bias + aux (a residual stream),
+    against NumPy float64; the K = 8192 case takes the split-K path, whose
+    reduce applies the add."""
+    import torch
+
+    from minitorch_amd import kernels as K_
+
+    _say(f"[gemm_residual] M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + 3 * N + K)
+    a = (rng.standard_normal((M, K), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
+    b = rng.standard_normal((K, N), dtype=np.float32)
+    bias = rng.standard_normal(N, dtype=np.float32)
+    res = rng.standard_normal((M, N), dtype=np.float32)
+    c = torch.empty((M, N), dtype=torch.float32, device=dev)
+    K_.gemm(T(a), T(b), c, bias=T(bias), act=K_.GEMM_ACT_ADD, aux=T(res))
+    ref = a.astype(np.float64) @ b.astype(np.float64) + bias + res
+    close(H(c), ref, atol=dot_tol(K), name="gemm_residual")
+    with pytest.raises(ValueError):
+        K_.gemm(T(a), T(b), c, act=K_.GEMM_ACT_ADD, aux=c)  # the residual cannot be C itself
