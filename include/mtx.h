@@ -103,6 +103,30 @@ int mtx_attn_bwd(int dtype, int B, int H, int Tq, int Tk, int D,
                  float scale, int causal, int accumulate, void* stream);
 
 /*
+ * mtx_attn_bwd without allocation: the same kernels and results (bit for bit),
+ * with the per-row delta held in a fixed device array the library owns
+ * (MTX_ATTN_SCRATCH_BYTES per GPU, kept until the process ends) instead of a
+ * caller workspace.  The caller passes inputs and outputs only; the call
+ * allocates nothing (no hipMalloc, no library allocation).  B*H*Tq must be at
+ * most MTX_ATTN_SCRATCH_BYTES / 4 rows (else MTX_ERR_SHAPE).  Calls that
+ * overlap on one GPU (two streams, two threads) share the array and race.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, serving loops that forbid allocation).
+ */
+#define MTX_ATTN_SCRATCH_BYTES (8u << 20)
+int mtx_attn_bwd_noalloc(int dtype, int B, int H, int Tq, int Tk, int D,
+                         const void* q, const int64_t* q_strides,
+                         const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides,
+                         const void* o, const int64_t* o_strides,
+                         const void* dout, const int64_t* do_strides,
+                         const float* lse,
+                         float* dq, const int64_t* dq_strides,
+                         float* dk, const int64_t* dk_strides,
+                         float* dv, const int64_t* dv_strides,
+                         float scale, int causal, int accumulate, void* stream);
+
+/*
  * The passes of mtx_attn_bwd, selectable by a bit mask, so a caller can time
  * them separately.  Same arguments as mtx_attn_bwd.  DELTA writes
  * delta = rowsum(dO*O) to the workspace; DKDV and DQ read it.  When DELTA and

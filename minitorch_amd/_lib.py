@@ -20,6 +20,7 @@ LIB_PATH = _PKG / "libmtx_hip.so"
 
 MTX_OK, MTX_ERR_ARG, MTX_ERR_SHAPE, MTX_ERR_DTYPE, MTX_ERR_HIP = range(5)
 MTX_F32, MTX_BF16 = 0, 1
+ATTN_SCRATCH_BYTES = 8 << 20  # MTX_ATTN_SCRATCH_BYTES (include/mtx.h)
 ATTN_BWD_DELTA, ATTN_BWD_DKDV, ATTN_BWD_DQ, ATTN_BWD_ALL = 1, 2, 4, 7
 
 _P = C.c_void_p
@@ -54,6 +55,11 @@ SIGNATURES = {
                                 _P,
                                 _P, _I64P, _P, _I64P, _P, _I64P,
                                 _P, _SZ, _F, _I, _I, _P]),
+    "mtx_attn_bwd_noalloc": (_I, [_I, _I, _I, _I, _I, _I,
+                                  _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
+                                  _P,
+                                  _P, _I64P, _P, _I64P, _P, _I64P,
+                                  _F, _I, _I, _P]),
     "mtx_attn_fwd_dropout": (_I, [_I, _I, _I, _I, _I, _I,
                                   _P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P,
                                   _P, _F, _I, _P, _I64, _F, _P]),

@@ -28,6 +28,7 @@
 #include "mtx_common.h"
 
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 // 1: the dK/dV tile body is instantiated twice (masked diagonal tiles,
@@ -1374,6 +1375,44 @@ extern "C" int mtx_attn_fwd_dropout(int dtype, int B, int H, int Tq, int Tk, int
                        lse, scale, causal, keep, keep_ld, keep_scale, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Backward without allocation: the delta rows live in a file-scope device
+// array instead of a caller-supplied workspace.  Each GPU holds its own copy
+// (MTX_ATTN_SCRATCH_BYTES, kept until the process ends); host code reaches it
+// only through the address hipGetSymbolAddress returns for the current device,
+// looked up once per device (at mtx_device_init, or on the first call).  Calls
+// that overlap on one GPU share the array and race.  Nothing in it needs to
+// start at zero: the dQ pass writes every delta row before the dK/dV pass
+// reads it.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[MTX_ATTN_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_rc[kMaxDevices];
+}  // namespace
+
+namespace mtx {
+// Address of the current device's scratch array (looked up on first use).
+int attn_scratch(void** out) {
+  int dev = -1;
+  MTX_HIP(hipGetDevice(&dev));
+  MTX_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+  });
+  if (g_scratch_rc[dev] != hipSuccess)
+    return fail(MTX_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(g_scratch_rc[dev]));
+  *out = g_scratch_ptr[dev];
+  return MTX_OK;
+}
+}  // namespace mtx
+
 extern "C" size_t mtx_attn_bwd_workspace_bytes(int B, int H, int Tq) {
   if (B < 1 || H < 1 || Tq < 1) return 0;
   return (size_t)B * H * Tq * sizeof(float);
@@ -1392,7 +1431,8 @@ int attn_bwd_impl(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
                             float* dv, const int64_t* dv_strides,
                             void* workspace, size_t workspace_bytes,
                             float scale, int causal, int accumulate,
-                            const uint8_t* keep, int64_t keep_ld, float keep_scale, void* stream) {
+                            const uint8_t* keep, int64_t keep_ld, float keep_scale, void* stream,
+                            bool use_scratch = false) {
   MTX_CHECK_ARG(phases > 0 && (phases & ~MTX_ATTN_BWD_ALL) == 0, "bad phase mask %d", phases);
   int rc = check_dims(dtype, B, H, Tq, Tk, D, causal);
   if (rc) return rc;
@@ -1406,12 +1446,15 @@ int attn_bwd_impl(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
   if ((rc = check_bhtd("dk", dk, dk_strides, 4))) return rc;
   if ((rc = check_bhtd("dv", dv, dv_strides, 4))) return rc;
   MTX_CHECK_ARG(lse != nullptr, "lse: null pointer");
-  MTX_CHECK_ARG(workspace != nullptr, "workspace: null pointer");
-  MTX_CHECK_ARG(workspace_bytes >= mtx_attn_bwd_workspace_bytes(B, H, Tq),
-                "workspace too small: %zu < %zu bytes", workspace_bytes,
-                mtx_attn_bwd_workspace_bytes(B, H, Tq));
+  if (!use_scratch) {
+    MTX_CHECK_ARG(workspace != nullptr, "workspace: null pointer");
+    MTX_CHECK_ARG(workspace_bytes >= mtx_attn_bwd_workspace_bytes(B, H, Tq),
+                  "workspace too small: %zu < %zu bytes", workspace_bytes,
+                  mtx_attn_bwd_workspace_bytes(B, H, Tq));
+  }
   MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
   if ((rc = check_keep(keep, keep_ld, keep_scale, Tk))) return rc;
+  if (use_scratch && (rc = attn_scratch(&workspace))) return rc;  // after validation: no HIP call before it
   BwdArgs a{q, s3(q_strides), k, s3(k_strides), v, s3(v_strides), o, s3(o_strides),
             dout, s3(do_strides), lse, static_cast<float*>(workspace),
             dq, s3(dq_strides), dk, s3(dk_strides), dv, s3(dv_strides),
@@ -1459,6 +1502,30 @@ extern "C" int mtx_attn_bwd_dropout(int dtype, int B, int H, int Tq, int Tk, int
                        v_strides, o, o_strides, dout, do_strides, lse, dq, dq_strides, dk, dk_strides,
                        dv, dv_strides, workspace, workspace_bytes, scale, causal, accumulate, keep,
                        keep_ld, keep_scale, stream);
+}
+
+extern "C" int mtx_attn_bwd_noalloc(int dtype, int B, int H, int Tq, int Tk, int D,
+                                    const void* q, const int64_t* q_strides,
+                                    const void* k, const int64_t* k_strides,
+                                    const void* v, const int64_t* v_strides,
+                                    const void* o, const int64_t* o_strides,
+                                    const void* dout, const int64_t* do_strides,
+                                    const float* lse,
+                                    float* dq, const int64_t* dq_strides,
+                                    float* dk, const int64_t* dk_strides,
+                                    float* dv, const int64_t* dv_strides,
+                                    float scale, int causal, int accumulate, void* stream) {
+  MTX_CHECK_SHAPE(B >= 1 && H >= 1 && Tq >= 1, "B,H,Tq must be >= 1 (got %d,%d,%d)", B, H, Tq);
+  const size_t need = mtx_attn_bwd_workspace_bytes(B, H, Tq);
+  MTX_CHECK_SHAPE(need <= (size_t)MTX_ATTN_SCRATCH_BYTES,
+                  "mtx_attn_bwd_noalloc: B*H*Tq = %lld rows need %zu bytes of delta, more than the "
+                  "library's fixed %zu-byte scratch (B*H*Tq <= %zu); use mtx_attn_bwd with a workspace",
+                  (long long)B * H * Tq, need, (size_t)MTX_ATTN_SCRATCH_BYTES,
+                  (size_t)MTX_ATTN_SCRATCH_BYTES / sizeof(float));
+  return attn_bwd_impl(MTX_ATTN_BWD_ALL, dtype, B, H, Tq, Tk, D, q, q_strides, k, k_strides, v,
+                       v_strides, o, o_strides, dout, do_strides, lse, dq, dq_strides, dk, dk_strides,
+                       dv, dv_strides, nullptr, (size_t)MTX_ATTN_SCRATCH_BYTES, scale, causal, accumulate,
+                       nullptr, 0, 1.f, stream, /*use_scratch=*/true);
 }
 
 extern "C" int mtx_attn_bwd(int dtype, int B, int H, int Tq, int Tk, int D,

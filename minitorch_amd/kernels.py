@@ -248,6 +248,25 @@ def attn_bwd(q, k, v, out, dout, lse, scale: float, causal: bool = True,
     return dq, dk, dv
 
 
+def attn_bwd_noalloc(q, k, v, out, dout, lse, scale: float, causal: bool, dq, dk, dv,
+                     accumulate: bool = False):
+    """mtx_attn_bwd_noalloc: attn_bwd into caller-given dq/dk/dv with the
+    library's fixed device scratch for delta (no allocation of any kind; at
+    most ATTN_SCRATCH_BYTES / 4 rows B*H*Tq)."""
+    _need_cuda(q, k, v, out, dout, lse, dq, dk, dv)
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out), ("dout", dout), ("dq", dq), ("dk", dk),
+                    ("dv", dv)):
+        _bhtd(name, t)
+    B, H, Tq, D = q.shape
+    Tk = k.shape[2]
+    L.call("mtx_attn_bwd_noalloc", L.dtype_code(q), B, H, Tq, Tk, D,
+           L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
+           L.ptr(out), L.strides(out), L.ptr(dout), L.strides(dout), L.ptr(lse),
+           L.ptr(dq), L.strides(dq), L.ptr(dk), L.strides(dk), L.ptr(dv), L.strides(dv),
+           float(scale), int(bool(causal)), int(bool(accumulate)), L.stream_handle(q.device))
+    return dq, dk, dv
+
+
 # ---------------------------------------------------------------------------
 # generic elementwise / reductions
 # ---------------------------------------------------------------------------
