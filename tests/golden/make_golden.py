@@ -213,6 +213,8 @@ def main():
     ap.add_argument("--only-c2", action="store_true")
     ap.add_argument("--only-sampling", action="store_true")
     ap.add_argument("--only-dropout", action="store_true")
+    ap.add_argument("--c2-out", default=str(HERE / "c2_train.npz"),
+                    help="where the C2 curve goes (a long run can write beside the committed fixture)")
     args = ap.parse_args()
     if args.only_sampling:
         sampling(HERE / "sampling_c0.npz")
@@ -230,7 +232,7 @@ def main():
         train_curve_dropout(C0, 0, 16, 10, 0.1, 1234, HERE / "c0_train_dropout.npz")
     if args.c2 or args.only_c2:
         print("C2 training, 20 steps")
-        train_curve(C2, 2, 64, 20, HERE / "c2_train.npz")
+        train_curve(C2, 2, 64, 20, Path(args.c2_out))
 
 
 if __name__ == "__main__":
