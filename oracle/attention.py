@@ -235,3 +235,88 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
     u = x.view(np.uint32).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
     return r.astype(np.uint32).view(F32)
+
+
+LOG2E = 1.4426950408889634
+
+
+def _lazy_reference(s2, tile, tau):
+    """The forward kernel's running reference per row: key tiles of `tile`
+    keys in ascending order; the reference is set by the first tile with a
+    visible key and moved to a later tile's max only when that max exceeds it
+    by more than `tau` (log2 units).  Returns m_t (..., Tq, ntile): the
+    reference in effect while tile t's probabilities are formed."""
+    Tk = s2.shape[-1]
+    nt = (Tk + tile - 1) // tile
+    m = np.full(s2.shape[:-1], -np.inf)
+    out = np.empty(s2.shape[:-1] + (nt,))
+    for t in range(nt):
+        tm = s2[..., t * tile:(t + 1) * tile].max(axis=-1)
+        fresh = ~np.isfinite(m)
+        move = np.where(fresh, np.isfinite(tm), tm - np.where(fresh, 0.0, m) > tau)
+        m = np.where(move, tm, m)
+        out[..., t] = m
+    return out
+
+
+def attention_bf16_emulated(q, k, v, dout, scale, causal=True, rounding=True, tile=64, tau=8.0):
+    """The bf16 kernels' arithmetic (mtx_attn_fwd / mtx_attn_bwd with bf16
+    inputs) restated in float64 with bf16 round-to-nearest-even at exactly
+    the points where the kernels round, for elementwise checks of the GPU
+    results (the reference, transformer.py:36-44, has no bf16 path; its
+    mathematics is attention_f64's).
+
+    q, k, v, dout: bf16-valued float32 arrays (..., T, D).  The kernels round
+      * the register operand pre-multiplied by c = scale*log2(e): Q*c in the
+        forward and dQ passes, K*c in the dK/dV pass (scores come out in log2
+        units);
+      * the forward probabilities exp2(s - m_t) before P V and the row sum,
+        with the running reference m_t of _lazy_reference (earlier tiles are
+        rescaled by exp2(m_t - m_final) in fp32);
+      * the output O (stored as bf16; delta = rowsum(dO * O) uses it);
+      * P before dV = P^T dO, and dS = P (dP - delta) before dK = scale dS^T Q
+        and dQ = scale dS K (P and dS themselves are formed in fp32 from the
+        unrounded scores).
+    rounding=False skips every rounding (then the result is attention_f64's
+    up to float64 rounding).  Returns (out, lse, dq, dk, dv) in float64."""
+    R = bf16_round if rounding else (lambda x: np.asarray(x, dtype=F64))
+    q32, k32, v32, g32 = (np.asarray(a, dtype=F32) for a in (q, k, v, dout))
+    q64, k64, v64, g64 = (a.astype(F64) for a in (q32, k32, v32, g32))
+    c = F32(F32(scale) * F32(LOG2E)) if rounding else scale * LOG2E
+    qs = R(q32 * c).astype(F64) if rounding else q64 * c
+    ks = R(k32 * c).astype(F64) if rounding else k64 * c
+    Tq, Tk = q32.shape[-2], k32.shape[-2]
+    hidden = causal_mask(Tq, Tk) if causal else np.zeros((Tq, Tk), bool)
+
+    # forward: S^T = K (Q c)^T, lazy reference, bf16 P for P V and the row sum
+    s2 = np.where(hidden, -np.inf, qs @ np.swapaxes(k64, -1, -2))
+    mt = _lazy_reference(s2, tile, tau)
+    m_fin = mt[..., -1:]
+    pt = np.empty_like(s2)
+    w = np.empty_like(s2)
+    for t in range(mt.shape[-1]):
+        sl = slice(t * tile, (t + 1) * tile)
+        mref = mt[..., t:t + 1]
+        e = np.where(np.isfinite(s2[..., sl]), np.exp2(s2[..., sl] - np.where(np.isfinite(mref), mref, 0.0)), 0.0)
+        pt[..., sl] = R(e).astype(F64)
+        w[..., sl] = np.exp2(np.where(np.isfinite(mref), mref - m_fin, 0.0))
+    pw = pt * w
+    l = pw.sum(axis=-1, keepdims=True)
+    out = (pw @ v64) / l
+    lse = (m_fin[..., 0] + np.log2(l[..., 0])) * np.log(2.0)
+    ob = R(out).astype(F64)
+
+    # backward
+    delta = (g64 * ob).sum(axis=-1, keepdims=True)
+    nl = lse[..., None] * LOG2E
+    dp = g64 @ np.swapaxes(v64, -1, -2)
+    # dK/dV pass: S = Q (K c)^T
+    pk = np.where(hidden, 0.0, np.exp2(np.where(hidden, 0.0, q64 @ np.swapaxes(ks, -1, -2)) - nl))
+    dsk = pk * (dp - delta)
+    dv = np.swapaxes(R(pk).astype(F64), -1, -2) @ g64
+    dk = scale * (np.swapaxes(R(dsk).astype(F64), -1, -2) @ q64)
+    # dQ pass: S^T = K (Q c)^T
+    pq = np.where(hidden, 0.0, np.exp2(np.where(hidden, 0.0, qs @ np.swapaxes(k64, -1, -2)) - nl))
+    dsq = pq * (dp - delta)
+    dq = scale * (R(dsq).astype(F64) @ k64)
+    return ob if rounding else out, lse, dq, dk, dv

@@ -137,6 +137,46 @@ def test_bf16_round_is_rne():
 # GPT pieces vs torch float64 and finite differences
 # ---------------------------------------------------------------------------
 
+def test_bf16_emulation_pinned():
+    """attention_bf16_emulated (the bf16 kernels' rounding points): without
+    rounding it is attention_f64 to float64 precision for causal, non-causal
+    and Tq < Tk, so its structure (every product, the lazy reference and its
+    tile weights, delta, the scale) is the reference mathematics; with
+    rounding the error against float64 is nonzero and within the size bf16
+    rounding of P, dS and the pre-scaled operand gives (2^-9 relative per
+    rounding)."""
+    rng = np.random.default_rng(21)
+    for (B, H, Tq, Tk, D, causal) in [(1, 2, 150, 150, 64, True), (2, 1, 70, 70, 16, False),
+                                      (1, 1, 40, 130, 32, True)]:
+        q = A.bf16_round(0.5 * rng.standard_normal((B, H, Tq, D), dtype=np.float32))
+        k, v = (A.bf16_round(0.5 * rng.standard_normal((B, H, Tk, D), dtype=np.float32)) for _ in range(2))
+        do = A.bf16_round(rng.standard_normal((B, H, Tq, D), dtype=np.float32))
+        ref = A.attention_f64(q, k, v, do, 1 / np.sqrt(D), causal)
+        _, lse = A.flash_forward(q, k, v, 1 / np.sqrt(D), causal)
+        refs = (ref[0], lse, ref[2], ref[3], ref[4])
+        exact = A.attention_bf16_emulated(q, k, v, do, 1 / np.sqrt(D), causal, rounding=False)
+        rounded = A.attention_bf16_emulated(q, k, v, do, 1 / np.sqrt(D), causal)
+        for name, e, r, b in zip(("out", "lse", "dq", "dk", "dv"), exact, refs, rounded):
+            amax = np.abs(r).max()
+            assert np.abs(e - r).max() <= 1e-12 * amax, name
+            rel = np.linalg.norm(b - r) / np.linalg.norm(r)
+            assert 1e-6 < rel < 1e-2, (name, rel)
+    # a tile reference that moves (scores growing along the keys) still
+    # reproduces the exact softmax: the tile weights exp2(m_t - m_final)
+    T = 200
+    q = np.ones((1, 1, T, 16), np.float32)
+    k = (np.arange(T, dtype=np.float32)[:, None] * np.ones((1, 16), np.float32) / 8)[None, None]
+    v = A.bf16_round(rng.standard_normal((1, 1, T, 16), dtype=np.float32))
+    do = A.bf16_round(rng.standard_normal((1, 1, T, 16), dtype=np.float32))
+    mt = A._lazy_reference(np.where(A.causal_mask(T, T), -np.inf,
+                                    (q[0, 0].astype(np.float64) * 0.25 * A.LOG2E) @ k[0, 0].T.astype(np.float64)),
+                           64, 8.0)
+    assert len(np.unique(mt[-1])) > 1  # the last row's reference moved
+    e = A.attention_bf16_emulated(q, k, v, do, 0.25, True, rounding=False)
+    r = A.attention_f64(q, k, v, do, 0.25, True)
+    assert np.abs(e[0] - r[0]).max() <= 1e-12 * np.abs(r[0]).max()
+
+
 def test_layernorm_gelu_ce_match_torch_f64():
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(21)
