@@ -44,54 +44,85 @@ def attn_flops(B, H, T, D):
     return 2 * u, 5 * u
 
 
-def _events():
-    import torch
+class _Event:
+    """A HIP event of the library runtime (mtx_event_*), recorded on the
+    stream the package launches on."""
 
-    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    def __init__(self):
+        import ctypes as C
+
+        from minitorch_amd import _lib as L
+
+        self._C, self._L = C, L
+        self.h = C.c_void_p()
+        L.call("mtx_event_create", C.byref(self.h))
+
+    def record(self):
+        self._L.call("mtx_event_record", self.h, self._L.stream_handle())
+
+    def elapsed_time(self, end) -> float:
+        ms = self._C.c_float(0.0)
+        self._L.call("mtx_event_elapsed_ms", self.h, end.h, self._C.byref(ms))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            self._L.lib().mtx_event_destroy(self.h)
+        except Exception:
+            pass
+
+
+def _events():
+    return _Event(), _Event()
+
+
+def _sync():
+    from minitorch_amd import device as D
+
+    D.synchronize()
 
 
 def time_loop(fn, steps, warmup):
     """Average ms per call of fn() over `steps` calls after `warmup` calls,
-    bracketed by device synchronisation and HIP events on the current stream."""
-    import torch
-
+    bracketed by device synchronisation and HIP events on the launch stream."""
     for _ in range(warmup):
         fn()
-    torch.cuda.synchronize()
+    _sync()
     e0, e1 = _events()
     e0.record()
     for _ in range(steps):
         fn()
     e1.record()
-    torch.cuda.synchronize()
+    _sync()
     return e0.elapsed_time(e1) / steps
 
 
 def make_inputs(B, H, T, D, dtype, seed, scale_qkv):
-    """Seeded inputs, drawn q, k, v, dO in that order; bf16 rounding (RNE) by
-    the device cast.  Returns (host fp32 copies of the device values, device
-    tensors)."""
-    import torch
+    """Seeded inputs, drawn q, k, v, dO in that order; bf16 rounding (RNE) on
+    the host copy to the device.  Returns (host fp32 copies of the device
+    values, device arrays)."""
+    from minitorch_amd import device as Dv
+    from oracle.attention import bf16_round
 
     rng = np.random.default_rng(seed)
     shp = (B, H, T, D)
     arrs = [scale_qkv * rng.standard_normal(shp, dtype=np.float32) for _ in range(3)]
     arrs.append(rng.standard_normal(shp, dtype=np.float32))
-    dev = [torch.from_numpy(a).to("cuda").to(dtype) for a in arrs]
-    host = [t.float().cpu().numpy() for t in dev]
+    dev = [Dv.from_host(a, dtype).t for a in arrs]
+    host = [bf16_round(a) if dtype == "bfloat16" else a for a in arrs]
     return host, dev
 
 
 def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup):
-    import torch
     from minitorch_amd import _lib as L
+    from minitorch_amd import device as Dv
     from minitorch_amd import kernels as K
 
     arrs, (q, k, v, do) = make_inputs(B, H, T, D, dtype, seed, scale_qkv)
     scale = 1.0 / math.sqrt(D)
     o, lse = K.attn_fwd(q, k, v, scale, True)
     dq, dk, dv = K.attn_bwd(q, k, v, o, do, lse, scale, True)
-    ws = torch.empty(L.lib().mtx_attn_bwd_workspace_bytes(B, H, T), dtype=torch.uint8, device="cuda")
+    ws = Dv.empty_buf((L.lib().mtx_attn_bwd_workspace_bytes(B, H, T),), "uint8")
 
     def step():
         K.attn_fwd(q, k, v, scale, True, out=o, lse=lse)
@@ -105,7 +136,7 @@ def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup):
     for name, mask in (("dq", L.ATTN_BWD_DELTA | L.ATTN_BWD_DQ), ("dkdv", L.ATTN_BWD_DKDV)):
         ph[name] = time_loop(lambda m=mask: K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk,
                                                        dv=dv, workspace=ws, phases=m), steps, 2)
-    torch.cuda.synchronize()
+    _sync()
     return dict(ms_step=ms_step, ms_fwd=ms_fwd, **{f"ms_{k}": v for k, v in ph.items()}), arrs
 
 
@@ -153,10 +184,10 @@ def bench_c4(n_new=224):
     generate call, ids on the host at the end.  Also times the decode
     attention kernel alone at the longest step (L = 256, fp32 cache) with HIP
     events and reports its read bandwidth (K and V once)."""
-    import torch
-
     import minitorch_amd as mt
+    from minitorch_amd import device as Dv
     from minitorch_amd import kernels as K
+    from minitorch_amd.graphs import Graph
 
     c = C2_CFG
     model = mt.GPT(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"], dropout=0.0)
@@ -164,7 +195,7 @@ def bench_c4(n_new=224):
     model.eval()
     prompts = np.random.default_rng(4).integers(0, c["vocab"], (64, 32))
     model.generate_greedy(prompts, 8)  # warm-up (library load, allocator)
-    torch.cuda.synchronize()
+    _sync()
     best = None
     for _ in range(2):
         t0 = time.perf_counter()
@@ -174,25 +205,21 @@ def bench_c4(n_new=224):
     assert toks.shape == (64, 32 + n_new)
     # decode kernel alone, L = 256
     B, H, L, D = 64, c["n_head"], 256, c["n_embd"] // c["n_head"]
-    g = torch.Generator(device="cuda").manual_seed(4)
-    q = torch.randn((B, H, 1, D), device="cuda", generator=g)
-    kc = torch.randn((B, L, H * D), device="cuda", generator=g)
-    vc = torch.randn((B, L, H * D), device="cuda", generator=g)
+    g = np.random.default_rng(4)
+    q = Dv.from_host(g.standard_normal((B, H, 1, D), dtype=np.float32)).t
+    kc = Dv.from_host(g.standard_normal((B, L, H * D), dtype=np.float32)).t
+    vc = Dv.from_host(g.standard_normal((B, L, H * D), dtype=np.float32)).t
     heads = lambda t: t.view(B, L, H, D).transpose(1, 2)
-    out = torch.empty_like(q)
+    out = Dv.empty_buf(q.shape)
     # 20 launches recorded in a HIP graph and replayed: launched one by one
     # from Python the loop is bound by the host's per-call path (~17 us),
     # not by the kernel
     launch = lambda: K.attn_decode(q, heads(kc), heads(vc), D ** -0.5, out=out)
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        launch()
-        launch()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    launch()
+    launch()
+    _sync()
+    graph = Graph()
+    with graph.capture():
         for _ in range(20):
             launch()
     ms = time_loop(graph.replay, 20, 3) / 20
@@ -215,8 +242,6 @@ def bench_gpt(c, seed, steps, warmup, graph=False):
     replayed from then on (each call copies its batch into the recorded
     step's input buffers), so the host's per-kernel dispatch leaves the
     timed loop.  Returns ms per step and the losses of the timed steps."""
-    import torch
-
     import minitorch_amd as mt
     from minitorch_amd import device as D
 
@@ -251,7 +276,7 @@ def bench_gpt(c, seed, steps, warmup, graph=False):
 
     for i in range(warmup):
         step(i)
-    torch.cuda.synchronize()
+    _sync()
     e0, e1 = _events()
     e0.record()
     last = []
@@ -260,8 +285,8 @@ def bench_gpt(c, seed, steps, warmup, graph=False):
         # a replayed step overwrites the recorded loss buffer: keep a copy
         last.append(loss.data.t.clone() if graph else loss)
     e1.record()
-    torch.cuda.synchronize()
-    losses = [float(l_.cpu()) if isinstance(l_, torch.Tensor) else float(l_) for l_ in last]
+    _sync()
+    losses = [float(l_.numpy()) if isinstance(l_, D.DevBuf) else float(l_) for l_ in last]
     return e0.elapsed_time(e1) / steps, losses
 
 
@@ -320,6 +345,32 @@ def pmc_traffic(kernel):
         return None
 
 
+def host_info():
+    """CPU model, visible cores and NumPy's BLAS, for the CPU-baseline record."""
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    blas = None
+    try:
+        cfg = np.show_config(mode="dicts")
+        b = cfg.get("Build Dependencies", {}).get("blas", {})
+        blas = f"{b.get('name', '?')} {b.get('version', '')}".strip()
+    except Exception:
+        pass
+    try:
+        ncpu = len(os.sched_getaffinity(0))
+    except Exception:
+        ncpu = os.cpu_count()
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": ncpu,
+            "numpy": np.__version__, "blas": blas, "blas_threads": blas_threads()}
+
+
 def blas_threads():
     for var in ("OPENBLAS_NUM_THREADS", "OMP_NUM_THREADS", "MKL_NUM_THREADS"):
         if os.environ.get(var):
@@ -349,19 +400,23 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    import torch
+    from minitorch_amd import device as Dv
 
-    if not torch.cuda.is_available():
-        print("no GPU visible", file=sys.stderr)
+    try:
+        Dv.device()
+    except RuntimeError as e:
+        print(f"no GPU visible: {e}", file=sys.stderr)
         sys.exit(1)
 
     if args.calibrate_copy:
+        from minitorch_amd import kernels as K
+
         n = args.calibrate_copy * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
+        src = Dv.full((n,), 1.0).t
+        dst = Dv.empty_buf((n,))
         for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+            K.ewise("COPY", dst, src)
+        _sync()
         print(f"[bench] copied {args.calibrate_copy} MiB x5", file=sys.stderr)
         return
     if args.only in ("gpt2", "gpt0"):
@@ -375,7 +430,7 @@ def main():
         print(f"[bench] C4 {bench_c4()}", file=sys.stderr)
         return
     if args.only == "c1":
-        r1, _ = bench_attention(32, 8, 256, 64, torch.float32, 1, 1.0, args.steps, args.warmup)
+        r1, _ = bench_attention(32, 8, 256, 64, "float32", 1, 1.0, args.steps, args.warmup)
         print(f"[bench] C1 {r1}", file=sys.stderr)
         return
 
@@ -383,7 +438,7 @@ def main():
     B, H, T, D = 8, 16, 2048, 64
     print(f"[bench] C3 bf16 B={B} H={H} T={T} D={D}: {args.warmup} warmup + {args.steps} steps",
           file=sys.stderr, flush=True)
-    r3, arrs3 = bench_attention(B, H, T, D, torch.bfloat16, 3, 0.5, args.steps, args.warmup)
+    r3, arrs3 = bench_attention(B, H, T, D, "bfloat16", 3, 0.5, args.steps, args.warmup)
     f3, b3 = attn_flops(B, H, T, D)
     tflops = (f3 + b3) / (r3["ms_step"] * 1e-3) / 1e12
     # dominant kernel and its algorithmic FLOPs: fwd kernel = 2u; dK/dV pass =
@@ -402,14 +457,15 @@ def main():
 
     # ---- C1: fp32 ----
     print("[bench] C1 fp32 B=32 H=8 T=256 D=64", file=sys.stderr, flush=True)
-    r1, _ = bench_attention(32, 8, 256, 64, torch.float32, 1, 1.0, args.steps, args.warmup)
+    r1, _ = bench_attention(32, 8, 256, 64, "float32", 1, 1.0, args.steps, args.warmup)
     f1, b1 = attn_flops(32, 8, 256, 64)
     tflops1 = (f1 + b1) / (r1["ms_step"] * 1e-3) / 1e12
 
     # ---- GPT training: C2 (GPT-small char model) and C0 (tiny) ----
     print("[bench] GPT C2 training (B=64, T=256, 6x384)", file=sys.stderr, flush=True)
-    ms_c2, losses_c2 = bench_gpt(C2_CFG, 2, max(3, args.steps // 4), 3, graph=True)
-    ms_c2_eager, _ = bench_gpt(C2_CFG, 2, max(3, args.steps // 4), 2)
+    # the mean over 20 steps, the length of the compared loss curve
+    ms_c2, losses_c2 = bench_gpt(C2_CFG, 2, 20, 3, graph=True)
+    ms_c2_eager, _ = bench_gpt(C2_CFG, 2, 5, 2)
     tok_c2 = C2_CFG["B"] * C2_CFG["block"] / (ms_c2 * 1e-3)
     fl_c2 = gpt_flops_per_step(C2_CFG)
     print(f"[bench] C2 {ms_c2:.2f} ms/step = {tok_c2:.0f} tokens/s, losses {losses_c2}", file=sys.stderr,
@@ -432,8 +488,7 @@ def main():
                "sample": f"{nsl} of {B * H} (b,h) slices of C3 (T=2048, D=64), fwd+bwd through the "
                          f"NumPy restatement of the reference sub-graph (fp32 q@k^T, fp64 from the "
                          f"scale on), {dt:.1f}s; TFLOP/s on the algorithmic causal count",
-               "host": platform.processor() or platform.machine(),
-               "numpy": np.__version__}
+               "host": host_info()}
         print("[bench] CPU baseline, GPT C2 step on 1 sequence (NumPy restatement)", file=sys.stderr, flush=True)
         tps2, n2, dt2 = cpu_baseline_gpt(C2_CFG, args.cpu_budget / 2, 1)
         tps0, n0, dt0 = cpu_baseline_gpt(C0_CFG, 3.0, C0_CFG["B"])

@@ -18,8 +18,11 @@
  *    (B,H,T,D) take 4 strides {b,h,t,d}; the d stride must be 1.
  *  - `stream` is a hipStream_t (NULL = the null stream).  Calls are
  *    asynchronous with respect to the host.
- *  - The library allocates nothing on its own: workspaces are sized by a
- *    *_workspace_bytes query and passed in by the caller.
+ *  - Compute entry points allocate nothing: workspaces are sized by a
+ *    *_workspace_bytes query and passed in by the caller.  Device memory may
+ *    come from any allocator; the library's own caching allocator
+ *    (mtx_malloc, with copies, streams, events and graphs, at the end of this
+ *    header) lets a caller use the library with no other GPU framework.
  *  - dtype codes: MTX_F32 (fp32 in / fp32 compute) and MTX_BF16 (bf16 storage,
  *    fp32 accumulation).
  */
@@ -487,6 +490,78 @@ int mtx_adam_bias_table(double beta1, double beta2, int first_step, int len, flo
 int mtx_adam_dev_f32(const void* table, int ntensors, int64_t total_blocks, double lr, double beta1,
                      double beta2, double eps, double weight_decay, int* step, const float* bias_table,
                      int table_len, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Runtime: devices, memory, copies, streams, events, graphs                 */
+/* ------------------------------------------------------------------------ */
+/*
+ * What the reference gets from NumPy (tensor.py:50-61: a Tensor owns its data
+ * array; .data is read on the host) a caller of this library gets here, with
+ * no other GPU framework: device memory it owns, copies to and from the host,
+ * a stream to order work on, events to time it and HIP graphs to replay it.
+ * The compute entry points above still take any device pointers.
+ */
+/* Number of visible GPUs (0, and MTX_OK, on a machine without one). */
+int mtx_device_count(int* n);
+/* Make `device` current for this thread and set up its per-device state. */
+int mtx_device_init(int device);
+/* Wait for all work on the current device. */
+int mtx_device_sync(void);
+
+/*
+ * Caching allocator.  mtx_malloc returns device memory of at least `bytes`
+ * (256-byte aligned); mtx_free gives it back to the library's cache, from
+ * which later requests of about the same size are served without hipMalloc.
+ * Reuse follows stream order: memory freed after the last work that uses it
+ * was issued may be handed to the next request, so callers that use more than
+ * one stream synchronise before freeing memory another stream still uses.
+ * During a graph capture (mtx_graph_begin .. mtx_graph_end) freed blocks go
+ * to that graph's private pool and are not handed out outside the graph while
+ * it exists.  mtx_empty_cache synchronises the device and releases the
+ * general pool's cached blocks; mtx_memory_stats reports bytes in use and
+ * cached (either pointer may be NULL).
+ */
+int mtx_malloc(void** out, size_t bytes);
+int mtx_free(void* p);
+int mtx_empty_cache(void);
+int mtx_memory_stats(size_t* in_use, size_t* cached);
+
+/*
+ * Copies.  h2d and d2h return when the copy is complete (they wait for the
+ * stream, so earlier work on it is finished too); d2d is asynchronous.
+ */
+int mtx_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int mtx_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int mtx_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/*
+ * Set `count` elements of `width` bytes (1, 2, 4 or 8; dst aligned to width)
+ * to the low `width` bytes of `pattern`.  A kernel (not hipMemsetAsync), so it
+ * may be recorded into a graph and replayed.
+ */
+int mtx_fill(void* dst, size_t count, uint64_t pattern, int width, void* stream);
+
+/* Streams (default priority) and events. */
+int mtx_stream_create(void** out);
+int mtx_stream_destroy(void* stream);
+int mtx_stream_sync(void* stream);
+int mtx_event_create(void** out);
+int mtx_event_destroy(void* event);
+int mtx_event_record(void* event, void* stream);
+/* Milliseconds between two recorded events (waits for `end`). */
+int mtx_event_elapsed_ms(void* start, void* end, float* ms);
+int mtx_stream_wait_event(void* stream, void* event);
+
+/*
+ * HIP graphs.  mtx_graph_begin starts recording the work issued on `stream`
+ * (a created stream, not NULL); mtx_graph_end stops and instantiates it into
+ * *graph.  mtx_graph_launch replays it on any stream; mtx_graph_destroy
+ * releases it (after synchronising the device) and returns its memory pool
+ * to the cache.  One capture at a time per process.
+ */
+int mtx_graph_begin(void* stream);
+int mtx_graph_end(void* stream, void** graph);
+int mtx_graph_launch(void* graph, void* stream);
+int mtx_graph_destroy(void* graph);
 
 #ifdef __cplusplus
 }

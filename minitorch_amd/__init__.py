@@ -4,7 +4,8 @@ The public surface mirrors the reference package (minitorch/__init__.py):
 Tensor, no_grad, Module, Sequential, Linear, LayerNorm, Embedding, GELU,
 Dropout, GPT, TransformerBlock, MultiHeadAttention, cross_entropy_loss, Adam,
 F.  Every operation runs in libmtx_hip.so (HIP, gfx950) through the C ABI in
-include/mtx.h; torch is used only for device memory and streams.
+include/mtx.h, device memory included (the library's caching allocator):
+no other GPU framework is imported.
 """
 __version__ = "0.1.0"
 

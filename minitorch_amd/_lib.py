@@ -3,8 +3,7 @@
 This module is the only place that touches the shared library.  It loads the
 in-tree build (``minitorch_amd/libmtx_hip.so``), declares every exported
 signature, turns non-zero status codes into Python exceptions and converts
-torch device tensors (used purely as device-memory handles) into pointers,
-element strides and the current HIP stream.
+device arrays into pointers, element strides and the current HIP stream.
 
 There is no fallback: if the library is missing or a call fails, an exception
 is raised.
@@ -112,6 +111,30 @@ SIGNATURES = {
     "mtx_adam_f32": (_I, [_P, _I, _I64, _D, _D, _D, _D, _D, _I, _P]),
     "mtx_adam_bias_table": (_I, [_D, _D, _I, _I, _P]),
     "mtx_adam_dev_f32": (_I, [_P, _I, _I64, _D, _D, _D, _D, _D, _P, _P, _I, _P]),
+    # runtime
+    "mtx_device_count": (_I, [_IP]),
+    "mtx_device_init": (_I, [_I]),
+    "mtx_device_sync": (_I, []),
+    "mtx_malloc": (_I, [C.POINTER(_P), _SZ]),
+    "mtx_free": (_I, [_P]),
+    "mtx_empty_cache": (_I, []),
+    "mtx_memory_stats": (_I, [C.POINTER(_SZ), C.POINTER(_SZ)]),
+    "mtx_memcpy_h2d": (_I, [_P, _P, _SZ, _P]),
+    "mtx_memcpy_d2h": (_I, [_P, _P, _SZ, _P]),
+    "mtx_memcpy_d2d": (_I, [_P, _P, _SZ, _P]),
+    "mtx_fill": (_I, [_P, _SZ, C.c_uint64, _I, _P]),
+    "mtx_stream_create": (_I, [C.POINTER(_P)]),
+    "mtx_stream_destroy": (_I, [_P]),
+    "mtx_stream_sync": (_I, [_P]),
+    "mtx_event_create": (_I, [C.POINTER(_P)]),
+    "mtx_event_destroy": (_I, [_P]),
+    "mtx_event_record": (_I, [_P, _P]),
+    "mtx_event_elapsed_ms": (_I, [_P, _P, C.POINTER(_F)]),
+    "mtx_stream_wait_event": (_I, [_P, _P]),
+    "mtx_graph_begin": (_I, [_P]),
+    "mtx_graph_end": (_I, [_P, C.POINTER(_P)]),
+    "mtx_graph_launch": (_I, [_P, _P]),
+    "mtx_graph_destroy": (_I, [_P]),
 }
 
 
@@ -160,8 +183,15 @@ def call(fn_name: str, *args) -> None:
 
 
 # ---------------------------------------------------------------------------
-# torch plumbing helpers (device memory + streams only)
+# argument helpers: device arrays (minitorch_amd.device.DevBuf, or any object
+# with data_ptr() / stride() / dtype, e.g. a framework tensor a test passes
+# in) -> pointers, element strides, dtype codes; the current stream
 # ---------------------------------------------------------------------------
+
+# The stream every launch goes to: None = the null stream (eager work);
+# graphs.capture() points it at its capture stream while recording.
+_STREAM = [None]
+
 
 def strides(t) -> C.Array:
     s = t.stride()
@@ -173,16 +203,20 @@ def ptr(t):
 
 
 def stream_handle(device=None):
-    import torch
+    return _STREAM[0]
 
-    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+def capturing() -> bool:
+    """True while a graph capture is recording this process's launches."""
+    return _STREAM[0] is not None
 
 
 def dtype_code(t) -> int:
-    import torch
+    from .device import dtype_name
 
-    if t.dtype == torch.float32:
+    name = dtype_name(t)
+    if name == "float32":
         return MTX_F32
-    if t.dtype == torch.bfloat16:
+    if name == "bfloat16":
         return MTX_BF16
-    raise ValueError(f"unsupported dtype {t.dtype} (float32 or bfloat16)")
+    raise ValueError(f"unsupported dtype {name} (float32 or bfloat16)")

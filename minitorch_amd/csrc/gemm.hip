@@ -654,11 +654,16 @@ using namespace mtx;
 
 extern "C" size_t mtx_gemm_workspace_bytes(int M, int N, int K, int batch) {
   if (M < 1 || N < 1 || K < 1 || batch < 1) return 0;
-  if (const int sp = skinny_splits(M, K)) return sp > 1 ? (size_t)sp * batch * (size_t)M * N * sizeof(float) : 0;
+  // The skinny kernel serves plain products with M <= 64; the same shape with
+  // an activation epilogue (mtx_gemm_act_f32) or column sums goes to the tile
+  // kernel, so the size covers both plans.
+  const int sp = skinny_splits(M, K);
+  const size_t skinny = sp > 1 ? (size_t)sp * batch * (size_t)M * N * sizeof(float) : 0;
   Plan p = plan_gemm(M, N, K, batch, (size_t)-1);
   // split partials [split][batch][M][N], then the weight-gradient variant's
   // column sums [split][N]
-  return p.ksplit > 1 ? (size_t)p.ksplit * batch * (size_t)(M + 1) * N * sizeof(float) : 0;
+  const size_t tiled = p.ksplit > 1 ? (size_t)p.ksplit * batch * (size_t)(M + 1) * N * sizeof(float) : 0;
+  return skinny > tiled ? skinny : tiled;
 }
 
 namespace {

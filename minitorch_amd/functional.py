@@ -270,8 +270,8 @@ def mlp_gelu(x, fc1, fc2, residual=None):
     lead = tuple(x.shape[:-1])
     rows = int(np.prod(lead)) if lead else 1
     x2 = x.data.t.reshape(rows, Cin)
-    h = torch_empty((rows, Hd), x2.dtype)
-    a = torch_empty((rows, Hd), x2.dtype)
+    h = _empty((rows, Hd), x2.dtype)
+    a = _empty((rows, Hd), x2.dtype)
     K.gemm(x2, W1.data.t, a, bias=b1.data.t, act=K.GEMM_ACT_GELU, aux=h)
     data = dev.empty(lead + (Cout,))
     if residual is not None:
@@ -292,7 +292,7 @@ def mlp_gelu(x, fc1, fc2, residual=None):
         need_h = x.requires_grad or W1.requires_grad or b1.requires_grad
         if not need_h:
             return
-        dh = torch_empty((rows, Hd), g2.dtype)
+        dh = _empty((rows, Hd), g2.dtype)
         K.gemm(g2, W2.data.t.transpose(0, 1), dh, act=K.GEMM_ACT_GELU_BWD, aux=h)
         _wgrad(x2.transpose(0, 1), dh, W1, b1, Cin, Hd, rows)
         if x.requires_grad:
@@ -347,7 +347,7 @@ def causal_attention_packed(qkv, n_head, scale=None, keep=None, keep_scale=1.0):
         scale = 1.0 / math.sqrt(D)
     heads = lambda a: [a.view(B, T, 3, n_head, D)[:, :, i].transpose(1, 2) for i in range(3)]
     qt, kt, vt = heads(t)
-    o = torch_empty((B, T, n_head, D), t.dtype).transpose(1, 2)
+    o = _empty((B, T, n_head, D), t.dtype).transpose(1, 2)
     drop = {} if keep is None else {"keep": keep, "keep_scale": float(keep_scale)}
     o, lse = K.attn_fwd(qt, kt, vt, scale, True, out=o, **drop)
     out = None
@@ -381,7 +381,7 @@ def causal_attention(q, k, v, scale=None, keep=None, keep_scale=1.0):
     B, H, Tq, _ = qt.shape
     # the output is stored as (B, T, H, D), so merging the heads back to
     # (B, T, C) (transformer.py:45) is a view, not a copy
-    o = torch_empty((B, Tq, H, D), qt.dtype).transpose(1, 2)
+    o = _empty((B, Tq, H, D), qt.dtype).transpose(1, 2)
     drop = {} if keep is None else {"keep": keep, "keep_scale": float(keep_scale)}
     o, lse = K.attn_fwd(qt, kt, vt, scale, True, out=o, **drop)
     out = None
@@ -398,7 +398,7 @@ def causal_attention(q, k, v, scale=None, keep=None, keep_scale=1.0):
                 _own_grad(t)
                 tgt.append((t.grad.t, True))
             else:
-                buf = dev.DeviceArray(torch_empty_like(t.data.t))
+                buf = dev.DeviceArray(_empty_like(t.data.t))
                 tgt.append((buf.t, False))
         acc_all = all(a for _, a in tgt)
         none_acc = not any(a for _, a in tgt)
@@ -438,9 +438,9 @@ def attention_keep_mask(shape, p: float):
     """Keep-mask of a (B, H, Tq, Tk) attention matrix for drop probability p,
     as the fused kernels take it (uint8 (B, H, Tq, ld), ld = Tk rounded up to
     a multiple of 4).  Returns (mask, keep_scale)."""
-    import torch
+    from . import _lib
 
-    if torch.cuda.is_current_stream_capturing():
+    if _lib.capturing():
         # a recorded step would replay this draw (host mask or Philox
         # offset) unchanged on every call
         raise RuntimeError("attention dropout masks cannot be drawn inside a recorded (captured) step")
@@ -448,7 +448,7 @@ def attention_keep_mask(shape, p: float):
     keep_scale = float(np.float32(1.0 / (1.0 - p)))
     if _DROPOUT_RNG["mode"] == "device":
         mask, _DROPOUT_RNG["offset"] = K.dropout_keep_philox(
-            (B, H, Tq, Tk), p, _DROPOUT_RNG["seed"], _DROPOUT_RNG["offset"], device=dev.device())
+            (B, H, Tq, Tk), p, _DROPOUT_RNG["seed"], _DROPOUT_RNG["offset"])
         return mask, keep_scale
     ld = K.keep_ld(Tk)
     host = np.zeros((B, H, Tq, ld), dtype=np.uint8)
@@ -456,10 +456,8 @@ def attention_keep_mask(shape, p: float):
     return dev.from_host(host, dtype=np.uint8).t, keep_scale
 
 
-def torch_empty(shape, dtype):
-    import torch
-
-    return torch.empty(shape, dtype=dtype, device=dev.device())
+def _empty(shape, dtype):
+    return dev.empty_buf(shape, dtype)
 
 
 def _kernel_layout(t):
@@ -470,11 +468,9 @@ def _kernel_layout(t):
             and all(s % vec == 0 for s in t.stride()[:-1]))
 
 
-def torch_empty_like(t):
-    """An uninitialised buffer with t's shape and (dense) strides."""
-    import torch
-
-    return torch.empty_like(t, dtype=torch.float32)
+def _empty_like(t):
+    """An uninitialised float32 buffer with t's shape in t's memory order."""
+    return dev.empty_like_layout(t, "float32")
 
 
 def cross_entropy(logits, labels):

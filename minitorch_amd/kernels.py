@@ -1,21 +1,24 @@
 """Thin Python wrappers over the libmtx_hip entry points.
 
-Each function takes torch device tensors (device memory only -- no torch
-compute is used), validates shapes on the host, calls the C ABI on the current
-HIP stream and returns the output tensors.  Errors raise ``ValueError`` (bad
+Each function takes device arrays (``device.DevBuf``: pointer, shape,
+element strides, dtype), validates shapes on the host, calls the C ABI on the
+current HIP stream and returns the outputs, allocating those not given with
+the library's caching allocator.  Errors raise ``ValueError`` (bad
 arguments, found before any HIP call) or ``MtxError`` (HIP failure).
 """
 from __future__ import annotations
 
-import torch
+import numpy as np
 
 from . import _lib as L
+from . import device as dev
+from .device import dtype_name as _dt
 
 
 def _need_cuda(*ts):
     for t in ts:
-        if not isinstance(t, torch.Tensor) or not t.is_cuda:
-            raise ValueError("minitorch_amd kernels take device tensors (torch.cuda)")
+        if not getattr(t, "is_cuda", False) or not hasattr(t, "data_ptr"):
+            raise ValueError("minitorch_amd kernels take device arrays")
 
 
 def _bhtd(name, t):
@@ -32,12 +35,12 @@ def pack3(srcs, dst):
     rows, cols = s0.shape
     _need_cuda(s0, s1, s2, dst)
     for t in (s0, s1, s2):
-        if tuple(t.shape) != (rows, cols) or not t.is_contiguous() or t.dtype != torch.float32:
+        if tuple(t.shape) != (rows, cols) or not t.is_contiguous() or _dt(t) != "float32":
             raise ValueError("pack3: sources must be contiguous fp32 tensors of one shape")
-    if tuple(dst.shape) != (rows, 3 * cols) or not dst.is_contiguous() or dst.dtype != torch.float32:
+    if tuple(dst.shape) != (rows, 3 * cols) or not dst.is_contiguous() or _dt(dst) != "float32":
         raise ValueError(f"pack3: dst must be contiguous fp32 ({rows}, {3 * cols})")
     L.call("mtx_pack3_f32", L.ptr(s0), L.ptr(s1), L.ptr(s2), rows, cols, L.ptr(dst),
-           L.stream_handle(dst.device))
+           L.stream_handle())
     return dst
 
 
@@ -47,24 +50,24 @@ def unpack3(src, dsts, accumulate=(False, False, False)):
     rows, cols = d0.shape
     _need_cuda(src, d0, d1, d2)
     for t in (d0, d1, d2):
-        if tuple(t.shape) != (rows, cols) or not t.is_contiguous() or t.dtype != torch.float32:
+        if tuple(t.shape) != (rows, cols) or not t.is_contiguous() or _dt(t) != "float32":
             raise ValueError("unpack3: targets must be contiguous fp32 tensors of one shape")
-    if tuple(src.shape) != (rows, 3 * cols) or not src.is_contiguous() or src.dtype != torch.float32:
+    if tuple(src.shape) != (rows, 3 * cols) or not src.is_contiguous() or _dt(src) != "float32":
         raise ValueError(f"unpack3: src must be contiguous fp32 ({rows}, {3 * cols})")
     mask = sum(1 << i for i, a in enumerate(accumulate) if a)
     L.call("mtx_unpack3_f32", L.ptr(src), rows, cols, L.ptr(d0), L.ptr(d1), L.ptr(d2), mask,
-           L.stream_handle(src.device))
+           L.stream_handle())
 
 
 def _check_keep(keep, B, H, Tq, Tk):
     """A dropout keep-mask as the kernels take it: contiguous uint8
     (B, H, Tq, ld) with ld >= Tk, ld % 4 == 0 (nonzero = kept)."""
-    if keep.dtype != torch.uint8 or not keep.is_contiguous() or keep.dim() != 4:
+    if _dt(keep) != "uint8" or not keep.is_contiguous() or keep.dim() != 4:
         raise ValueError("keep must be a contiguous uint8 (B,H,Tq,ld) tensor")
     if tuple(keep.shape[:3]) != (B, H, Tq) or keep.shape[3] < Tk or keep.shape[3] % 4:
         raise ValueError(f"keep shape {tuple(keep.shape)} does not fit (B,H,Tq)={(B, H, Tq)}, Tk={Tk}")
-    if keep.device.type != "cuda":
-        raise ValueError("keep must be a device tensor")
+    if not getattr(keep, "is_cuda", False):
+        raise ValueError("keep must be a device array")
     return keep.shape[3]
 
 
@@ -73,7 +76,7 @@ def keep_ld(Tk: int) -> int:
     return (Tk + 3) // 4 * 4
 
 
-def dropout_keep_philox(shape, p: float, seed: int, offset: int, out=None, device=None):
+def dropout_keep_philox(shape, p: float, seed: int, offset: int, out=None):
     """Keep-mask (B, H, Tq, keep_ld(Tk)) uint8 for dropout probability p, from
     the device Philox4x32-10 generator (mtx_dropout_keep_philox): element
     e of the logical (B*H*Tq, Tk) array uses output word e % 4 of counter
@@ -81,10 +84,10 @@ def dropout_keep_philox(shape, p: float, seed: int, offset: int, out=None, devic
     B, H, Tq, Tk = (int(x) for x in shape)
     ld = keep_ld(Tk)
     if out is None:
-        out = torch.zeros((B, H, Tq, ld), dtype=torch.uint8, device=device if device is not None else "cuda")
+        out = dev.empty_buf((B, H, Tq, ld), "uint8").fill_(0)
     rows = B * H * Tq
     L.call("mtx_dropout_keep_philox", L.ptr(out), rows, Tk, ld, float(p), int(seed) & (2**64 - 1),
-           int(offset) & (2**64 - 1), L.stream_handle(out.device))
+           int(offset) & (2**64 - 1), L.stream_handle())
     return out, offset + (rows * Tk + 3) // 4
 
 
@@ -101,26 +104,26 @@ def attn_fwd(q, k, v, scale: float, causal: bool = True, out=None, lse=None, kee
     Tk = k.shape[2]
     if k.shape != (B, H, Tk, D) or v.shape != (B, H, Tk, D):
         raise ValueError(f"shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
-    if not (q.dtype == k.dtype == v.dtype):
+    if not (_dt(q) == _dt(k) == _dt(v)):
         raise ValueError("q, k, v must share a dtype")
     if out is None:
-        out = torch.empty((B, H, Tq, D), dtype=q.dtype, device=q.device)
+        out = dev.empty_buf((B, H, Tq, D), _dt(q))
     if lse is None:
-        lse = torch.empty((B, H, Tq), dtype=torch.float32, device=q.device)
+        lse = dev.empty_buf((B, H, Tq), "float32")
     _bhtd("out", out)
-    if not lse.is_contiguous() or lse.shape != (B, H, Tq) or lse.dtype != torch.float32:
+    if not lse.is_contiguous() or tuple(lse.shape) != (B, H, Tq) or _dt(lse) != "float32":
         raise ValueError("lse must be a contiguous fp32 (B,H,Tq) tensor")
     if keep is not None:
         ld = _check_keep(keep, B, H, Tq, Tk)
         L.call("mtx_attn_fwd_dropout", L.dtype_code(q), B, H, Tq, Tk, D,
                L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
                L.ptr(out), L.strides(out), L.ptr(lse), float(scale), int(bool(causal)),
-               L.ptr(keep), ld, float(keep_scale), L.stream_handle(q.device))
+               L.ptr(keep), ld, float(keep_scale), L.stream_handle())
         return out, lse
     L.call("mtx_attn_fwd", L.dtype_code(q), B, H, Tq, Tk, D,
            L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
            L.ptr(out), L.strides(out), L.ptr(lse), float(scale), int(bool(causal)),
-           L.stream_handle(q.device))
+           L.stream_handle())
     return out, lse
 
 
@@ -136,21 +139,21 @@ def attn_decode(q, k, v, scale: float, out=None, lse=None, lengths=None):
     Lk = k.shape[2]
     if Tq != 1 or k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
         raise ValueError(f"shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
-    if not (q.dtype == k.dtype == v.dtype):
+    if not (_dt(q) == _dt(k) == _dt(v)):
         raise ValueError("q, k, v must share a dtype")
     if out is None:
-        out = torch.empty((B, H, 1, D), dtype=q.dtype, device=q.device)
+        out = dev.empty_buf((B, H, 1, D), _dt(q))
     _bhtd("out", out)
-    if lse is not None and (not lse.is_contiguous() or lse.shape != (B, H) or lse.dtype != torch.float32):
+    if lse is not None and (not lse.is_contiguous() or tuple(lse.shape) != (B, H) or _dt(lse) != "float32"):
         raise ValueError("lse must be a contiguous fp32 (B,H) tensor")
-    if lengths is not None and (lengths.dtype != torch.int32 or lengths.shape != (B,)
+    if lengths is not None and (_dt(lengths) != "int32" or tuple(lengths.shape) != (B,)
                                 or not lengths.is_contiguous() or not lengths.is_cuda):
         raise ValueError("lengths must be a contiguous int32 device tensor of shape (B,)")
     L.call("mtx_attn_decode", L.dtype_code(q), B, H, Lk, D,
            L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
            L.ptr(out), L.strides(out), L.ptr(lse) if lse is not None else None,
            L.ptr(lengths) if lengths is not None else None, float(scale),
-           L.stream_handle(q.device))
+           L.stream_handle())
     return out, lse
 
 
@@ -159,18 +162,18 @@ def argmax_rows(x, idx=None, margin=None):
     (np.argmax) and, if `margin` is given, largest - second largest.  idx:
     int64 (rows,) or a strided column view; returns (idx, margin)."""
     _need_cuda(x)
-    if x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1:
+    if _dt(x) != "float32" or x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("x must be a fp32 (rows, cols) tensor with contiguous rows")
     rows, cols = x.shape
     if idx is None:
-        idx = torch.empty((rows,), dtype=torch.int64, device=x.device)
-    if idx.dtype != torch.int64 or idx.numel() != rows:
+        idx = dev.empty_buf((rows,), "int64")
+    if _dt(idx) != "int64" or idx.numel() != rows:
         raise ValueError("idx must be int64 with one entry per row")
-    if margin is not None and (margin.dtype != torch.float32 or margin.numel() != rows):
+    if margin is not None and (_dt(margin) != "float32" or margin.numel() != rows):
         raise ValueError("margin must be fp32 with one entry per row")
     L.call("mtx_argmax_f32", rows, cols, L.ptr(x), x.stride(0), L.ptr(idx), idx.stride(0) if idx.dim() else 1,
            L.ptr(margin) if margin is not None else None, margin.stride(0) if margin is not None else 0,
-           L.stream_handle(x.device))
+           L.stream_handle())
     return idx, margin
 
 
@@ -179,23 +182,23 @@ def kv_append(x, cache, lengths):
     (B, T, C) fp32 with contiguous rows, lengths int32 device (B,)."""
     _need_cuda(x, cache, lengths)
     B, T, C = cache.shape
-    if x.dtype != torch.float32 or cache.dtype != torch.float32 or x.shape != (B, 1, C):
+    if _dt(x) != "float32" or _dt(cache) != "float32" or tuple(x.shape) != (B, 1, C):
         raise ValueError(f"kv_append: x{tuple(x.shape)} / cache{tuple(cache.shape)} mismatch (fp32 needed)")
-    if x.stride(2) != 1 or cache.stride(2) != 1 or lengths.dtype != torch.int32 or lengths.shape != (B,):
+    if x.stride(2) != 1 or cache.stride(2) != 1 or _dt(lengths) != "int32" or tuple(lengths.shape) != (B,):
         raise ValueError("kv_append: contiguous rows and int32 lengths (B,) needed")
     L.call("mtx_kv_append_f32", B, C, T, L.ptr(x), x.stride(0), L.ptr(cache), cache.stride(0), cache.stride(1),
-           L.ptr(lengths), L.stream_handle(x.device))
+           L.ptr(lengths), L.stream_handle())
 
 
 def decode_advance(lengths, pos=None):
     """lengths += 1 (int32 device (B,)) and pos += 1 (int64 device (1,))."""
     _need_cuda(lengths)
-    if lengths.dtype != torch.int32 or lengths.dim() != 1 or not lengths.is_contiguous():
+    if _dt(lengths) != "int32" or lengths.dim() != 1 or not lengths.is_contiguous():
         raise ValueError("lengths must be a contiguous int32 device vector")
-    if pos is not None and (pos.dtype != torch.int64 or not pos.is_cuda):
+    if pos is not None and (_dt(pos) != "int64" or not pos.is_cuda):
         raise ValueError("pos must be an int64 device tensor")
     L.call("mtx_decode_advance", lengths.numel(), L.ptr(lengths), L.ptr(pos) if pos is not None else None,
-           L.stream_handle(lengths.device))
+           L.stream_handle())
 
 
 def attn_bwd(q, k, v, out, dout, lse, scale: float, causal: bool = True,
@@ -209,24 +212,23 @@ def attn_bwd(q, k, v, out, dout, lse, scale: float, causal: bool = True,
         _bhtd(name, t)
     B, H, Tq, D = q.shape
     Tk = k.shape[2]
-    if out.shape != q.shape or dout.shape != q.shape:
+    if tuple(out.shape) != tuple(q.shape) or tuple(dout.shape) != tuple(q.shape):
         raise ValueError("out and dout must have q's shape")
-    if not (q.dtype == k.dtype == v.dtype == out.dtype == dout.dtype):
+    if not (_dt(q) == _dt(k) == _dt(v) == _dt(out) == _dt(dout)):
         raise ValueError("q, k, v, out, dout must share a dtype")
-    f32 = torch.float32
     if dq is None:
-        dq = torch.empty((B, H, Tq, D), dtype=f32, device=q.device)
+        dq = dev.empty_buf((B, H, Tq, D), "float32")
     if dk is None:
-        dk = torch.empty((B, H, Tk, D), dtype=f32, device=q.device)
+        dk = dev.empty_buf((B, H, Tk, D), "float32")
     if dv is None:
-        dv = torch.empty((B, H, Tk, D), dtype=f32, device=q.device)
+        dv = dev.empty_buf((B, H, Tk, D), "float32")
     for name, t, shp in (("dq", dq, (B, H, Tq, D)), ("dk", dk, (B, H, Tk, D)), ("dv", dv, (B, H, Tk, D))):
-        if tuple(t.shape) != shp or t.dtype != f32:
+        if tuple(t.shape) != shp or _dt(t) != "float32":
             raise ValueError(f"{name} must be fp32 with shape {shp}")
         _bhtd(name, t)
     nbytes = L.lib().mtx_attn_bwd_workspace_bytes(B, H, Tq)
     if workspace is None:
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        workspace = dev.empty_buf((nbytes,), "uint8")
     if keep is not None:
         if int(phases) != L.ATTN_BWD_ALL:
             raise ValueError("the dropout backward runs all phases")
@@ -237,14 +239,14 @@ def attn_bwd(q, k, v, out, dout, lse, scale: float, causal: bool = True,
                L.ptr(dq), L.strides(dq), L.ptr(dk), L.strides(dk), L.ptr(dv), L.strides(dv),
                L.ptr(workspace), workspace.numel() * workspace.element_size(),
                float(scale), int(bool(causal)), int(bool(accumulate)), L.ptr(keep), ld,
-               float(keep_scale), L.stream_handle(q.device))
+               float(keep_scale), L.stream_handle())
         return dq, dk, dv
     L.call("mtx_attn_bwd_phase", int(phases), L.dtype_code(q), B, H, Tq, Tk, D,
            L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
            L.ptr(out), L.strides(out), L.ptr(dout), L.strides(dout), L.ptr(lse),
            L.ptr(dq), L.strides(dq), L.ptr(dk), L.strides(dk), L.ptr(dv), L.strides(dv),
            L.ptr(workspace), workspace.numel() * workspace.element_size(),
-           float(scale), int(bool(causal)), int(bool(accumulate)), L.stream_handle(q.device))
+           float(scale), int(bool(causal)), int(bool(accumulate)), L.stream_handle())
     return dq, dk, dv
 
 
@@ -263,7 +265,7 @@ def attn_bwd_noalloc(q, k, v, out, dout, lse, scale: float, causal: bool, dq, dk
            L.ptr(q), L.strides(q), L.ptr(k), L.strides(k), L.ptr(v), L.strides(v),
            L.ptr(out), L.strides(out), L.ptr(dout), L.strides(dout), L.ptr(lse),
            L.ptr(dq), L.strides(dq), L.ptr(dk), L.strides(dk), L.ptr(dv), L.strides(dv),
-           float(scale), int(bool(causal)), int(bool(accumulate)), L.stream_handle(q.device))
+           float(scale), int(bool(causal)), int(bool(accumulate)), L.stream_handle())
     return dq, dk, dv
 
 
@@ -330,7 +332,7 @@ def reduce(a, axes, out, op=L.RED_SUM, alpha: float = 1.0, accumulate=False):
     mask = (L.C.c_int * max(1, nd))(*[1 if d in axes else 0 for d in range(nd)])
     shp = _i64(shape)
     ws_bytes = L.lib().mtx_reduce_workspace_bytes(nd, shp, mask)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
+    ws = dev.empty_buf((ws_bytes,), "uint8") if ws_bytes else None
     if not out.is_contiguous():
         raise ValueError("reduce output must be contiguous")
     L.call("mtx_reduce_f32", int(op), nd, shp, L.ptr(a), _i64(a.stride()), mask, L.ptr(out),
@@ -366,15 +368,15 @@ def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=
     K = a.shape[-1] if K is None else K
     N = b.shape[-1] if N is None else N
     for name, t in (("A", a), ("B", b), ("C", c), ("bias", bias), ("aux", aux)):
-        if t is not None and t.dtype != torch.float32:
+        if t is not None and _dt(t) != "float32":
             raise ValueError(f"gemm: {name} must be fp32 (got {t.dtype})")
     # one operand stride must be unit; otherwise the caller passes a copy
     ws_bytes = L.lib().mtx_gemm_workspace_bytes(M, N, K, batch)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=c.device) if ws_bytes else None
+    ws = dev.empty_buf((ws_bytes,), "uint8") if ws_bytes else None
     if colsum is not None:
         if batch != 1 or alpha != 1.0 or bias is not None or act != GEMM_ACT_NONE:
             raise ValueError("gemm: colsum needs batch 1, alpha 1 and no bias or activation")
-        if colsum.dtype != torch.float32 or colsum.numel() != N or not colsum.is_contiguous():
+        if _dt(colsum) != "float32" or colsum.numel() != N or not colsum.is_contiguous():
             raise ValueError(f"gemm: colsum must be a contiguous fp32 tensor of N={N} elements")
         L.call("mtx_gemm_wgrad_f32", int(M), int(N), int(K), L.ptr(a), int(sa[0]), int(sa[1]),
                L.ptr(b), int(sb[0]), int(sb[1]), float(beta), L.ptr(c), int(sc[0]), int(sc[1]),
@@ -383,7 +385,7 @@ def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=
         return c
     if act != GEMM_ACT_NONE:
         if aux is not None:
-            if tuple(aux.shape[-2:]) != (M, N) or aux.dtype != torch.float32:
+            if tuple(aux.shape[-2:]) != (M, N) or _dt(aux) != "float32":
                 raise ValueError(f"gemm: aux must be fp32 with C's shape ({M}, {N})")
             sx = (aux.stride(-2), aux.stride(-1), aux.stride(0) if aux.dim() == 3 else 0)
         elif act in (GEMM_ACT_GELU_BWD, GEMM_ACT_ADD):
@@ -430,9 +432,10 @@ def gemm_step(a, b, bias=None, c=None, beta=0.0, act=ACT_NONE, kv=None):
         kc, vc, lengths = kv
         _need_cuda(kc, vc, lengths)
         Bc, T, Ck = kc.shape
-        if vc.shape != kc.shape or vc.stride() != kc.stride() or kc.stride(2) != 1 or Bc < M:
+        if tuple(vc.shape) != tuple(kc.shape) or tuple(vc.stride()) != tuple(kc.stride()) or kc.stride(2) != 1 \
+                or Bc < M:
             raise ValueError("gemm_step: k/v caches must be (B >= M, T, C) with equal strides")
-        if lengths.dtype != torch.int32 or lengths.numel() < M:
+        if _dt(lengths) != "int32" or lengths.numel() < M:
             raise ValueError("gemm_step: lengths must be int32 with >= M entries")
         nc = N - 2 * Ck
         cache_args = (L.ptr(kc), L.ptr(vc), kc.stride(0), kc.stride(1), T, L.ptr(lengths))
@@ -442,12 +445,12 @@ def gemm_step(a, b, bias=None, c=None, beta=0.0, act=ACT_NONE, kv=None):
     if nc < 0:
         raise ValueError("gemm_step: N too small for the cache columns")
     if nc > 0:
-        if c is None or c.shape != (M, nc) or c.stride(1) != 1:
+        if c is None or tuple(c.shape) != (M, nc) or c.stride(1) != 1:
             raise ValueError(f"gemm_step: c must be ({M}, {nc}) with unit column stride")
     L.call("mtx_gemm_step_f32", int(M), int(N), int(Kd), L.ptr(a), a.stride(0), L.ptr(b), b.stride(0),
            float(beta), L.ptr(c) if nc > 0 else None, c.stride(0) if nc > 0 else 0,
            L.ptr(bias) if bias is not None else None, int(act), int(nc), *cache_args,
-           L.stream_handle(a.device))
+           L.stream_handle())
     return c
 
 
@@ -514,7 +517,7 @@ def layernorm_bwd(x, gamma, mean, std, dy, dx=None, dgamma=None, dbeta=None, acc
     ws_bytes = 0
     if dgamma is not None:
         ws_bytes = L.lib().mtx_layernorm_bwd_workspace_bytes(r, C)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+        ws = dev.empty_buf((ws_bytes,), "uint8")
     L.call("mtx_layernorm_bwd_f32", L.ptr(x), ldx, L.ptr(gamma), L.ptr(mean), L.ptr(std),
            L.ptr(dy), lddy, L.ptr(dx) if dx is not None else None, lddx,
            L.ptr(dgamma) if dgamma is not None else None, L.ptr(dbeta) if dbeta is not None else None,
@@ -564,7 +567,7 @@ def embedding_bwd(idx, grad, dweight, accumulate=False):
     V, C = dweight.shape
     n = idx.numel()
     if V <= 4096 and n * V <= (1 << 27):
-        onehot = torch.empty((n, V), dtype=torch.float32, device=grad.device)
+        onehot = dev.empty_buf((n, V), "float32")
         L.call("mtx_onehot_f32", L.ptr(idx), n, V, L.ptr(onehot), L.stream_handle())
         gemm(onehot.t(), grad, dweight, beta=1.0 if accumulate else 0.0, M=V, N=C, K=n, batch=1,
              sa=(1, V, 0), sb=(grad.stride(0), grad.stride(1), 0), sc=(dweight.stride(0), dweight.stride(1), 0))
@@ -587,10 +590,8 @@ class AdamTable:
         for i in range(n):
             rows.append([params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(),
                          params[i].numel(), b0[i]])
-        import numpy as np
-
-        host = np.array(rows, dtype=np.int64)
-        self.table = torch.from_numpy(host).to(params[0].device)
+        host = np.array(rows, dtype=np.int64).reshape(n, 6)
+        self.table = dev.from_host(host, np.int64).t
         self.n = n
         self.total_blocks = int(b0[n - 1] + (params[n - 1].numel() + 255) // 256) if n else 0
 
@@ -598,8 +599,6 @@ class AdamTable:
 def adam_bias_table(beta1, beta2, first_step, length):
     """Host float32 table of the bias corrections (1 - beta1^t, 1 - beta2^t)
     for steps first_step .. first_step + length - 1, entry (t - 1) % length."""
-    import numpy as np
-
     out = np.empty(2 * length, dtype=np.float32)
     L.call("mtx_adam_bias_table", float(beta1), float(beta2), int(first_step), int(length),
            out.ctypes.data_as(L.C.c_void_p))

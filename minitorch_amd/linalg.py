@@ -11,7 +11,6 @@ stride swaps.  Two launch shapes avoid per-matrix loops:
 from __future__ import annotations
 
 import numpy as np
-import torch
 
 from . import device as dev
 from . import kernels as K
@@ -63,7 +62,7 @@ def _rows_fold(t, nb):
 
 
 def bmm(at, bt, ct, alpha=1.0, beta=0.0, bias=None):
-    """ct[...] = alpha * at @ bt + beta * ct (+ bias), torch tensors with
+    """ct[...] = alpha * at @ bt + beta * ct (+ bias), device arrays with
     broadcastable batch axes; ct has the full batch shape."""
     at, bt = _fix(at), _fix(bt)
     batch = tuple(ct.shape[:-2])
@@ -103,8 +102,8 @@ def matmul_data(a: DeviceArray, b: DeviceArray) -> DeviceArray:
         bt = bt.unsqueeze(-1)
     if at.shape[-1] != bt.shape[-2]:
         raise ValueError(f"matmul: shapes {tuple(a.shape)} and {tuple(b.shape)} not aligned")
-    batch = tuple(torch.broadcast_shapes(at.shape[:-2], bt.shape[:-2]))
-    out = torch.empty(batch + (at.shape[-2], bt.shape[-1]), dtype=torch.float32, device=at.device)
+    batch = tuple(np.broadcast_shapes(tuple(at.shape[:-2]), tuple(bt.shape[:-2])))
+    out = dev.empty_buf(batch + (at.shape[-2], bt.shape[-1]), "float32")
     bmm(at, bt, out)
     if a1:
         out = out.squeeze(-2)
@@ -143,8 +142,7 @@ def matmul_grad_b(a: DeviceArray, g: DeviceArray, other, bias=None):
                    sa=(ae.stride(-1), ra, 0), sb=(rg, gt.stride(-1), 0), sc=(tt.stride(0), tt.stride(1), 0),
                    colsum=tb.t if tb is not None else None, colsum_accumulate=accb)
             return tb is not None
-    res = DeviceArray(torch.empty(batch + (at.shape[-1], gt.shape[-1]), dtype=torch.float32,
-                                  device=gt.device))
+    res = dev.empty(batch + (at.shape[-1], gt.shape[-1]))
     bmm(at.transpose(-1, -2), gt, res.t)
     if other.ndim == 1:
         res = res.reshape(*res.shape[:-1])

@@ -2,7 +2,6 @@
 from __future__ import annotations
 
 import numpy as np
-import torch
 
 from . import functional as F
 from .device import DeviceArray
@@ -17,7 +16,7 @@ def cross_entropy_loss(input, target):
     """Softmax cross-entropy of (N, V) logits (loss.py:17-27).  `target` holds
     class indices (a Tensor, array or list; one per row) or one-hot rows."""
     t = target.data if isinstance(target, Tensor) else target
-    if isinstance(t, DeviceArray) and t.t.dtype == torch.int64:
+    if isinstance(t, DeviceArray) and t.t.dtype == "int64":
         return F.cross_entropy(input, t)  # device-resident class indices
     if isinstance(t, DeviceArray):
         t = t.numpy()

@@ -51,14 +51,21 @@ class Adam(Optimizer):
         zero_grad; accumulating into zeros gives the same bits as a first
         write), and the step count lives in device memory, the bias
         corrections coming from a host-filled table that covers `window`
-        steps at a time (refilled between steps by prepare()).  Returns self."""
-        import torch
+        steps at a time (refilled between steps by prepare()).  Returns self.
 
+        Difference from the reference in this mode: the reference's Adam
+        skips a parameter whose grad is None (optim.py:47-48), but here every
+        trainable parameter always holds a (possibly all-zero) gradient, so a
+        parameter that receives no gradient in some step after earlier steps
+        gave it one is still updated (its m and v decay and it moves by
+        lr * m_hat / (sqrt(v_hat) + eps)).  GPT training uses every parameter
+        in every step, where the two agree; use the eager mode for models that
+        leave parameters out of some steps."""
         for p in self.params:
             if p.requires_grad and p.grad is None:
                 p.grad = dev.zeros(p.shape)
-        self._step_dev = torch.full((1,), self.t, dtype=torch.int32, device=dev.device())
-        self._bias_dev = torch.empty(2 * window, dtype=torch.float32, device=dev.device())
+        self._step_dev = dev.full((1,), self.t, "int32").t
+        self._bias_dev = dev.empty((2 * window,)).t
         self._bias_first = None
         self._capturable = True
         self.prepare()
@@ -72,14 +79,12 @@ class Adam(Optimizer):
         the bias table cover step t + 1.  A no-op unless capturable."""
         if not self._capturable:
             return
-        import torch
-
         t_next = self.t + 1
         n = self._bias_dev.numel() // 2
         f = self._bias_first
         if f is None or not (f <= t_next < f + n):
             host = K.adam_bias_table(self.beta1, self.beta2, t_next, n)
-            self._bias_dev.copy_(torch.from_numpy(host))
+            self._bias_dev.copy_(host)
             self._bias_first = t_next
 
     def step(self):

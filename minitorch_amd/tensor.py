@@ -141,7 +141,7 @@ class Tensor:
     def __init__(self, data, *, requires_grad=False):
         if isinstance(data, DeviceArray):
             self.data = data
-        elif type(data).__module__.startswith("torch"):
+        elif isinstance(data, dev.DevBuf):
             self.data = DeviceArray(data)
         else:
             self.data = dev.from_host(data)

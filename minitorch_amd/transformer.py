@@ -10,7 +10,6 @@ from __future__ import annotations
 import math
 
 import numpy as np
-import torch
 
 from . import device as dev
 from . import functional as F
@@ -129,8 +128,7 @@ class MultiHeadAttention(Module):
             q, k, v = qkv[..., :C], qkv[..., C:2 * C], qkv[..., 2 * C:]
             K.kv_append(k, kc.t, lengths)
             K.kv_append(v, vc.t, lengths)
-        heads = lambda t: t.view(t.shape[0], t.shape[1], H, D).transpose(1, 2) if t.is_contiguous() \
-            else t.unflatten(2, (H, D)).transpose(1, 2)
+        heads = lambda t: t.unflatten(2, (H, D)).transpose(1, 2)
         out = dev.empty((B, 1, H, D))
         K.attn_decode(heads(q), heads(kc.t), heads(vc.t), 1.0 / math.sqrt(D),
                       out=out.t.transpose(1, 2), lengths=lengths)
@@ -142,9 +140,15 @@ class MultiHeadAttention(Module):
         """Concatenate the q/k/v projections into one (C, 3C) weight and (3C,)
         bias for decode steps (one GEMM instead of three).  A snapshot: call
         again after the weights change (generate_greedy does, per call)."""
-        W = torch.cat([p.weight.data.t for p in (self.q_proj, self.k_proj, self.v_proj)], dim=1)
-        b = torch.cat([p.bias.data.t for p in (self.q_proj, self.k_proj, self.v_proj)], dim=0)
-        self._qkv = (Tensor(DeviceArray(W.contiguous())), Tensor(DeviceArray(b.contiguous())))
+        from . import kernels as K
+
+        lins = (self.q_proj, self.k_proj, self.v_proj)
+        Cin, C = self.q_proj.weight.shape
+        W = dev.empty((Cin, 3 * C))
+        b = dev.empty((3 * C,))
+        K.pack3([p.weight.data.t.contiguous() for p in lins], W.t)
+        K.pack3([p.bias.data.t.contiguous().view(1, C) for p in lins], b.t.view(1, 3 * C))
+        self._qkv = (Tensor(W), Tensor(b))
 
 
 class TransformerBlock(Module):
@@ -277,7 +281,7 @@ class GPT(Module):
             return (idx.copy(), np.empty((B, 0))) if return_margins else idx.copy()
         C = self.tok_emb.weight.shape[1]
         caches = [(dev.empty((B, Tmax, C)), dev.empty((B, Tmax, C))) for _ in self.blocks]
-        ids = dev.empty((Tmax, B), dtype=torch.int64)  # time-major: a step's ids are contiguous
+        ids = dev.empty((Tmax, B), dtype="int64")  # time-major: a step's ids are contiguous
         margins = dev.empty((n, B))
         pos = self._positions(Tmax)
 
@@ -293,9 +297,9 @@ class GPT(Module):
                 for block in self.blocks:
                     block.attn.fuse_qkv()
                 cur = ids.t[T0].clone()              # ids fed to the next step, then overwritten
-                mcur = torch.empty((B,), dtype=torch.float32, device=cur.device)
-                lengths = torch.full((B,), T0 + 1, dtype=torch.int32, device=cur.device)
-                posd = torch.full((1,), T0, dtype=torch.int64, device=cur.device)
+                mcur = dev.empty((B,)).t
+                lengths = dev.full((B,), T0 + 1, "int32").t
+                posd = dev.full((1,), T0, "int64").t
 
                 def step():
                     x = self.tok_emb(DeviceArray(cur.view(B, 1))) + self.pos_emb(DeviceArray(posd))
@@ -312,8 +316,10 @@ class GPT(Module):
                 step()
                 record(1)
                 if graph and n > 2:
-                    g = torch.cuda.CUDAGraph()
-                    with torch.cuda.graph(g):
+                    from .graphs import Graph
+
+                    g = Graph()
+                    with g.capture():
                         step()
                     for s in range(2, n):
                         g.replay()
@@ -322,10 +328,10 @@ class GPT(Module):
                     for s in range(2, n):
                         step()
                         record(s)
-        out = ids.t.t().cpu().numpy()
+        out = ids.t.numpy().T.copy()
         out[:, :T0] = idx
         if return_margins:
-            return out, margins.t.t().cpu().numpy().astype(np.float64)
+            return out, margins.t.numpy().T.astype(np.float64)
         return out
 
     def generate(self, idx, max_new_tokens, temperature=1.0):

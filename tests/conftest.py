@@ -21,10 +21,15 @@ def pytest_configure(config):
 
 
 def _has_gpu():
+    """A GPU is visible to the HIP runtime (asked through the library's own
+    mtx_device_count; False when the library is not built)."""
     try:
-        import torch
+        import ctypes
 
-        return torch.cuda.is_available()
+        from minitorch_amd import _lib
+
+        n = ctypes.c_int(0)
+        return _lib.lib().mtx_device_count(ctypes.byref(n)) == 0 and n.value > 0
     except Exception:
         return False
 
@@ -40,9 +45,8 @@ def pytest_collection_modifyitems(config, items):
 
 @pytest.fixture(scope="session")
 def dev():
-    import torch
+    """GPU 0, initialised through the library (loud failure if it is not
+    built or no GPU is visible)."""
+    from minitorch_amd import device
 
-    from minitorch_amd import _lib
-
-    _lib.lib()  # loud failure if the library is not built
-    return torch.device("cuda:0")
+    return device.device()

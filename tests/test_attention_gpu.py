@@ -21,6 +21,7 @@ import sys
 import numpy as np
 import pytest
 
+from devarrays import T as _T, empty, full, sync
 from oracle.attention import attention_bf16_emulated, bf16_round, reference_attention
 
 pytestmark = pytest.mark.gpu
@@ -80,14 +81,11 @@ def _emu_bar(got, emu, name):
 
 
 def _to_dev(x, dev, dtype):
-    import torch
-
-    return torch.from_numpy(np.ascontiguousarray(x)).to(dev).to(dtype)
+    return _T(x, dtype)
 
 
 def _run(dev, q, k, v, do, scale, causal, dtype, views=None):
     """Run fwd+bwd on the device; returns numpy (o, dq, dk, dv, lse)."""
-    import torch
     from minitorch_amd import kernels as K
 
     tq, tk, tv, tdo = (_to_dev(x, dev, dtype) for x in (q, k, v, do))
@@ -95,8 +93,8 @@ def _run(dev, q, k, v, do, scale, causal, dtype, views=None):
         tq, tk, tv, tdo = (views(t) for t in (tq, tk, tv, tdo))
     o, lse = K.attn_fwd(tq, tk, tv, scale, causal)
     dq, dk, dv = K.attn_bwd(tq, tk, tv, o, tdo, lse, scale, causal)
-    torch.cuda.synchronize()
-    f = lambda t: t.float().cpu().numpy()
+    sync()
+    f = lambda t: t.numpy()
     return f(o), f(dq), f(dk), f(dv), f(lse)
 
 
@@ -124,9 +122,7 @@ def test_fp32_small(dev, B, H, Tq, Tk, D, causal):
     v = rng.standard_normal((B, H, Tk, D), dtype=np.float32)
     do = rng.standard_normal((B, H, Tq, D), dtype=np.float32)
     scale = 1.0 / math.sqrt(D)
-    import torch
-
-    o, dq, dk, dv, lse = _run(dev, q, k, v, do, scale, causal, torch.float32)
+    o, dq, dk, dv, lse = _run(dev, q, k, v, do, scale, causal, "float32")
     ro, rdq, rdk, rdv = reference_attention(q, k, v, do, scale, causal)
     _fp32_bar(o, ro, "o")
     _fp32_bar(dq, rdq, "dq")
@@ -152,9 +148,7 @@ def test_bf16_small(dev, B, H, Tq, Tk, D, causal):
     v = bf16_round(0.5 * rng.standard_normal((B, H, Tk, D), dtype=np.float32))
     do = bf16_round(rng.standard_normal((B, H, Tq, D), dtype=np.float32))
     scale = 1.0 / math.sqrt(D)
-    import torch
-
-    o, dq, dk, dv, lse = _run(dev, q, k, v, do, scale, causal, torch.bfloat16)
+    o, dq, dk, dv, lse = _run(dev, q, k, v, do, scale, causal, "bfloat16")
     ro, rdq, rdk, rdv = reference_attention(q, k, v, do, scale, causal)
     _bf16_bar(o, ro, "o")
     _bf16_bar(dq, rdq, "dq")
@@ -175,10 +169,8 @@ def test_fp32_strided_split_heads(dev):
     _say(f"[attn fp32 views] B={B} T={T} H={H} D={D}")
     rng = np.random.default_rng(7)
     xs = [rng.standard_normal((B, T, C), dtype=np.float32) for _ in range(4)]
-    import torch
-
     split = lambda t: t.view(B, T, H, D).transpose(1, 2)
-    o, dq, dk, dv, _ = _run(dev, *xs, 1 / 8, True, torch.float32, views=split)
+    o, dq, dk, dv, _ = _run(dev, *xs, 1 / 8, True, "float32", views=split)
     q, k, v, do = (x.reshape(B, T, H, D).transpose(0, 2, 1, 3) for x in xs)
     ro, rdq, rdk, rdv = reference_attention(q, k, v, do, 1 / 8, True)
     _fp32_bar(o, ro, "o")
@@ -189,20 +181,19 @@ def test_fp32_strided_split_heads(dev):
 
 def test_accumulate_flag(dev):
     """accumulate=1 adds into existing gradients (_accum_grad, tensor.py:29-33)."""
-    import torch
     from minitorch_amd import kernels as K
 
     _say("[attn accumulate]")
     rng = np.random.default_rng(3)
     shp = (1, 2, 50, 64)
-    q, k, v, do = (_to_dev(rng.standard_normal(shp, dtype=np.float32), dev, torch.float32) for _ in range(4))
+    q, k, v, do = (_to_dev(rng.standard_normal(shp, dtype=np.float32), dev, "float32") for _ in range(4))
     o, lse = K.attn_fwd(q, k, v, 0.125, True)
     dq, dk, dv = K.attn_bwd(q, k, v, o, do, lse, 0.125, True)
     base = [t.clone() for t in (dq, dk, dv)]
     K.attn_bwd(q, k, v, o, do, lse, 0.125, True, dq=dq, dk=dk, dv=dv, accumulate=True)
-    torch.cuda.synchronize()
+    sync()
     for a, b in zip((dq, dk, dv), base):
-        np.testing.assert_allclose(a.cpu().numpy(), 2 * b.cpu().numpy(), rtol=1e-6, atol=1e-7)
+        np.testing.assert_allclose(a.numpy(), 2 * b.numpy(), rtol=1e-6, atol=1e-7)
 
 
 @pytest.mark.parametrize("dtype_name", ["float32", "bfloat16"])
@@ -210,45 +201,42 @@ def test_phases_split_match_fused(dev, dtype_name):
     """mtx_attn_bwd_phase run as three calls (standalone delta kernel, then
     dQ, then dK/dV) gives the oracle's gradients and agrees with the fused
     DELTA|DQ path of mtx_attn_bwd up to the summation order of delta."""
-    import torch
     from minitorch_amd import _lib as L
     from minitorch_amd import kernels as K
 
-    dtype = getattr(torch, dtype_name)
+    dtype = dtype_name
     _say(f"[attn phases split vs fused] {dtype_name}")
     rng = np.random.default_rng(17)
     B, H, Tq, Tk, D = 2, 3, 150, 190, 64
     arrs = [rng.standard_normal((B, H, T, D), dtype=np.float32) for T in (Tq, Tk, Tk, Tq)]
-    if dtype == torch.bfloat16:
+    if dtype == "bfloat16":
         arrs = [bf16_round(0.5 * x) for x in arrs]
     q, k, v, do = (_to_dev(x, dev, dtype) for x in arrs)
     o, lse = K.attn_fwd(q, k, v, 0.125, True)
     fused = K.attn_bwd(q, k, v, o, do, lse, 0.125, True)
-    split = [torch.full_like(t, float("nan")) for t in fused]
-    ws = torch.empty(L.lib().mtx_attn_bwd_workspace_bytes(B, H, Tq), dtype=torch.uint8, device=dev)
+    split = [full(t.shape, float("nan")) for t in fused]
+    ws = empty((L.lib().mtx_attn_bwd_workspace_bytes(B, H, Tq),), "uint8")
     for ph in (L.ATTN_BWD_DELTA, L.ATTN_BWD_DQ, L.ATTN_BWD_DKDV):
         K.attn_bwd(q, k, v, o, do, lse, 0.125, True, dq=split[0], dk=split[1], dv=split[2],
                    workspace=ws, phases=ph)
-    torch.cuda.synchronize()
+    sync()
     refs = reference_attention(*arrs, 0.125, True)[1:]
     for name, a, b, r in zip(("dq", "dk", "dv"), fused, split, refs):
-        a, b = a.cpu().numpy(), b.cpu().numpy()
+        a, b = a.numpy(), b.numpy()
         assert np.all(np.isfinite(b)), name
         scale = float(np.abs(r).max())
         assert np.abs(a - b).max() <= 1e-5 * scale, (name, float(np.abs(a - b).max()), scale)
-        (_fp32_bar if dtype == torch.float32 else _bf16_bar)(b, r, name)
+        (_fp32_bar if dtype == "float32" else _bf16_bar)(b, r, name)
 
 
 def test_c1_full(dev):
     """Config C1: B=32, H=8, T=256, D=64 fp32, q,k,v,dO ~ N(0,1) drawn in that
     order from default_rng(1); scale 1/8.  Full tensors vs the oracle."""
-    import torch
-
     _say("[attn C1 full] B=32 H=8 T=256 D=64 fp32")
     rng = np.random.default_rng(1)
     shp = (32, 8, 256, 64)
     q, k, v, do = (rng.standard_normal(shp, dtype=np.float32) for _ in range(4))
-    o, dq, dk, dv, _ = _run(dev, q, k, v, do, 0.125, True, torch.float32)
+    o, dq, dk, dv, _ = _run(dev, q, k, v, do, 0.125, True, "float32")
     ro, rdq, rdk, rdv = reference_attention(q, k, v, do, 0.125, True)
     w = [_fp32_bar(o, ro, "o"), _fp32_bar(dq, rdq, "dq"), _fp32_bar(dk, rdk, "dk"), _fp32_bar(dv, rdv, "dv")]
     _say(f"  worst err/limit o,dq,dk,dv = {[round(x, 4) for x in w]}")
@@ -270,14 +258,12 @@ def test_bf16_elementwise_ragged_t(dev):
     """bf16 kernels elementwise against the rounding emulation at a T that is
     not a multiple of the 64-row tiles (ragged last query and key tiles,
     diagonal tiles in every slice): all B*H = 16 slices."""
-    import torch
-
     B, H, T, D = 2, 8, 1000, 64
     _say(f"[attn bf16 elementwise] B={B} H={H} T={T} D={D}")
     rng = np.random.default_rng(31)
     q, k, v = (bf16_round(0.5 * rng.standard_normal((B, H, T, D), dtype=np.float32)) for _ in range(3))
     do = bf16_round(rng.standard_normal((B, H, T, D), dtype=np.float32))
-    o, dq, dk, dv, lse = _run(dev, q, k, v, do, 0.125, True, torch.bfloat16)
+    o, dq, dk, dv, lse = _run(dev, q, k, v, do, 0.125, True, "bfloat16")
     _emu_slices("T=1000", q, k, v, do, 0.125, (o, lse, dq, dk, dv),
                 [(b, h) for b in range(B) for h in range(H)])
 
@@ -286,8 +272,6 @@ def test_c3_full(dev):
     """Config C3: B=8, H=16, T=2048, D=64; q,k,v = 0.5*N(0,1), dO = N(0,1), all
     rounded to bf16, drawn in that order from default_rng(3).  Six (b,h)
     slices vs the oracle; every slice through the dV / dK sum identities."""
-    import torch
-
     _say("[attn C3 full] B=8 H=16 T=2048 D=64 bf16")
     rng = np.random.default_rng(3)
     shp = (8, 16, 2048, 64)
@@ -295,7 +279,7 @@ def test_c3_full(dev):
     k = bf16_round(0.5 * rng.standard_normal(shp, dtype=np.float32))
     v = bf16_round(0.5 * rng.standard_normal(shp, dtype=np.float32))
     do = bf16_round(rng.standard_normal(shp, dtype=np.float32))
-    o, dq, dk, dv, lse = _run(dev, q, k, v, do, 0.125, True, torch.bfloat16)
+    o, dq, dk, dv, lse = _run(dev, q, k, v, do, 0.125, True, "bfloat16")
     assert np.all(np.isfinite(o)) and np.all(np.isfinite(dq))
     # 16 slices elementwise against the bf16 rounding emulation (every XCD
     # and both ends of the heaviest-first order are represented)

@@ -13,6 +13,7 @@ import sys
 
 import numpy as np
 import pytest
+from devarrays import T, T as _T, empty, full
 
 from oracle.attention import bf16_round, flash_forward
 
@@ -26,24 +27,22 @@ def _say(msg):
 
 def _cache(rng, B, H, Lmax, D, dtype):
     """q (B,H,1,D) and (B,Lmax,H*D) key/value caches with their head views."""
-    import torch
 
     q = rng.standard_normal((B, H, 1, D), dtype=np.float32)
     kc = rng.standard_normal((B, Lmax, H * D), dtype=np.float32)
     vc = rng.standard_normal((B, Lmax, H * D), dtype=np.float32)
-    if dtype == torch.bfloat16:
+    if dtype == "bfloat16":
         q, kc, vc = (bf16_round(0.5 * x) for x in (q, kc, vc))
     heads = lambda t: t.view(B, Lmax, H, D).transpose(1, 2)
-    tq, tk, tv = (torch.from_numpy(x).cuda().to(dtype) for x in (q, kc, vc))
+    tq, tk, tv = (T(x, dtype) for x in (q, kc, vc))
     host = lambda x: x.reshape(B, Lmax, H, D).transpose(0, 2, 1, 3)
     return (tq, heads(tk), heads(tv)), (q, host(kc), host(vc))
 
 
 def _check(got, ref, dtype, name):
-    import torch
 
     got = got.astype(np.float64)
-    if dtype == torch.float32:
+    if dtype == "float32":
         err = np.abs(got - ref)
         assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), (name, float(err.max()))
     else:
@@ -55,68 +54,60 @@ def _check(got, ref, dtype, name):
 @pytest.mark.parametrize("dtype_name", ["float32", "bfloat16"])
 @pytest.mark.parametrize("D", [16, 64, 128])
 def test_decode_matches_oracle_ragged(dev, dtype_name, D):
-    import torch
     from minitorch_amd import kernels as K
 
-    dtype = getattr(torch, dtype_name)
+    dtype = dtype_name
     B, H, Lmax = 4, 3, 300
     lengths = [1, 137, 256, 300]
     _say(f"[decode] {dtype_name} D={D} B={B} H={H} lengths={lengths}")
     rng = np.random.default_rng(40 + D)
     (tq, tk, tv), (q, k, v) = _cache(rng, B, H, Lmax, D, dtype)
-    lens = torch.tensor(lengths, dtype=torch.int32, device="cuda")
-    lse = torch.empty((B, H), dtype=torch.float32, device="cuda")
+    lens = T(np.array(lengths), "int32")
+    lse = empty((B, H))
     o, _ = K.attn_decode(tq, tk, tv, D ** -0.5, lse=lse, lengths=lens)
-    torch.cuda.synchronize()
-    o = o.float().cpu().numpy()
-    lse = lse.cpu().numpy()
+    o = o.numpy()
+    lse = lse.numpy()
     for b, Lb in enumerate(lengths):
         ro, rl = flash_forward(q[b:b + 1], k[b:b + 1, :, :Lb], v[b:b + 1, :, :Lb], D ** -0.5, causal=False)
         _check(o[b:b + 1], ro, dtype, f"o b={b}")
-        np.testing.assert_allclose(lse[b], rl[0, :, 0], rtol=1e-4 if dtype == torch.float32 else 2e-2,
-                                   atol=1e-5 if dtype == torch.float32 else 2e-2)
+        np.testing.assert_allclose(lse[b], rl[0, :, 0], rtol=1e-4 if dtype == "float32" else 2e-2,
+                                   atol=1e-5 if dtype == "float32" else 2e-2)
 
 
 def test_decode_full_cache_and_empty(dev):
     """No lengths: every sequence uses all L keys (L = 8192, the maximum);
     length 0 gives o = 0 and lse = -inf."""
-    import torch
     from minitorch_amd import kernels as K
 
     _say("[decode] L=8192 fp32, and a zero length")
     rng = np.random.default_rng(7)
-    (tq, tk, tv), (q, k, v) = _cache(rng, 1, 2, 8192, 64, torch.float32)
-    lse = torch.empty((1, 2), dtype=torch.float32, device="cuda")
+    (tq, tk, tv), (q, k, v) = _cache(rng, 1, 2, 8192, 64, "float32")
+    lse = empty((1, 2))
     o, _ = K.attn_decode(tq, tk, tv, 0.125, lse=lse)
     ro, rl = flash_forward(q, k, v, 0.125, causal=False)
-    torch.cuda.synchronize()
-    _check(o.cpu().numpy(), ro, torch.float32, "o")
-    np.testing.assert_allclose(lse.cpu().numpy(), rl[..., 0], rtol=1e-5, atol=1e-5)
-    zero = torch.zeros((1,), dtype=torch.int32, device="cuda")
+    _check(o.numpy(), ro, "float32", "o")
+    np.testing.assert_allclose(lse.numpy(), rl[..., 0], rtol=1e-5, atol=1e-5)
+    zero = full((1,), 0, "int32")
     o, _ = K.attn_decode(tq, tk, tv, 0.125, lse=lse, lengths=zero)
-    torch.cuda.synchronize()
-    assert np.all(o.cpu().numpy() == 0) and np.all(np.isneginf(lse.cpu().numpy()))
+    assert np.all(o.numpy() == 0) and np.all(np.isneginf(lse.numpy()))
 
 
 def test_decode_matches_fused_forward_at_last_position(dev):
     """A decode step equals the fused causal forward's last query row."""
-    import torch
     from minitorch_amd import kernels as K
 
     _say("[decode] vs fused forward, last row")
     rng = np.random.default_rng(11)
     B, H, T, D = 2, 6, 97, 64
-    q, k, v = (torch.from_numpy(rng.standard_normal((B, H, T, D), dtype=np.float32)).cuda() for _ in range(3))
+    q, k, v = (_T(rng.standard_normal((B, H, T, D), dtype=np.float32)) for _ in range(3))
     o_full, lse_full = K.attn_fwd(q, k, v, 0.125, True)
-    lse = torch.empty((B, H), dtype=torch.float32, device="cuda")
+    lse = empty((B, H))
     o, _ = K.attn_decode(q[:, :, T - 1:T], k, v, 0.125, lse=lse)
-    torch.cuda.synchronize()
-    np.testing.assert_allclose(o.cpu().numpy(), o_full[:, :, T - 1:T].cpu().numpy(), rtol=1e-4, atol=1e-5)
-    np.testing.assert_allclose(lse.cpu().numpy(), lse_full[:, :, T - 1].cpu().numpy(), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(o.numpy(), o_full[:, :, T - 1:T].numpy(), rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(lse.numpy(), lse_full[:, :, T - 1].numpy(), rtol=1e-5, atol=1e-5)
 
 
 def test_argmax_matches_numpy(dev):
-    import torch
     from minitorch_amd import kernels as K
 
     _say("[argmax] rows of 65 and 200 columns, with ties")
@@ -127,13 +118,12 @@ def test_argmax_matches_numpy(dev):
         x[1, -1] = 50.0                   # maximum in the last column
         x[2, :] = 1.0                     # all equal
         x[3, 64 % cols] = x[3, 0] = 7.0   # tie across lanes
-        t = torch.from_numpy(x).cuda()
-        margin = torch.empty((70,), dtype=torch.float32, device="cuda")
+        t = T(x)
+        margin = empty((70,))
         idx, _ = K.argmax_rows(t, margin=margin)
-        torch.cuda.synchronize()
-        np.testing.assert_array_equal(idx.cpu().numpy(), np.argmax(x, axis=1))
+        np.testing.assert_array_equal(idx.numpy(), np.argmax(x, axis=1))
         top2 = np.sort(x, axis=1)[:, -2:]
-        np.testing.assert_array_equal(margin.cpu().numpy(), top2[:, 1] - top2[:, 0])
+        np.testing.assert_array_equal(margin.numpy(), top2[:, 1] - top2[:, 0])
 
 
 def _gelu64(x):
@@ -145,7 +135,6 @@ def _gelu64(x):
                                             (5, 100, 70, 1, 0.5), (64, 512, 16, 0, 0.0)])
 def test_gemm_step_matches_float64(dev, M, K, N, act, beta):
     """mtx_gemm_step_f32 without cache columns: C = act(A @ B + bias + beta*C)."""
-    import torch
     from minitorch_amd import kernels as Kn
 
     _say(f"[gemm_step] M={M} K={K} N={N} act={act} beta={beta}")
@@ -154,12 +143,12 @@ def test_gemm_step_matches_float64(dev, M, K, N, act, beta):
     b = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
     bias = rng.standard_normal(N, dtype=np.float32)
     c0 = rng.standard_normal((M, N), dtype=np.float32)
-    ta, tb, tbias, tc = (torch.from_numpy(x).cuda() for x in (a, b, bias, c0))
+    ta, tb, tbias, tc = (T(x) for x in (a, b, bias, c0))
     Kn.gemm_step(ta, tb, bias=tbias, c=tc, beta=beta, act=act)
     ref = a.astype(np.float64) @ b + bias + beta * c0
     if act:
         ref = _gelu64(ref)
-    got = tc.cpu().numpy()
+    got = tc.numpy()
     err = np.abs(got - ref)
     assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), f"max err {err.max():.3e}"
 
@@ -167,7 +156,6 @@ def test_gemm_step_matches_float64(dev, M, K, N, act, beta):
 def test_gemm_step_writes_kv_cache_rows(dev):
     """The q/k/v step projection: q columns to c, k and v columns to cache row
     lengths[m] - 1; rows of sequences with lengths 0 or past T untouched."""
-    import torch
     from minitorch_amd import kernels as Kn
 
     _say("[gemm_step] kv scatter")
@@ -180,14 +168,14 @@ def test_gemm_step_writes_kv_cache_rows(dev):
     lengths[3], lengths[10] = 0, T + 1  # skipped
     kc0 = rng.standard_normal((B, T, C), dtype=np.float32)
     vc0 = rng.standard_normal((B, T, C), dtype=np.float32)
-    ta, tw, tb = (torch.from_numpy(x).cuda() for x in (a, w, bias))
-    tk, tv, tl = torch.from_numpy(kc0.copy()).cuda(), torch.from_numpy(vc0.copy()).cuda(), torch.from_numpy(lengths).cuda()
-    q = torch.empty(B, C, device="cuda")
+    ta, tw, tb = (_T(x) for x in (a, w, bias))
+    tk, tv, tl = _T(kc0), _T(vc0), _T(lengths, "int32")
+    q = empty((B, C))
     Kn.gemm_step(ta, tw, bias=tb, c=q, kv=(tk, tv, tl))
     P = a.astype(np.float64) @ w + bias
     tol = lambda r: 1e-5 + 1e-4 * np.abs(r)
-    assert np.all(np.abs(q.cpu().numpy() - P[:, :C]) <= tol(P[:, :C]))
-    kg, vg = tk.cpu().numpy(), tv.cpu().numpy()
+    assert np.all(np.abs(q.numpy() - P[:, :C]) <= tol(P[:, :C]))
+    kg, vg = tk.numpy(), tv.numpy()
     kref, vref = kc0.copy(), vc0.copy()
     for m in range(B):
         t = lengths[m] - 1

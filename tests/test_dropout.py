@@ -25,6 +25,7 @@ from pathlib import Path
 
 import numpy as np
 import pytest
+from devarrays import T, T as _T, full
 
 from oracle import attention as A
 from oracle.philox import keep_mask, philox4x32_10
@@ -113,18 +114,16 @@ def test_dropout_reference_flow_matches_f64_and_no_dropout():
     (64 * 6 * 256, 256, 0.1, 12345, 0),  # one C2 layer's attention matrix
 ])
 def test_device_keep_mask_matches_oracle(dev, rows, cols, p, seed, offset):
-    import torch
 
     from minitorch_amd import _lib as L
     from minitorch_amd import kernels as K
 
     _say(f"[dropout] philox mask rows={rows} cols={cols} p={p} seed={seed} offset={offset}")
     ld = K.keep_ld(cols) + 4
-    out = torch.full((rows, ld), 0xAB, dtype=torch.uint8, device=dev)
+    out = full((rows, ld), 0xAB, "uint8")
     L.call("mtx_dropout_keep_philox", L.ptr(out), rows, cols, ld, float(p), seed, offset,
-           L.stream_handle(out.device))
-    torch.cuda.synchronize()
-    got = out.cpu().numpy()
+           L.stream_handle())
+    got = out.numpy()
     np.testing.assert_array_equal(got[:, :cols], keep_mask(rows, cols, p, seed, offset))
     assert np.all(got[:, cols:] == 0xAB), "padding bytes were written"
 
@@ -153,7 +152,6 @@ DROP_CASES = [
 @pytest.mark.parametrize("dtype_name", ["fp32", "bf16"])
 @pytest.mark.parametrize("B,H,Tq,Tk,D,p", DROP_CASES)
 def test_fused_dropout_attention_matches_oracle(dev, dtype_name, B, H, Tq, Tk, D, p):
-    import torch
 
     from minitorch_amd import kernels as K
 
@@ -166,17 +164,16 @@ def test_fused_dropout_attention_matches_oracle(dev, dtype_name, B, H, Tq, Tk, D
     if bf:
         q, k, v, do = (A.bf16_round(x) for x in (q, k, v, do))
     keep = _host_keep(rng, B, H, Tq, Tk, p)
-    tdt = torch.bfloat16 if bf else torch.float32
-    tq, tk, tv, tdo = (torch.from_numpy(x).to(dev).to(tdt) for x in (q, k, v, do))
-    tkeep = torch.from_numpy(keep).to(dev)
+    tdt = "bfloat16" if bf else "float32"
+    tq, tk, tv, tdo = (T(x, tdt) for x in (q, k, v, do))
+    tkeep = T(keep, "uint8")
     ks = float(np.float32(1.0 / (1.0 - p)))
     scale = 1.0 / math.sqrt(D)
     o, lse = K.attn_fwd(tq, tk, tv, scale, True, keep=tkeep, keep_scale=ks)
     dq, dk, dv = K.attn_bwd(tq, tk, tv, o, tdo, lse, scale, True, keep=tkeep, keep_scale=ks)
-    torch.cuda.synchronize()
     ref = A.reference_attention(q, k, v, do, scale, True, keep=keep[..., :Tk], p=p)
     for name, got, r in zip(("o", "dq", "dk", "dv"), (o, dq, dk, dv), ref):
-        g = got.float().cpu().numpy().astype(np.float64)
+        g = got.numpy().astype(np.float64)
         if bf:
             amax = max(float(np.abs(r).max()), 1e-30)
             nmax = float(np.abs(g - r).max()) / amax
@@ -193,23 +190,20 @@ def test_all_kept_dropout_equals_plain_attention_fp32(dev):
     kernels' values bit for bit (same row-sum order, same products); the
     backward forms dS = P ((dP - delta) + delta - delta) with one extra
     rounding, so its gradients agree to the fp32 bar."""
-    import torch
 
     from minitorch_amd import kernels as K
 
     rng = np.random.default_rng(77)
     B, H, T, D = 2, 2, 96, 64
-    q, k, v, do = (torch.from_numpy(rng.standard_normal((B, H, T, D), dtype=np.float32)).to(dev)
-                   for _ in range(4))
-    ones = torch.ones((B, H, T, K.keep_ld(T)), dtype=torch.uint8, device=dev)
+    q, k, v, do = (_T(rng.standard_normal((B, H, T, D), dtype=np.float32)) for _ in range(4))
+    ones = full((B, H, T, K.keep_ld(T)), 1, "uint8")
     o1, l1 = K.attn_fwd(q, k, v, 0.125, True)
     o2, l2 = K.attn_fwd(q, k, v, 0.125, True, keep=ones, keep_scale=1.0)
     g1 = K.attn_bwd(q, k, v, o1, do, l1, 0.125, True)
     g2 = K.attn_bwd(q, k, v, o2, do, l2, 0.125, True, keep=ones, keep_scale=1.0)
-    torch.cuda.synchronize()
-    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    assert np.array_equal(o1.numpy(), o2.numpy()) and np.array_equal(l1.numpy(), l2.numpy())
     for a, b in zip(g1, g2):
-        a, b = a.cpu().numpy(), b.cpu().numpy()
+        a, b = a.numpy(), b.numpy()
         assert np.all(np.abs(a - b) <= 1e-5 + 1e-4 * np.abs(a)), float(np.abs(a - b).max())
 
 

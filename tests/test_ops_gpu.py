@@ -8,6 +8,7 @@ import sys
 
 import numpy as np
 import pytest
+from devarrays import H, T as _T, empty
 
 pytestmark = pytest.mark.gpu
 
@@ -18,16 +19,7 @@ def _say(msg):
 
 
 def T(x):
-    import torch
-
-    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).cuda()
-
-
-def H(t):
-    import torch
-
-    torch.cuda.synchronize()
-    return t.cpu().numpy()
+    return _T(np.ascontiguousarray(x, dtype=np.float32))
 
 
 def close(got, ref, rtol=1e-4, atol=1e-5, name=""):
@@ -64,7 +56,6 @@ def dot_tol(K):
     (64, 64, 4100, False, False, 1, False),     # K past the skinny range: tiled split-K
 ])
 def test_gemm(dev, M, N, K, ta, tb, batch, bias):
-    import torch
     from minitorch_amd import kernels as Kn
 
     _say(f"[gemm] M={M} N={N} K={K} ta={ta} tb={tb} batch={batch} bias={bias}")
@@ -84,14 +75,13 @@ def test_gemm(dev, M, N, K, ta, tb, batch, bias):
 
 
 def test_ewise_broadcast_and_accumulate(dev):
-    import torch
     from minitorch_amd import kernels as Kn
 
     _say("[ewise]")
     rng = np.random.default_rng(1)
     a = rng.standard_normal((4, 1, 6), dtype=np.float32)
     b = rng.standard_normal((3, 1), dtype=np.float32) + 3.0
-    out = torch.empty((4, 3, 6), device="cuda")
+    out = empty((4, 3, 6))
     for op, f in (("ADD", np.add), ("SUB", np.subtract), ("MUL", np.multiply), ("DIV", np.divide)):
         Kn.ewise(op, out, T(a), T(b))
         close(H(out), f(a.astype(np.float64), b), name=op)
@@ -99,7 +89,7 @@ def test_ewise_broadcast_and_accumulate(dev):
     close(H(out), (np.abs(a) + 0.5).astype(np.float64) ** b, rtol=2e-6 * 10, name="pow")
     for op, f in (("EXP", np.exp), ("TANH", np.tanh), ("NEG", np.negative),
                   ("LOG", lambda x: np.log(np.maximum(x, 1e-12)))):
-        o = torch.empty((4, 1, 6), device="cuda")
+        o = empty((4, 1, 6))
         Kn.ewise(op, o, T(a))
         close(H(o), f(a.astype(np.float64)), rtol=1e-5, name=op)
     # accumulate into a strided (transposed) output
@@ -115,14 +105,13 @@ def test_ewise_broadcast_and_accumulate(dev):
                                         ((64, 256, 384), [0, 1]), ((1, 5, 1, 7), [0, 2]),
                                         ((3, 1, 4, 5), [0, 1, 2]), ((4, 6, 8), [0, 2])])
 def test_reduce_sum(dev, shape, axes):
-    import torch
     from minitorch_amd import kernels as Kn
 
     _say(f"[reduce] {shape} {axes}")
     rng = np.random.default_rng(2)
     a = rng.standard_normal(shape, dtype=np.float32)
     kept = [s for i, s in enumerate(shape) if i not in axes]
-    out = torch.empty(kept if kept else (1,), device="cuda")
+    out = empty(kept if kept else (1,))
     Kn.reduce(T(a), axes, out, alpha=0.5)
     ref = 0.5 * a.astype(np.float64).sum(axis=tuple(axes))
     R = int(np.prod([shape[i] for i in axes]))
@@ -134,25 +123,23 @@ def test_reduce_merged_dims_bit_identical(dev):
     B*T rows; the result must be bit-identical to reducing the (B*T, C) view,
     and a transposed (non-mergeable) input must still match float64."""
     from minitorch_amd import kernels as Kn
-    import torch
 
     rng = np.random.default_rng(9)
     a = rng.standard_normal((64, 256, 384), dtype=np.float32)
     ta = T(a)
-    o3 = torch.empty(384, device="cuda")
-    o2 = torch.empty(384, device="cuda")
+    o3 = empty((384,))
+    o2 = empty((384,))
     Kn.reduce(ta, [0, 1], o3)
     Kn.reduce(ta.reshape(64 * 256, 384), [0], o2)
     assert np.array_equal(H(o3), H(o2))
     tt = ta.transpose(0, 2)  # (384, 256, 64), strides (1, 384, 98304)
-    ot = torch.empty(256, device="cuda")
+    ot = empty((256,))
     Kn.reduce(tt, [0, 2], ot)
     close(H(ot), a.astype(np.float64).sum(axis=(0, 2)), atol=dot_tol(64 * 384), name="reduce-strided")
 
 
 @pytest.mark.parametrize("rows,L,causal", [(3, 5, 0), (64, 65, 0), (40, 256, 256), (8, 1000, 0)])
 def test_softmax_and_log_softmax(dev, rows, L, causal):
-    import torch
     from minitorch_amd import kernels as Kn
     from oracle.attention import causal_mask
 
@@ -166,15 +153,15 @@ def test_softmax_and_log_softmax(dev, rows, L, causal):
         xs = np.where(m, -np.inf, xs)
     p = np.exp(xs - xs.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
-    y = torch.empty((rows, L), device="cuda")
+    y = empty((rows, L))
     Kn.softmax_fwd(T(x), y, causal_tq=causal)
     close(H(y), p, name="softmax")
-    dx = torch.empty((rows, L), device="cuda")
+    dx = empty((rows, L))
     Kn.softmax_bwd(y, T(dy), dx)
     g = dy * p
     close(H(dx), g - p * g.sum(-1, keepdims=True), name="softmax_bwd")
     if not causal:
-        ly = torch.empty((rows, L), device="cuda")
+        ly = empty((rows, L))
         Kn.softmax_fwd(T(x), ly, log=True)
         lp = np.log(p)
         close(H(ly), lp, atol=1e-5, name="log_softmax")
@@ -182,9 +169,9 @@ def test_softmax_and_log_softmax(dev, rows, L, causal):
         close(H(dx), dy - p * dy.sum(-1, keepdims=True), name="log_softmax_bwd")
 
 
-@pytest.mark.parametrize("rows,C", [(5, 64), (300, 384), (17, 1536), (3, 33), (4099, 384), (1000, 2048)])
+@pytest.mark.parametrize("rows,C", [(5, 64), (300, 384), (17, 1536), (3, 33), (4099, 384), (1000, 2048),
+                                    (301, 128), (301, 256), (301, 512), (301, 768), (301, 1024)])
 def test_layernorm(dev, rows, C):
-    import torch
     from minitorch_amd import kernels as Kn
     from oracle.gpt import Holder, ln_bwd, ln_fwd
 
@@ -194,16 +181,16 @@ def test_layernorm(dev, rows, C):
     gam = rng.standard_normal(C, dtype=np.float32)
     bet = rng.standard_normal(C, dtype=np.float32)
     dy = rng.standard_normal((rows, C), dtype=np.float32)
-    y = torch.empty((rows, C), device="cuda")
-    mean = torch.empty(rows, device="cuda")
-    std = torch.empty(rows, device="cuda")
+    y = empty((rows, C))
+    mean = empty((rows,))
+    std = empty((rows,))
     tx = T(x)
     Kn.layernorm_fwd(tx, T(gam), T(bet), y, mean, std, float(np.float32(1e-5)))
     ry, cache = ln_fwd(x.astype(np.float64), gam, bet)
     close(H(y), ry, name="ln_fwd")
-    dx = torch.empty((rows, C), device="cuda")
-    dg = torch.empty(C, device="cuda")
-    db = torch.empty(C, device="cuda")
+    dx = empty((rows, C))
+    dg = empty((C,))
+    db = empty((C,))
     Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dx=dx)
     Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dgamma=dg, dbeta=db)
     hx, hg, hb = Holder(x.shape, np.float64), Holder((C,), np.float64), Holder((C,), np.float64)
@@ -229,7 +216,6 @@ def test_layernorm(dev, rows, C):
 
 
 def test_gelu(dev):
-    import torch
     from minitorch_amd import kernels as Kn
     from oracle.gpt import Holder, gelu_bwd, gelu_fwd
 
@@ -237,11 +223,11 @@ def test_gelu(dev):
     rng = np.random.default_rng(5)
     x = rng.standard_normal(10001, dtype=np.float32) * 3
     dy = rng.standard_normal(10001, dtype=np.float32)
-    y = torch.empty(10001, device="cuda")
+    y = empty((10001,))
     Kn.gelu_fwd(T(x), y)
     ry, cache = gelu_fwd(x.astype(np.float64))
     close(H(y), ry, name="gelu")
-    dx = torch.empty(10001, device="cuda")
+    dx = empty((10001,))
     Kn.gelu_bwd(T(x), T(dy), dx)
     h = Holder(x.shape, np.float64)
     gelu_bwd(dy.astype(np.float64), cache, h)
@@ -249,7 +235,6 @@ def test_gelu(dev):
 
 
 def test_cross_entropy_and_embedding(dev):
-    import torch
     import minitorch_amd as mt
     from oracle.gpt import cross_entropy, cross_entropy_bwd
 
@@ -341,7 +326,6 @@ def test_tensor_autograd_like_reference_checks(dev):
 def test_embedding_backward_both_paths(dev):
     """Small tables take the one-hot GEMM path, large ones (V > 4096) the
     row-owner scatter kernel; both must equal np.add.at with repeated ids."""
-    import torch
     from minitorch_amd import kernels as Kn
 
     for V, n, C in ((65, 5000, 96), (5000, 700, 40)):
@@ -351,7 +335,7 @@ def test_embedding_backward_both_paths(dev):
         g = rng.standard_normal((n, C), dtype=np.float32)
         base = rng.standard_normal((V, C), dtype=np.float32)
         dw = T(base)
-        Kn.embedding_bwd(torch.from_numpy(ids).cuda(), T(g), dw, accumulate=True)
+        Kn.embedding_bwd(_T(ids, "int64"), T(g), dw, accumulate=True)
         ref = base.astype(np.float64).copy()
         np.add.at(ref, ids, g)
         close(H(dw), ref, atol=dot_tol(n), name=f"embedding_bwd V={V}")
@@ -418,24 +402,23 @@ def test_view_gradients_alias_and_accumulate_like_reference(dev):
 def test_pack3_unpack3(dev, rows, cols):
     """mtx_pack3_f32 / mtx_unpack3_f32 against NumPy concatenation and
     slicing, with every accumulate-mask bit (vector and scalar paths)."""
-    import torch
 
     from minitorch_amd import kernels as K
 
     rng = np.random.default_rng(rows * 1000 + cols)
     src = [rng.standard_normal((rows, cols), dtype=np.float32) for _ in range(3)]
-    ts = [torch.from_numpy(a).to(dev) for a in src]
-    packed = torch.empty((rows, 3 * cols), dtype=torch.float32, device=dev)
+    ts = [_T(a) for a in src]
+    packed = empty((rows, 3 * cols))
     K.pack3(ts, packed)
-    np.testing.assert_array_equal(packed.cpu().numpy(), np.concatenate(src, axis=1))
+    np.testing.assert_array_equal(packed.numpy(), np.concatenate(src, axis=1))
     base = [rng.standard_normal((rows, cols), dtype=np.float32) for _ in range(3)]
     for mask in range(8):
         acc = [bool(mask >> i & 1) for i in range(3)]
-        outs = [torch.from_numpy(b.copy()).to(dev) for b in base]
+        outs = [_T(b.copy()) for b in base]
         K.unpack3(packed, outs, acc)
         for i in range(3):
             expect = src[i] + base[i] if acc[i] else src[i]
-            np.testing.assert_array_equal(outs[i].cpu().numpy(), expect)
+            np.testing.assert_array_equal(outs[i].numpy(), expect)
 
 
 @pytest.mark.parametrize("M,N,K", [(37, 50, 23), (512, 1536, 384), (96, 80, 8192)])
@@ -443,7 +426,6 @@ def test_gemm_gelu_epilogues(dev, M, N, K):
     """mtx_gemm_act_f32: act 1 = gelu(A@B + bias) with the pre-activation in
     aux, act 2 = (A@B) * gelu'(aux), against NumPy float64 (the K = 8192 case
     takes the split-K path, whose reduce applies the epilogue)."""
-    import torch
 
     from minitorch_amd import kernels as K_
 
@@ -451,9 +433,9 @@ def test_gemm_gelu_epilogues(dev, M, N, K):
     a = (rng.standard_normal((M, K), dtype=np.float32) / np.float32(np.sqrt(K))).astype(np.float32)
     b = rng.standard_normal((K, N), dtype=np.float32)
     bias = rng.standard_normal(N, dtype=np.float32)
-    ta, tb, tbias = (torch.from_numpy(x).to(dev) for x in (a, b, bias))
-    c = torch.empty((M, N), dtype=torch.float32, device=dev)
-    h = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ta, tb, tbias = (_T(x) for x in (a, b, bias))
+    c = empty((M, N))
+    h = empty((M, N))
     K_.gemm(ta, tb, c, bias=tbias, act=K_.GEMM_ACT_GELU, aux=h)
     v = a.astype(np.float64) @ b.astype(np.float64) + bias
     c0, c1 = 0.7978845834732056, 0.044714998453855515
@@ -461,12 +443,12 @@ def test_gemm_gelu_epilogues(dev, M, N, K):
     gelu = 0.5 * v * (1 + t)
     dgelu = 0.5 * (1 + t) + 0.5 * v * (1 - t * t) * c0 * (1 + 3 * c1 * v * v)
     tol = lambda r: 1e-5 + 1e-4 * np.abs(r)
-    assert np.all(np.abs(h.cpu().numpy() - v) <= tol(v))
-    assert np.all(np.abs(c.cpu().numpy() - gelu) <= tol(gelu))
-    d = torch.empty((M, N), dtype=torch.float32, device=dev)
+    assert np.all(np.abs(h.numpy() - v) <= tol(v))
+    assert np.all(np.abs(c.numpy() - gelu) <= tol(gelu))
+    d = empty((M, N))
     K_.gemm(ta, tb, d, act=K_.GEMM_ACT_GELU_BWD, aux=h)
     ref = (a.astype(np.float64) @ b.astype(np.float64)) * dgelu
-    assert np.all(np.abs(d.cpu().numpy() - ref) <= tol(ref) + 1e-5 * np.abs(ref).max())
+    assert np.all(np.abs(d.numpy() - ref) <= tol(ref) + 1e-5 * np.abs(ref).max())
 
 
 @pytest.mark.gpu
@@ -477,7 +459,6 @@ def test_gemm_wgrad_colsum(dev, M, N, K, acc):
     Linear's bias gradient) from one launch, against NumPy float64.  The
     first case takes the split-K path (the sums go through the reduce), the
     odd shapes the edge-tile loaders, K = 0 gives C = beta C and sums of 0."""
-    import torch
 
     from minitorch_amd import kernels as K_
 
@@ -507,12 +488,11 @@ def test_gemm_wgrad_colsum(dev, M, N, K, acc):
         close(H(c2), H(c), atol=dot_tol(max(K, 1)) * 2, name="wgrad_vs_plain")
 
 
-@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (16384, 384, 384), (96, 80, 8192)])
+@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (16384, 384, 384), (96, 80, 8192), (64, 384, 2048)])
 def test_gemm_residual_epilogue(dev, M, N, K):
     """mtx_gemm_act_f32 act 4: C = A@B + bias + aux (a residual stream),
     against NumPy float64; the K = 8192 case takes the split-K path, whose
     reduce applies the add."""
-    import torch
 
     from minitorch_amd import kernels as K_
 
@@ -522,7 +502,7 @@ def test_gemm_residual_epilogue(dev, M, N, K):
     b = rng.standard_normal((K, N), dtype=np.float32)
     bias = rng.standard_normal(N, dtype=np.float32)
     res = rng.standard_normal((M, N), dtype=np.float32)
-    c = torch.empty((M, N), dtype=torch.float32, device=dev)
+    c = empty((M, N))
     K_.gemm(T(a), T(b), c, bias=T(bias), act=K_.GEMM_ACT_ADD, aux=T(res))
     ref = a.astype(np.float64) @ b.astype(np.float64) + bias + res
     close(H(c), ref, atol=dot_tol(K), name="gemm_residual")

@@ -10,6 +10,7 @@ import sys
 import numpy as np
 import pytest
 
+from devarrays import T, full, sync
 from oracle.attention import bf16_round
 
 pytestmark = pytest.mark.gpu
@@ -21,18 +22,14 @@ def _say(msg):
 
 
 def _inputs(rng, shp_q, shp_k, bf16):
-    import torch
-
     arrs = [rng.standard_normal(s, dtype=np.float32) for s in (shp_q, shp_k, shp_k, shp_q)]
     if bf16:
         arrs = [bf16_round(0.5 * a) for a in arrs]
-    dt = torch.bfloat16 if bf16 else torch.float32
-    return [torch.from_numpy(a).cuda().to(dt) for a in arrs]
+    return [T(a, "bfloat16" if bf16 else "float32") for a in arrs]
 
 
 @pytest.mark.parametrize("bf16", [False, True])
 def test_noalloc_matches_workspace_entry_point(dev, bf16):
-    import torch
     from minitorch_amd import kernels as K
 
     rng = np.random.default_rng(77)
@@ -43,11 +40,11 @@ def test_noalloc_matches_workspace_entry_point(dev, bf16):
         q, k, v, do = _inputs(rng, (B, H, Tq, D), (B, H, Tk, D), bf16)
         o, lse = K.attn_fwd(q, k, v, 0.125, True)
         ref = K.attn_bwd(q, k, v, o, do, lse, 0.125, True)
-        got = [torch.full((B, H, T, D), float("nan"), device=q.device) for T in (Tq, Tk, Tk)]
+        got = [full((B, H, t, D), float("nan")) for t in (Tq, Tk, Tk)]
         K.attn_bwd_noalloc(q, k, v, o, do, lse, 0.125, True, *got)
-        torch.cuda.synchronize()
+        sync()
         for name, a, b in zip(("dq", "dk", "dv"), ref, got):
-            a, b = a.cpu().numpy(), b.cpu().numpy()
+            a, b = a.numpy(), b.numpy()
             assert np.all(np.isfinite(b)), name
             assert np.array_equal(a, b), (name, float(np.abs(a - b).max()))
 
