@@ -276,6 +276,32 @@ int mtx_kv_append_f32(int B, int C, int T, const float* x, int64_t x_stride_b, f
  */
 int mtx_decode_advance(int B, int* lengths, int64_t* pos, void* stream);
 
+/*
+ * The greedy step's pick and bookkeeping in one launch.  Replaces, per
+ * generated token, the harness's np.argmax of the last logits and the
+ * np.concatenate of idx_next onto idx (transformer.py:97-103, argmax in place
+ * of the sampling), plus mtx_decode_advance: for each row b of x (rows x
+ * cols, row stride ld) the first-maximum index goes to cur[b] and to
+ * ids[lengths[b] * rows + b] (a time-major (Tmax, rows) int64 buffer; rows
+ * with lengths[b] outside [0, Tmax) skip it), the top-2 margin to
+ * margins[(lengths[b] - t_base) * rows + b] when margins != NULL and that
+ * row is in [0, n_margins); then lengths[b] += 1 and, if pos != NULL,
+ * pos[0] += 1.  lengths holds `rows` entries.
+ */
+int mtx_greedy_pick_f32(int rows, int cols, const float* x, int64_t ld, int64_t* cur, int64_t* ids, int Tmax,
+                        float* margins, int t_base, int n_margins, int* lengths, int64_t* pos, void* stream);
+
+/*
+ * out[i, :] = wa[ia[i], :] + wb[ib[i * ib_stride], :] for i < n: the token
+ * and position embeddings and their sum, transformer.py:84-87 (Embedding
+ * lookups, layers.py:102-104 / tensor.py:374-387, then Tensor.__add__,
+ * tensor.py:111-113), in one pass.  ib_stride 0 broadcasts one position id
+ * (a decode step).  Ids outside a table are clamped (the caller validates).
+ */
+int mtx_embedding2_fwd_f32(const float* wa, int64_t lda, int64_t Va, const int64_t* ia, const float* wb,
+                           int64_t ldb, int64_t Vb, const int64_t* ib, int64_t ib_stride, float* out, int64_t ldo,
+                           int64_t n, int C, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* GEMM                                                                     */
 /* ------------------------------------------------------------------------ */

@@ -200,17 +200,17 @@ typedef __attribute__((address_space(1))) void glb_void;
 // lane loads the global chunk that belongs at its LDS position.  Rows >=
 // nrows repeat row nrows-1 (finite data the kernels mask or weight by 0).
 // Completion: s_waitcnt vmcnt(0) by every wave, then a barrier.
-template <typename T, int R, int D>
+template <typename T, int R, int D, int NW = kWaves>
 struct TileDma {
   using LY = Lay<T, D>;
-  static constexpr int NI = R * LY::CPR / 64;           // wave-loads per tile
-  static constexpr int PW = (NI + kWaves - 1) / kWaves;  // per wave
-  int off[PW];                                          // lane offsets for whole tiles
+  static constexpr int NI = R * LY::CPR / 64;     // wave-loads per tile
+  static constexpr int PW = (NI + NW - 1) / NW;   // per wave
+  int off[PW];                                    // lane offsets for whole tiles
 
   __device__ __forceinline__ void init(int64_t ts, int wid, int lane) {
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
-      const int c = (wid + j * kWaves) * 64 + lane;
+      const int c = (wid + j * NW) * 64 + lane;
       const int row = c / LY::CPR, pch = c % LY::CPR;
       off[j] = row * (int)ts + (pch ^ LY::swz(row)) * LY::EPC;
     }
@@ -221,8 +221,8 @@ struct TileDma {
     const bool full = r0 + R <= nrows;
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
-      const int ins = wid + j * kWaves;
-      if (NI % kWaves != 0 && ins >= NI) continue;
+      const int ins = wid + j * NW;
+      if (NI % NW != 0 && ins >= NI) continue;
       int o = off[j];
       if (!full) {
         const int c = ins * 64 + lane;
@@ -707,15 +707,23 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const BwdArgs a) {
 // ---------------------------------------------------------------------------
 // backward, pass 1: dK, dV (key-outer).  Each wave owns NK*16 keys.
 // ---------------------------------------------------------------------------
+// waves per workgroup of the bf16 dK/dV pass (they share each Q/dO tile)
+#ifndef MTX_DKDV_WAVES
+#define MTX_DKDV_WAVES 4
+#endif
+template <typename T>
+constexpr int dkdv_waves() { return sizeof(T) == 2 ? MTX_DKDV_WAVES : kWaves; }
+
 template <typename T, int D, int NK, bool DROP>
-__global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void attn_dkdv_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 1 : 2) void attn_dkdv_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
   constexpr bool BF = sizeof(T) == 2;
   constexpr int KC = DM::KC;
   constexpr int DT = D / 16;
-  constexpr int BKV = kWaves * NK * 16;
+  constexpr int NWV = dkdv_waves<T>();
+  constexpr int BKV = NWV * NK * 16;
   constexpr int BQ = 64;
   constexpr int NS = BQ / MF::KI;
   using LY = Lay<T, D>;
@@ -763,8 +771,8 @@ __global__ __launch_bounds__(kThreads, D == 128 && sizeof(T) == 4 ? 1 : 2) void 
   qstart = (qstart / BQ) * BQ;
   const int ntile = qstart < a.Tq ? (a.Tq - qstart + BQ - 1) / BQ : 0;
   const LaneOffs<T, D> lo(n, g);
-  TileDma<T, BQ, D> qdma, ddma;  // bf16: direct global -> LDS
-  TileRegs<T, BQ, D> qreg, dreg;  // fp32: through registers
+  TileDma<T, BQ, D, NWV> qdma, ddma;  // bf16: direct global -> LDS
+  TileRegs<T, BQ, D> qreg, dreg;       // fp32: through registers
   if constexpr (LY::DIRECT) {
     qdma.init(a.sq.t, wid, lane);
     ddma.init(a.sdo.t, wid, lane);
@@ -1285,11 +1293,12 @@ int launch_bwd(const BwdArgs& a, int phases, hipStream_t st) {
     MTX_LAUNCHED();
   }
   if (phases & MTX_ATTN_BWD_DKDV) {
-    const int gk = cdiv(a.Tk, kWaves * NK * 16) * a.B * a.H;
+    constexpr int NWV = dkdv_waves<T>();
+    const int gk = cdiv(a.Tk, NWV * NK * 16) * a.B * a.H;
     if (a.keep)
-      hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, true>), dim3(gk), dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, true>), dim3(gk), dim3(64 * NWV), 0, st, a);
     else
-      hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, false>), dim3(gk), dim3(kThreads), 0, st, a);
+      hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, false>), dim3(gk), dim3(64 * NWV), 0, st, a);
     MTX_LAUNCHED();
   }
   return MTX_OK;

@@ -23,6 +23,7 @@
 // device memory, so one recorded step (a HIP graph) replays for every token.
 #include "mtx_common.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace mtx {
@@ -214,6 +215,71 @@ __global__ __launch_bounds__(256) void kv_append_kernel(int B, int C, int T, con
 }
 
 // lengths[b] += 1 for every b; pos[0] += 1
+// The greedy step's pick, record and bookkeeping in one launch: row b's
+// first-maximum index goes to cur[b] (the next step's input) and to the
+// time-major id buffer at row lengths[b] (the position the token takes), the
+// top-2 margin to margins at row lengths[b] - t_base, then lengths[b] += 1;
+// row 0 also advances the position id.  Each row's lengths entry is read and
+// written by that row's lane 0 only.
+__global__ __launch_bounds__(256) void greedy_pick_kernel(int rows, int cols, const float* __restrict__ x,
+                                                          int64_t ld, int64_t* __restrict__ cur,
+                                                          int64_t* __restrict__ ids, int Tmax,
+                                                          float* __restrict__ margins, int t_base, int nm,
+                                                          int* __restrict__ lengths, int64_t* __restrict__ pos) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;  // wave-uniform
+  const float* __restrict__ xr = x + (int64_t)row * ld;
+  Top2 t{-INFINITY, -INFINITY, cols};
+  for (int c = lane; c < cols; c += 64) {
+    const float v = xr[c];
+    if (v > t.m1) {
+      t.m2 = t.m1;
+      t.m1 = v;
+      t.i1 = c;
+    } else if (v > t.m2) {
+      t.m2 = v;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    Top2 o;
+    o.m1 = __shfl_xor(t.m1, m, 64);
+    o.m2 = __shfl_xor(t.m2, m, 64);
+    o.i1 = __shfl_xor(t.i1, m, 64);
+    t = merge(t, o);
+  }
+  if (lane == 0) {
+    const int L = lengths[row];
+    cur[row] = t.i1;
+    if (L >= 0 && L < Tmax) ids[(int64_t)L * rows + row] = t.i1;
+    const int s = L - t_base;
+    if (margins != nullptr && s >= 0 && s < nm) margins[(int64_t)s * rows + row] = t.m1 - t.m2;
+    lengths[row] = L + 1;
+    if (row == 0 && pos != nullptr) pos[0] += 1;
+  }
+}
+
+// out[i] = wa[ia[i]] + wb[ib[i * ib_stride]]: the token and position
+// embeddings and their sum (transformer.py:84-87) in one pass; ids are
+// clamped to the tables (they are validated on the host)
+__global__ __launch_bounds__(256) void embed2_kernel(const float* __restrict__ wa, int64_t lda, int64_t Va,
+                                                     const int64_t* __restrict__ ia,
+                                                     const float* __restrict__ wb, int64_t ldb, int64_t Vb,
+                                                     const int64_t* __restrict__ ib, int64_t ib_stride,
+                                                     float* __restrict__ out, int64_t ldo, int64_t n, int C) {
+  const int64_t total = n * C;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = e / C;
+    const int c = (int)(e % C);
+    int64_t ra = ia[i], rb = ib[i * ib_stride];
+    ra = ra < 0 ? 0 : (ra >= Va ? Va - 1 : ra);
+    rb = rb < 0 ? 0 : (rb >= Vb ? Vb - 1 : rb);
+    out[i * ldo + c] = wa[ra * lda + c] + wb[rb * ldb + c];
+  }
+}
+
 __global__ void advance_kernel(int B, int* __restrict__ lengths, int64_t* __restrict__ pos) {
   const int i = threadIdx.x + blockIdx.x * blockDim.x;
   if (i < B) lengths[i] += 1;
@@ -305,6 +371,34 @@ extern "C" int mtx_kv_append_f32(int B, int C, int T, const float* x, int64_t x_
   hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), B, C, T, x, x_stride_b, cache, cache_stride_b,
                      cache_stride_t, lengths);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_greedy_pick_f32(int rows, int cols, const float* x, int64_t ld, int64_t* cur, int64_t* ids,
+                                   int Tmax, float* margins, int t_base, int n_margins, int* lengths,
+                                   int64_t* pos, void* stream) {
+  MTX_CHECK_SHAPE(rows >= 1 && cols >= 1 && Tmax >= 1, "rows, cols, Tmax must be >= 1 (got %d, %d, %d)", rows,
+                  cols, Tmax);
+  MTX_CHECK_ARG(x && cur && ids && lengths, "x, cur, ids, lengths: null pointer");
+  MTX_CHECK_ARG(ld >= cols, "ld=%lld < cols=%d", (long long)ld, cols);
+  MTX_CHECK_ARG(margins == nullptr || n_margins >= 1, "n_margins must be >= 1 with a margin buffer");
+  hipLaunchKernelGGL(greedy_pick_kernel, dim3((rows + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     rows, cols, x, ld, cur, ids, Tmax, margins, t_base, n_margins, lengths, pos);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_embedding2_fwd_f32(const float* wa, int64_t lda, int64_t Va, const int64_t* ia, const float* wb,
+                                      int64_t ldb, int64_t Vb, const int64_t* ib, int64_t ib_stride, float* out,
+                                      int64_t ldo, int64_t n, int C, void* stream) {
+  MTX_CHECK_ARG(wa && ia && wb && ib && out, "embedding2: null pointer");
+  MTX_CHECK_SHAPE(n >= 0 && C >= 1 && Va >= 1 && Vb >= 1 && lda >= C && ldb >= C && ldo >= C && ib_stride >= 0,
+                  "embedding2: bad shape");
+  if (n == 0) return MTX_OK;
+  const int blocks = (int)std::min<int64_t>((n * C + 255) / 256, 16384);
+  hipLaunchKernelGGL(embed2_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), wa, lda, Va, ia,
+                     wb, ldb, Vb, ib, ib_stride, out, ldo, n, C);
   MTX_LAUNCHED();
   return MTX_OK;
 }

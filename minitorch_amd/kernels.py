@@ -449,9 +449,51 @@ def gemm_step(a, b, bias=None, c=None, beta=0.0, act=ACT_NONE, kv=None):
             raise ValueError(f"gemm_step: c must be ({M}, {nc}) with unit column stride")
     L.call("mtx_gemm_step_f32", int(M), int(N), int(Kd), L.ptr(a), a.stride(0), L.ptr(b), b.stride(0),
            float(beta), L.ptr(c) if nc > 0 else None, c.stride(0) if nc > 0 else 0,
-           L.ptr(bias) if bias is not None else None, int(act), int(nc), *cache_args,
-           L.stream_handle())
+           L.ptr(bias) if bias is not None else None, int(act), int(nc), *cache_args, L.stream_handle())
     return c
+
+
+def greedy_pick(x, cur, ids, lengths, pos=None, margins=None, t_base=0):
+    """mtx_greedy_pick_f32: per row of x (rows, cols) the first-maximum index
+    to cur (int64 (rows,)) and to ids[lengths[row], row] (int64 (Tmax, rows)),
+    the top-2 margin to margins[lengths[row] - t_base, row] (float32
+    (n, rows)); then lengths += 1 (int32 (rows,)) and pos += 1."""
+    _need_cuda(x, cur, ids, lengths)
+    rows, cols = x.shape
+    if _dt(x) != "float32" or x.stride(1) != 1:
+        raise ValueError("greedy_pick: x must be fp32 with contiguous rows")
+    if _dt(cur) != "int64" or cur.numel() != rows or not cur.is_contiguous():
+        raise ValueError("greedy_pick: cur must be contiguous int64 (rows,)")
+    if _dt(ids) != "int64" or ids.dim() != 2 or ids.shape[1] != rows or not ids.is_contiguous():
+        raise ValueError("greedy_pick: ids must be contiguous int64 (Tmax, rows)")
+    if _dt(lengths) != "int32" or lengths.numel() != rows or not lengths.is_contiguous():
+        raise ValueError("greedy_pick: lengths must be contiguous int32 (rows,)")
+    if pos is not None and _dt(pos) != "int64":
+        raise ValueError("greedy_pick: pos must be int64")
+    if margins is not None and (_dt(margins) != "float32" or margins.dim() != 2 or margins.shape[1] != rows
+                                or not margins.is_contiguous()):
+        raise ValueError("greedy_pick: margins must be contiguous fp32 (n, rows)")
+    L.call("mtx_greedy_pick_f32", rows, cols, L.ptr(x), x.stride(0), L.ptr(cur), L.ptr(ids), ids.shape[0],
+           L.ptr(margins) if margins is not None else None, int(t_base),
+           margins.shape[0] if margins is not None else 0, L.ptr(lengths),
+           L.ptr(pos) if pos is not None else None, L.stream_handle())
+
+
+def embedding2_fwd(wa, ia, wb, ib, out, ib_stride=1):
+    """out (n, C) = wa[ia] + wb[ib] (mtx_embedding2_fwd_f32); ib_stride 0
+    broadcasts ib[0]."""
+    Va, C = wa.shape
+    Vb = wb.shape[0]
+    n = ia.numel()
+    if _dt(ia) != "int64" or _dt(ib) != "int64" or wb.shape[1] != C or out.shape[-1] != C:
+        raise ValueError("embedding2: int64 ids and tables / output of one width")
+    if wa.stride(1) != 1 or wb.stride(1) != 1 or out.stride(-1) != 1 or not ia.is_contiguous():
+        raise ValueError("embedding2: rows must be contiguous")
+    if ib_stride and ib.numel() < n:
+        raise ValueError("embedding2: ib has fewer ids than ia")
+    L.call("mtx_embedding2_fwd_f32", L.ptr(wa), wa.stride(0), Va, L.ptr(ia), L.ptr(wb), wb.stride(0), Vb,
+           L.ptr(ib), int(ib_stride), L.ptr(out), out.stride(-2) if out.dim() >= 2 else C, n, C, L.stream_handle())
+    return out
 
 
 # ---------------------------------------------------------------------------

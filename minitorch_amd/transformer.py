@@ -297,24 +297,23 @@ class GPT(Module):
                 for block in self.blocks:
                     block.attn.fuse_qkv()
                 cur = ids.t[T0].clone()              # ids fed to the next step, then overwritten
-                mcur = dev.empty((B,)).t
                 lengths = dev.full((B,), T0 + 1, "int32").t
                 posd = dev.full((1,), T0, "int64").t
+                x = dev.empty((B, 1, C))
 
                 def step():
-                    x = self.tok_emb(DeviceArray(cur.view(B, 1))) + self.pos_emb(DeviceArray(posd))
+                    # embeddings of this token and position in one launch;
+                    # the pick writes the next input, the id and margin
+                    # records, and advances the positions (mtx_greedy_pick_f32)
+                    K.embedding2_fwd(self.tok_emb.weight.data.t, cur, self.pos_emb.weight.data.t, posd,
+                                     x.t.view(B, C), ib_stride=0)
+                    h = Tensor(x)
                     for block, cache in zip(self.blocks, caches):
-                        x = block.forward_step(x, cache, lengths)
-                    logits = self.lm_head(self.ln_f(x)).data.t.view(B, -1)
-                    K.argmax_rows(logits, idx=cur, margin=mcur)
-                    K.decode_advance(lengths, posd)
-
-                def record(s):
-                    ids.t[T0 + s].copy_(cur)
-                    margins.t[s].copy_(mcur)
+                        h = block.forward_step(h, cache, lengths)
+                    logits = self.lm_head(self.ln_f(h)).data.t.view(B, -1)
+                    K.greedy_pick(logits, cur, ids.t, lengths, posd, margins.t, t_base=T0)
 
                 step()
-                record(1)
                 if graph and n > 2:
                     from .graphs import Graph
 
@@ -323,11 +322,9 @@ class GPT(Module):
                         step()
                     for s in range(2, n):
                         g.replay()
-                        record(s)
                 else:
                     for s in range(2, n):
                         step()
-                        record(s)
         out = ids.t.numpy().T.copy()
         out[:, :T0] = idx
         if return_margins:

@@ -184,3 +184,57 @@ def test_gemm_step_writes_kv_cache_rows(dev):
             assert np.all(np.abs(vg[m, t] - P[m, 2 * C:]) <= tol(P[m, 2 * C:])), m
             kref[m, t], vref[m, t] = kg[m, t], vg[m, t]
     assert np.array_equal(kg, kref) and np.array_equal(vg, vref), "rows other than lengths-1 changed"
+
+
+def test_greedy_pick_matches_argmax_advance_and_records(dev):
+    """mtx_greedy_pick_f32 against mtx_argmax_f32 + mtx_decode_advance and
+    the host-side record of the pick: cur, the id row lengths[b], the margin
+    row lengths[b] - t_base, lengths + 1, pos + 1; rows whose length falls
+    outside the buffers skip the record."""
+    from minitorch_amd import kernels as Kn
+
+    _say("[greedy_pick]")
+    rng = np.random.default_rng(9)
+    rows, cols, Tmax, T0, n = 64, 65, 40, 10, 30
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    x[5, 3] = x[5, 9] = 10.0  # tie: first index
+    lengths = rng.integers(T0 + 1, Tmax, rows).astype(np.int32)
+    lengths[7] = Tmax + 3     # past the id buffer: no record
+    ids0 = rng.integers(0, 65, (Tmax, rows)).astype(np.int64)
+    m0 = rng.standard_normal((n, rows)).astype(np.float32)
+    tx, cur, ids, mg, tl, pos = _T(x), _T(np.zeros(rows, np.int64), "int64"), _T(ids0, "int64"), _T(m0), \
+        _T(lengths, "int32"), _T(np.array([17], np.int64), "int64")
+    Kn.greedy_pick(tx, cur, ids, tl, pos, mg, t_base=T0)
+    ref_idx, ref_m = np.argmax(x, axis=1), np.sort(x, axis=1)
+    ref_m = ref_m[:, -1] - ref_m[:, -2]
+    np.testing.assert_array_equal(cur.numpy(), ref_idx)
+    want_ids, want_m = ids0.copy(), m0.copy()
+    for b in range(rows):
+        L = lengths[b]
+        if 0 <= L < Tmax:
+            want_ids[L, b] = ref_idx[b]
+        if 0 <= L - T0 < n:
+            want_m[L - T0, b] = ref_m[b]
+    np.testing.assert_array_equal(ids.numpy(), want_ids)
+    np.testing.assert_array_equal(mg.numpy(), want_m)
+    np.testing.assert_array_equal(tl.numpy(), lengths + 1)
+    assert int(pos.numpy()[0]) == 18
+
+
+def test_embedding2_matches_gathers_plus_add(dev):
+    """mtx_embedding2_fwd_f32: token rows + position rows in one pass, equal
+    bit for bit to the two gathers and the add (one fp32 addition each);
+    ib_stride 0 broadcasts one position."""
+    from minitorch_amd import kernels as Kn
+
+    _say("[embedding2]")
+    rng = np.random.default_rng(10)
+    Wt = rng.standard_normal((65, 384)).astype(np.float32)
+    Wp = rng.standard_normal((256, 384)).astype(np.float32)
+    ia = rng.integers(0, 65, 64)
+    ib = rng.integers(0, 256, 64)
+    out = empty((64, 384))
+    Kn.embedding2_fwd(_T(Wt), _T(ia, "int64"), _T(Wp), _T(ib, "int64"), out)
+    np.testing.assert_array_equal(out.numpy(), Wt[ia] + Wp[ib])
+    Kn.embedding2_fwd(_T(Wt), _T(ia, "int64"), _T(Wp), _T(np.array([37]), "int64"), out, ib_stride=0)
+    np.testing.assert_array_equal(out.numpy(), Wt[ia] + Wp[37])
