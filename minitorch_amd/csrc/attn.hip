@@ -194,43 +194,52 @@ struct Lay {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 
-// bf16 tile of R rows staged by direct global -> LDS loads
-// (global_load_lds_dwordx4: lane i of a wave writes bytes [16i, 16i+16) of
-// the wave's 1 KiB destination), so no registers hold the next tile.  Each
-// lane loads the global chunk that belongs at its LDS position.  Rows >=
-// nrows repeat row nrows-1 (finite data the kernels mask or weight by 0).
+// bf16 tile of R rows staged by direct global -> LDS loads through a buffer
+// resource (buffer_load_dwordx4 ... lds: lane i of a wave writes bytes
+// [16i, 16i+16) of the wave's 1 KiB destination), so no registers hold the
+// next tile.  Each lane loads the global chunk that belongs at its LDS
+// position, at a 32-bit byte offset that is the same for every tile; the
+// resource (scalar registers) starts at the tile's first row and spans the
+// rows left in the (b,h) slice, so rows >= nrows read as zeros (finite data
+// the kernels mask or weight by 0) with no per-lane test or address math.
 // Completion: s_waitcnt vmcnt(0) by every wave, then a barrier.
 template <typename T, int R, int D, int NW = kWaves>
 struct TileDma {
   using LY = Lay<T, D>;
   static constexpr int NI = R * LY::CPR / 64;     // wave-loads per tile
   static constexpr int PW = (NI + NW - 1) / NW;   // per wave
-  int off[PW];                                    // lane offsets for whole tiles
+  const T* base;
+  int64_t ts;
+  int nrows;
+  uint32_t off[PW];  // byte offsets of this lane's chunks inside a tile
 
-  __device__ __forceinline__ void init(int64_t ts, int wid, int lane) {
+  // base: row 0 of the (b,h) slice; ts: its row stride (elements); the host
+  // has checked nrows * ts * sizeof(T) < 2^31
+  __device__ __forceinline__ void init(const T* b, int64_t t, int n, int wid, int lane) {
+    base = b;
+    ts = t;
+    nrows = n;
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
       const int c = (wid + j * NW) * 64 + lane;
       const int row = c / LY::CPR, pch = c % LY::CPR;
-      off[j] = row * (int)ts + (pch ^ LY::swz(row)) * LY::EPC;
+      off[j] = (uint32_t)(row * (int)t + (pch ^ LY::swz(row)) * LY::EPC) * (uint32_t)sizeof(T);
     }
   }
-  __device__ __forceinline__ void issue(const T* __restrict__ g, int64_t ts, int r0, int nrows, T* buf, int wid,
-                                        int lane) const {
-    const T* base = g + (int64_t)r0 * ts;
-    const bool full = r0 + R <= nrows;
+  __device__ __forceinline__ void issue(int r0, T* buf, int wid) const {
+    // device pass only: the host pass would otherwise drop the stubs of the
+    // kernels that use the AMDGPU buffer-resource type
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int bytes = (nrows - r0) * (int)ts * (int)sizeof(T);
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + (int64_t)r0 * ts), (short)0, bytes, 0x00020000);
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
       const int ins = wid + j * NW;
       if (NI % NW != 0 && ins >= NI) continue;
-      int o = off[j];
-      if (!full) {
-        const int c = ins * 64 + lane;
-        const int row = c / LY::CPR, pch = c % LY::CPR;
-        o = min(row, nrows - r0 - 1) * (int)ts + (pch ^ LY::swz(row)) * LY::EPC;
-      }
-      __builtin_amdgcn_global_load_lds((glb_void*)(base + o), (lds_void*)(buf + ins * 64 * LY::EPC), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(buf + ins * 64 * LY::EPC), 16, off[j], 0, 0, 0);
     }
+#endif
   }
 };
 
@@ -514,11 +523,11 @@ void attn_fwd_kernel(const FwdArgs a) {
   TileDma<T, BK, D> kdma, vdma;  // bf16: direct global -> LDS
   TileRegs<T, BK, D> kreg, vreg;  // fp32: through registers
   if constexpr (LY::DIRECT) {
-    kdma.init(a.sk.t, wid, lane);
-    vdma.init(a.sv.t, wid, lane);
+    kdma.init(kp, a.sk.t, a.Tk, wid, lane);
+    vdma.init(vp, a.sv.t, a.Tk, wid, lane);
     if (ntile > 0) {
-      kdma.issue(kp, a.sk.t, 0, a.Tk, K0, wid, lane);
-      vdma.issue(vp, a.sv.t, 0, a.Tk, V0, wid, lane);
+      kdma.issue(0, K0, wid);
+      vdma.issue(0, V0, wid);
     }
   } else if (ntile > 0) {
     kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
@@ -542,8 +551,8 @@ void attn_fwd_kernel(const FwdArgs a) {
     __syncthreads();
     if (it + 1 < ntile) {
       if constexpr (LY::DIRECT) {
-        kdma.issue(kp, a.sk.t, kb + BK, a.Tk, PN ? K1 : K0, wid, lane);
-        vdma.issue(vp, a.sv.t, kb + BK, a.Tk, PN ? V1 : V0, wid, lane);
+        kdma.issue(kb + BK, PN ? K1 : K0, wid);
+        vdma.issue(kb + BK, PN ? V1 : V0, wid);
       } else {
         kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
         vreg.fetch(vp, a.sv.t, kb + BK, a.Tk, tid);
@@ -774,8 +783,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
   TileDma<T, BQ, D, NWV> qdma, ddma;  // bf16: direct global -> LDS
   TileRegs<T, BQ, D> qreg, dreg;       // fp32: through registers
   if constexpr (LY::DIRECT) {
-    qdma.init(a.sq.t, wid, lane);
-    ddma.init(a.sdo.t, wid, lane);
+    qdma.init(qp, a.sq.t, a.Tq, wid, lane);
+    ddma.init(dop, a.sdo.t, a.Tq, wid, lane);
   }
   float lse_r = 0.f, del_r = 0.f;
   // the next tile's loads: lse / delta (through registers, raw; converted
@@ -788,8 +797,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
       del_r = delp[qi];
     }
     if constexpr (LY::DIRECT) {
-      qdma.issue(qp, a.sq.t, qt, a.Tq, qdst, wid, lane);
-      ddma.issue(dop, a.sdo.t, qt, a.Tq, ddst, wid, lane);
+      qdma.issue(qt, qdst, wid);
+      ddma.issue(qt, ddst, wid);
     } else {
       qreg.fetch(qp, a.sq.t, qt, a.Tq, tid);
       dreg.fetch(dop, a.sdo.t, qt, a.Tq, tid);
@@ -1067,11 +1076,11 @@ void attn_dq_kernel(const BwdArgs a) {
   TileDma<T, BK, D> kdma, vdma;  // bf16: direct global -> LDS
   TileRegs<T, BK, D> kreg, vreg;  // fp32: through registers
   if constexpr (LY::DIRECT) {
-    kdma.init(a.sk.t, wid, lane);
-    vdma.init(a.sv.t, wid, lane);
+    kdma.init(kp, a.sk.t, a.Tk, wid, lane);
+    vdma.init(vp, a.sv.t, a.Tk, wid, lane);
     if (ntile > 0) {
-      kdma.issue(kp, a.sk.t, 0, a.Tk, K0, wid, lane);
-      vdma.issue(vp, a.sv.t, 0, a.Tk, V0, wid, lane);
+      kdma.issue(0, K0, wid);
+      vdma.issue(0, V0, wid);
     }
   } else if (ntile > 0) {
     kreg.fetch(kp, a.sk.t, 0, a.Tk, tid);
@@ -1095,8 +1104,8 @@ void attn_dq_kernel(const BwdArgs a) {
     __syncthreads();
     if (it + 1 < ntile) {
       if constexpr (LY::DIRECT) {
-        kdma.issue(kp, a.sk.t, kb + BK, a.Tk, PN ? K1 : K0, wid, lane);
-        vdma.issue(vp, a.sv.t, kb + BK, a.Tk, PN ? V1 : V0, wid, lane);
+        kdma.issue(kb + BK, PN ? K1 : K0, wid);
+        vdma.issue(kb + BK, PN ? V1 : V0, wid);
       } else {
         kreg.fetch(kp, a.sk.t, kb + BK, a.Tk, tid);
         vreg.fetch(vp, a.sv.t, kb + BK, a.Tk, tid);
@@ -1239,6 +1248,16 @@ int check_bhtd(const char* name, const void* p, const int64_t* s, int esize) {
   return MTX_OK;
 }
 
+// bf16 tiles load through a buffer resource spanning one (b,h) slice's rows:
+// rows * t_stride * 2 bytes must stay below 2^31
+int check_slice_bytes(const char* name, const int64_t* s, int rows, int esize) {
+  if (esize != 2) return MTX_OK;
+  MTX_CHECK_SHAPE((int64_t)rows * s[2] * esize < ((int64_t)1 << 31),
+                  "%s: %d rows x t stride %lld x 2 bytes must be < 2^31 (bf16 tile loads)", name, rows,
+                  (long long)s[2]);
+  return MTX_OK;
+}
+
 int check_dims(int dtype, int B, int H, int Tq, int Tk, int D, int causal) {
   if (dtype != MTX_F32 && dtype != MTX_BF16) return fail(MTX_ERR_DTYPE, "unsupported dtype %d", dtype);
   MTX_CHECK_SHAPE(B >= 1 && H >= 1 && Tq >= 1 && Tk >= 1, "B,H,Tq,Tk must be >= 1 (got %d,%d,%d,%d)",
@@ -1351,6 +1370,8 @@ int attn_fwd_impl(int dtype, int B, int H, int Tq, int Tk, int D,
   if ((rc = check_bhtd("k", k, k_strides, es))) return rc;
   if ((rc = check_bhtd("v", v, v_strides, es))) return rc;
   if ((rc = check_bhtd("o", o, o_strides, es))) return rc;
+  if ((rc = check_slice_bytes("k", k_strides, Tk, es))) return rc;
+  if ((rc = check_slice_bytes("v", v_strides, Tk, es))) return rc;
   if ((rc = check_keep(keep, keep_ld, keep_scale, Tk))) return rc;
   MTX_CHECK_ARG(lse != nullptr, "lse: null pointer");
   MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
@@ -1454,6 +1475,10 @@ int attn_bwd_impl(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
   if ((rc = check_bhtd("dq", dq, dq_strides, 4))) return rc;
   if ((rc = check_bhtd("dk", dk, dk_strides, 4))) return rc;
   if ((rc = check_bhtd("dv", dv, dv_strides, 4))) return rc;
+  if ((rc = check_slice_bytes("q", q_strides, Tq, es))) return rc;
+  if ((rc = check_slice_bytes("k", k_strides, Tk, es))) return rc;
+  if ((rc = check_slice_bytes("v", v_strides, Tk, es))) return rc;
+  if ((rc = check_slice_bytes("dout", do_strides, Tq, es))) return rc;
   MTX_CHECK_ARG(lse != nullptr, "lse: null pointer");
   if (!use_scratch) {
     MTX_CHECK_ARG(workspace != nullptr, "workspace: null pointer");

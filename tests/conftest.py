@@ -22,16 +22,29 @@ def pytest_configure(config):
 
 def _has_gpu():
     """A GPU is visible to the HIP runtime (asked through the library's own
-    mtx_device_count; False when the library is not built)."""
+    mtx_device_count).  On a machine with a GPU driver (/dev/kfd) a library
+    that does not load or a failing device query is an error, never a reason
+    to skip: the GPU tests must run there."""
+    import ctypes
+
+    from minitorch_amd import _lib
+
+    gpu_machine = os.path.exists("/dev/kfd")
     try:
-        import ctypes
-
-        from minitorch_amd import _lib
-
-        n = ctypes.c_int(0)
-        return _lib.lib().mtx_device_count(ctypes.byref(n)) == 0 and n.value > 0
+        lib = _lib.lib()
     except Exception:
+        if gpu_machine:
+            raise
         return False
+    n = ctypes.c_int(0)
+    rc = lib.mtx_device_count(ctypes.byref(n))
+    if rc != 0:
+        if gpu_machine:
+            raise RuntimeError(f"mtx_device_count failed: {lib.mtx_last_error().decode()}")
+        return False
+    if gpu_machine and n.value < 1:
+        raise RuntimeError("/dev/kfd exists but the HIP runtime sees no GPU")
+    return n.value > 0
 
 
 def pytest_collection_modifyitems(config, items):
