@@ -825,7 +825,12 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
   }
   // one query tile; P = buffer parity (for direct loads the loop below is
   // unrolled by two so that P is a compile-time constant)
-  auto step = [&](auto par, const int it) {
+  // `open`: the tile is known to be fully visible to every wave of the
+  // block (no skip, no mask), so the body has no branch around its MFMAs
+  // and the accumulators stay in place (a branch there makes the compiler
+  // copy all 64 of them per tile)
+  auto step = [&](auto par, const int it, auto open) {
+    constexpr bool OPEN = decltype(open)::value;
     const int P = int(par) % NBUF;
     const int PN = (P + 1) % NBUF;
     const int qt = qstart + it * BQ;
@@ -849,8 +854,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
     if (it + 1 < ntile) fetch(qt + BQ, PN ? Q1 : Q0, PN ? D1 : D0);
 
     // wave-level causal skip: every key of the wave is after every query of the tile
-    if (a.causal && kw0 > qt + BQ - 1 + off) return;
-    const bool need_mask = a.causal && (kw0 + NK * 16 - 1 > qt + off);
+    if (!OPEN && a.causal && kw0 > qt + BQ - 1 + off) return;
+    const bool need_mask = !OPEN && a.causal && (kw0 + NK * 16 - 1 > qt + off);
     // dropout keep bytes of this lane's keys for queries qt + 16qs + 4g + r,
     // packed one query quad per word
     uint32_t kwd[BQ / 16][NK];
@@ -943,20 +948,40 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
       }
     }
       };
+    if constexpr (OPEN) {
+      tile(std::false_type{});
+    } else {
 #if MTX_DKDV_SPLIT
-    if (need_mask) tile(std::true_type{});
-    else tile(std::false_type{});
+      if (need_mask) tile(std::true_type{});
+      else tile(std::false_type{});
 #else
-    tile(std::true_type{});
+      tile(std::true_type{});
 #endif
+    }
   };
+  // Tiles from query qfull on see every key of the block: the first tiles
+  // (at most BKV / BQ + 1 of them, rounded up to an even count for the
+  // buffer parity) take the general body, the rest the open one.
+  int itA = 0;
+  if (a.causal) {
+    const int qfull = k0 + BKV - 1 - off;
+    itA = qfull > qstart ? (qfull - qstart + BQ - 1) / BQ : 0;
+    itA = min(ntile, (itA + 1) & ~1);
+  }
   if constexpr (LY::DIRECT) {
-    for (int it = 0; it < ntile; it += 2) {
-      step(std::integral_constant<int, 0>{}, it);
-      if (it + 1 < ntile) step(std::integral_constant<int, 1>{}, it + 1);
+    for (int it = 0; it < itA; it += 2) {
+      step(std::integral_constant<int, 0>{}, it, std::false_type{});
+      if (it + 1 < itA) step(std::integral_constant<int, 1>{}, it + 1, std::false_type{});
+    }
+    for (int it = itA; it < ntile; it += 2) {
+      step(std::integral_constant<int, 0>{}, it, std::true_type{});
+      if (it + 1 < ntile) step(std::integral_constant<int, 1>{}, it + 1, std::true_type{});
     }
   } else {
-    for (int it = 0; it < ntile; ++it) step(it & 1, it);
+    for (int it = 0; it < ntile; ++it) {
+      if (it < itA) step(it & 1, it, std::false_type{});
+      else step(it & 1, it, std::true_type{});
+    }
   }
 
   float* __restrict__ dkp = a.dk + b * a.sdk.b + h * a.sdk.h;
