@@ -1113,7 +1113,11 @@ void attn_dq_kernel(const BwdArgs a) {
   }
   // one key tile; P = buffer parity (for direct loads the loop below is
   // unrolled by two so that P is a compile-time constant)
-  auto step = [&](auto par, const int it) {
+  // `open`: every key of the tile is visible to every query of the block
+  // (no skip, no mask), so the body has no branch around its MFMAs and the
+  // accumulators stay in place
+  auto step = [&](auto par, const int it, auto open) {
+    constexpr bool OPEN = decltype(open)::value;
     const int P = int(par) % NBUF;  // a constant for the unrolled (direct-load) loop
     const int PN = (P + 1) % NBUF;
     const int kb = it * BK;
@@ -1137,8 +1141,8 @@ void attn_dq_kernel(const BwdArgs a) {
       }
     }
 
-    if (a.causal && kb > qw0 + NQ * 16 - 1 + off) return;
-    const bool need_mask = (kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off);
+    if (!OPEN && a.causal && kb > qw0 + NQ * 16 - 1 + off) return;
+    const bool need_mask = !OPEN && ((kb + BK > a.Tk) || (a.causal && kb + BK - 1 > qw0 + off));
     // dropout keep bytes of this lane's query, keys kb + 16kt + 4g + 0..3
     uint32_t kwd[NQ][4];
     if constexpr (DROP) {
@@ -1208,16 +1212,32 @@ void attn_dq_kernel(const BwdArgs a) {
     }
     }
       };
-    if (need_mask) tile(std::true_type{});
-    else tile(std::false_type{});
+    if constexpr (OPEN) {
+      tile(std::false_type{});
+    } else {
+      if (need_mask) tile(std::true_type{});
+      else tile(std::false_type{});
+    }
   };
+  // Key tiles below kopen are visible to every query of the block: those
+  // (an even count, for the buffer parity) take the open body, the rest
+  // (the diagonal and the ragged end) the general one.
+  const int kopen = a.causal ? min(a.Tk, q0 + off + 1) : a.Tk;
+  const int itB = min(ntile, kopen / BK) & ~1;
   if constexpr (LY::DIRECT) {
-    for (int it = 0; it < ntile; it += 2) {
-      step(std::integral_constant<int, 0>{}, it);
-      if (it + 1 < ntile) step(std::integral_constant<int, 1>{}, it + 1);
+    for (int it = 0; it < itB; it += 2) {
+      step(std::integral_constant<int, 0>{}, it, std::true_type{});
+      step(std::integral_constant<int, 1>{}, it + 1, std::true_type{});
+    }
+    for (int it = itB; it < ntile; it += 2) {
+      step(std::integral_constant<int, 0>{}, it, std::false_type{});
+      if (it + 1 < ntile) step(std::integral_constant<int, 1>{}, it + 1, std::false_type{});
     }
   } else {
-    for (int it = 0; it < ntile; ++it) step(it & 1, it);
+    for (int it = 0; it < ntile; ++it) {
+      if (it < itB) step(it & 1, it, std::true_type{});
+      else step(it & 1, it, std::false_type{});
+    }
   }
 
   float* __restrict__ dqp = a.dq + b * a.sdq.b + h * a.sdq.h;
