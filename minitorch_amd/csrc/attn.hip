@@ -603,13 +603,16 @@ void attn_fwd_kernel(const FwdArgs a) {
           for (int r = 0; r < 4; ++r)
             if (16 * kt + r > lim) s[qs][kt][r] = -INFINITY;
       }
+      // a row's max exceeds lim iff one of its four lanes' maxima does, so
+      // the lanes' own maxima decide the (wave-uniform) branch and the
+      // cross-lane reduction runs only inside it
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[qs][kt][r]);
-      mx = max4l(mx);
       if (__builtin_amdgcn_ballot_w64(mx > lim[qs]) != 0ull) {
+        mx = max4l(mx);
         // move this lane's reference up by d (0 for lanes that keep theirs);
         // everything is updated in place
         const bool move = mx > lim[qs];
