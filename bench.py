@@ -185,9 +185,6 @@ def bench_c4(n_new=224):
     attention kernel alone at the longest step (L = 256, fp32 cache) with HIP
     events and reports its read bandwidth (K and V once)."""
     import minitorch_amd as mt
-    from minitorch_amd import device as Dv
-    from minitorch_amd import kernels as K
-    from minitorch_amd.graphs import Graph
 
     c = C2_CFG
     model = mt.GPT(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"], dropout=0.0)
@@ -203,7 +200,22 @@ def bench_c4(n_new=224):
         dt = time.perf_counter() - t0
         best = dt if best is None else min(best, dt)
     assert toks.shape == (64, 32 + n_new)
-    # decode kernel alone, L = 256
+    dk = bench_decode_kernel(c)
+    return {"tokens_per_s": round(64 * n_new / best, 1), "ms_total": round(best * 1e3, 2),
+            "ms_per_token_step": round(best * 1e3 / n_new, 4),
+            "decode_kernel": dk,
+            "config": "C2 model (6x384, 6 heads), 64 prompts x 32 ids, +224 greedy tokens, fp32, KV cache"}
+
+
+def bench_decode_kernel(c, graph=True):
+    """The decode attention kernel alone at the longest C4 step (B = 64, the
+    C2 model's heads, L = 256, fp32 cache): microseconds per launch from HIP
+    events and the read bandwidth (K and V once).  graph=False launches it 25
+    times eagerly and times nothing (a short workload for counter passes)."""
+    from minitorch_amd import device as Dv
+    from minitorch_amd import kernels as K
+    from minitorch_amd.graphs import Graph
+
     B, H, L, D = 64, c["n_head"], 256, c["n_embd"] // c["n_head"]
     g = np.random.default_rng(4)
     q = Dv.from_host(g.standard_normal((B, H, 1, D), dtype=np.float32)).t
@@ -211,27 +223,29 @@ def bench_c4(n_new=224):
     vc = Dv.from_host(g.standard_normal((B, L, H * D), dtype=np.float32)).t
     heads = lambda t: t.view(B, L, H, D).transpose(1, 2)
     out = Dv.empty_buf(q.shape)
-    # 20 launches recorded in a HIP graph and replayed: launched one by one
-    # from Python the loop is bound by the host's per-call path (~17 us),
-    # not by the kernel
     launch = lambda: K.attn_decode(q, heads(kc), heads(vc), D ** -0.5, out=out)
+    if not graph:
+        for _ in range(25):
+            launch()
+        _sync()
+        return None
     launch()
     launch()
     _sync()
+    # 20 launches recorded in a HIP graph and replayed: launched one by one
+    # from Python the loop is bound by the host's per-call path (~17 us),
+    # not by the kernel
     graph = Graph()
     with graph.capture():
         for _ in range(20):
             launch()
     ms = time_loop(graph.replay, 20, 3) / 20
     nbytes = 2 * B * H * L * D * 4
-    return {"tokens_per_s": round(64 * n_new / best, 1), "ms_total": round(best * 1e3, 2),
-            "ms_per_token_step": round(best * 1e3 / n_new, 4),
-            "decode_kernel": {"L": L, "us_per_launch": round(ms * 1e3, 3),
-                              "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                              "frac_of_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4),
-                              "bytes_per_launch": nbytes,
-                              "note": "K+V (50 MB) fit the 256 MB MALL, so repeated launches read it from there"},
-            "config": "C2 model (6x384, 6 heads), 64 prompts x 32 ids, +224 greedy tokens, fp32, KV cache"}
+    return {"L": L, "us_per_launch": round(ms * 1e3, 3),
+            "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4),
+            "bytes_per_launch": nbytes,
+            "note": "K+V (50 MB) fit the 256 MB MALL, so repeated launches read it from there"}
 
 
 def bench_gpt(c, seed, steps, warmup, graph=False):
@@ -388,7 +402,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=("all", "c3", "c1", "c4", "gpt2", "gpt0"), default="all",
+    ap.add_argument("--only", choices=("all", "c3", "c1", "c4", "c4kernel", "gpt2", "gpt0"), default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run 5 device copies of MIB MiB (a kernel of known HBM "
@@ -425,6 +439,10 @@ def main():
             ms, losses = bench_gpt(c, 2, args.steps, args.warmup, graph=graph)
             print(f"[bench] {args.only} ({'graph' if graph else 'eager'}): {ms:.3f} ms/step, "
                   f"{c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, losses {losses}", file=sys.stderr)
+        return
+    if args.only == "c4kernel":
+        bench_decode_kernel(C2_CFG, graph=False)
+        print("[bench] decode kernel x25 (B=64, H=6, L=256, D=64, fp32)", file=sys.stderr)
         return
     if args.only == "c4":
         print(f"[bench] C4 {bench_c4()}", file=sys.stderr)

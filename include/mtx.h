@@ -495,10 +495,11 @@ int mtx_onehot_f32(const int64_t* idx, int64_t n, int64_t V, float* out, void* s
 /*
  * Adam over many tensors in one launch (optim.py:37-59).  `table` is a device
  * array of ntensors entries {float* p; const float* g; float* m; float* v;
- * int64_t n; int64_t block0}, block0 from mtx_adam_blocks (host helper);
- * total_blocks = last block0 + ceil(last n / 256).
+ * int64_t n; int64_t block0}, block0 and total_blocks from mtx_adam_blocks
+ * (host helper: each launch block covers 2048 elements of one tensor).
+ * Tensors whose four pointers are 16-byte aligned are accessed as float4.
  */
-int mtx_adam_blocks(const int64_t* sizes, int ntensors, int64_t* block0_out);
+int mtx_adam_blocks(const int64_t* sizes, int ntensors, int64_t* block0_out, int64_t* total_blocks);
 int mtx_adam_f32(const void* table, int ntensors, int64_t total_blocks, double lr, double beta1,
                  double beta2, double eps, double weight_decay, int step, void* stream);
 
@@ -516,6 +517,15 @@ int mtx_adam_bias_table(double beta1, double beta2, int first_step, int len, flo
 int mtx_adam_dev_f32(const void* table, int ntensors, int64_t total_blocks, double lr, double beta1,
                      double beta2, double eps, double weight_decay, int* step, const float* bias_table,
                      int table_len, void* stream);
+
+/*
+ * Zero the gradient of every tensor in an Adam table (the g field of each
+ * entry, n floats) in one launch.  Replaces Optimizer.zero_grad
+ * (optim.py:11-13) for callers that keep persistent gradient buffers so a
+ * recorded step replays unchanged: the reference drops the gradients (sets
+ * them to None); accumulating into zeros gives the same values.
+ */
+int mtx_zero_grads_f32(const void* table, int ntensors, int64_t total_blocks, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Runtime: devices, memory, copies, streams, events, graphs                 */

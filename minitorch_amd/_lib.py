@@ -108,11 +108,12 @@ SIGNATURES = {
     "mtx_xent_bwd_f32": (_I, [_P, _I64, _P, _P, _P, _F, _P, _I64, _I64, _I, _I, _P]),
     "mtx_embedding_fwd_f32": (_I, [_P, _I64, _I64, _P, _I64, _P, _I64, _I, _P]),
     "mtx_embedding_bwd_f32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I, _I, _P]),
-    "mtx_adam_blocks": (_I, [_I64P, _I, _I64P]),
+    "mtx_adam_blocks": (_I, [_I64P, _I, _I64P, _I64P]),
     "mtx_onehot_f32": (_I, [_P, _I64, _I64, _P, _P]),
     "mtx_adam_f32": (_I, [_P, _I, _I64, _D, _D, _D, _D, _D, _I, _P]),
     "mtx_adam_bias_table": (_I, [_D, _D, _I, _I, _P]),
     "mtx_adam_dev_f32": (_I, [_P, _I, _I64, _D, _D, _D, _D, _D, _P, _P, _I, _P]),
+    "mtx_zero_grads_f32": (_I, [_P, _I, _I64, _P]),
     # runtime
     "mtx_device_count": (_I, [_IP]),
     "mtx_device_init": (_I, [_I]),

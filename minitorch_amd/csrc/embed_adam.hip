@@ -79,30 +79,76 @@ struct AdamEntry {
   int64_t block0;  // first block of this tensor
 };
 
-// one element's update; bc1, bc2 = the step's bias corrections 1 - b^t
-__device__ __forceinline__ void adam_update(const AdamEntry* __restrict__ tab, int ntab, float lr, float b1, float b2,
-                                            float c1, float c2, float bc1, float bc2, float eps, float wd) {
-  // locate this block's tensor (tables are short: linear scan)
-  int t = 0;
-  while (t + 1 < ntab && tab[t + 1].block0 <= (int64_t)blockIdx.x) ++t;
-  const AdamEntry e = tab[t];
-  const int64_t i = ((int64_t)blockIdx.x - e.block0) * 256 + threadIdx.x;
-  if (i >= e.n) return;
-  float g = e.g[i];
-  if (wd != 0.f) g = g + wd * e.p[i];
-  const float m = b1 * e.m[i] + c1 * g;
-  const float v = b2 * e.v[i] + c2 * (g * g);
-  e.m[i] = m;
-  e.v[i] = v;
-  const float mh = m / bc1;
-  const float vh = v / bc2;
-  e.p[i] = e.p[i] - (lr * mh) / (sqrtf(vh) + eps);
+// Elements one 256-thread block of the multi-tensor kernels covers: 8 per
+// thread, as two float4 accesses per array (the launch count of blocks stays
+// in the thousands for a GPT's ~10M parameters, and each block locates its
+// tensor once).
+constexpr int kAdamChunk = 2048;
+
+// The table entry whose blocks include this one: the last entry with
+// block0 <= blockIdx.x (binary search; block0 ascends with the entry).
+__device__ __forceinline__ const AdamEntry& adam_owner(const AdamEntry* __restrict__ tab, int ntab) {
+  const int64_t bx = blockIdx.x;
+  int lo = 0, hi = ntab - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].block0 <= bx) lo = mid; else hi = mid - 1;
+  }
+  return tab[lo];
 }
 
-__global__ __launch_bounds__(256) void adam_kernel(const AdamEntry* __restrict__ tab, int ntab, float lr, float b1,
-                                                   float b2, float c1, float c2, float bc1, float bc2, float eps,
-                                                   float wd) {
-  adam_update(tab, ntab, lr, b1, b2, c1, c2, bc1, bc2, eps, wd);
+struct AdamCoef {
+  float lr, b1, b2, c1, c2, bc1, bc2, eps, wd;
+};
+
+// one element's update; bc1, bc2 = the step's bias corrections 1 - b^t.
+// Every product and sum is rounded on its own (no fused multiply-add), as
+// NumPy evaluates the reference's float32 expressions, so the update is
+// bit-identical to it for the same gradient.
+__device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v, const AdamCoef& k) {
+#pragma clang fp contract(off)
+  if (k.wd != 0.f) g = g + k.wd * p;
+  m = k.b1 * m + k.c1 * g;
+  v = k.b2 * v + k.c2 * (g * g);
+  const float mh = m / k.bc1;
+  const float vh = v / k.bc2;
+  p = p - (k.lr * mh) / (sqrtf(vh) + k.eps);
+}
+
+__device__ __forceinline__ void adam_update(const AdamEntry* __restrict__ tab, int ntab, const AdamCoef& k) {
+  const AdamEntry e = adam_owner(tab, ntab);
+  const int64_t base = ((int64_t)blockIdx.x - e.block0) * kAdamChunk;
+  const bool vec = ((reinterpret_cast<uintptr_t>(e.p) | reinterpret_cast<uintptr_t>(e.g) |
+                     reinterpret_cast<uintptr_t>(e.m) | reinterpret_cast<uintptr_t>(e.v)) & 15) == 0;
+#pragma unroll
+  for (int j = 0; j < kAdamChunk / 1024; ++j) {
+    const int64_t i = base + j * 1024 + threadIdx.x * 4;
+    if (vec && i + 4 <= e.n) {
+      float4 p = *reinterpret_cast<const float4*>(e.p + i);
+      const float4 g = *reinterpret_cast<const float4*>(e.g + i);
+      float4 m = *reinterpret_cast<const float4*>(e.m + i);
+      float4 v = *reinterpret_cast<const float4*>(e.v + i);
+      adam_elem(p.x, g.x, m.x, v.x, k);
+      adam_elem(p.y, g.y, m.y, v.y, k);
+      adam_elem(p.z, g.z, m.z, v.z, k);
+      adam_elem(p.w, g.w, m.w, v.w, k);
+      *reinterpret_cast<float4*>(e.m + i) = m;
+      *reinterpret_cast<float4*>(e.v + i) = v;
+      *reinterpret_cast<float4*>(e.p + i) = p;
+    } else {
+      for (int64_t q = i; q < i + 4 && q < e.n; ++q) {
+        float p = e.p[q], m = e.m[q], v = e.v[q];
+        adam_elem(p, e.g[q], m, v, k);
+        e.m[q] = m;
+        e.v[q] = v;
+        e.p[q] = p;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void adam_kernel(const AdamEntry* __restrict__ tab, int ntab, AdamCoef k) {
+  adam_update(tab, ntab, k);
 }
 
 // Graph-replayable Adam: the step count lives in device memory (incremented
@@ -111,18 +157,47 @@ __global__ __launch_bounds__(256) void adam_kernel(const AdamEntry* __restrict__
 // values mtx_adam_f32 computes, entry (t - 1) % len for step t.
 __global__ void adam_count_kernel(int* __restrict__ step) { step[0] += 1; }
 
-__global__ __launch_bounds__(256) void adam_dev_kernel(const AdamEntry* __restrict__ tab, int ntab, float lr, float b1,
-                                                       float b2, float c1, float c2, const int* __restrict__ step,
-                                                       const float* __restrict__ bc, int bc_len, float eps,
-                                                       float wd) {
+__global__ __launch_bounds__(256) void adam_dev_kernel(const AdamEntry* __restrict__ tab, int ntab, AdamCoef k,
+                                                       const int* __restrict__ step, const float* __restrict__ bc,
+                                                       int bc_len) {
   const int j = (step[0] - 1) % bc_len;
-  adam_update(tab, ntab, lr, b1, b2, c1, c2, bc[2 * j], bc[2 * j + 1], eps, wd);
+  k.bc1 = bc[2 * j];
+  k.bc2 = bc[2 * j + 1];
+  adam_update(tab, ntab, k);
+}
+
+// Zero every tensor's gradient in one launch (the capturable optimizer's
+// zero_grad): same table and block layout as the update.
+__global__ __launch_bounds__(256) void zero_grads_kernel(const AdamEntry* __restrict__ tab, int ntab) {
+  const AdamEntry e = adam_owner(tab, ntab);
+  float* g = const_cast<float*>(e.g);
+  const int64_t base = ((int64_t)blockIdx.x - e.block0) * kAdamChunk;
+  const bool vec = (reinterpret_cast<uintptr_t>(g) & 15) == 0;
+#pragma unroll
+  for (int j = 0; j < kAdamChunk / 1024; ++j) {
+    const int64_t i = base + j * 1024 + threadIdx.x * 4;
+    if (vec && i + 4 <= e.n) {
+      *reinterpret_cast<float4*>(g + i) = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      for (int64_t q = i; q < i + 4 && q < e.n; ++q) g[q] = 0.f;
+    }
+  }
 }
 
 }  // namespace
 }  // namespace mtx
 
 using namespace mtx;
+
+extern "C" int mtx_zero_grads_f32(const void* table, int ntensors, int64_t total_blocks, void* stream) {
+  MTX_CHECK_ARG(table && ntensors >= 1, "zero_grads: empty table");
+  MTX_CHECK_SHAPE(total_blocks >= 0 && total_blocks < (1LL << 31), "zero_grads: bad block count");
+  if (total_blocks == 0) return MTX_OK;
+  hipLaunchKernelGGL(zero_grads_kernel, dim3((unsigned)total_blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const AdamEntry*>(table), ntensors);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
 
 extern "C" int mtx_adam_bias_table(double beta1, double beta2, int first_step, int len, float* out) {
   MTX_CHECK_ARG(out != nullptr && len >= 1 && first_step >= 1, "adam_bias_table: bad argument");
@@ -143,10 +218,10 @@ extern "C" int mtx_adam_dev_f32(const void* table, int ntensors, int64_t total_b
   hipLaunchKernelGGL(adam_count_kernel, dim3(1), dim3(1), 0, st, step);
   MTX_LAUNCHED();
   if (total_blocks == 0) return MTX_OK;
-  const float c1 = (float)(1.0 - beta1), c2 = (float)(1.0 - beta2);
+  const AdamCoef k{(float)lr, (float)beta1, (float)beta2, (float)(1.0 - beta1), (float)(1.0 - beta2), 1.f, 1.f,
+                   (float)eps, (float)weight_decay};
   hipLaunchKernelGGL(adam_dev_kernel, dim3((unsigned)total_blocks), dim3(256), 0, st,
-                     static_cast<const AdamEntry*>(table), ntensors, (float)lr, (float)beta1, (float)beta2, c1, c2,
-                     step, bias_table, table_len, (float)eps, (float)weight_decay);
+                     static_cast<const AdamEntry*>(table), ntensors, k, step, bias_table, table_len);
   MTX_LAUNCHED();
   return MTX_OK;
 }
@@ -183,13 +258,15 @@ extern "C" int mtx_onehot_f32(const int64_t* idx, int64_t n, int64_t V, float* o
   return MTX_OK;
 }
 
-extern "C" int mtx_adam_blocks(const int64_t* sizes, int ntensors, int64_t* block0_out) {
-  MTX_CHECK_ARG(sizes && block0_out && ntensors >= 0, "adam_blocks: bad argument");
+extern "C" int mtx_adam_blocks(const int64_t* sizes, int ntensors, int64_t* block0_out, int64_t* total_blocks) {
+  MTX_CHECK_ARG(sizes && block0_out && total_blocks && ntensors >= 0, "adam_blocks: bad argument");
   int64_t b = 0;
   for (int i = 0; i < ntensors; ++i) {
+    MTX_CHECK_SHAPE(sizes[i] >= 0, "adam_blocks: negative size");
     block0_out[i] = b;
-    b += (sizes[i] + 255) / 256;
+    b += (sizes[i] + kAdamChunk - 1) / kAdamChunk;
   }
+  *total_blocks = b;
   return MTX_OK;
 }
 
@@ -200,12 +277,11 @@ extern "C" int mtx_adam_f32(const void* table, int ntensors, int64_t total_block
   MTX_CHECK_SHAPE(total_blocks >= 0 && total_blocks < (1LL << 31), "adam: bad block count");
   if (total_blocks == 0) return MTX_OK;
   // scalars rounded to float32 exactly as NumPy does for python-float * float32 array
-  const float c1 = (float)(1.0 - beta1), c2 = (float)(1.0 - beta2);
-  const float bc1 = (float)(1.0 - std::pow(beta1, (double)step));
-  const float bc2 = (float)(1.0 - std::pow(beta2, (double)step));
+  const AdamCoef k{(float)lr, (float)beta1, (float)beta2, (float)(1.0 - beta1), (float)(1.0 - beta2),
+                   (float)(1.0 - std::pow(beta1, (double)step)), (float)(1.0 - std::pow(beta2, (double)step)),
+                   (float)eps, (float)weight_decay};
   hipLaunchKernelGGL(adam_kernel, dim3((unsigned)total_blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const AdamEntry*>(table), ntensors, (float)lr, (float)beta1, (float)beta2, c1, c2,
-                     bc1, bc2, (float)eps, (float)weight_decay);
+                     static_cast<const AdamEntry*>(table), ntensors, k);
   MTX_LAUNCHED();
   return MTX_OK;
 }

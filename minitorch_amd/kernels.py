@@ -627,7 +627,8 @@ class AdamTable:
         n = len(params)
         sizes = (L.C.c_int64 * n)(*[p.numel() for p in params])
         b0 = (L.C.c_int64 * n)()
-        L.call("mtx_adam_blocks", sizes, n, b0)
+        total = L.C.c_int64()
+        L.call("mtx_adam_blocks", sizes, n, b0, L.C.byref(total))
         rows = []
         for i in range(n):
             rows.append([params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(),
@@ -635,7 +636,7 @@ class AdamTable:
         host = np.array(rows, dtype=np.int64).reshape(n, 6)
         self.table = dev.from_host(host, np.int64).t
         self.n = n
-        self.total_blocks = int(b0[n - 1] + (params[n - 1].numel() + 255) // 256) if n else 0
+        self.total_blocks = int(total.value)
 
 
 def adam_bias_table(beta1, beta2, first_step, length):
@@ -654,6 +655,11 @@ def adam_step_dev(table: AdamTable, lr, beta1, beta2, eps, weight_decay, step_de
     L.call("mtx_adam_dev_f32", L.ptr(table.table), table.n, table.total_blocks, float(lr), float(beta1),
            float(beta2), float(eps), float(weight_decay), L.ptr(step_dev), L.ptr(bias_dev),
            bias_dev.numel() // 2, L.stream_handle())
+
+
+def zero_grads(table: AdamTable):
+    """Zero every gradient the table points at, in one launch."""
+    L.call("mtx_zero_grads_f32", L.ptr(table.table), table.n, table.total_blocks, L.stream_handle())
 
 
 def adam_step(table: AdamTable, lr, beta1, beta2, eps, weight_decay, step):

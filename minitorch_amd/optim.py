@@ -17,16 +17,28 @@ class Optimizer:
         self.lr = lr
         self.weight_decay = weight_decay
         self._capturable = False
+        self._table = None
+        self._key = None
 
     def zero_grad(self):
         """Drop the gradients (optim.py:11-13); in capturable mode the
         persistent buffers are refilled with zeros instead, so their addresses
         stay the ones a recorded step uses."""
+        if self._capturable and self._table is not None and self._table_current():
+            # the persistent buffers are the ones the pointer table lists:
+            # one launch zeroes them all
+            K.zero_grads(self._table)
+            return
         for p in self.params:
             if self._capturable and p.grad is not None:
                 K.fill(p.grad.t, 0.0)
             else:
                 p.grad = None
+
+    def _table_current(self):
+        live = [i for i, p in enumerate(self.params) if p.requires_grad and p.grad is not None]
+        key = tuple((self.params[i].data.t.data_ptr(), self.params[i].grad.t.data_ptr()) for i in live)
+        return key == self._key and all(self.params[i].grad.t.is_contiguous() for i in live)
 
     def step(self):
         raise NotImplementedError

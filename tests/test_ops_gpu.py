@@ -263,6 +263,7 @@ def test_cross_entropy_and_embedding(dev):
 
 def test_adam_matches_oracle(dev):
     import minitorch_amd as mt
+    from minitorch_amd.device import DeviceArray
     from oracle.gpt import Adam as OAdam
 
     _say("[adam]")
@@ -277,10 +278,48 @@ def test_adam_matches_oracle(dev):
         gs = [rng.standard_normal(s).astype(np.float32) for s in shapes]
         for t, g in zip(tp, gs):
             t.grad = mt.Tensor(g).data
+        # one gradient a view at a 4-byte offset: that tensor takes the
+        # kernel's scalar (unaligned) path
+        wide = mt.Tensor(np.concatenate([[0.0], gs[2]]).astype(np.float32)).data
+        tp[2].grad = DeviceArray(wide.t[1:])
         opt.step()
         oopt.step(op, {str(i): g for i, g in enumerate(gs)})
+    # every operation is a separately rounded float32 one, as in NumPy
     for i, t in enumerate(tp):
-        close(t.numpy(), op[str(i)], rtol=1e-6, atol=1e-7, name=f"adam p{i}")
+        assert np.array_equal(t.numpy(), op[str(i)]), f"adam p{i} differs from the float32 oracle"
+
+
+def test_adam_capturable_zero_grad_and_step(dev):
+    """Capturable Adam: zero_grad zeroes every persistent gradient buffer in
+    one launch (the pointer table's g fields; sizes straddle the 256-element
+    blocks), the buffers keep their addresses, and steps with the device step
+    count match the oracle's Adam."""
+    import minitorch_amd as mt
+    from minitorch_amd import device as mdev
+    from oracle.gpt import Adam as OAdam
+
+    _say("[adam capturable zero_grad]")
+    rng = np.random.default_rng(17)
+    shapes = [(5,), (33, 8), (256,), (257,), (2, 3, 4)]
+    ps = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+    tp = [mt.Tensor(p.copy(), requires_grad=True) for p in ps]
+    opt = mt.Adam(tp, lr=3e-4).capturable(window=2)
+    addrs = [t.grad.t.data_ptr() for t in tp]
+    op = {str(i): p.copy() for i, p in enumerate(ps)}
+    oopt = OAdam(op, lr=3e-4)
+    for step in range(3):
+        gs = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+        for t, g in zip(tp, gs):
+            t.grad.t.copy_(mdev.from_host(g).t)
+        opt.step()
+        oopt.step(op, {str(i): g for i, g in enumerate(gs)})
+        opt.zero_grad()
+        mdev.synchronize()
+        for i, t in enumerate(tp):
+            assert t.grad.t.data_ptr() == addrs[i]
+            assert not np.any(t.grad.numpy()), f"grad {i} not zeroed after step {step}"
+    for i, t in enumerate(tp):
+        assert np.array_equal(t.numpy(), op[str(i)]), f"adam p{i} differs from the float32 oracle"
 
 
 def test_tensor_autograd_like_reference_checks(dev):
