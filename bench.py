@@ -207,11 +207,15 @@ def bench_c4(n_new=224):
             "config": "C2 model (6x384, 6 heads), 64 prompts x 32 ids, +224 greedy tokens, fp32, KV cache"}
 
 
-def bench_decode_kernel(c, graph=True):
+def bench_decode_kernel(c, graph=True, sets=8):
     """The decode attention kernel alone at the longest C4 step (B = 64, the
     C2 model's heads, L = 256, fp32 cache): microseconds per launch from HIP
-    events and the read bandwidth (K and V once).  graph=False launches it 25
-    times eagerly and times nothing (a short workload for counter passes)."""
+    events and the read bandwidth (K and V once), twice: on one cache (its
+    50 MB stay in the 256 MB MALL between launches) and cycling over `sets`
+    caches (8 x 50 MB: each launch reads a cache the previous 7 launches have
+    pushed out, i.e. from HBM -- the situation of the decode step, whose 6
+    layers hold 6 such caches).  graph=False launches it 25 times eagerly on
+    one cache and times nothing (a short workload for counter passes)."""
     from minitorch_amd import device as Dv
     from minitorch_amd import kernels as K
     from minitorch_amd.graphs import Graph
@@ -219,33 +223,41 @@ def bench_decode_kernel(c, graph=True):
     B, H, L, D = 64, c["n_head"], 256, c["n_embd"] // c["n_head"]
     g = np.random.default_rng(4)
     q = Dv.from_host(g.standard_normal((B, H, 1, D), dtype=np.float32)).t
-    kc = Dv.from_host(g.standard_normal((B, L, H * D), dtype=np.float32)).t
-    vc = Dv.from_host(g.standard_normal((B, L, H * D), dtype=np.float32)).t
+    caches = []
+    for _ in range(sets if graph else 1):
+        caches.append((Dv.from_host(g.standard_normal((B, L, H * D), dtype=np.float32)).t,
+                       Dv.from_host(g.standard_normal((B, L, H * D), dtype=np.float32)).t))
     heads = lambda t: t.view(B, L, H, D).transpose(1, 2)
     out = Dv.empty_buf(q.shape)
-    launch = lambda: K.attn_decode(q, heads(kc), heads(vc), D ** -0.5, out=out)
+
+    def launch(i=0):
+        kc, vc = caches[i]
+        K.attn_decode(q, heads(kc), heads(vc), D ** -0.5, out=out)
+
     if not graph:
         for _ in range(25):
             launch()
         _sync()
         return None
-    launch()
-    launch()
+    for i in range(sets):
+        launch(i)
     _sync()
-    # 20 launches recorded in a HIP graph and replayed: launched one by one
-    # from Python the loop is bound by the host's per-call path (~17 us),
-    # not by the kernel
-    graph = Graph()
-    with graph.capture():
-        for _ in range(20):
-            launch()
-    ms = time_loop(graph.replay, 20, 3) / 20
     nbytes = 2 * B * H * L * D * 4
-    return {"L": L, "us_per_launch": round(ms * 1e3, 3),
-            "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "frac_of_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4),
-            "bytes_per_launch": nbytes,
-            "note": "K+V (50 MB) fit the 256 MB MALL, so repeated launches read it from there"}
+    res = {"L": L, "bytes_per_launch": nbytes}
+    # launches recorded in a HIP graph and replayed: launched one by one from
+    # Python the loop is bound by the host's per-call path (~17 us), not by
+    # the kernel
+    for name, order in (("one_cache", [0] * 24), ("rotating", [i % sets for i in range(3 * sets)])):
+        graph = Graph()
+        with graph.capture():
+            for i in order:
+                launch(i)
+        ms = time_loop(graph.replay, 20, 3) / len(order)
+        res[name] = {"us_per_launch": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_of_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4)}
+    res["note"] = (f"one_cache: the same 50 MB K+V every launch (MALL-resident); rotating: {sets} caches "
+                   f"({sets * nbytes / 1e6:.0f} MB) in turn, each read after the other {sets - 1} evicted it")
+    return res
 
 
 def bench_gpt(c, seed, steps, warmup, graph=False):
