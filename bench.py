@@ -140,6 +140,29 @@ def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup):
     return dict(ms_step=ms_step, ms_fwd=ms_fwd, **{f"ms_{k}": v for k, v in ph.items()}), arrs
 
 
+def attn_bytes(B, H, T, D, esize):
+    """Algorithmic HBM bytes (read, write) per launch of each attention pass:
+    every input read once, every output written once.  q/k/v/o/dO have
+    `esize`-byte elements, lse/delta and the gradients are fp32."""
+    t, r = B * H * T * D * esize, B * H * T * 4
+    g = B * H * T * D * 4
+    return {"fwd": (3 * t, t + r),                      # q, k, v -> o, lse
+            "dq": (5 * t + r, g + r),                   # q, k, v, o, dO, lse -> dQ, delta
+            "dkdv": (4 * t + 2 * r, 2 * g)}             # q, k, v, dO, lse, delta -> dK, dV
+
+
+def short_t_report(name, B, H, T, D, r):
+    """Per-pass time and algorithmic HBM rate of a short-T attention config."""
+    out = {}
+    for ph, (rd, wr) in attn_bytes(B, H, T, D, 4).items():
+        ms = r[f"ms_{ph}"]
+        out[ph] = {"us": round(ms * 1e3, 2), "bytes": rd + wr,
+                   "GBps": round((rd + wr) / (ms * 1e-3) / 1e9, 1),
+                   "frac_of_hbm": round((rd + wr) / (ms * 1e-3) / 1e9 / PEAK_HBM, 4)}
+    print(f"[bench] {name} B={B} H={H} T={T} D={D} fp32: step {r['ms_step'] * 1e3:.2f} us; {out}",
+          file=sys.stderr)
+
+
 def cpu_baseline_attention(arrs, T, D, budget_s=15.0):
     """Time the NumPy restatement of the reference sub-graph (fwd + autograd
     bwd, transformer.py:36-44 with its float64 promotion) over successive
@@ -414,7 +437,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=("all", "c3", "c1", "c4", "c4kernel", "gpt2", "gpt0"), default="all",
+    ap.add_argument("--only", choices=("all", "c3", "c1", "c0attn", "c4", "c4kernel", "gpt2", "gpt0"),
+                    default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run 5 device copies of MIB MiB (a kernel of known HBM "
@@ -462,6 +486,12 @@ def main():
     if args.only == "c1":
         r1, _ = bench_attention(32, 8, 256, 64, "float32", 1, 1.0, args.steps, args.warmup)
         print(f"[bench] C1 {r1}", file=sys.stderr)
+        short_t_report("C1", 32, 8, 256, 64, r1)
+        return
+    if args.only == "c0attn":
+        # the attention of the C0 model (4 heads of 16, T = 32, batch 16)
+        r0, _ = bench_attention(16, 4, 32, 16, "float32", 1, 1.0, args.steps, args.warmup)
+        short_t_report("C0 attention", 16, 4, 32, 16, r0)
         return
 
     # ---- C3: headline ----
