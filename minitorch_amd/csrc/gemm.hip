@@ -135,20 +135,28 @@ __device__ __forceinline__ void load_a(const GemmArgs& g, const float* __restric
   }
 }
 
+// LDS tiles are k-major, [BK][BM] (A) and [BK][BN] (B), unpadded; within row
+// k the 16-float column blocks are XOR-permuted by tswz(k).  A wave's
+// fragment read takes 16 consecutive columns from each of 4 consecutive
+// rows, and the transposing scalar stores write 16 columns x 4 rows 4 apart:
+// with the permutation both touch 64 distinct banks (a padded row of BM + 4
+// floats gave the reads 4-way conflicts).  Needs BM, BN >= 64.
+__device__ __forceinline__ int tswz(int k) { return ((k + (k >> 2)) & 3) << 4; }
+
 template <int BM, bool AK>
 __device__ __forceinline__ void store_a(float* __restrict__ As, const f32x4 (&r)[BM * BK / 4 / kGT], int tid) {
   constexpr int NV = BM * BK / 4 / kGT;
-  constexpr int LD = BM + 4;
+  static_assert(BM >= 64, "the LDS permutation spans 64 columns");
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = tid + i * kGT;
     if constexpr (AK) {
       const int m = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) As[(k + j) * LD + m] = r[i][j];
+      for (int j = 0; j < 4; ++j) As[(k + j) * BM + (m ^ tswz(k + j))] = r[i][j];
     } else {
       const int k = idx / (BM / 4), m = (idx % (BM / 4)) * 4;
-      *reinterpret_cast<f32x4*>(As + k * LD + m) = r[i];
+      *reinterpret_cast<f32x4*>(As + k * BM + (m ^ tswz(k))) = r[i];
     }
   }
 }
@@ -194,17 +202,17 @@ __device__ __forceinline__ void load_b(const GemmArgs& g, const float* __restric
 template <int BN, bool BN1>
 __device__ __forceinline__ void store_b(float* __restrict__ Bs, const f32x4 (&r)[BN * BK / 4 / kGT], int tid) {
   constexpr int NV = BN * BK / 4 / kGT;
-  constexpr int LD = BN + 4;
+  static_assert(BN >= 64, "the LDS permutation spans 64 columns");
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = tid + i * kGT;
     if constexpr (BN1) {
       const int k = idx / (BN / 4), n = (idx % (BN / 4)) * 4;
-      *reinterpret_cast<f32x4*>(Bs + k * LD + n) = r[i];
+      *reinterpret_cast<f32x4*>(Bs + k * BN + (n ^ tswz(k))) = r[i];
     } else {
       const int n = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) Bs[(k + j) * LD + n] = r[i][j];
+      for (int j = 0; j < 4; ++j) Bs[(k + j) * BN + (n ^ tswz(k + j))] = r[i][j];
     }
   }
 }
@@ -213,9 +221,8 @@ template <int BM, int BN, bool AK, bool BN1, int ACT>
 __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
   constexpr int WM = BM / 2, WN = BN / 2;  // wave tile
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int LDA = BM + 4, LDB = BN + 4;
-  __shared__ __attribute__((aligned(16))) float As[BK * LDA];
-  __shared__ __attribute__((aligned(16))) float Bs[BK * LDB];
+  __shared__ __attribute__((aligned(16))) float As[BK * BM];
+  __shared__ __attribute__((aligned(16))) float Bs[BK * BN];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
@@ -286,9 +293,9 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
     for (int kk = 0; kk < BK; kk += 4) {
       float af[TM], bf[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = As[(kk + grp) * LDA + wm + 16 * i + n16];
+      for (int i = 0; i < TM; ++i) af[i] = As[(kk + grp) * BM + ((wm + 16 * i + n16) ^ tswz(kk + grp))];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = Bs[(kk + grp) * LDB + wn + 16 * j + n16];
+      for (int j = 0; j < TN; ++j) bf[j] = Bs[(kk + grp) * BN + ((wn + 16 * j + n16) ^ tswz(kk + grp))];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
