@@ -428,12 +428,22 @@ __device__ __forceinline__ void store4(T* __restrict__ p, f32x4 v) {
   }
 }
 
+#ifndef MTX_GRAD_NT
+#define MTX_GRAD_NT 1
+#endif
+// Gradients are written once and not read again by the attention passes:
+// non-temporal stores, so they do not displace the q/k/v/o/dO tiles the
+// other passes re-read from the caches
 __device__ __forceinline__ void store_grad4(float* __restrict__ p, f32x4 v, bool acc) {
   if (acc) {
     const f32x4 old = *reinterpret_cast<const f32x4*>(p);
     v += old;
   }
+#if MTX_GRAD_NT
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+#else
   *reinterpret_cast<f32x4*>(p) = v;
+#endif
 }
 
 
