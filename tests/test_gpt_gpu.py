@@ -66,16 +66,22 @@ def test_mha_module_matches_reference(dev):
             assert np.all(np.abs(got - ref) <= tol), (name, part, np.abs(got - ref).max())
 
 
-def test_c0_step0_matches_reference(dev):
+@pytest.mark.parametrize("cfg_name,fixture", [("C0", "c0_train.npz"), ("C2", "c2_train.npz")])
+def test_step0_matches_reference(dev, cfg_name, fixture):
+    """Step 0 of the training loop at C0 and C2 against the reference's own
+    values (tests/golden/make_golden.py): the logits of batch row 0, the
+    loss, every parameter gradient's L2 norm, and each gradient's entries
+    (all of the small ones, 64 sampled entries of each large one)."""
     import minitorch_amd as mt
-    from oracle.gpt import C0, draw_batch, init_params
+    from oracle import gpt as G
 
-    _say("[gpt] C0 step 0 vs reference golden")
-    g = load("c0_train.npz")
+    cfg = getattr(G, cfg_name)
+    _say(f"[gpt] {cfg_name} step 0 vs reference golden")
+    g = load(fixture)
     rng = np.random.default_rng(int(g["seed"]))
-    P = init_params(C0, rng)
-    model = gpu_gpt(C0, P)
-    x, y = draw_batch(rng, C0.vocab, int(g["B"]), C0.block)
+    P = G.init_params(cfg, rng)
+    model = gpu_gpt(cfg, P)
+    x, y = G.draw_batch(rng, cfg.vocab, int(g["B"]), cfg.block)
     logits = model(x)
     B, Tt, V = logits.shape
     loss = mt.cross_entropy_loss(logits.reshape(B * Tt, V), mt.Tensor(y.reshape(-1)))
@@ -98,6 +104,12 @@ def test_c0_step0_matches_reference(dev):
             ix = g[f"gidx.{n}"]
             ref = g[f"gval.{n}"]
             gr = gr[tuple(ix.T)]
+        if ref_norm <= 1e-8:
+            # zero in exact arithmetic (the key bias: softmax ignores a
+            # constant added to a row's scores); both sides hold rounding
+            # noise, bounded far below the real gradients (~1e-3 .. 1e-1)
+            assert np.max(np.abs(gr)) <= 1e-6, (n, np.max(np.abs(gr)))
+            continue
         scale = max(np.abs(ref).max(), 1e-8)
         assert np.max(np.abs(gr - ref)) <= 1e-3 * scale + 1e-9, (n, np.max(np.abs(gr - ref)), scale)
 
@@ -141,9 +153,11 @@ def test_c2_loss_curve_matches_reference(dev):
 
     g = load("c2_train.npz")
     n = int(g["steps"])
+    # the configuration's contract: the curve is compared over 20 steps
+    assert n == 20 and len(g["losses"]) == 20, f"the fixture holds {n} steps, not 20"
     _say(f"[gpt] C2 {n}-step loss curve vs reference golden")
     losses = _train_gpu(C2, int(g["seed"]), int(g["B"]), n)
-    ref = g["losses"][:n]
+    ref = g["losses"]
     rel = np.abs(losses - ref) / ref
     _say(f"  max relative loss difference {rel.max():.2e}")
     assert np.all(rel <= 1e-4), rel
