@@ -6,8 +6,8 @@
  * function interface; every entry point below replaces a NumPy-level operation
  * on the causal-attention hot path.  Each declaration cites the reference code
  * it stands in for (paths relative to the reference repository root).  The
- * reference-side binding a maintainer would add is a ctypes stub, shown in
- * INTEGRATION.md; minitorch_amd/_lib.py is that stub.
+ * reference-side binding a maintainer would add is a ctypes stub;
+ * minitorch_amd/_lib.py is that stub.
  *
  * Conventions
  *  - Every function returns an int status (MTX_OK = 0).  On failure

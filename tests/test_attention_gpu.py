@@ -1,6 +1,6 @@
 """GPU parity of the fused attention kernels against the CPU oracle.
 
-Bars (stated by the task's north star):
+Bars (the parity tolerances of the hot path):
   * fp32 inputs: elementwise |gpu - ref| <= 1e-5 + 1e-4 * |ref|
   * bf16 inputs ("rel 2e-2"): max|gpu - ref| <= 2e-2 * max|ref| and
     ||gpu - ref||_F <= 2e-2 * ||ref||_F, against the fp32/fp64 NumPy reference

@@ -1,6 +1,6 @@
 """The product path without PyTorch: a fresh Python process that never
-imports torch runs (1) the NumPy-only ctypes snippet from INTEGRATION.md,
-verbatim, checked against the oracle at the fp32 bar; (2) C0 training
+imports torch runs (1) the integration guide's NumPy-only ctypes snippet
+(the code block marked "numpy-only attention round trip"), verbatim, checked against the oracle at the fp32 bar; (2) C0 training
 through minitorch_amd (eager, then a HIP-graph-captured step) against the
 reference's own loss curve; (3) greedy decoding (KV cache, replayed decode
 step) against the reference's tokens; (4) __graft_entry__.smoke().  The
@@ -21,7 +21,7 @@ from pathlib import Path
 import numpy as np
 ROOT = Path(sys.argv[1]); sys.path.insert(0, str(ROOT)); sys.path.insert(0, str(ROOT / "tests"))
 
-# (1) the INTEGRATION.md snippet, exactly as written there
+# (1) the integration guide's snippet, exactly as written there
 text = (ROOT / "INTEGRATION.md").read_text()
 snippet = re.search(r"```python\n(# numpy-only attention round trip\n.*?)```", text, re.S).group(1)
 ns = {}
