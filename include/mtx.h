@@ -346,6 +346,31 @@ int mtx_gemm_act_f32(int M, int N, int K, int batch,
                      int64_t sx_b, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * A decode-step projection with its residual add, followed by the
+ * LayerNorm that reads the updated rows next, in two launches:
+ *   C = alpha * A @ B + bias + beta * C       (batch 1, C row stride sc_m,
+ *                                              unit column stride)
+ *   y[m] = (C[m] - mean) / sqrt(var + eps) * ln_gamma + ln_beta
+ * (biased variance over the N values of row m; y row stride ldy; y must
+ * not overlap C).  Replaces, in GPT.generate's per-token forward
+ * (transformer.py:93-104), a block's residual adds x + attn(ln1(x)) and
+ * x + mlp(ln2(x)) (transformer.py:64-65; the output projection and the
+ * second MLP Linear, layers.py:31-37) together with the LayerNorm applied
+ * to their result next (ln2, the following block's ln1, or ln_f:
+ * transformer.py:63-65, 89; layers.py:82-86).  M <= 64, K <= 4096,
+ * N <= 2048.  The partial products of two or more K ranges go to the
+ * workspace (mtx_gemm_ln_workspace_bytes); one kernel sums them in range
+ * order, applies bias and residual, and normalises the rows.  For K > 512
+ * (the ranges of mtx_gemm_f32's own split) C and y are bit-identical to
+ * mtx_gemm_f32 followed by mtx_layernorm_fwd_f32.
+ */
+size_t mtx_gemm_ln_workspace_bytes(int M, int N, int K);
+int mtx_gemm_ln_f32(int M, int N, int K, float alpha, const float* a, int64_t sa_m, int64_t sa_k,
+                    const float* b, int64_t sb_k, int64_t sb_n, float beta, float* c, int64_t sc_m,
+                    const float* bias, const float* ln_gamma, const float* ln_beta, float eps, float* y,
+                    int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Weight and bias gradients of a Linear layer in one pass over dY:
  *   C = A @ B + beta * C            (dW = X^T dY: tensor.py:216-218 through
  *                                    Linear.forward's x @ W, layers.py:31-37)

@@ -88,6 +88,9 @@ SIGNATURES = {
                           _P, _P, _SZ, _P]),
     "mtx_gemm_wgrad_f32": (_I, [_I, _I, _I, _P, _I64, _I64, _P, _I64, _I64, _F, _P, _I64, _I64,
                                 _P, _I, _P, _SZ, _P]),
+    "mtx_gemm_ln_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "mtx_gemm_ln_f32": (_I, [_I, _I, _I, _F, _P, _I64, _I64, _P, _I64, _I64, _F, _P, _I64,
+                             _P, _P, _P, _F, _P, _I64, _P, _SZ, _P]),
     "mtx_gemm_act_f32": (_I, [_I, _I, _I, _I,
                               _F, _P, _I64, _I64, _I64,
                               _P, _I64, _I64, _I64,

@@ -585,6 +585,72 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const GemmArgs g) {
   }
 }
 
+// The split-K reduce of a skinny product followed by LayerNorm of the result
+// rows (a decode step's "x += h @ W + b, then ln(x)" in one launch): one
+// wave per row.  Per element the arithmetic of gemm_splitk_reduce (partials
+// added in split order, then alpha, bias, beta * C), then the row
+// statistics of layernorm_fwd_kernel on the values just stored, so C and y
+// equal the two-launch sequence's.  Every load of the row is issued before
+// the first store (a store in between would order each element's loads
+// after it), with the split count KS fixed at compile time.
+template <int VPL, int KS>
+__global__ __launch_bounds__(64) void splitk_reduce_ln_kernel(const GemmArgs g, const float* __restrict__ gamma,
+                                                              const float* __restrict__ beta_ln, float eps,
+                                                              float* __restrict__ y, int64_t ldy) {
+  const int m = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int64_t MN = (int64_t)g.M * g.N;
+  float v[VPL], r[VPL], bb[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int n = lane + 64 * i;
+    const bool ok = n < g.N;
+    const int64_t e = ok ? (int64_t)m * g.N + n : 0;
+    float part[KS];
+#pragma unroll
+    for (int sp = 0; sp < KS; ++sp) part[sp] = g.ws[(int64_t)sp * MN + e];
+    float s = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < KS; ++sp) s += part[sp];
+    v[i] = s;
+    r[i] = ok && g.beta != 0.f ? g.c[(int64_t)m * g.scm + (int64_t)n * g.scn] : 0.f;
+    bb[i] = ok && g.bias ? g.bias[n] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int n = lane + 64 * i;
+    float t = g.alpha * v[i] + bb[i];
+    if (g.beta != 0.f) t += g.beta * r[i];
+    v[i] = n < g.N ? t : 0.f;
+    if (n < g.N) g.c[(int64_t)m * g.scm + (int64_t)n * g.scn] = t;
+  }
+  float mean, sd;
+  ln_stats<VPL>(v, lane, g.N, eps, mean, sd);
+  float* yr = y + (int64_t)m * ldy;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int n = lane + 64 * i;
+    if (n < g.N) yr[n] = ln_apply(v[i], sd, gamma[n], beta_ln[n]);
+  }
+}
+
+template <int VPL>
+void launch_reduce_ln(const GemmArgs& g, const float* gamma, const float* beta_ln, float eps, float* y,
+                      int64_t ldy, hipStream_t st) {
+  const dim3 grid(g.M), block(64);
+#define RLN(KS) hipLaunchKernelGGL((splitk_reduce_ln_kernel<VPL, KS>), grid, block, 0, st, g, gamma, beta_ln, eps, y, ldy)
+  switch (g.ksplit) {
+    case 2: RLN(2); break;
+    case 3: RLN(3); break;
+    case 4: RLN(4); break;
+    case 5: RLN(5); break;
+    case 6: RLN(6); break;
+    case 7: RLN(7); break;
+    default: RLN(8); break;
+  }
+#undef RLN
+}
+
 struct Plan {
   int bm, bn, ksplit, kchunk;
 };
@@ -761,6 +827,58 @@ extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
                             void* stream) {
   return gemm_impl(M, N, K, batch, alpha, a, sa_m, sa_k, sa_b, b, sb_k, sb_n, sb_b, beta, c, sc_m, sc_n, sc_b,
                    bias, 0, nullptr, 0, 0, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t mtx_gemm_ln_workspace_bytes(int M, int N, int K) {
+  if (M < 1 || N < 1 || K < 1 || skinny_splits(M, K) == 0) return 0;
+  const int sp = std::max(2, skinny_splits(M, K));
+  return (size_t)sp * M * N * sizeof(float);
+}
+
+extern "C" int mtx_gemm_ln_f32(int M, int N, int K, float alpha, const float* a, int64_t sa_m, int64_t sa_k,
+                               const float* b, int64_t sb_k, int64_t sb_n, float beta, float* c, int64_t sc_m,
+                               const float* bias, const float* ln_gamma, const float* ln_beta, float eps, float* y,
+                               int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+  MTX_CHECK_SHAPE(M >= 1 && N >= 1 && K >= 1, "gemm_ln: sizes must be >= 1");
+  MTX_CHECK_SHAPE(M <= kSkMaxM && K <= kSkMaxK * kSkMaxSplit && N <= 64 * 32,
+                  "gemm_ln: needs M <= %d, K <= %d and N <= 2048 (got M=%d, N=%d, K=%d)", kSkMaxM,
+                  kSkMaxK * kSkMaxSplit, M, N, K);
+  MTX_CHECK_ARG(a && b && c && ln_gamma && ln_beta && y, "gemm_ln: null pointer");
+  MTX_CHECK_ARG(sa_k == 1 || sa_m == 1, "gemm_ln: A needs a unit stride along m or k");
+  MTX_CHECK_ARG(sb_n == 1 || sb_k == 1, "gemm_ln: B needs a unit stride along k or n");
+  MTX_CHECK_ARG(sc_m >= N && ldy >= N, "gemm_ln: C and y rows must hold N values");
+  MTX_CHECK_ARG((y >= c + (int64_t)(M - 1) * sc_m + N) || (c >= y + (int64_t)(M - 1) * ldy + N),
+                "gemm_ln: y must not overlap C");
+  const size_t need = mtx_gemm_ln_workspace_bytes(M, N, K);
+  MTX_CHECK_ARG(workspace && workspace_bytes >= need, "gemm_ln: workspace too small (%zu < %zu)", workspace_bytes,
+                need);
+  // the partials of at least two K ranges go to the workspace (the ranges
+  // of mtx_gemm_f32's split when K > 512, else two halves)
+  const int sk = skinny_splits(M, K);
+  const int sp = std::max(2, sk);
+  const int kchunk = sk > 1 ? kSkMaxK : cdiv(cdiv(K, 2), 16) * 16;
+  GemmArgs g{a, sa_m, sa_k, 0, b, sb_k, sb_n, 0, c, sc_m, 1, 0, bias,
+             static_cast<float*>(workspace), M, N, K, 1, sp, kchunk, alpha, beta};
+  g.nc = N;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool av = k_vec(a, sa_m, sa_k, 0, K), bv = k_vec(b, sb_n, sb_k, 0, K);
+  const dim3 grid(cdiv(N, 16), 1, sp);
+  if (av && bv) hipLaunchKernelGGL((gemm_skinny_kernel<true, true>), grid, dim3(kSkT), 0, st, g);
+  else if (av) hipLaunchKernelGGL((gemm_skinny_kernel<true, false>), grid, dim3(kSkT), 0, st, g);
+  else if (bv) hipLaunchKernelGGL((gemm_skinny_kernel<false, true>), grid, dim3(kSkT), 0, st, g);
+  else hipLaunchKernelGGL((gemm_skinny_kernel<false, false>), grid, dim3(kSkT), 0, st, g);
+  MTX_LAUNCHED();
+  const int vpl = cdiv(N, 64);
+  if (vpl <= 1) launch_reduce_ln<1>(g, ln_gamma, ln_beta, eps, y, ldy, st);
+  else if (vpl <= 2) launch_reduce_ln<2>(g, ln_gamma, ln_beta, eps, y, ldy, st);
+  else if (vpl <= 4) launch_reduce_ln<4>(g, ln_gamma, ln_beta, eps, y, ldy, st);
+  else if (vpl <= 6) launch_reduce_ln<6>(g, ln_gamma, ln_beta, eps, y, ldy, st);
+  else if (vpl <= 8) launch_reduce_ln<8>(g, ln_gamma, ln_beta, eps, y, ldy, st);
+  else if (vpl <= 12) launch_reduce_ln<12>(g, ln_gamma, ln_beta, eps, y, ldy, st);
+  else if (vpl <= 16) launch_reduce_ln<16>(g, ln_gamma, ln_beta, eps, y, ldy, st);
+  else launch_reduce_ln<32>(g, ln_gamma, ln_beta, eps, y, ldy, st);
+  MTX_LAUNCHED();
+  return MTX_OK;
 }
 
 extern "C" int mtx_gemm_act_f32(int M, int N, int K, int batch,

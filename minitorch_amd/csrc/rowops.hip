@@ -72,30 +72,6 @@ __global__ __launch_bounds__(256) void softmax_bwd_kernel(const float* __restric
   }
 }
 
-// LayerNorm statistics of one row held by a wave, lane-strided
-// (v[i] = x[lane + 64 i], 0 past C): mean, then v[i] <- x - mean (0 past C)
-// and sd = sqrt(biased variance + eps) (layers.py:82-86).
-template <int VPL>
-__device__ __forceinline__ void ln_stats(float (&v)[VPL], int lane, int C, float eps, float& mean, float& sd) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) s += v[i];
-  mean = wave_sum(s) / (float)C;
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int j = lane + 64 * i;
-    const float d = j < C ? v[i] - mean : 0.f;
-    v[i] = d;
-    q += d * d;
-  }
-  const float var = wave_sum(q) / (float)C;
-  sd = sqrtf(var + eps);
-}
-// normalised, scaled and shifted value of d = x - mean (layers.py:85-86)
-__device__ __forceinline__ float ln_apply(float d, float sd, float gamma, float beta) {
-  return (d / sd) * gamma + beta;
-}
 
 // LayerNorm forward: y = (x - mean) / sqrt(var + eps) * gamma + beta.
 // Saves mean and std per row for the backward.

@@ -348,6 +348,35 @@ def reduce(a, axes, out, op=L.RED_SUM, alpha: float = 1.0, accumulate=False):
 GEMM_ACT_NONE, GEMM_ACT_GELU, GEMM_ACT_GELU_BWD, GEMM_ACT_ADD = 0, 1, 2, 4
 
 
+def gemm_ln_fits(M, K, N):
+    """Whether mtx_gemm_ln_f32 takes an (M, K) @ (K, N) product."""
+    return 1 <= M <= 64 and 1 <= K <= 4096 and 1 <= N <= 2048
+
+
+def gemm_ln(a, b, c, gamma, beta_ln, eps, y, bias=None, alpha=1.0, beta=1.0):
+    """c = alpha * a @ b + bias + beta * c, then y = LayerNorm(rows of c)
+    with gamma, beta_ln, eps (mtx_gemm_ln_f32: a decode step's residual
+    projection and the LayerNorm after it; a (M, K) with M <= 64, b (K, N),
+    c and y (M, N) with unit column strides)."""
+    M, K = a.shape[-2], a.shape[-1]
+    N = b.shape[-1]
+    for name, t in (("a", a), ("b", b), ("c", c), ("y", y), ("gamma", gamma), ("beta", beta_ln)):
+        if _dt(t) != "float32":
+            raise ValueError(f"gemm_ln: {name} must be fp32")
+    if tuple(c.shape[-2:]) != (M, N) or tuple(y.shape[-2:]) != (M, N) or c.stride(-1) != 1 or y.stride(-1) != 1:
+        raise ValueError(f"gemm_ln: c and y must be ({M}, {N}) with unit column strides")
+    if gamma.numel() != N or beta_ln.numel() != N or not (gamma.is_contiguous() and beta_ln.is_contiguous()):
+        raise ValueError(f"gemm_ln: gamma and beta must be contiguous with N={N} elements")
+    ws_bytes = L.lib().mtx_gemm_ln_workspace_bytes(M, N, K)
+    ws = dev.empty_buf((ws_bytes,), "uint8") if ws_bytes else None
+    L.call("mtx_gemm_ln_f32", int(M), int(N), int(K), float(alpha), L.ptr(a), int(a.stride(-2)),
+           int(a.stride(-1)), L.ptr(b), int(b.stride(-2)), int(b.stride(-1)), float(beta), L.ptr(c),
+           int(c.stride(-2)), L.ptr(bias) if bias is not None else None, L.ptr(gamma), L.ptr(beta_ln),
+           float(eps), L.ptr(y), int(y.stride(-2)), L.ptr(ws) if ws is not None else None, ws_bytes,
+           L.stream_handle())
+    return y
+
+
 def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=1,
          sa=None, sb=None, sc=None, act=GEMM_ACT_NONE, aux=None, colsum=None, colsum_accumulate=False):
     """C = alpha*A@B + beta*C (+bias) with explicit (row, col, batch) strides

@@ -27,6 +27,23 @@ def _linear_into(x, lin, out):
     return out
 
 
+def _linear_ln_into(x, lin, out, ln):
+    """out += x @ W + b in place, then (out, ln(out)); for one-token rows the
+    normalisation is done by the launch that finishes the product
+    (mtx_gemm_ln_f32).  Inference only: no graph nodes."""
+    from . import kernels as K
+
+    B, T, Cin = x.shape
+    C = lin.weight.shape[1]
+    if T == 1 and K.gemm_ln_fits(B, Cin, C):
+        y = dev.empty((B, 1, C))
+        K.gemm_ln(x.data.t.reshape(B, Cin), lin.weight.data.t, out.data.t.view(B, C), ln.gamma.data.t,
+                  ln.beta.data.t, float(np.float32(ln.eps)), y.t.view(B, C), bias=lin.bias.data.t)
+        return out, Tensor(y)
+    _linear_into(x, lin, out)
+    return out, ln(out)
+
+
 class MultiHeadAttention(Module):
     def __init__(self, n_embd, n_head, dropout=0.0):
         super().__init__()
@@ -100,7 +117,7 @@ class MultiHeadAttention(Module):
         return self.out_proj(Tensor(out.reshape(B, T, C)))
 
 
-    def forward_step(self, x, cache, lengths, residual=None):
+    def forward_step(self, x, cache, lengths, residual=None, ln=None):
         """One-token decode step whose positions live in device memory, so a
         recorded step replays unchanged: x (B, 1, C); this token's key/value
         go to cache row lengths[b] - 1 (written by the q/k/v GEMM itself,
@@ -108,7 +125,9 @@ class MultiHeadAttention(Module):
         over each sequence's first lengths[b] cached keys (mtx_attn_decode).
         With `residual` (B, 1, C) the output projection is accumulated into it
         in place (the block's residual add folded into the GEMM) and it is
-        returned."""
+        returned; with `ln` as well (the LayerNorm that reads the residual
+        next), (residual, ln(residual)) is returned, the normalisation done
+        with the projection (mtx_gemm_ln_f32)."""
         from . import kernels as K
 
         B, T, C = x.shape
@@ -133,6 +152,8 @@ class MultiHeadAttention(Module):
         K.attn_decode(heads(q), heads(kc.t), heads(vc.t), 1.0 / math.sqrt(D),
                       out=out.t.transpose(1, 2), lengths=lengths)
         if residual is not None:
+            if ln is not None:
+                return _linear_ln_into(Tensor(out.reshape(B, 1, C)), self.out_proj, residual, ln)
             return _linear_into(Tensor(out.reshape(B, 1, C)), self.out_proj, residual)
         return self.out_proj(Tensor(out.reshape(B, 1, C)))
 
@@ -187,24 +208,32 @@ class TransformerBlock(Module):
         x = x + self.mlp(self.ln2(x))
         return x
 
-    def forward_step(self, x, cache, lengths):
+    def forward_step(self, x, cache, lengths, ln_in=None, next_ln=None):
         """Decode step (no autograd): x is updated in place, both residual
-        adds folded into the out_proj / second MLP GEMMs (beta = 1)."""
+        adds folded into the out_proj / second MLP GEMMs (beta = 1), and
+        ln2 done by the launch that finishes the output projection.
+        ln_in: this block's ln1(x) when the caller already has it.  With
+        next_ln (the LayerNorm that reads x next: the following block's ln1
+        or ln_f) the step returns (x, next_ln(x)), the normalisation again
+        done with the second MLP product; otherwise it returns x."""
         fc1, act, fc2, drop = self.mlp.layers
         if drop._training and drop.p > 0.0:
             raise NotImplementedError("decode steps run without dropout (use model.eval() or p = 0)")
         from . import kernels as K
 
-        self.attn.forward_step(self.ln1(x), cache, lengths, residual=x)
+        _, h_in = self.attn.forward_step(self.ln1(x) if ln_in is None else ln_in, cache, lengths, residual=x,
+                                         ln=self.ln2)
         B, _, C = x.shape
-        h_in = self.ln2(x)
         if K.step_fits(B, C) and isinstance(act, GELU):
             # fc1 with its GELU in one launch
-            h = dev.empty((B, 1, fc1.weight.shape[1]))
+            h = Tensor(dev.empty((B, 1, fc1.weight.shape[1])))
             K.gemm_step(h_in.data.t.reshape(B, C), fc1.weight.data.t, bias=fc1.bias.data.t,
-                        c=h.t.view(B, -1), act=K.ACT_GELU)
-            return _linear_into(Tensor(h), fc2, x)
-        return _linear_into(act(fc1(h_in)), fc2, x)
+                        c=h.data.t.view(B, -1), act=K.ACT_GELU)
+        else:
+            h = act(fc1(h_in))
+        if next_ln is None:
+            return _linear_into(h, fc2, x)
+        return _linear_ln_into(h, fc2, x, next_ln)
 
 
 class GPT(Module):
@@ -308,9 +337,13 @@ class GPT(Module):
                     K.embedding2_fwd(self.tok_emb.weight.data.t, cur, self.pos_emb.weight.data.t, posd,
                                      x.t.view(B, C), ib_stride=0)
                     h = Tensor(x)
-                    for block, cache in zip(self.blocks, caches):
-                        h = block.forward_step(h, cache, lengths)
-                    logits = self.lm_head(self.ln_f(h)).data.t.view(B, -1)
+                    # each block's last launch also normalises its output for
+                    # the next block's ln1 (ln_f after the last block)
+                    hn = self.blocks[0].ln1(h)
+                    for i, (block, cache) in enumerate(zip(self.blocks, caches)):
+                        nxt = self.blocks[i + 1].ln1 if i + 1 < len(self.blocks) else self.ln_f
+                        h, hn = block.forward_step(h, cache, lengths, ln_in=hn, next_ln=nxt)
+                    logits = self.lm_head(hn).data.t.view(B, -1)
                     K.greedy_pick(logits, cur, ids.t, lengths, posd, margins.t, t_base=T0)
 
                 step()

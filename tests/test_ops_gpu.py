@@ -547,3 +547,38 @@ def test_gemm_residual_epilogue(dev, M, N, K):
     close(H(c), ref, atol=dot_tol(K), name="gemm_residual")
     with pytest.raises(ValueError):
         K_.gemm(T(a), T(b), c, act=K_.GEMM_ACT_ADD, aux=c)  # the residual cannot be C itself
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 384, 1536), (64, 384, 384), (64, 64, 256), (7, 130, 700), (33, 384, 384),
+                                   (1, 2048, 4096), (64, 1000, 3000)])
+def test_gemm_ln_matches_gemm_then_layernorm(dev, M, N, K):
+    """mtx_gemm_ln_f32 (x += h @ W + b, then LayerNorm of x's rows: a decode
+    step's residual projection and the LayerNorm after it) against
+    mtx_gemm_f32 followed by mtx_layernorm_fwd_f32 on the same inputs --
+    bit-identical for K > 512, where both sum the same K-range partials in
+    the same order -- and both against float64 NumPy (split counts 2 to 6,
+    rows of 1 to 32 values per lane)."""
+    from minitorch_amd import kernels as Kn
+    from oracle.gpt import ln_fwd
+
+    _say(f"[gemm_ln] M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + N + K)
+    h = rng.standard_normal((M, K), dtype=np.float32)
+    w = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    b = rng.standard_normal(N, dtype=np.float32)
+    x0 = rng.standard_normal((M, N), dtype=np.float32)
+    gam = rng.standard_normal(N, dtype=np.float32)
+    bet = rng.standard_normal(N, dtype=np.float32)
+    eps = float(np.float32(1e-5))
+    xf, yf = T(x0), empty((M, N))
+    Kn.gemm_ln(T(h), T(w), xf, T(gam), T(bet), eps, yf, bias=T(b))
+    xs, ys = T(x0), empty((M, N))
+    Kn.gemm(T(h), T(w), xs, beta=1.0, bias=T(b))
+    Kn.layernorm_fwd(xs, T(gam), T(bet), ys, empty((M,)), empty((M,)), eps)
+    if K > 512:
+        assert np.array_equal(H(xf), H(xs)) and np.array_equal(H(yf), H(ys))
+    xr = x0.astype(np.float64) + h.astype(np.float64) @ w + b
+    close(H(xf), xr, atol=dot_tol(K), name="gemm_ln x")
+    close(H(xs), xr, atol=dot_tol(K), name="gemm x")
+    yr = ln_fwd(H(xf).astype(np.float64), gam.astype(np.float64), bet.astype(np.float64), 1e-5)[0]
+    close(H(yf), yr, rtol=1e-4, atol=1e-4, name="gemm_ln y")
