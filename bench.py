@@ -437,7 +437,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=("all", "c3", "c1", "c0attn", "c4", "c4kernel", "gpt2", "gpt0"),
+    ap.add_argument("--only", choices=("all", "c3", "c1", "c0attn", "c4", "c4eager", "c4kernel", "gpt2", "gpt0"),
                     default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -475,6 +475,23 @@ def main():
             ms, losses = bench_gpt(c, 2, args.steps, args.warmup, graph=graph)
             print(f"[bench] {args.only} ({'graph' if graph else 'eager'}): {ms:.3f} ms/step, "
                   f"{c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, losses {losses}", file=sys.stderr)
+        return
+    if args.only == "c4eager":
+        # the C4 run with every decode step launched eagerly (no HIP graph):
+        # the same kernels, for a kernel-by-kernel trace
+        import minitorch_amd as mt
+
+        c = C2_CFG
+        model = mt.GPT(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"], dropout=0.0)
+        model.init_weights(np.random.default_rng(2))
+        model.eval()
+        prompts = np.random.default_rng(4).integers(0, c["vocab"], (64, 32))
+        model.generate_greedy(prompts, 8, graph=False)
+        _sync()
+        t0 = time.perf_counter()
+        model.generate_greedy(prompts, 224, graph=False)
+        dt = time.perf_counter() - t0
+        print(f"[bench] C4 eager steps: {dt * 1e3 / 224:.3f} ms per token step", file=sys.stderr)
         return
     if args.only == "c4kernel":
         bench_decode_kernel(C2_CFG, graph=False)

@@ -358,11 +358,12 @@ int mtx_gemm_act_f32(int M, int N, int K, int batch,
  * second MLP Linear, layers.py:31-37) together with the LayerNorm applied
  * to their result next (ln2, the following block's ln1, or ln_f:
  * transformer.py:63-65, 89; layers.py:82-86).  M <= 64, K <= 4096,
- * N <= 2048.  The partial products of two or more K ranges go to the
- * workspace (mtx_gemm_ln_workspace_bytes); one kernel sums them in range
- * order, applies bias and residual, and normalises the rows.  For K > 512
- * (the ranges of mtx_gemm_f32's own split) C and y are bit-identical to
- * mtx_gemm_f32 followed by mtx_layernorm_fwd_f32.
+ * N <= 2048.  K is split into 2 to 8 ranges (enough workgroups for a
+ * narrow N); their partial products go to the workspace
+ * (mtx_gemm_ln_workspace_bytes) and one kernel sums them in range order,
+ * applies bias and residual, and normalises the rows with the arithmetic
+ * of mtx_layernorm_fwd_f32.  Deterministic; the product's rounding differs
+ * from mtx_gemm_f32's only by the grouping of the K sums.
  */
 size_t mtx_gemm_ln_workspace_bytes(int M, int N, int K);
 int mtx_gemm_ln_f32(int M, int N, int K, float alpha, const float* a, int64_t sa_m, int64_t sa_k,

@@ -288,10 +288,10 @@ class GPT(Module):
         position's logits -- the C4 harness over transformer.py:93-104 -- with
         a KV cache: one prefill over the prompt, then one-token steps whose
         attention is the decode kernel against the cached keys and values.
-        The loop stays on the device: each step's pick (mtx_argmax_f32) lands
-        in the id buffer the next step's embedding reads, and the step's
-        positions (cache row, key count, position id) are device counters
-        advanced by mtx_decode_advance.  A step therefore replays unchanged:
+        The loop stays on the device: each step's pick (mtx_greedy_pick_f32)
+        lands in the id buffer the next step's embedding reads, and the same
+        launch advances the step's positions (cache row, key count, position
+        id), device counters.  A step therefore replays unchanged:
         with graph=True the first one-token step runs eagerly, the second is
         recorded as a HIP graph and replayed for the rest.  The host
         synchronises once, at the end.  Needs T0 + max_new_tokens <=
