@@ -302,6 +302,35 @@ int mtx_embedding2_fwd_f32(const float* wa, int64_t lda, int64_t Va, const int64
                            int64_t ldb, int64_t Vb, const int64_t* ib, int64_t ib_stride, float* out, int64_t ldo,
                            int64_t n, int C, void* stream);
 
+/*
+ * mtx_embedding2_fwd_f32 and then the first block's LayerNorm of its rows in
+ * one launch: out[i] = wa[ia[i]] + wb[ib[i * ib_stride]] and
+ * y[i] = (out[i] - mean) / sqrt(var + eps) * gamma + beta (biased variance
+ * over the C values; the arithmetic of mtx_embedding2_fwd_f32 followed by
+ * mtx_layernorm_fwd_f32).  Replaces, in GPT.generate's per-token forward,
+ * transformer.py:84-87 (token + position embeddings) and the first block's
+ * ln1 (transformer.py:63, layers.py:82-86).  C <= 2048.
+ */
+int mtx_embedding2_ln_fwd_f32(const float* wa, int64_t lda, int64_t Va, const int64_t* ia, const float* wb,
+                              int64_t ldb, int64_t Vb, const int64_t* ib, int64_t ib_stride, float* out,
+                              int64_t ldo, int64_t n, int C, const float* gamma, const float* beta, float eps,
+                              float* y, int64_t ldy, void* stream);
+
+/*
+ * The output projection (lm_head) and mtx_greedy_pick_f32 of a decode step
+ * in one launch: per row r of x (rows, K), logits[c] = sum_k x[r][k] *
+ * W[k][c] + bias[c] (W (K, V) row stride ldw; K cut into 16 equal ranges,
+ * each summed k ascending with fused multiply-adds, the range sums added in
+ * range order, then the bias), then the first-maximum pick and its bookkeeping
+ * exactly as mtx_greedy_pick_f32 (cur, ids, margins, lengths, pos).
+ * Replaces, in the greedy harness over transformer.py:93-104, the head
+ * Linear of transformer.py:91 (layers.py:31-37) and np.argmax of the last
+ * position's logits.  V <= 256, K <= 8192.
+ */
+int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const float* W, int64_t ldw,
+                      const float* bias, int64_t* cur, int64_t* ids, int Tmax, float* margins, int t_base,
+                      int n_margins, int* lengths, int64_t* pos, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* GEMM                                                                     */
 /* ------------------------------------------------------------------------ */

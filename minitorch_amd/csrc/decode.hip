@@ -280,6 +280,144 @@ __global__ __launch_bounds__(256) void embed2_kernel(const float* __restrict__ w
   }
 }
 
+// The pick's bookkeeping for one row (lane 0): the next input id, the id
+// and margin records, the row's length and (row 0) the position id.
+__device__ __forceinline__ void pick_record(int row, int rows, const Top2& t, int64_t* __restrict__ cur,
+                                            int64_t* __restrict__ ids, int Tmax, float* __restrict__ margins,
+                                            int t_base, int nm, int* __restrict__ lengths,
+                                            int64_t* __restrict__ pos) {
+  const int L = lengths[row];
+  cur[row] = t.i1;
+  if (L >= 0 && L < Tmax) ids[(int64_t)L * rows + row] = t.i1;
+  const int s = L - t_base;
+  if (margins != nullptr && s >= 0 && s < nm) margins[(int64_t)s * rows + row] = t.m1 - t.m2;
+  lengths[row] = L + 1;
+  if (row == 0 && pos != nullptr) pos[0] += 1;
+}
+
+// The output projection and the greedy pick of one decode step in one
+// launch: one 16-wave workgroup per row.  Wave w sums the K range
+// [w * kc, (w + 1) * kc) for the lane's logits j, j + 64, ... (x's row staged
+// in LDS and read as a broadcast, one fused multiply-add per term, k
+// ascending), the 16 partial sums are added in wave order with the bias,
+// then the top two over the row and the pick's bookkeeping as
+// greedy_pick_kernel.
+constexpr int kHpW = 16;  // waves per head_pick workgroup
+template <int VPL>
+__global__ __launch_bounds__(64 * kHpW) void head_pick_kernel(int rows, int K, int V, const float* __restrict__ x,
+                                                              int64_t ldx, const float* __restrict__ W, int64_t ldw,
+                                                              const float* __restrict__ bias,
+                                                              int64_t* __restrict__ cur, int64_t* __restrict__ ids,
+                                                              int Tmax, float* __restrict__ margins, int t_base,
+                                                              int nm, int* __restrict__ lengths,
+                                                              int64_t* __restrict__ pos) {
+  extern __shared__ float smem[];
+  float* xs = smem;                       // K floats
+  float* part = smem + ((K + 3) & ~3);    // kHpW x 64 * VPL partial sums
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const float* __restrict__ xr = x + (int64_t)row * ldx;
+  for (int k = tid; k < K; k += 64 * kHpW) xs[k] = xr[k];
+  __syncthreads();
+  const int kc = (K + kHpW - 1) / kHpW;
+  const int k0 = w * kc, k1 = min(K, k0 + kc);
+  float acc[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) acc[i] = 0.f;
+  // the weight rows of the wave's K range in batches of kHpB, every load of
+  // a batch issued before its products
+  constexpr int kHpB = 32 / VPL;
+  for (int kb = k0; kb < k1; kb += kHpB) {
+    float wv[kHpB][VPL];
+#pragma unroll
+    for (int j = 0; j < kHpB; ++j) {
+      const int k = min(kb + j, K - 1);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = min(lane + 64 * i, V - 1);
+        wv[j][i] = W[(int64_t)k * ldw + c];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kHpB; ++j) {
+      if (kb + j < k1) {
+        const float xv = xs[kb + j];
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) acc[i] = fmaf(xv, wv[j][i], acc[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) part[w * 64 * VPL + lane + 64 * i] = acc[i];
+  __syncthreads();
+  if (w != 0) return;
+  Top2 t{-INFINITY, -INFINITY, V};
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < V) {
+      float v = 0.f;
+#pragma unroll
+      for (int q = 0; q < kHpW; ++q) v += part[q * 64 * VPL + c];
+      if (bias) v += bias[c];
+      if (v > t.m1) {
+        t.m2 = t.m1;
+        t.m1 = v;
+        t.i1 = c;
+      } else if (v > t.m2) {
+        t.m2 = v;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    Top2 o;
+    o.m1 = __shfl_xor(t.m1, m, 64);
+    o.m2 = __shfl_xor(t.m2, m, 64);
+    o.i1 = __shfl_xor(t.i1, m, 64);
+    t = merge(t, o);
+  }
+  if (lane == 0) pick_record(row, rows, t, cur, ids, Tmax, margins, t_base, nm, lengths, pos);
+}
+
+// The token and position embeddings, their sum, and the first block's
+// LayerNorm of it in one launch: one wave per row, the sum written to out
+// and normalised into y (the arithmetic of embed2_kernel and
+// layernorm_fwd_kernel).
+template <int VPL>
+__global__ __launch_bounds__(64) void embed2_ln_kernel(const float* __restrict__ wa, int64_t lda, int64_t Va,
+                                                       const int64_t* __restrict__ ia,
+                                                       const float* __restrict__ wb, int64_t ldb, int64_t Vb,
+                                                       const int64_t* __restrict__ ib, int64_t ib_stride,
+                                                       float* __restrict__ out, int64_t ldo, int C,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta, float eps,
+                                                       float* __restrict__ y, int64_t ldy) {
+  const int64_t i = blockIdx.x;
+  const int lane = threadIdx.x;
+  int64_t ra = ia[i], rb = ib[i * ib_stride];
+  ra = ra < 0 ? 0 : (ra >= Va ? Va - 1 : ra);
+  rb = rb < 0 ? 0 : (rb >= Vb ? Vb - 1 : rb);
+  float v[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c = lane + 64 * j;
+    v[j] = c < C ? wa[ra * lda + c] + wb[rb * ldb + c] : 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < C) out[i * ldo + c] = v[j];
+  }
+  float mean, sd;
+  ln_stats<VPL>(v, lane, C, eps, mean, sd);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < C) y[i * ldy + c] = ln_apply(v[j], sd, gamma[c], beta[c]);
+  }
+}
+
 __global__ void advance_kernel(int B, int* __restrict__ lengths, int64_t* __restrict__ pos) {
   const int i = threadIdx.x + blockIdx.x * blockDim.x;
   if (i < B) lengths[i] += 1;
@@ -385,6 +523,53 @@ extern "C" int mtx_greedy_pick_f32(int rows, int cols, const float* x, int64_t l
   MTX_CHECK_ARG(margins == nullptr || n_margins >= 1, "n_margins must be >= 1 with a margin buffer");
   hipLaunchKernelGGL(greedy_pick_kernel, dim3((rows + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream),
                      rows, cols, x, ld, cur, ids, Tmax, margins, t_base, n_margins, lengths, pos);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const float* W, int64_t ldw,
+                                 const float* bias, int64_t* cur, int64_t* ids, int Tmax, float* margins,
+                                 int t_base, int n_margins, int* lengths, int64_t* pos, void* stream) {
+  MTX_CHECK_SHAPE(rows >= 1 && K >= 1 && V >= 1 && Tmax >= 1, "rows, K, V, Tmax must be >= 1");
+  MTX_CHECK_SHAPE(V <= 64 * 4 && K <= 8192, "head_pick: needs V <= 256 and K <= 8192 (got V=%d, K=%d)", V, K);
+  MTX_CHECK_ARG(x && W && cur && ids && lengths, "x, W, cur, ids, lengths: null pointer");
+  MTX_CHECK_ARG(ldx >= K && ldw >= V, "head_pick: bad row strides");
+  MTX_CHECK_ARG(margins == nullptr || n_margins >= 1, "n_margins must be >= 1 with a margin buffer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int vpl = (V + 63) / 64;
+  const int vp = vpl <= 1 ? 1 : (vpl <= 2 ? 2 : 4);
+  const size_t lds = ((size_t)((K + 3) & ~3) + (size_t)kHpW * 64 * vp) * sizeof(float);
+#define HP(VP) hipLaunchKernelGGL(head_pick_kernel<VP>, dim3(rows), dim3(64 * kHpW), lds, st, rows, K, V, x, ldx, W, ldw, bias, cur, ids, Tmax, margins, t_base, n_margins, lengths, pos)
+  if (vpl <= 1) HP(1);
+  else if (vpl <= 2) HP(2);
+  else HP(4);
+#undef HP
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_embedding2_ln_fwd_f32(const float* wa, int64_t lda, int64_t Va, const int64_t* ia,
+                                         const float* wb, int64_t ldb, int64_t Vb, const int64_t* ib,
+                                         int64_t ib_stride, float* out, int64_t ldo, int64_t n, int C,
+                                         const float* gamma, const float* beta, float eps, float* y, int64_t ldy,
+                                         void* stream) {
+  MTX_CHECK_ARG(wa && ia && wb && ib && out && gamma && beta && y, "embedding2_ln: null pointer");
+  MTX_CHECK_SHAPE(n >= 0 && C >= 1 && C <= 64 * 32 && Va >= 1 && Vb >= 1 && lda >= C && ldb >= C && ldo >= C &&
+                      ldy >= C && ib_stride >= 0,
+                  "embedding2_ln: bad shape (C must be in [1, 2048])");
+  if (n == 0) return MTX_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int vpl = (C + 63) / 64;
+#define E2L(VP) hipLaunchKernelGGL(embed2_ln_kernel<VP>, dim3((unsigned)n), dim3(64), 0, st, wa, lda, Va, ia, wb, ldb, Vb, ib, ib_stride, out, ldo, C, gamma, beta, eps, y, ldy)
+  if (vpl <= 1) E2L(1);
+  else if (vpl <= 2) E2L(2);
+  else if (vpl <= 4) E2L(4);
+  else if (vpl <= 6) E2L(6);
+  else if (vpl <= 8) E2L(8);
+  else if (vpl <= 12) E2L(12);
+  else if (vpl <= 16) E2L(16);
+  else E2L(32);
+#undef E2L
   MTX_LAUNCHED();
   return MTX_OK;
 }

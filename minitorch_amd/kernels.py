@@ -525,6 +525,57 @@ def embedding2_fwd(wa, ia, wb, ib, out, ib_stride=1):
     return out
 
 
+def embedding2_ln_fwd(wa, ia, wb, ib, out, gamma, beta, eps, y, ib_stride=1):
+    """out (n, C) = wa[ia] + wb[ib] and y = LayerNorm(out) with gamma, beta,
+    eps in one launch (mtx_embedding2_ln_fwd_f32)."""
+    Va, C = wa.shape
+    Vb = wb.shape[0]
+    n = ia.numel()
+    if _dt(ia) != "int64" or _dt(ib) != "int64" or wb.shape[1] != C or out.shape[-1] != C or y.shape[-1] != C:
+        raise ValueError("embedding2_ln: int64 ids and tables / outputs of one width")
+    if (wa.stride(1) != 1 or wb.stride(1) != 1 or out.stride(-1) != 1 or y.stride(-1) != 1
+            or not ia.is_contiguous()):
+        raise ValueError("embedding2_ln: rows must be contiguous")
+    if gamma.numel() != C or beta.numel() != C or not (gamma.is_contiguous() and beta.is_contiguous()):
+        raise ValueError("embedding2_ln: gamma and beta must be contiguous with C elements")
+    if ib_stride and ib.numel() < n:
+        raise ValueError("embedding2_ln: ib has fewer ids than ia")
+    L.call("mtx_embedding2_ln_fwd_f32", L.ptr(wa), wa.stride(0), Va, L.ptr(ia), L.ptr(wb), wb.stride(0), Vb,
+           L.ptr(ib), int(ib_stride), L.ptr(out), out.stride(-2) if out.dim() >= 2 else C, n, C,
+           L.ptr(gamma), L.ptr(beta), float(eps), L.ptr(y), y.stride(-2) if y.dim() >= 2 else C,
+           L.stream_handle())
+    return y
+
+
+def head_pick(x, w, bias, cur, ids, lengths, pos=None, margins=None, t_base=0):
+    """mtx_head_pick_f32: logits = x @ w + bias per row of x (rows, K), w
+    (K, V), then the pick of greedy_pick on them (cur, ids, margins,
+    lengths, pos) in one launch."""
+    _need_cuda(x, w, cur, ids, lengths)
+    rows, Kd = x.shape
+    V = w.shape[1]
+    if _dt(x) != "float32" or _dt(w) != "float32" or x.stride(1) != 1 or w.stride(1) != 1:
+        raise ValueError("head_pick: x and w must be fp32 with contiguous rows")
+    if w.shape[0] != Kd or (bias is not None and (bias.numel() != V or not bias.is_contiguous())):
+        raise ValueError("head_pick: w must be (K, V) and bias (V,)")
+    if _dt(cur) != "int64" or cur.numel() != rows or not cur.is_contiguous():
+        raise ValueError("head_pick: cur must be contiguous int64 (rows,)")
+    if _dt(ids) != "int64" or ids.dim() != 2 or ids.shape[1] != rows or not ids.is_contiguous():
+        raise ValueError("head_pick: ids must be contiguous int64 (Tmax, rows)")
+    if _dt(lengths) != "int32" or lengths.numel() != rows or not lengths.is_contiguous():
+        raise ValueError("head_pick: lengths must be contiguous int32 (rows,)")
+    if pos is not None and _dt(pos) != "int64":
+        raise ValueError("head_pick: pos must be int64")
+    if margins is not None and (_dt(margins) != "float32" or margins.dim() != 2 or margins.shape[1] != rows
+                                or not margins.is_contiguous()):
+        raise ValueError("head_pick: margins must be contiguous fp32 (n, rows)")
+    L.call("mtx_head_pick_f32", rows, Kd, V, L.ptr(x), x.stride(0), L.ptr(w), w.stride(0),
+           L.ptr(bias) if bias is not None else None, L.ptr(cur), L.ptr(ids), ids.shape[0],
+           L.ptr(margins) if margins is not None else None, int(t_base),
+           margins.shape[0] if margins is not None else 0, L.ptr(lengths),
+           L.ptr(pos) if pos is not None else None, L.stream_handle())
+
+
 # ---------------------------------------------------------------------------
 # row kernels
 # ---------------------------------------------------------------------------

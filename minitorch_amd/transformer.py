@@ -330,21 +330,26 @@ class GPT(Module):
                 posd = dev.full((1,), T0, "int64").t
                 x = dev.empty((B, 1, C))
 
+                ln0 = self.blocks[0].ln1
+                xn = dev.empty((B, 1, C))
+
                 def step():
-                    # embeddings of this token and position in one launch;
-                    # the pick writes the next input, the id and margin
-                    # records, and advances the positions (mtx_greedy_pick_f32)
-                    K.embedding2_fwd(self.tok_emb.weight.data.t, cur, self.pos_emb.weight.data.t, posd,
-                                     x.t.view(B, C), ib_stride=0)
-                    h = Tensor(x)
+                    # embeddings of this token and position and the first
+                    # block's ln1 in one launch (mtx_embedding2_ln_fwd_f32)
+                    K.embedding2_ln_fwd(self.tok_emb.weight.data.t, cur, self.pos_emb.weight.data.t, posd,
+                                        x.t.view(B, C), ln0.gamma.data.t, ln0.beta.data.t,
+                                        float(np.float32(ln0.eps)), xn.t.view(B, C), ib_stride=0)
+                    h, hn = Tensor(x), Tensor(xn)
                     # each block's last launch also normalises its output for
                     # the next block's ln1 (ln_f after the last block)
-                    hn = self.blocks[0].ln1(h)
                     for i, (block, cache) in enumerate(zip(self.blocks, caches)):
                         nxt = self.blocks[i + 1].ln1 if i + 1 < len(self.blocks) else self.ln_f
                         h, hn = block.forward_step(h, cache, lengths, ln_in=hn, next_ln=nxt)
-                    logits = self.lm_head(hn).data.t.view(B, -1)
-                    K.greedy_pick(logits, cur, ids.t, lengths, posd, margins.t, t_base=T0)
+                    # lm_head and the pick in one launch: the pick writes the
+                    # next input, the id and margin records, and advances the
+                    # positions (mtx_head_pick_f32)
+                    K.head_pick(hn.data.t.view(B, C), self.lm_head.weight.data.t, self.lm_head.bias.data.t, cur,
+                                ids.t, lengths, posd, margins.t, t_base=T0)
 
                 step()
                 if graph and n > 2:

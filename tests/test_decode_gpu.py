@@ -238,3 +238,70 @@ def test_embedding2_matches_gathers_plus_add(dev):
     np.testing.assert_array_equal(out.numpy(), Wt[ia] + Wp[ib])
     Kn.embedding2_fwd(_T(Wt), _T(ia, "int64"), _T(Wp), _T(np.array([37]), "int64"), out, ib_stride=0)
     np.testing.assert_array_equal(out.numpy(), Wt[ia] + Wp[37])
+
+
+@pytest.mark.parametrize("C", [384, 64, 1000])
+def test_embedding2_ln_matches_embedding2_then_layernorm(dev, C):
+    """mtx_embedding2_ln_fwd_f32: the embedding sum and the first LayerNorm
+    of a decode step in one launch, bit for bit the two launches'
+    (mtx_embedding2_fwd_f32, mtx_layernorm_fwd_f32), and the LayerNorm
+    against float64."""
+    from minitorch_amd import kernels as Kn
+    from oracle.gpt import ln_fwd
+
+    _say(f"[embedding2_ln] C={C}")
+    rng = np.random.default_rng(11 + C)
+    Wt = rng.standard_normal((65, C)).astype(np.float32)
+    Wp = rng.standard_normal((256, C)).astype(np.float32)
+    gam = rng.standard_normal(C).astype(np.float32)
+    bet = rng.standard_normal(C).astype(np.float32)
+    ia = rng.integers(0, 65, 64)
+    eps = float(np.float32(1e-5))
+    pos = _T(np.array([37]), "int64")
+    out, y = empty((64, C)), empty((64, C))
+    Kn.embedding2_ln_fwd(_T(Wt), _T(ia, "int64"), _T(Wp), pos, out, _T(gam), _T(bet), eps, y, ib_stride=0)
+    out2, y2 = empty((64, C)), empty((64, C))
+    Kn.embedding2_fwd(_T(Wt), _T(ia, "int64"), _T(Wp), pos, out2, ib_stride=0)
+    Kn.layernorm_fwd(out2, _T(gam), _T(bet), y2, empty((64,)), empty((64,)), eps)
+    np.testing.assert_array_equal(out.numpy(), Wt[ia] + Wp[37])
+    np.testing.assert_array_equal(y.numpy(), y2.numpy())
+    ref = ln_fwd((Wt[ia] + Wp[37]).astype(np.float64), gam.astype(np.float64), bet.astype(np.float64), 1e-5)[0]
+    assert np.max(np.abs(y.numpy() - ref)) <= 1e-4 * (1 + np.abs(ref).max())
+
+
+@pytest.mark.parametrize("rows,K,V", [(64, 384, 65), (5, 64, 65), (64, 1000, 200), (3, 17, 1)])
+def test_head_pick_matches_product_then_pick(dev, rows, K, V):
+    """mtx_head_pick_f32: the head product and the greedy pick of a decode
+    step in one launch.  Logits against float64 (each an fp32 fused
+    multiply-add chain); the pick and its bookkeeping against the same
+    records computed on the host from float64 logits (the
+    rows whose top two float64 logits are within 1e-3 are not compared)."""
+    from minitorch_amd import kernels as Kn
+
+    _say(f"[head_pick] rows={rows} K={K} V={V}")
+    rng = np.random.default_rng(12 + K)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    w = (rng.standard_normal((K, V)) / np.sqrt(K)).astype(np.float32)
+    b = rng.standard_normal(V).astype(np.float32)
+    logits = x.astype(np.float64) @ w + b
+    top = np.argmax(logits, axis=1)
+    Tmax, T0, n = 40, 10, 30
+    lengths = rng.integers(T0 + 1, Tmax, rows).astype(np.int32)
+    ids0 = rng.integers(0, 65, (Tmax, rows)).astype(np.int64)
+    m0 = rng.standard_normal((n, rows)).astype(np.float32)
+    cur, ids, mg, tl, pos = _T(np.zeros(rows, np.int64), "int64"), _T(ids0, "int64"), _T(m0), \
+        _T(lengths, "int32"), _T(np.array([17], np.int64), "int64")
+    Kn.head_pick(_T(x), _T(w), _T(b), cur, ids, tl, pos, mg, t_base=T0)
+    srt = np.sort(logits, axis=1)
+    marg = srt[:, -1] - (srt[:, -2] if V > 1 else -np.inf)
+    clear = marg > 1e-3 if V > 1 else np.ones(rows, bool)
+    got = cur.numpy()
+    np.testing.assert_array_equal(got[clear], top[clear])
+    for r in range(rows):
+        L = lengths[r]
+        if 0 <= L < Tmax:
+            assert ids.numpy()[L, r] == got[r]
+        if V > 1 and 0 <= L - T0 < n and clear[r]:
+            assert abs(mg.numpy()[L - T0, r] - marg[r]) <= 1e-4 * (1 + abs(logits[r]).max())
+    np.testing.assert_array_equal(tl.numpy(), lengths + 1)
+    assert int(pos.numpy()[0]) == 18
