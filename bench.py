@@ -19,7 +19,10 @@ TFLOP/s.  The same JSON line carries:
                    bounded sample of (b,h) slices of the same workload;
   also          -- config C1 (fp32, B=32,H=8,T=256,D=64) on the same kernels,
                    and per-phase timings.
-Only one GPU is used: --gpus > 1 exits with a message.
+Every timed loop runs after ~30 ms of its own launches, untimed (SETTLE_MS:
+the GPU's clock transient after idle gaps), and W warm-up calls; the C3 leg
+also reports its cold-start step time.  Only one GPU is used: --gpus > 1 exits
+with a message.
 """
 from __future__ import annotations
 
@@ -82,9 +85,41 @@ def _sync():
     D.synchronize()
 
 
-def time_loop(fn, steps, warmup):
-    """Average ms per call of fn() over `steps` calls after `warmup` calls,
-    bracketed by device synchronisation and HIP events on the launch stream."""
+# Every timed loop first runs its own launches, untimed, for SETTLE_MS of GPU
+# time, then its warm-up calls, then the timed calls.  After an idle gap of
+# more than a few milliseconds (host work between legs: input generation,
+# model construction) the GPU runs the first ~2 ms of a heavy MFMA load at
+# full speed and the next ~20 ms about 20% slower before it settles; on the C3
+# step, 5 warm-up + 20 timed steps measured 0.39 ms per step after 10 ms to 1 s
+# of idle and 0.33 ms right after the same load (profiles/attn_c3_power_transient.md).
+# A 20-step window would otherwise time that transient instead of the rate a
+# continuously running job sees.  The C3 leg also reports its cold-start time
+# (no settling, right after the inputs are uploaded) beside the settled one.
+SETTLE_MS = 30.0
+SETTLE_MAX_CALLS = 1000
+
+
+def settle(fn, ms=SETTLE_MS):
+    """Run fn() untimed for about `ms` of GPU time (its duration estimated
+    from one call, at most SETTLE_MAX_CALLS calls), ending without a
+    synchronisation so the GPU does not idle before what follows."""
+    if ms <= 0:
+        return
+    e0, e1 = _events()
+    e0.record()
+    fn()
+    e1.record()
+    _sync()
+    t = max(e0.elapsed_time(e1), 1e-3)
+    for _ in range(min(SETTLE_MAX_CALLS, int(math.ceil(ms / t)))):
+        fn()
+
+
+def time_loop(fn, steps, warmup, settle_ms=SETTLE_MS):
+    """Average ms per call of fn() over `steps` calls after `warmup` calls
+    (preceded by `settle_ms` of untimed calls), bracketed by device
+    synchronisation and HIP events on the launch stream."""
+    settle(fn, settle_ms)
     for _ in range(warmup):
         fn()
     _sync()
@@ -113,7 +148,7 @@ def make_inputs(B, H, T, D, dtype, seed, scale_qkv):
     return host, dev
 
 
-def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup):
+def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup, cold=False):
     from minitorch_amd import _lib as L
     from minitorch_amd import device as Dv
     from minitorch_amd import kernels as K
@@ -128,6 +163,7 @@ def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup):
         K.attn_fwd(q, k, v, scale, True, out=o, lse=lse)
         K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk, dv=dv, workspace=ws)
 
+    cold_ms = time_loop(step, steps, warmup, settle_ms=0) if cold else None
     ms_step = time_loop(step, steps, warmup)
     # per-kernel averages (each phase is one kernel launch; the dQ pass also
     # computes delta = rowsum(dO*O), which the dK/dV pass reads)
@@ -137,7 +173,51 @@ def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup):
         ph[name] = time_loop(lambda m=mask: K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk,
                                                        dv=dv, workspace=ws, phases=m), steps, 2)
     _sync()
-    return dict(ms_step=ms_step, ms_fwd=ms_fwd, **{f"ms_{k}": v for k, v in ph.items()}), arrs
+    r = dict(ms_step=ms_step, ms_fwd=ms_fwd, **{f"ms_{k}": v for k, v in ph.items()})
+    if cold:
+        r["ms_step_cold"] = cold_ms
+    return r, arrs
+
+
+def c3_series(nwin=30, per=5):
+    """The C3 step's time over consecutive windows of `per` steps (HIP events
+    between the windows, no synchronisation inside a run of windows): once
+    right after the same load, and after idle gaps of 10 ms to 1 s.  Prints
+    one line per run, ms per step for each window."""
+    from minitorch_amd import _lib as L
+    from minitorch_amd import device as Dv
+    from minitorch_amd import kernels as K
+
+    B, H, T, D = 8, 16, 2048, 64
+    _, (q, k, v, do) = make_inputs(B, H, T, D, "bfloat16", 3, 0.5)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = K.attn_fwd(q, k, v, scale, True)
+    dq, dk, dv = K.attn_bwd(q, k, v, o, do, lse, scale, True)
+    ws = Dv.empty_buf((L.lib().mtx_attn_bwd_workspace_bytes(B, H, T),), "uint8")
+
+    def step():
+        K.attn_fwd(q, k, v, scale, True, out=o, lse=lse)
+        K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk, dv=dv, workspace=ws)
+
+    def run(tag):
+        evs = [_Event() for _ in range(nwin + 1)]
+        evs[0].record()
+        for w in range(nwin):
+            for _ in range(per):
+                step()
+            evs[w + 1].record()
+        _sync()
+        ms = [evs[i].elapsed_time(evs[i + 1]) / per for i in range(nwin)]
+        print(f"[series] {tag}: " + " ".join(f"{x:.3f}" for x in ms), file=sys.stderr, flush=True)
+
+    step()
+    _sync()
+    run("after setup (~1 s idle)")
+    run("right after the same load")
+    for idle in (0.01, 0.05, 0.2, 1.0):
+        time.sleep(idle)
+        run(f"after {idle * 1e3:.0f} ms idle")
+    run("right after the same load")
 
 
 def attn_bytes(B, H, T, D, esize):
@@ -437,7 +517,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=("all", "c3", "c1", "c0attn", "c4", "c4eager", "c4kernel", "gpt2", "gpt0"),
+    ap.add_argument("--only", choices=("all", "c3", "c3series", "c1", "c0attn", "c4", "c4eager", "c4kernel", "gpt2", "gpt0"),
                     default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -475,6 +555,9 @@ def main():
             ms, losses = bench_gpt(c, 2, args.steps, args.warmup, graph=graph)
             print(f"[bench] {args.only} ({'graph' if graph else 'eager'}): {ms:.3f} ms/step, "
                   f"{c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, losses {losses}", file=sys.stderr)
+        return
+    if args.only == "c3series":
+        c3_series()
         return
     if args.only == "c4eager":
         # the C4 run with every decode step launched eagerly (no HIP graph):
@@ -515,7 +598,8 @@ def main():
     B, H, T, D = 8, 16, 2048, 64
     print(f"[bench] C3 bf16 B={B} H={H} T={T} D={D}: {args.warmup} warmup + {args.steps} steps",
           file=sys.stderr, flush=True)
-    r3, arrs3 = bench_attention(B, H, T, D, "bfloat16", 3, 0.5, args.steps, args.warmup)
+    r3, arrs3 = bench_attention(B, H, T, D, "bfloat16", 3, 0.5, args.steps, args.warmup, cold=True)
+    ms_cold = r3.pop("ms_step_cold")
     f3, b3 = attn_flops(B, H, T, D)
     tflops = (f3 + b3) / (r3["ms_step"] * 1e-3) / 1e12
     # dominant kernel and its algorithmic FLOPs: fwd kernel = 2u; dK/dV pass =
@@ -527,8 +611,8 @@ def main():
     dom = max(kern, key=lambda k_: kern[k_][0])
     ms_dom, fl_dom = kern[dom]
     achieved = fl_dom / (ms_dom * 1e-3) / 1e12
-    print(f"[bench] C3 step {r3['ms_step']:.3f} ms = {tflops:.1f} TFLOP/s; phases {r3}",
-          file=sys.stderr, flush=True)
+    print(f"[bench] C3 step {r3['ms_step']:.3f} ms = {tflops:.1f} TFLOP/s (cold start {ms_cold:.3f} ms = "
+          f"{(f3 + b3) / (ms_cold * 1e-3) / 1e12:.1f}); phases {r3}", file=sys.stderr, flush=True)
     if args.only == "c3":
         return
 
@@ -601,8 +685,14 @@ def main():
                      "traffic": pmc_traffic(dom), "ms_per_launch": round(ms_dom, 4),
                      "flops_per_launch": fl_dom},
         "cpu_baseline": cpu,
+        "settle_ms": SETTLE_MS,
         "also": {
             "C3_phase_ms": {k_: round(v_, 4) for k_, v_ in r3.items()},
+            "C3_cold_start": {"ms_per_step": round(ms_cold, 4),
+                              "tflops": round((f3 + b3) / (ms_cold * 1e-3) / 1e12, 2),
+                              "note": f"{args.warmup} warm-up + {args.steps} timed steps right after the "
+                                      "inputs are uploaded (about 1 s of GPU idle), without the settling "
+                                      "period: the GPU's clock transient after idle"},
             "C1_fp32": {"tflops": round(tflops1, 3), "pct_of_fp32_peak": round(100 * tflops1 / PEAK_FP32, 2),
                         "ms_per_step": round(r1["ms_step"], 4),
                         "phase_ms": {k_: round(v_, 4) for k_, v_ in r1.items()}},
