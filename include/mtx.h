@@ -249,6 +249,26 @@ int mtx_attn_decode(int dtype, int B, int H, int L, int D,
                     float* lse, const int* lengths, float scale, void* stream);
 
 /*
+ * A decode step's q/k/v projection and its attention in one launch (fp32):
+ * for each sequence b and head h, [q | k | v] = x[b] @ W + bias restricted to
+ * head h's D columns of each third (W the packed (C, 3C) projection, row
+ * stride ldw; C = H*D; the C-long sums cut into 16 ranges, each k ascending
+ * with fused multiply-adds, added in range order, then the bias), k and v
+ * written to row lengths[b] - 1 of the caches kc / vc ((B, Tmax, C), row
+ * stride cst, sequence stride csb; skipped unless 1 <= lengths[b] <= Tmax),
+ * and o[b][hD .. hD+D) = softmax(scale q k^T) v over the first
+ * min(lengths[b], Tmax) cache rows, the new row taken from the projection.
+ * Replaces, in GPT.generate's per-token forward (transformer.py:93-104), the
+ * q/k/v projections of MultiHeadAttention.forward (transformer.py:32-34,
+ * layers.py:31-37) and its attention sub-graph (transformer.py:36-44) at the
+ * last position: the pair mtx_gemm_step_f32 + mtx_attn_decode.  D in
+ * {64, 128}, C <= 1024, 1 <= Tmax <= 2048; cache rows 16-byte aligned.
+ */
+int mtx_decode_qkv_attn_f32(int B, int H, int D, const float* x, int64_t ldx, const float* W, int64_t ldw,
+                            const float* bias, float* kc, float* vc, int64_t csb, int64_t cst, int Tmax,
+                            const int* lengths, float scale, float* o, int64_t ldo, void* stream);
+
+/*
  * Greedy pick over rows of x (rows, cols; row stride ld): idx[r * idx_stride]
  * = first index of the row maximum (np.argmax, the build's greedy harness over
  * the logits of transformer.py:97-98) and, if margin != NULL,

@@ -156,6 +156,190 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_kernel(const DecArgs 
   }
 }
 
+// ---- a decode step's q/k/v projection and attention in one launch (fp32) ----
+// One workgroup of kQaW waves per head h and group of S sequences.  It forms
+// the group's q, k and v rows of head h from the step's (normalised) input
+// rows x[b] and the packed (C, 3C) projection (each wave a range of C, the
+// wave sums added in wave order, then the bias), writes k and v to cache row
+// lengths[b] - 1, and runs the attention of mtx_attn_decode over the first
+// lengths[b] cached rows, kQaW / S waves per sequence, taking the new row from
+// LDS (the cache write is not read back).  Each weight element is loaded once
+// per group: the workgroups of a head share the 3 x C x D slab through the
+// XCD's L2, so S sequences per workgroup divide that traffic by S.
+#ifndef MTX_QA_WAVES
+#define MTX_QA_WAVES 16
+#endif
+#ifndef MTX_QA_SEQ
+#define MTX_QA_SEQ 2
+#endif
+constexpr int kQaW = MTX_QA_WAVES;
+constexpr int kQaThreads = 64 * kQaW;
+constexpr int kQaS = MTX_QA_SEQ;  // sequences per workgroup for D = 64 (D = 128: 1)
+constexpr int kQaMaxC = 1024;
+constexpr int kQaMaxT = 2048;      // scores of S sequences in dynamic LDS
+
+template <int D, int S>
+__global__ __launch_bounds__(kQaThreads) void qkv_attn_kernel(int B, int H, int C, const float* __restrict__ x,
+                                                              int64_t ldx, const float* __restrict__ W, int64_t ldw,
+                                                              const float* __restrict__ bias, float* __restrict__ kc,
+                                                              float* __restrict__ vc, int64_t csb, int64_t cst,
+                                                              int Tmax, const int* __restrict__ lengths, float scale,
+                                                              float* __restrict__ o, int64_t ldo) {
+  constexpr int NC = 3 * D;     // head h's q, k and v columns
+  constexpr int NPL = NC / 64;  // of which each lane owns NPL
+  constexpr int WS = kQaW / S;  // waves per sequence in the attention
+  constexpr int TPS = 64 * WS;
+  constexpr int DV = D / 4, NGS = TPS / DV;  // value slices, key groups per sequence
+  constexpr int GPF = kQaW * S * NC;          // wave partial sums
+  constexpr int PTF = S * NGS * D;            // key-group partial outputs
+  static_assert(kQaW % S == 0 && NPL * 64 == NC, "workgroup shape");
+  extern __shared__ float sc[];                                     // [S][Tmax] scores
+  __shared__ __attribute__((aligned(16))) float xs[S][kQaMaxC];
+  __shared__ __attribute__((aligned(16))) float buf[GPF > PTF ? GPF : PTF];  // wave sums, then key groups
+  __shared__ __attribute__((aligned(16))) float qkv[S][NC];
+  __shared__ float red[kQaW];
+
+  const int b0 = (blockIdx.x / H) * S, h = blockIdx.x % H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < S * C; i += kQaThreads) {
+    const int s = i / C, k = i % C;
+    xs[s][k] = b0 + s < B ? x[(int64_t)(b0 + s) * ldx + k] : 0.f;
+  }
+  __syncthreads();
+
+  // ---- q, k, v: wave w sums over rows [k0, k1) of the weight ----
+  int64_t col[NPL];
+#pragma unroll
+  for (int t = 0; t < NPL; ++t) {
+    const int jj = lane + 64 * t;
+    col[t] = (int64_t)(jj / D) * C + h * D + jj % D;
+  }
+  const int kcnt = (C + kQaW - 1) / kQaW;
+  const int k0 = w * kcnt, k1 = min(C, k0 + kcnt);
+  float acc[S][NPL];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int t = 0; t < NPL; ++t) acc[s][t] = 0.f;
+  constexpr int kB = 72 / NPL;  // weight rows per batch, every load issued before the products
+  for (int kb = k0; kb < k1; kb += kB) {
+    float wv[kB][NPL];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const int64_t r = min(kb + j, C - 1);
+#pragma unroll
+      for (int t = 0; t < NPL; ++t) wv[j][t] = W[r * ldw + col[t]];
+    }
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      if (kb + j < k1) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const float xv = xs[s][kb + j];
+#pragma unroll
+          for (int t = 0; t < NPL; ++t) acc[s][t] = fmaf(xv, wv[j][t], acc[s][t]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int t = 0; t < NPL; ++t) buf[(w * S + s) * NC + lane + 64 * t] = acc[s][t];
+  __syncthreads();
+  for (int i = tid; i < S * NC; i += kQaThreads) {
+    const int s = i / NC, jj = i % NC;
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < kQaW; ++q) v += buf[(q * S + s) * NC + jj];
+    const int pt = jj / D, e = jj % D;
+    if (bias) v += bias[pt * C + h * D + e];
+    qkv[s][jj] = v;
+    const int b = b0 + s;
+    if (pt > 0 && b < B) {
+      const int t = lengths[b] - 1;
+      if (t >= 0 && t < Tmax) (pt == 1 ? kc : vc)[(int64_t)b * csb + (int64_t)t * cst + h * D + e] = v;
+    }
+  }
+  __syncthreads();
+
+  // ---- attention: waves [sg*WS, sg*WS + WS) take sequence b0 + sg ----
+  const int sg = w / WS, lt = tid % TPS;
+  const int b = b0 + sg;
+  const int len = b < B ? lengths[b] : 0;
+  const int L = min(max(len, 0), Tmax);
+  const int newrow = (len >= 1 && len <= Tmax) ? len - 1 : -1;  // the row this step wrote
+  float* __restrict__ scs = sc + sg * Tmax;
+  const float* __restrict__ qv = qkv[sg];
+  // scores (log2 units): four threads per key, a quarter of D each
+  const float c = scale * kLog2e;
+  constexpr int DQ = D / 4;
+  const int kq = lt >> 2, qd = lt & 3;
+  float qr[DQ];
+#pragma unroll
+  for (int e = 0; e < DQ; ++e) qr[e] = qv[qd * DQ + e] * c;
+  const float* __restrict__ kb0 = kc + (int64_t)min(b, B - 1) * csb + h * D + qd * DQ;
+  float mx = -INFINITY;
+  for (int j = kq; j < L; j += TPS / 4) {
+    float kr[DQ];
+    if (j == newrow) {
+#pragma unroll
+      for (int e = 0; e < DQ; ++e) kr[e] = qv[D + qd * DQ + e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < DQ; e += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(kb0 + (int64_t)j * cst + e);
+        kr[e] = v[0]; kr[e + 1] = v[1]; kr[e + 2] = v[2]; kr[e + 3] = v[3];
+      }
+    }
+    float sv = 0.f;
+#pragma unroll
+    for (int e = 0; e < DQ; ++e) sv = fmaf(qr[e], kr[e], sv);
+    sv += __shfl_xor(sv, 1, 64);
+    sv += __shfl_xor(sv, 2, 64);
+    if (qd == 0) scs[j] = sv;
+    mx = fmaxf(mx, sv);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[w] = mx;
+  __syncthreads();
+  mx = red[sg * WS];
+#pragma unroll
+  for (int q = 1; q < WS; ++q) mx = fmaxf(mx, red[sg * WS + q]);
+  __syncthreads();
+  float sum = 0.f;
+  for (int j = lt; j < L; j += TPS) {
+    const float p = __builtin_amdgcn_exp2f(scs[j] - mx);
+    scs[j] = p;
+    sum += p;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[w] = sum;
+  __syncthreads();  // also publishes every p_j
+  float l = 0.f;
+#pragma unroll
+  for (int q = 0; q < WS; ++q) l += red[sg * WS + q];
+
+  // o[d] = sum_j p_j v[j][d] / l
+  const int dv = lt % DV, kg = lt / DV;
+  const float* __restrict__ vb0 = vc + (int64_t)min(b, B - 1) * csb + h * D + 4 * dv;
+  f32x4 av = zero4();
+#pragma unroll 4
+  for (int j = kg; j < L; j += NGS) {
+    const f32x4 vv = j == newrow ? *reinterpret_cast<const f32x4*>(qv + 2 * D + 4 * dv)
+                                 : *reinterpret_cast<const f32x4*>(vb0 + (int64_t)j * cst);
+    av += scs[j] * vv;
+  }
+  *reinterpret_cast<f32x4*>(buf + (sg * NGS + kg) * D + 4 * dv) = av;
+  __syncthreads();
+  if (lt < D && b < B) {
+    float r = 0.f;
+#pragma unroll 8
+    for (int g = 0; g < NGS; ++g) r += buf[(sg * NGS + g) * D + lt];
+    o[(int64_t)b * ldo + h * D + lt] = L > 0 ? r / l : 0.f;
+  }
+}
+
 // ---- greedy pick: first maximum per row and top-2 margin ----
 struct Top2 {
   float m1, m2;
@@ -459,6 +643,34 @@ int dispatch_decode(int D, const DecArgs& a, hipStream_t st) {
 }  // namespace mtx
 
 using namespace mtx;
+
+extern "C" int mtx_decode_qkv_attn_f32(int B, int H, int D, const float* x, int64_t ldx, const float* W,
+                                       int64_t ldw, const float* bias, float* kc, float* vc, int64_t csb,
+                                       int64_t cst, int Tmax, const int* lengths, float scale, float* o,
+                                       int64_t ldo, void* stream) {
+  MTX_CHECK_ARG(x && W && kc && vc && lengths && o, "decode_qkv_attn: null pointer");
+  const int64_t C = (int64_t)H * D;
+  MTX_CHECK_SHAPE(B >= 1 && H >= 1 && (D == 64 || D == 128) && C <= kQaMaxC && Tmax >= 1 && Tmax <= kQaMaxT,
+                  "decode_qkv_attn: needs D in {64, 128}, H*D <= %d and 1 <= Tmax <= %d (got H=%d D=%d Tmax=%d)",
+                  kQaMaxC, kQaMaxT, H, D, Tmax);
+  MTX_CHECK_SHAPE(ldx >= C && ldw >= 3 * C && ldo >= C && cst >= C && csb >= (int64_t)Tmax * cst,
+                  "decode_qkv_attn: bad strides");
+  MTX_CHECK_ARG(cst % 4 == 0 && csb % 4 == 0 && ((uintptr_t)kc & 15u) == 0 && ((uintptr_t)vc & 15u) == 0,
+                "decode_qkv_attn: cache rows must be 16-byte aligned");
+  MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64) {
+    const size_t lds = (size_t)kQaS * Tmax * sizeof(float);
+    hipLaunchKernelGGL((qkv_attn_kernel<64, kQaS>), dim3(((B + kQaS - 1) / kQaS) * H), dim3(kQaThreads), lds, st, B,
+                       H, (int)C, x, ldx, W, ldw, bias, kc, vc, csb, cst, Tmax, lengths, scale, o, ldo);
+  } else {
+    const size_t lds = (size_t)Tmax * sizeof(float);
+    hipLaunchKernelGGL((qkv_attn_kernel<128, 1>), dim3(B * H), dim3(kQaThreads), lds, st, B, H, (int)C, x, ldx, W,
+                       ldw, bias, kc, vc, csb, cst, Tmax, lengths, scale, o, ldo);
+  }
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
 
 extern "C" int mtx_attn_decode(int dtype, int B, int H, int L, int D,
                                const void* q, const int64_t* q_strides,

@@ -157,6 +157,43 @@ def attn_decode(q, k, v, scale: float, out=None, lse=None, lengths=None):
     return out, lse
 
 
+QKV_ATTN_MAX_C, QKV_ATTN_MAX_T = 1024, 2048
+
+
+def qkv_attn_fits(H, D, Tmax):
+    """True when mtx_decode_qkv_attn_f32 takes heads of size D, H*D columns
+    and caches of Tmax rows."""
+    return D in (64, 128) and H * D <= QKV_ATTN_MAX_C and 1 <= Tmax <= QKV_ATTN_MAX_T
+
+
+def qkv_attn_step(x, w, bias, kc, vc, lengths, n_head, scale, out):
+    """mtx_decode_qkv_attn_f32: one decode step's q/k/v projection and
+    attention in one launch.  x (B, C) the normalised input rows, w (C, 3C)
+    and bias (3C,) the packed [q | k | v] projection; this step's k and v go
+    to row lengths[b] - 1 of the caches kc / vc (B, Tmax, C), and out (B, C)
+    receives softmax(scale q k^T) v over each sequence's first lengths[b]
+    cached rows, head h in columns h*D .. h*D + D - 1."""
+    _need_cuda(x, w, kc, vc, lengths, out)
+    B, C = x.shape
+    H = int(n_head)
+    D = C // H
+    Bc, Tmax, Ck = kc.shape
+    if H * D != C or tuple(w.shape) != (C, 3 * C) or Ck != C or Bc < B or tuple(out.shape) != (B, C):
+        raise ValueError("qkv_attn_step: x (B, C), w (C, 3C), caches (>= B, T, C), out (B, C)")
+    if tuple(vc.shape) != tuple(kc.shape) or tuple(vc.stride()) != tuple(kc.stride()) or kc.stride(2) != 1:
+        raise ValueError("qkv_attn_step: k/v caches must share shape and strides, unit column stride")
+    if x.stride(1) != 1 or w.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("qkv_attn_step: x, w and out need unit column strides")
+    if bias is not None and (bias.numel() != 3 * C or not bias.is_contiguous()):
+        raise ValueError("qkv_attn_step: bias must be contiguous (3C,)")
+    if _dt(lengths) != "int32" or lengths.numel() < B or not lengths.is_contiguous():
+        raise ValueError("qkv_attn_step: lengths must be contiguous int32 with >= B entries")
+    L.call("mtx_decode_qkv_attn_f32", B, H, D, L.ptr(x), x.stride(0), L.ptr(w), w.stride(0),
+           L.ptr(bias) if bias is not None else None, L.ptr(kc), L.ptr(vc), kc.stride(0), kc.stride(1), Tmax,
+           L.ptr(lengths), float(scale), L.ptr(out), out.stride(0), L.stream_handle())
+    return out
+
+
 def argmax_rows(x, idx=None, margin=None):
     """First-maximum index of each row of a fp32 (rows, cols) device tensor
     (np.argmax) and, if `margin` is given, largest - second largest.  idx:

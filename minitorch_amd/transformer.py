@@ -120,9 +120,11 @@ class MultiHeadAttention(Module):
     def forward_step(self, x, cache, lengths, residual=None, ln=None):
         """One-token decode step whose positions live in device memory, so a
         recorded step replays unchanged: x (B, 1, C); this token's key/value
-        go to cache row lengths[b] - 1 (written by the q/k/v GEMM itself,
-        mtx_gemm_step_f32, or by mtx_kv_append_f32 past its size limits) and attention runs
-        over each sequence's first lengths[b] cached keys (mtx_attn_decode).
+        go to cache row lengths[b] - 1 and attention runs over each
+        sequence's first lengths[b] cached keys: one launch for both
+        (mtx_decode_qkv_attn_f32) within its size limits, else the q/k/v
+        GEMM writing the caches itself (mtx_gemm_step_f32, or
+        mtx_kv_append_f32 past its limits) and mtx_attn_decode.
         With `residual` (B, 1, C) the output projection is accumulated into it
         in place (the block's residual add folded into the GEMM) and it is
         returned; with `ln` as well (the LayerNorm that reads the residual
@@ -136,6 +138,14 @@ class MultiHeadAttention(Module):
         if self._qkv is None:
             self.fuse_qkv()
         kc, vc = cache
+        if K.qkv_attn_fits(H, D, kc.shape[1]):
+            # one launch: the projection of this head's q, k, v (k and v into
+            # the caches) and its attention (mtx_decode_qkv_attn_f32)
+            out = dev.empty((B, 1, C))
+            W, b = self._qkv
+            K.qkv_attn_step(x.data.t.reshape(B, C), W.data.t, b.data.t, kc.t, vc.t, lengths, H,
+                            1.0 / math.sqrt(D), out.t.view(B, C))
+            return self._project_out(out, B, C, residual, ln)
         if K.step_fits(B, C):
             # one launch: q to its buffer, k and v straight into the caches
             q = dev.empty((B, 1, C)).t
@@ -151,11 +161,15 @@ class MultiHeadAttention(Module):
         out = dev.empty((B, 1, H, D))
         K.attn_decode(heads(q), heads(kc.t), heads(vc.t), 1.0 / math.sqrt(D),
                       out=out.t.transpose(1, 2), lengths=lengths)
+        return self._project_out(out.reshape(B, 1, C), B, C, residual, ln)
+
+    def _project_out(self, out, B, C, residual, ln):
+        """The output projection of a decode step's attention rows out (B, 1, C)."""
         if residual is not None:
             if ln is not None:
-                return _linear_ln_into(Tensor(out.reshape(B, 1, C)), self.out_proj, residual, ln)
-            return _linear_into(Tensor(out.reshape(B, 1, C)), self.out_proj, residual)
-        return self.out_proj(Tensor(out.reshape(B, 1, C)))
+                return _linear_ln_into(Tensor(out), self.out_proj, residual, ln)
+            return _linear_into(Tensor(out), self.out_proj, residual)
+        return self.out_proj(Tensor(out))
 
     def fuse_qkv(self):
         """Concatenate the q/k/v projections into one (C, 3C) weight and (3C,)

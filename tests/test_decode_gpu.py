@@ -305,3 +305,72 @@ def test_head_pick_matches_product_then_pick(dev, rows, K, V):
             assert abs(mg.numpy()[L - T0, r] - marg[r]) <= 1e-4 * (1 + abs(logits[r]).max())
     np.testing.assert_array_equal(tl.numpy(), lengths + 1)
     assert int(pos.numpy()[0]) == 18
+
+
+@pytest.mark.parametrize("B,H,D,T,with_bias", [(64, 6, 64, 256, True), (5, 4, 128, 40, True),
+                                               (3, 16, 64, 17, False), (7, 8, 128, 300, True)])
+def test_qkv_attn_step_matches_projection_then_attention(dev, B, H, D, T, with_bias):
+    """mtx_decode_qkv_attn_f32: a decode step's q/k/v projection and
+    attention in one launch.  Against float64: the projection P = x @ W + b,
+    k and v rows at cache row lengths[b] - 1 (other rows untouched; lengths 0
+    and T + 1 write nothing), and softmax(scale q k^T) v over the first
+    min(lengths[b], T) rows of the updated cache (fp32 bar 1e-5 + 1e-4|ref|).
+    The same step through mtx_gemm_step_f32 + mtx_attn_decode agrees to the
+    same bar."""
+    from minitorch_amd import kernels as Kn
+
+    _say(f"[qkv_attn] B={B} H={H} D={D} T={T} bias={with_bias}")
+    rng = np.random.default_rng(1000 + B + D + T)
+    C = H * D
+    x = rng.standard_normal((B, C), dtype=np.float32)
+    w = (rng.standard_normal((C, 3 * C)) / np.sqrt(C)).astype(np.float32)
+    bias = rng.standard_normal(3 * C).astype(np.float32) if with_bias else None
+    lengths = rng.integers(1, T + 1, B).astype(np.int32)
+    lengths[0] = T
+    if B > 2:
+        lengths[1], lengths[2] = 0, T + 1
+    kc0 = rng.standard_normal((B, T, C), dtype=np.float32)
+    vc0 = rng.standard_normal((B, T, C), dtype=np.float32)
+    scale = 1.0 / np.sqrt(D)
+    tk, tv, tl = _T(kc0), _T(vc0), _T(lengths, "int32")
+    out = empty((B, C))
+    Kn.qkv_attn_step(_T(x), _T(w), _T(bias) if with_bias else None, tk, tv, tl, H, scale, out)
+
+    P = x.astype(np.float64) @ w + (bias if with_bias else 0.0)
+    tol = lambda r: 1e-5 + 1e-4 * np.abs(r)
+    kg, vg = tk.numpy(), tv.numpy()
+    kref, vref = kc0.astype(np.float64), vc0.astype(np.float64)
+    for b in range(B):
+        t = lengths[b] - 1
+        if 0 <= t < T:
+            assert np.all(np.abs(kg[b, t] - P[b, C:2 * C]) <= tol(P[b, C:2 * C])), b
+            assert np.all(np.abs(vg[b, t] - P[b, 2 * C:]) <= tol(P[b, 2 * C:])), b
+            kref[b, t], vref[b, t] = P[b, C:2 * C], P[b, 2 * C:]
+            kc0[b, t], vc0[b, t] = kg[b, t], vg[b, t]
+    assert np.array_equal(kg, kc0) and np.array_equal(vg, vc0), "rows other than lengths-1 changed"
+    ref = np.zeros((B, C))
+    for b in range(B):
+        Lb = min(max(int(lengths[b]), 0), T)
+        for h in range(H):
+            sl = slice(h * D, (h + 1) * D)
+            if Lb == 0:
+                continue
+            s = (kref[b, :Lb, sl] @ P[b, sl]) * scale
+            p = np.exp(s - s.max())
+            ref[b, sl] = (p / p.sum()) @ vref[b, :Lb, sl]
+    got = out.numpy()
+    err = np.abs(got - ref)
+    assert np.all(err <= tol(ref)), f"max err {err.max():.3e}"
+
+    # the two-launch form of the same step (where mtx_gemm_step_f32 takes it)
+    if not Kn.step_fits(B, C):
+        return
+    tk2, tv2 = _T(tk.numpy()), _T(tv.numpy())
+    q = empty((B, C))
+    Kn.gemm_step(_T(x), _T(w), bias=_T(bias) if with_bias else None, c=q, kv=(tk2, tv2, tl))
+    heads = lambda a: a.view(B, T, H, D).transpose(1, 2)
+    o2 = empty((B, 1, H, D))
+    Kn.attn_decode(q.view(B, 1, H, D).transpose(1, 2), heads(tk2), heads(tv2), scale,
+                   out=o2.transpose(1, 2), lengths=tl)
+    got2 = o2.numpy().reshape(B, C)
+    assert np.all(np.abs(got - got2) <= tol(got2)), f"vs two launches: {np.abs(got - got2).max():.3e}"
