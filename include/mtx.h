@@ -263,10 +263,21 @@ int mtx_attn_decode(int dtype, int B, int H, int L, int D,
  * layers.py:31-37) and its attention sub-graph (transformer.py:36-44) at the
  * last position: the pair mtx_gemm_step_f32 + mtx_attn_decode.  D in
  * {64, 128}, C <= 1024, 1 <= Tmax <= 2048; cache rows 16-byte aligned.
+ * Input rows: with ln_gamma NULL, x holds the normalised rows (pws, x_out
+ * NULL).  With ln_gamma set, x holds raw residual rows and the projection
+ * reads LayerNorm(r) (gamma, ln_beta, eps: the block's ln1, layers.py:82-86)
+ * where r = x[b] or, with pws, r = (sum_s pws[s][b] + pbias) + x[b]: the
+ * pending second residual add of the previous block (x + mlp(ln2(x)),
+ * transformer.py:65), pks partial products [pks][B][C] of
+ * mtx_gemm_partials_f32 summed in s order, the arithmetic of
+ * mtx_gemm_ln_f32's reduce; r is then written to x_out[b] (row stride ldxo,
+ * not overlapping x) when x_out is set.
  */
-int mtx_decode_qkv_attn_f32(int B, int H, int D, const float* x, int64_t ldx, const float* W, int64_t ldw,
-                            const float* bias, float* kc, float* vc, int64_t csb, int64_t cst, int Tmax,
-                            const int* lengths, float scale, float* o, int64_t ldo, void* stream);
+int mtx_decode_qkv_attn_f32(int B, int H, int D, const float* x, int64_t ldx, const float* pws, int pks,
+                            const float* pbias, float* x_out, int64_t ldxo, const float* ln_gamma,
+                            const float* ln_beta, float eps, const float* W, int64_t ldw, const float* bias,
+                            float* kc, float* vc, int64_t csb, int64_t cst, int Tmax, const int* lengths,
+                            float scale, float* o, int64_t ldo, void* stream);
 
 /*
  * Greedy pick over rows of x (rows, cols; row stride ld): idx[r * idx_stride]
@@ -346,10 +357,15 @@ int mtx_embedding2_ln_fwd_f32(const float* wa, int64_t lda, int64_t Va, const in
  * Replaces, in the greedy harness over transformer.py:93-104, the head
  * Linear of transformer.py:91 (layers.py:31-37) and np.argmax of the last
  * position's logits.  V <= 256, K <= 8192.
+ * With ln_gamma set, x holds raw rows: the row used is LayerNorm(r) (gamma,
+ * ln_beta, eps; K <= 1024), r = x[row] or, with pws, the pending update of
+ * mtx_decode_qkv_attn_f32, r = (sum_s pws[s][row] + pbias) + x[row] -- the
+ * last block's second residual add and ln_f (transformer.py:65, 90).
  */
-int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const float* W, int64_t ldw,
-                      const float* bias, int64_t* cur, int64_t* ids, int Tmax, float* margins, int t_base,
-                      int n_margins, int* lengths, int64_t* pos, void* stream);
+int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const float* pws, int pks,
+                      const float* pbias, const float* ln_gamma, const float* ln_beta, float eps, const float* W,
+                      int64_t ldw, const float* bias, int64_t* cur, int64_t* ids, int Tmax, float* margins,
+                      int t_base, int n_margins, int* lengths, int64_t* pos, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* GEMM                                                                     */
@@ -407,7 +423,7 @@ int mtx_gemm_act_f32(int M, int N, int K, int batch,
  * second MLP Linear, layers.py:31-37) together with the LayerNorm applied
  * to their result next (ln2, the following block's ln1, or ln_f:
  * transformer.py:63-65, 89; layers.py:82-86).  M <= 64, K <= 4096,
- * N <= 2048.  K is split into 2 to 8 ranges (enough workgroups for a
+ * N <= 2048.  K is split into 2 to 8 ranges (one for K <= 16; enough workgroups for a
  * narrow N); their partial products go to the workspace
  * (mtx_gemm_ln_workspace_bytes) and one kernel sums them in range order,
  * applies bias and residual, and normalises the rows with the arithmetic
@@ -419,6 +435,21 @@ int mtx_gemm_ln_f32(int M, int N, int K, float alpha, const float* a, int64_t sa
                     const float* b, int64_t sb_k, int64_t sb_n, float beta, float* c, int64_t sc_m,
                     const float* bias, const float* ln_gamma, const float* ln_beta, float eps, float* y,
                     int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The first half of mtx_gemm_ln_f32 alone: the K ranges' partial products
+ * P_s = A[:, range s] @ B[range s, :] (M x N each, row-major, P_s at
+ * workspace + s*M*N floats; the ranges and their count *nsplit, set on the
+ * host, are mtx_gemm_ln_f32's).  Sum_s P_s in s order equals the product that
+ * mtx_gemm_ln_f32 reduces; a later launch that reads the rows anyway adds
+ * them (mtx_decode_qkv_attn_f32, mtx_head_pick_f32), so a decode step's
+ * second MLP product (layers.py:31-37 inside TransformerBlock.forward's
+ * x + mlp(ln2(x)), transformer.py:64-65) needs no reduce launch of its own.
+ * Same limits and workspace size as mtx_gemm_ln_f32.
+ */
+int mtx_gemm_partials_f32(int M, int N, int K, const float* a, int64_t sa_m, int64_t sa_k, const float* b,
+                          int64_t sb_k, int64_t sb_n, void* workspace, size_t workspace_bytes, int* nsplit,
+                          void* stream);
 
 /*
  * Weight and bias gradients of a Linear layer in one pass over dY:

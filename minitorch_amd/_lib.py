@@ -79,9 +79,11 @@ SIGNATURES = {
     "mtx_greedy_pick_f32": (_I, [_I, _I, _P, _I64, _P, _P, _I, _P, _I, _I, _P, _P, _P]),
     "mtx_embedding2_ln_fwd_f32": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I,
                                        _P, _P, _F, _P, _I64, _P]),
-    "mtx_head_pick_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _P, _P, _P, _I, _P, _I, _I, _P, _P, _P]),
-    "mtx_decode_qkv_attn_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I, _P, _F, _P,
-                                     _I64, _P]),
+    "mtx_head_pick_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I, _P, _P, _P, _F, _P, _I64, _P, _P, _P, _I, _P, _I,
+                               _I, _P, _P, _P]),
+    "mtx_decode_qkv_attn_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I, _P, _P, _I64, _P, _P, _F, _P, _I64, _P, _P,
+                                     _P, _I64, _I64, _I, _P, _F, _P, _I64, _P]),
+    "mtx_gemm_partials_f32": (_I, [_I, _I, _I, _P, _I64, _I64, _P, _I64, _I64, _P, _SZ, _P, _P]),
     "mtx_embedding2_fwd_f32": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I, _P]),
     "mtx_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "mtx_gemm_step_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _F, _P, _I64, _P, _I, _I,

@@ -178,9 +178,62 @@ constexpr int kQaS = MTX_QA_SEQ;  // sequences per workgroup for D = 64 (D = 128
 constexpr int kQaMaxC = 1024;
 constexpr int kQaMaxT = 2048;      // scores of S sequences in dynamic LDS
 
+// A decode step's input rows given raw: r = x[b], plus, with pending partial
+// products pws (pks of them, [pks][B][C]), r = (sum_s pws[s][b] + pbias) + r,
+// the arithmetic of splitk_reduce_ln_kernel with alpha = beta = 1 (written to
+// x_out[b] when x_out is set); the kernel then reads the LayerNorm of r
+// (gamma, beta, eps; C <= 1024).
+struct PendingLn {
+  const float* pws;
+  int pks;
+  const float* pbias;
+  float* x_out;
+  int64_t ldxo;
+  const float* gamma;
+  const float* beta;
+  float eps;
+};
+
+// element n of row b of the updated residual: x[b][n] or, with pending
+// partial products, (sum_s pws[s][b][n] + pbias[n]) + x[b][n]; the pks <= 8
+// loads are independent (indices clamped, the unused ones discarded)
+__device__ __forceinline__ float pending_elem(const PendingLn& pl, const float* __restrict__ x, int64_t ldx, int B,
+                                              int C, int b, int n) {
+  const float r = x[(int64_t)b * ldx + n];
+  if (!pl.pws) return r;
+  float pv[8];
+#pragma unroll
+  for (int sp = 0; sp < 8; ++sp) pv[sp] = pl.pws[((int64_t)min(sp, pl.pks - 1) * B + b) * C + n];
+  float s = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < 8; ++sp)
+    if (sp < pl.pks) s += pv[sp];
+  float t = s + (pl.pbias ? pl.pbias[n] : 0.f);
+  t += r;
+  return t;
+}
+
+// LayerNorm of one LDS row of C <= 1024 values by one wave, in place
+__device__ __forceinline__ void ln_row_lds(float* __restrict__ row, int C, int lane, const PendingLn& pl) {
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int n = lane + 64 * i;
+    v[i] = n < C ? row[n] : 0.f;
+  }
+  float mean, sd;
+  ln_stats<16>(v, lane, C, pl.eps, mean, sd);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int n = lane + 64 * i;
+    if (n < C) row[n] = ln_apply(v[i], sd, pl.gamma[n], pl.beta[n]);
+  }
+}
+
 template <int D, int S>
 __global__ __launch_bounds__(kQaThreads) void qkv_attn_kernel(int B, int H, int C, const float* __restrict__ x,
-                                                              int64_t ldx, const float* __restrict__ W, int64_t ldw,
+                                                              int64_t ldx, const PendingLn pl,
+                                                              const float* __restrict__ W, int64_t ldw,
                                                               const float* __restrict__ bias, float* __restrict__ kc,
                                                               float* __restrict__ vc, int64_t csb, int64_t cst,
                                                               int Tmax, const int* __restrict__ lengths, float scale,
@@ -201,13 +254,10 @@ __global__ __launch_bounds__(kQaThreads) void qkv_attn_kernel(int B, int H, int 
 
   const int b0 = (blockIdx.x / H) * S, h = blockIdx.x % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int i = tid; i < S * C; i += kQaThreads) {
-    const int s = i / C, k = i % C;
-    xs[s][k] = b0 + s < B ? x[(int64_t)(b0 + s) * ldx + k] : 0.f;
-  }
-  __syncthreads();
 
-  // ---- q, k, v: wave w sums over rows [k0, k1) of the weight ----
+  // q, k, v: wave w sums over rows [k0, k1) of the weight, in batches of kB
+  // rows whose loads are all issued before their products; the first batch
+  // is requested before the input rows are read, so both latencies overlap
   int64_t col[NPL];
 #pragma unroll
   for (int t = 0; t < NPL; ++t) {
@@ -216,20 +266,48 @@ __global__ __launch_bounds__(kQaThreads) void qkv_attn_kernel(int B, int H, int 
   }
   const int kcnt = (C + kQaW - 1) / kQaW;
   const int k0 = w * kcnt, k1 = min(C, k0 + kcnt);
-  float acc[S][NPL];
-#pragma unroll
-  for (int s = 0; s < S; ++s)
-#pragma unroll
-    for (int t = 0; t < NPL; ++t) acc[s][t] = 0.f;
-  constexpr int kB = 72 / NPL;  // weight rows per batch, every load issued before the products
-  for (int kb = k0; kb < k1; kb += kB) {
-    float wv[kB][NPL];
+  constexpr int kB = (NPL >= 6 ? 60 : 72) / NPL;
+  float wv[kB][NPL];
+  auto load_batch = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < kB; ++j) {
       const int64_t r = min(kb + j, C - 1);
 #pragma unroll
       for (int t = 0; t < NPL; ++t) wv[j][t] = W[r * ldw + col[t]];
     }
+  };
+  load_batch(k0);
+
+  if (pl.gamma) {
+    // raw rows (plus pending partial products), one element per thread; the
+    // head-0 workgroup of the group writes the updated rows; then wave s
+    // normalises row s
+    for (int i = tid; i < S * C; i += kQaThreads) {
+      const int s = i / C, n = i % C;
+      float t = 0.f;
+      if (b0 + s < B) {
+        t = pending_elem(pl, x, ldx, B, C, b0 + s, n);
+        if (h == 0 && pl.x_out) pl.x_out[(int64_t)(b0 + s) * pl.ldxo + n] = t;
+      }
+      xs[s][n] = t;
+    }
+    __syncthreads();
+    if (w < S) ln_row_lds(xs[w], C, lane, pl);
+  } else {
+    for (int i = tid; i < S * C; i += kQaThreads) {
+      const int s = i / C, k = i % C;
+      xs[s][k] = b0 + s < B ? x[(int64_t)(b0 + s) * ldx + k] : 0.f;
+    }
+  }
+  __syncthreads();
+
+  float acc[S][NPL];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int t = 0; t < NPL; ++t) acc[s][t] = 0.f;
+  for (int kb = k0; kb < k1; kb += kB) {
+    if (kb != k0) load_batch(kb);
 #pragma unroll
     for (int j = 0; j < kB; ++j) {
       if (kb + j < k1) {
@@ -489,7 +567,8 @@ __device__ __forceinline__ void pick_record(int row, int rows, const Top2& t, in
 constexpr int kHpW = 16;  // waves per head_pick workgroup
 template <int VPL>
 __global__ __launch_bounds__(64 * kHpW) void head_pick_kernel(int rows, int K, int V, const float* __restrict__ x,
-                                                              int64_t ldx, const float* __restrict__ W, int64_t ldw,
+                                                              int64_t ldx, const PendingLn pl,
+                                                              const float* __restrict__ W, int64_t ldw,
                                                               const float* __restrict__ bias,
                                                               int64_t* __restrict__ cur, int64_t* __restrict__ ids,
                                                               int Tmax, float* __restrict__ margins, int t_base,
@@ -500,19 +579,14 @@ __global__ __launch_bounds__(64 * kHpW) void head_pick_kernel(int rows, int K, i
   float* part = smem + ((K + 3) & ~3);    // kHpW x 64 * VPL partial sums
   const int row = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const float* __restrict__ xr = x + (int64_t)row * ldx;
-  for (int k = tid; k < K; k += 64 * kHpW) xs[k] = xr[k];
-  __syncthreads();
+  // the weight rows of the wave's K range in batches of kHpB, every load of
+  // a batch issued before its products; the first batch is requested before
+  // the input row is read, so both latencies overlap
   const int kc = (K + kHpW - 1) / kHpW;
   const int k0 = w * kc, k1 = min(K, k0 + kc);
-  float acc[VPL];
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) acc[i] = 0.f;
-  // the weight rows of the wave's K range in batches of kHpB, every load of
-  // a batch issued before its products
-  constexpr int kHpB = 32 / VPL;
-  for (int kb = k0; kb < k1; kb += kHpB) {
-    float wv[kHpB][VPL];
+  constexpr int kHpB = VPL == 1 ? 32 : 48 / VPL;
+  float wv[kHpB][VPL];
+  auto load_batch = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < kHpB; ++j) {
       const int k = min(kb + j, K - 1);
@@ -522,6 +596,24 @@ __global__ __launch_bounds__(64 * kHpW) void head_pick_kernel(int rows, int K, i
         wv[j][i] = W[(int64_t)k * ldw + c];
       }
     }
+  };
+  load_batch(k0);
+  if (pl.gamma) {
+    // the raw row (plus pending partial products), one element per thread,
+    // normalised by wave 0
+    for (int n = tid; n < K; n += 64 * kHpW) xs[n] = pending_elem(pl, x, ldx, rows, K, row, n);
+    __syncthreads();
+    if (w == 0) ln_row_lds(xs, K, lane, pl);
+  } else {
+    const float* __restrict__ xr = x + (int64_t)row * ldx;
+    for (int k = tid; k < K; k += 64 * kHpW) xs[k] = xr[k];
+  }
+  __syncthreads();
+  float acc[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) acc[i] = 0.f;
+  for (int kb = k0; kb < k1; kb += kHpB) {
+    if (kb != k0) load_batch(kb);
 #pragma unroll
     for (int j = 0; j < kHpB; ++j) {
       if (kb + j < k1) {
@@ -644,11 +736,18 @@ int dispatch_decode(int D, const DecArgs& a, hipStream_t st) {
 
 using namespace mtx;
 
-extern "C" int mtx_decode_qkv_attn_f32(int B, int H, int D, const float* x, int64_t ldx, const float* W,
-                                       int64_t ldw, const float* bias, float* kc, float* vc, int64_t csb,
-                                       int64_t cst, int Tmax, const int* lengths, float scale, float* o,
-                                       int64_t ldo, void* stream) {
+extern "C" int mtx_decode_qkv_attn_f32(int B, int H, int D, const float* x, int64_t ldx, const float* pws, int pks,
+                                       const float* pbias, float* x_out, int64_t ldxo, const float* ln_gamma,
+                                       const float* ln_beta, float eps, const float* W, int64_t ldw,
+                                       const float* bias, float* kc, float* vc, int64_t csb, int64_t cst, int Tmax,
+                                       const int* lengths, float scale, float* o, int64_t ldo, void* stream) {
   MTX_CHECK_ARG(x && W && kc && vc && lengths && o, "decode_qkv_attn: null pointer");
+  MTX_CHECK_ARG(ln_gamma ? ln_beta != nullptr : (pws == nullptr && x_out == nullptr),
+                "decode_qkv_attn: pending partials and x_out need the LayerNorm (gamma and beta)");
+  MTX_CHECK_ARG(!pws || (pks >= 1 && pks <= 8), "decode_qkv_attn: 1 to 8 pending partial products");
+  MTX_CHECK_ARG(!x_out || (ldxo >= (int64_t)H * D && (x_out >= x + (int64_t)(B - 1) * ldx + (int64_t)H * D ||
+                                                       x >= x_out + (int64_t)(B - 1) * ldxo + (int64_t)H * D)),
+                "decode_qkv_attn: x_out must hold H*D values per row and not overlap x");
   const int64_t C = (int64_t)H * D;
   MTX_CHECK_SHAPE(B >= 1 && H >= 1 && (D == 64 || D == 128) && C <= kQaMaxC && Tmax >= 1 && Tmax <= kQaMaxT,
                   "decode_qkv_attn: needs D in {64, 128}, H*D <= %d and 1 <= Tmax <= %d (got H=%d D=%d Tmax=%d)",
@@ -658,15 +757,17 @@ extern "C" int mtx_decode_qkv_attn_f32(int B, int H, int D, const float* x, int6
   MTX_CHECK_ARG(cst % 4 == 0 && csb % 4 == 0 && ((uintptr_t)kc & 15u) == 0 && ((uintptr_t)vc & 15u) == 0,
                 "decode_qkv_attn: cache rows must be 16-byte aligned");
   MTX_CHECK_ARG(std::isfinite(scale) && scale > 0.f, "scale must be finite and > 0");
+  MTX_CHECK_ARG(std::isfinite(eps) && eps >= 0.f, "decode_qkv_attn: eps must be finite and >= 0");
+  const PendingLn pl{pws, pks, pbias, x_out, ldxo, ln_gamma, ln_beta, eps};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64) {
     const size_t lds = (size_t)kQaS * Tmax * sizeof(float);
     hipLaunchKernelGGL((qkv_attn_kernel<64, kQaS>), dim3(((B + kQaS - 1) / kQaS) * H), dim3(kQaThreads), lds, st, B,
-                       H, (int)C, x, ldx, W, ldw, bias, kc, vc, csb, cst, Tmax, lengths, scale, o, ldo);
+                       H, (int)C, x, ldx, pl, W, ldw, bias, kc, vc, csb, cst, Tmax, lengths, scale, o, ldo);
   } else {
     const size_t lds = (size_t)Tmax * sizeof(float);
-    hipLaunchKernelGGL((qkv_attn_kernel<128, 1>), dim3(B * H), dim3(kQaThreads), lds, st, B, H, (int)C, x, ldx, W,
-                       ldw, bias, kc, vc, csb, cst, Tmax, lengths, scale, o, ldo);
+    hipLaunchKernelGGL((qkv_attn_kernel<128, 1>), dim3(B * H), dim3(kQaThreads), lds, st, B, H, (int)C, x, ldx, pl,
+                       W, ldw, bias, kc, vc, csb, cst, Tmax, lengths, scale, o, ldo);
   }
   MTX_LAUNCHED();
   return MTX_OK;
@@ -739,19 +840,27 @@ extern "C" int mtx_greedy_pick_f32(int rows, int cols, const float* x, int64_t l
   return MTX_OK;
 }
 
-extern "C" int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const float* W, int64_t ldw,
-                                 const float* bias, int64_t* cur, int64_t* ids, int Tmax, float* margins,
-                                 int t_base, int n_margins, int* lengths, int64_t* pos, void* stream) {
+extern "C" int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const float* pws, int pks,
+                                 const float* pbias, const float* ln_gamma, const float* ln_beta, float eps,
+                                 const float* W, int64_t ldw, const float* bias, int64_t* cur, int64_t* ids, int Tmax,
+                                 float* margins, int t_base, int n_margins, int* lengths, int64_t* pos,
+                                 void* stream) {
   MTX_CHECK_SHAPE(rows >= 1 && K >= 1 && V >= 1 && Tmax >= 1, "rows, K, V, Tmax must be >= 1");
   MTX_CHECK_SHAPE(V <= 64 * 4 && K <= 8192, "head_pick: needs V <= 256 and K <= 8192 (got V=%d, K=%d)", V, K);
   MTX_CHECK_ARG(x && W && cur && ids && lengths, "x, W, cur, ids, lengths: null pointer");
   MTX_CHECK_ARG(ldx >= K && ldw >= V, "head_pick: bad row strides");
   MTX_CHECK_ARG(margins == nullptr || n_margins >= 1, "n_margins must be >= 1 with a margin buffer");
+  MTX_CHECK_ARG(ln_gamma ? ln_beta != nullptr : pws == nullptr,
+                "head_pick: pending partials need the LayerNorm (gamma and beta)");
+  MTX_CHECK_SHAPE(!ln_gamma || K <= 1024, "head_pick: the LayerNorm input mode needs K <= 1024 (got %d)", K);
+  MTX_CHECK_ARG(!pws || (pks >= 1 && pks <= 8), "head_pick: 1 to 8 pending partial products");
+  MTX_CHECK_ARG(std::isfinite(eps) && eps >= 0.f, "head_pick: eps must be finite and >= 0");
+  const PendingLn pl{pws, pks, pbias, nullptr, 0, ln_gamma, ln_beta, eps};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int vpl = (V + 63) / 64;
   const int vp = vpl <= 1 ? 1 : (vpl <= 2 ? 2 : 4);
   const size_t lds = ((size_t)((K + 3) & ~3) + (size_t)kHpW * 64 * vp) * sizeof(float);
-#define HP(VP) hipLaunchKernelGGL(head_pick_kernel<VP>, dim3(rows), dim3(64 * kHpW), lds, st, rows, K, V, x, ldx, W, ldw, bias, cur, ids, Tmax, margins, t_base, n_margins, lengths, pos)
+#define HP(VP) hipLaunchKernelGGL(head_pick_kernel<VP>, dim3(rows), dim3(64 * kHpW), lds, st, rows, K, V, x, ldx, pl, W, ldw, bias, cur, ids, Tmax, margins, t_base, n_margins, lengths, pos)
   if (vpl <= 1) HP(1);
   else if (vpl <= 2) HP(2);
   else HP(4);

@@ -76,6 +76,9 @@ struct GemmArgs {
   // C partials, [split][N], and the reduce adds them in split order
   float* colsum;
   int colsum_acc;
+  // skinny kernel: write the partial product to ws even when K is not split
+  // (the split-K entry points of one range, K <= 16)
+  int to_ws;
 };
 
 // the value stored at C[m][n] of batch b from the product's value v
@@ -499,7 +502,7 @@ __global__ __launch_bounds__(kSkT) void gemm_skinny_kernel(const GemmArgs g) {
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < kSkW; ++w) v += red[w][e];
-    if (row < g.M && col < g.N && g.ksplit > 1) {
+    if (row < g.M && col < g.N && (g.ksplit > 1 || g.to_ws)) {
       g.ws[((int64_t)split * g.batch + bidx) * g.M * g.N + (int64_t)row * g.N + col] = v;
     } else if (row < g.M && col < g.N) {
       float o = g.alpha * v + (g.bias ? g.bias[col] : 0.f);
@@ -640,6 +643,7 @@ void launch_reduce_ln(const GemmArgs& g, const float* gamma, const float* beta_l
   const dim3 grid(g.M), block(64);
 #define RLN(KS) hipLaunchKernelGGL((splitk_reduce_ln_kernel<VPL, KS>), grid, block, 0, st, g, gamma, beta_ln, eps, y, ldy)
   switch (g.ksplit) {
+    case 1: RLN(1); break;
     case 2: RLN(2); break;
     case 3: RLN(3); break;
     case 4: RLN(4); break;
@@ -832,6 +836,27 @@ extern "C" int mtx_gemm_f32(int M, int N, int K, int batch,
 // workgroups a mtx_gemm_ln_f32 product aims at (by splitting K)
 constexpr int kLnWgs = 144;
 
+// The split-K product of mtx_gemm_ln_f32 / mtx_gemm_partials_f32: K cut into
+// 2..8 ranges of whole 16-wide slices, as many as bring the launch to about
+// kLnWgs workgroups (a projection to N = 384 has only 24 column tiles;
+// measured at C4: 96 workgroups 0.327, 144 0.315, 192 0.313-0.317 ms per
+// token step against 0.340 with mtx_gemm_f32's ranges); range s's partial
+// product A[:, range] @ B[range, :] goes to g.ws + s*M*N.  Sets g.ksplit and
+// g.kchunk.
+void launch_ln_partials(GemmArgs& g, hipStream_t st) {
+  const int want = std::min(kSkMaxSplit, std::max({2, skinny_splits(g.M, g.K), cdiv(kLnWgs, cdiv(g.N, 16))}));
+  g.kchunk = cdiv(cdiv(g.K, want), 16) * 16;
+  g.ksplit = cdiv(g.K, g.kchunk);
+  g.nc = g.N;
+  g.to_ws = 1;
+  const bool av = k_vec(g.a, g.sam, g.sak, 0, g.K), bv = k_vec(g.b, g.sbn, g.sbk, 0, g.K);
+  const dim3 grid(cdiv(g.N, 16), 1, g.ksplit);
+  if (av && bv) hipLaunchKernelGGL((gemm_skinny_kernel<true, true>), grid, dim3(kSkT), 0, st, g);
+  else if (av) hipLaunchKernelGGL((gemm_skinny_kernel<true, false>), grid, dim3(kSkT), 0, st, g);
+  else if (bv) hipLaunchKernelGGL((gemm_skinny_kernel<false, true>), grid, dim3(kSkT), 0, st, g);
+  else hipLaunchKernelGGL((gemm_skinny_kernel<false, false>), grid, dim3(kSkT), 0, st, g);
+}
+
 extern "C" size_t mtx_gemm_ln_workspace_bytes(int M, int N, int K) {
   if (M < 1 || N < 1 || K < 1 || skinny_splits(M, K) == 0) return 0;
   return (size_t)kSkMaxSplit * M * N * sizeof(float);
@@ -854,24 +879,10 @@ extern "C" int mtx_gemm_ln_f32(int M, int N, int K, float alpha, const float* a,
   const size_t need = mtx_gemm_ln_workspace_bytes(M, N, K);
   MTX_CHECK_ARG(workspace && workspace_bytes >= need, "gemm_ln: workspace too small (%zu < %zu)", workspace_bytes,
                 need);
-  // K is split into 2..8 ranges of whole 16-wide slices, as many as bring the
-  // launch to about kLnWgs workgroups (a projection to N = 384 has only 24
-  // column tiles; measured at C4: 96 workgroups 0.327, 144 0.315, 192
-  // 0.313-0.317 ms per token step against 0.340 with mtx_gemm_f32's ranges);
-  // each range's partial product goes to the workspace
-  const int want = std::min(kSkMaxSplit, std::max({2, skinny_splits(M, K), cdiv(kLnWgs, cdiv(N, 16))}));
-  const int kchunk = cdiv(cdiv(K, want), 16) * 16;
-  const int sp = cdiv(K, kchunk);
-  GemmArgs g{a, sa_m, sa_k, 0, b, sb_k, sb_n, 0, c, sc_m, 1, 0, bias,
-             static_cast<float*>(workspace), M, N, K, 1, sp, kchunk, alpha, beta};
-  g.nc = N;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool av = k_vec(a, sa_m, sa_k, 0, K), bv = k_vec(b, sb_n, sb_k, 0, K);
-  const dim3 grid(cdiv(N, 16), 1, sp);
-  if (av && bv) hipLaunchKernelGGL((gemm_skinny_kernel<true, true>), grid, dim3(kSkT), 0, st, g);
-  else if (av) hipLaunchKernelGGL((gemm_skinny_kernel<true, false>), grid, dim3(kSkT), 0, st, g);
-  else if (bv) hipLaunchKernelGGL((gemm_skinny_kernel<false, true>), grid, dim3(kSkT), 0, st, g);
-  else hipLaunchKernelGGL((gemm_skinny_kernel<false, false>), grid, dim3(kSkT), 0, st, g);
+  GemmArgs g{a, sa_m, sa_k, 0, b, sb_k, sb_n, 0, c, sc_m, 1, 0, bias,
+             static_cast<float*>(workspace), M, N, K, 1, 0, 0, alpha, beta};
+  launch_ln_partials(g, st);
   MTX_LAUNCHED();
   const int vpl = cdiv(N, 64);
   if (vpl <= 1) launch_reduce_ln<1>(g, ln_gamma, ln_beta, eps, y, ldy, st);
@@ -883,6 +894,27 @@ extern "C" int mtx_gemm_ln_f32(int M, int N, int K, float alpha, const float* a,
   else if (vpl <= 16) launch_reduce_ln<16>(g, ln_gamma, ln_beta, eps, y, ldy, st);
   else launch_reduce_ln<32>(g, ln_gamma, ln_beta, eps, y, ldy, st);
   MTX_LAUNCHED();
+  return MTX_OK;
+}
+
+extern "C" int mtx_gemm_partials_f32(int M, int N, int K, const float* a, int64_t sa_m, int64_t sa_k,
+                                     const float* b, int64_t sb_k, int64_t sb_n, void* workspace,
+                                     size_t workspace_bytes, int* nsplit, void* stream) {
+  MTX_CHECK_SHAPE(M >= 1 && N >= 1 && K >= 1, "gemm_partials: sizes must be >= 1");
+  MTX_CHECK_SHAPE(M <= kSkMaxM && K <= kSkMaxK * kSkMaxSplit && N <= 64 * 32,
+                  "gemm_partials: needs M <= %d, K <= %d and N <= 2048 (got M=%d, N=%d, K=%d)", kSkMaxM,
+                  kSkMaxK * kSkMaxSplit, M, N, K);
+  MTX_CHECK_ARG(a && b && nsplit, "gemm_partials: null pointer");
+  MTX_CHECK_ARG(sa_k == 1 || sa_m == 1, "gemm_partials: A needs a unit stride along m or k");
+  MTX_CHECK_ARG(sb_n == 1 || sb_k == 1, "gemm_partials: B needs a unit stride along k or n");
+  const size_t need = mtx_gemm_ln_workspace_bytes(M, N, K);
+  MTX_CHECK_ARG(workspace && workspace_bytes >= need, "gemm_partials: workspace too small (%zu < %zu)",
+                workspace_bytes, need);
+  GemmArgs g{a, sa_m, sa_k, 0, b, sb_k, sb_n, 0, nullptr, N, 1, 0, nullptr,
+             static_cast<float*>(workspace), M, N, K, 1, 0, 0, 1.f, 0.f};
+  launch_ln_partials(g, static_cast<hipStream_t>(stream));
+  MTX_LAUNCHED();
+  *nsplit = g.ksplit;
   return MTX_OK;
 }
 

@@ -166,13 +166,60 @@ def qkv_attn_fits(H, D, Tmax):
     return D in (64, 128) and H * D <= QKV_ATTN_MAX_C and 1 <= Tmax <= QKV_ATTN_MAX_T
 
 
-def qkv_attn_step(x, w, bias, kc, vc, lengths, n_head, scale, out):
+def _pending_args(pending, ln, rows, C):
+    """ctypes arguments (pws, pks, pbias) and (gamma, beta, eps) of the
+    pending-update input mode of mtx_decode_qkv_attn_f32 / mtx_head_pick_f32."""
+    if ln is None:
+        if pending is not None:
+            raise ValueError("pending partial products need the LayerNorm (ln)")
+        return (None, 0, None), (None, None, 0.0)
+    gamma, beta, eps = ln
+    if gamma.numel() != C or beta.numel() != C or not (gamma.is_contiguous() and beta.is_contiguous()):
+        raise ValueError(f"ln: gamma and beta must be contiguous with {C} elements")
+    if C > 1024:
+        raise ValueError("the LayerNorm input mode needs rows of at most 1024 values")
+    lnargs = (L.ptr(gamma), L.ptr(beta), float(eps))
+    if pending is None:
+        return (None, 0, None), lnargs
+    ws, ks, pbias = pending
+    if not 1 <= int(ks) <= 8 or ws.numel() * ws.element_size() < int(ks) * rows * C * 4:
+        raise ValueError("pending: 1 to 8 partial products of (rows, C) fp32")
+    if pbias is not None and (pbias.numel() != C or not pbias.is_contiguous()):
+        raise ValueError(f"pending: bias must be contiguous with {C} elements")
+    return (L.ptr(ws), int(ks), L.ptr(pbias) if pbias is not None else None), lnargs
+
+
+def gemm_partials(a, b, ws=None):
+    """mtx_gemm_partials_f32: the K ranges' partial products of a (M, K) @
+    b (K, N) into ws ([ks][M][N] fp32; allocated when None).  Returns
+    (ws, ks).  Summed in range order they are mtx_gemm_ln_f32's product."""
+    import ctypes
+
+    M, Kd = a.shape[-2], a.shape[-1]
+    N = b.shape[-1]
+    if _dt(a) != "float32" or _dt(b) != "float32" or b.shape[-2] != Kd:
+        raise ValueError("gemm_partials: fp32 a (M, K) and b (K, N)")
+    nbytes = L.lib().mtx_gemm_ln_workspace_bytes(M, N, Kd)
+    if ws is None:
+        ws = dev.empty_buf((nbytes // 4,), "float32")
+    ks = ctypes.c_int(0)
+    L.call("mtx_gemm_partials_f32", int(M), int(N), int(Kd), L.ptr(a), int(a.stride(-2)), int(a.stride(-1)),
+           L.ptr(b), int(b.stride(-2)), int(b.stride(-1)), L.ptr(ws), ws.numel() * ws.element_size(),
+           ctypes.byref(ks), L.stream_handle())
+    return ws, ks.value
+
+
+def qkv_attn_step(x, w, bias, kc, vc, lengths, n_head, scale, out, pending=None, x_out=None, ln=None):
     """mtx_decode_qkv_attn_f32: one decode step's q/k/v projection and
-    attention in one launch.  x (B, C) the normalised input rows, w (C, 3C)
-    and bias (3C,) the packed [q | k | v] projection; this step's k and v go
-    to row lengths[b] - 1 of the caches kc / vc (B, Tmax, C), and out (B, C)
+    attention in one launch.  x (B, C) the input rows, w (C, 3C) and bias
+    (3C,) the packed [q | k | v] projection; this step's k and v go to row
+    lengths[b] - 1 of the caches kc / vc (B, Tmax, C), and out (B, C)
     receives softmax(scale q k^T) v over each sequence's first lengths[b]
-    cached rows, head h in columns h*D .. h*D + D - 1."""
+    cached rows, head h in columns h*D .. h*D + D - 1.  Without ln the rows
+    of x are the normalised input; with ln = (gamma, beta, eps) they are raw
+    residual rows r (plus, with pending = (ws, ks, bias), the previous
+    block's pending update r = (sum of the ks partial products + bias) + x,
+    written to x_out) and the projection reads LayerNorm(r)."""
     _need_cuda(x, w, kc, vc, lengths, out)
     B, C = x.shape
     H = int(n_head)
@@ -188,9 +235,14 @@ def qkv_attn_step(x, w, bias, kc, vc, lengths, n_head, scale, out):
         raise ValueError("qkv_attn_step: bias must be contiguous (3C,)")
     if _dt(lengths) != "int32" or lengths.numel() < B or not lengths.is_contiguous():
         raise ValueError("qkv_attn_step: lengths must be contiguous int32 with >= B entries")
-    L.call("mtx_decode_qkv_attn_f32", B, H, D, L.ptr(x), x.stride(0), L.ptr(w), w.stride(0),
-           L.ptr(bias) if bias is not None else None, L.ptr(kc), L.ptr(vc), kc.stride(0), kc.stride(1), Tmax,
-           L.ptr(lengths), float(scale), L.ptr(out), out.stride(0), L.stream_handle())
+    pargs, lnargs = _pending_args(pending, ln, B, C)
+    if x_out is not None and (ln is None or tuple(x_out.shape) != (B, C) or x_out.stride(1) != 1):
+        raise ValueError("qkv_attn_step: x_out (B, C) with a unit column stride, with ln")
+    L.call("mtx_decode_qkv_attn_f32", B, H, D, L.ptr(x), x.stride(0), *pargs,
+           L.ptr(x_out) if x_out is not None else None, x_out.stride(0) if x_out is not None else 0, *lnargs,
+           L.ptr(w), w.stride(0), L.ptr(bias) if bias is not None else None, L.ptr(kc), L.ptr(vc),
+           kc.stride(0), kc.stride(1), Tmax, L.ptr(lengths), float(scale), L.ptr(out), out.stride(0),
+           L.stream_handle())
     return out
 
 
@@ -584,10 +636,12 @@ def embedding2_ln_fwd(wa, ia, wb, ib, out, gamma, beta, eps, y, ib_stride=1):
     return y
 
 
-def head_pick(x, w, bias, cur, ids, lengths, pos=None, margins=None, t_base=0):
+def head_pick(x, w, bias, cur, ids, lengths, pos=None, margins=None, t_base=0, pending=None, ln=None):
     """mtx_head_pick_f32: logits = x @ w + bias per row of x (rows, K), w
     (K, V), then the pick of greedy_pick on them (cur, ids, margins,
-    lengths, pos) in one launch."""
+    lengths, pos) in one launch.  With ln = (gamma, beta, eps) the rows are
+    raw (plus pending = (ws, ks, bias) as in qkv_attn_step) and the product
+    reads their LayerNorm."""
     _need_cuda(x, w, cur, ids, lengths)
     rows, Kd = x.shape
     V = w.shape[1]
@@ -606,7 +660,8 @@ def head_pick(x, w, bias, cur, ids, lengths, pos=None, margins=None, t_base=0):
     if margins is not None and (_dt(margins) != "float32" or margins.dim() != 2 or margins.shape[1] != rows
                                 or not margins.is_contiguous()):
         raise ValueError("head_pick: margins must be contiguous fp32 (n, rows)")
-    L.call("mtx_head_pick_f32", rows, Kd, V, L.ptr(x), x.stride(0), L.ptr(w), w.stride(0),
+    pargs, lnargs = _pending_args(pending, ln, rows, Kd)
+    L.call("mtx_head_pick_f32", rows, Kd, V, L.ptr(x), x.stride(0), *pargs, *lnargs, L.ptr(w), w.stride(0),
            L.ptr(bias) if bias is not None else None, L.ptr(cur), L.ptr(ids), ids.shape[0],
            L.ptr(margins) if margins is not None else None, int(t_base),
            margins.shape[0] if margins is not None else 0, L.ptr(lengths),

@@ -19,6 +19,12 @@ from .module import Module, Sequential
 from .tensor import Tensor, no_grad
 
 
+# decode steps leave each block's second residual add to the next launch that
+# reads the rows (TransformerBlock.forward_step_deferred) where the size
+# limits allow; False keeps one reduce launch per block (forward_step)
+_DEFERRED_STEP = True
+
+
 def _linear_into(x, lin, out):
     """out += x @ W + b, in place (inference only: no graph node)."""
     from .linalg import bmm
@@ -250,6 +256,54 @@ class TransformerBlock(Module):
         return _linear_ln_into(h, fc2, x, next_ln)
 
 
+    def deferred_step_fits(self, B, Tmax):
+        """Whether forward_step_deferred takes B sequences with caches of Tmax
+        rows (the size limits of its four launches)."""
+        from . import kernels as K
+
+        fc1, act, fc2, drop = self.mlp.layers
+        C = self.ln1.gamma.shape[0]
+        H = self.attn.n_head
+        hid = fc1.weight.shape[1]
+        return (isinstance(act, GELU) and not (drop._training and drop.p > 0.0)
+                and K.qkv_attn_fits(H, C // H, Tmax) and C <= 1024
+                and K.gemm_ln_fits(B, C, C) and K.step_fits(B, C) and K.gemm_ln_fits(B, hid, C))
+
+    def forward_step_deferred(self, X, xi, pending, cache, lengths):
+        """Decode step with the block's second residual add left pending: X is
+        a pair of (B, 1, C) residual buffers, X[xi] the current one.  With
+        pending = (partial products, count, bias) of the previous block's
+        second MLP product, the q/k/v + attention launch adds them to X[xi]
+        into X[1 - xi] (mtx_decode_qkv_attn_f32, which also applies ln1);
+        out_proj adds its result into that buffer and applies ln2
+        (mtx_gemm_ln_f32); fc1 with GELU (mtx_gemm_step_f32); fc2 only
+        writes its partial products (mtx_gemm_partials_f32).  Returns the
+        index of the buffer that now holds x and this block's pending update
+        (the next block's launch, or the head's, adds it)."""
+        from . import kernels as K
+
+        fc1, act, fc2, drop = self.mlp.layers
+        attn = self.attn
+        if attn._qkv is None:
+            attn.fuse_qkv()
+        B, _, C = X[xi].shape
+        H = attn.n_head
+        kc, vc = cache
+        cur = xi if pending is None else 1 - xi
+        out = dev.empty((B, 1, C))
+        W, b = attn._qkv
+        K.qkv_attn_step(X[xi].t.view(B, C), W.data.t, b.data.t, kc.t, vc.t, lengths, H,
+                        1.0 / math.sqrt(C // H), out.t.view(B, C), pending=pending,
+                        x_out=X[cur].t.view(B, C) if pending is not None else None,
+                        ln=(self.ln1.gamma.data.t, self.ln1.beta.data.t, float(np.float32(self.ln1.eps))))
+        _, h_in = _linear_ln_into(Tensor(out), attn.out_proj, Tensor(X[cur]), self.ln2)
+        h = dev.empty((B, 1, fc1.weight.shape[1]))
+        K.gemm_step(h_in.data.t.reshape(B, C), fc1.weight.data.t, bias=fc1.bias.data.t, c=h.t.view(B, -1),
+                    act=K.ACT_GELU)
+        ws, ks = K.gemm_partials(h.t.view(B, -1), fc2.weight.data.t)
+        return cur, (ws, ks, fc2.bias.data.t)
+
+
 class GPT(Module):
     def __init__(self, vocab_size, block_size, n_embd=64, n_head=4, n_layer=2, dropout=0.0):
         super().__init__()
@@ -346,8 +400,29 @@ class GPT(Module):
 
                 ln0 = self.blocks[0].ln1
                 xn = dev.empty((B, 1, C))
+                X = (x, dev.empty((B, 1, C)))
+                V = self.lm_head.weight.shape[1]
+                deferred = (_DEFERRED_STEP and C <= 1024 and V <= 256
+                            and all(blk.deferred_step_fits(B, Tmax) for blk in self.blocks))
+
+                def step_deferred():
+                    # the token + position embeddings; each block's q/k/v +
+                    # attention launch applies the previous block's pending
+                    # second residual add and its own ln1, and the head launch
+                    # the last block's and ln_f (mtx_head_pick_f32)
+                    K.embedding2_fwd(self.tok_emb.weight.data.t, cur, self.pos_emb.weight.data.t, posd,
+                                     x.t.view(B, C), ib_stride=0)
+                    xi, pending = 0, None
+                    for block, cache in zip(self.blocks, caches):
+                        xi, pending = block.forward_step_deferred(X, xi, pending, cache, lengths)
+                    lnf = self.ln_f
+                    K.head_pick(X[xi].t.view(B, C), self.lm_head.weight.data.t, self.lm_head.bias.data.t, cur,
+                                ids.t, lengths, posd, margins.t, t_base=T0, pending=pending,
+                                ln=(lnf.gamma.data.t, lnf.beta.data.t, float(np.float32(lnf.eps))))
 
                 def step():
+                    if deferred:
+                        return step_deferred()
                     # embeddings of this token and position and the first
                     # block's ln1 in one launch (mtx_embedding2_ln_fwd_f32)
                     K.embedding2_ln_fwd(self.tok_emb.weight.data.t, cur, self.pos_emb.weight.data.t, posd,

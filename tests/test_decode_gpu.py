@@ -374,3 +374,75 @@ def test_qkv_attn_step_matches_projection_then_attention(dev, B, H, D, T, with_b
                    out=o2.transpose(1, 2), lengths=tl)
     got2 = o2.numpy().reshape(B, C)
     assert np.all(np.abs(got - got2) <= tol(got2)), f"vs two launches: {np.abs(got - got2).max():.3e}"
+
+
+@pytest.mark.parametrize("B,H,D,Khid,T", [(64, 6, 64, 1536, 64), (5, 2, 128, 300, 20), (3, 3, 64, 16, 9)])
+def test_pending_update_modes_match_reduce_ln(dev, B, H, D, Khid, T):
+    """The deferred second residual add of a decode step: the partial
+    products of mtx_gemm_partials_f32, summed with bias and residual inside
+    mtx_decode_qkv_attn_f32 (rows written to x_out) and mtx_head_pick_f32,
+    then normalised there, give bit for bit what mtx_gemm_ln_f32 (reduce +
+    LayerNorm launch) and the normalised-input forms of the two entry points
+    give on the same inputs; the partials summed in order on the host match
+    float64 within the fp32 dot bound."""
+    from minitorch_amd import kernels as Kn
+
+    _say(f"[pending] B={B} H={H} D={D} K={Khid} T={T}")
+    rng = np.random.default_rng(5000 + B + Khid)
+    C = H * D
+    hmid = rng.standard_normal((B, Khid), dtype=np.float32)
+    w2 = (rng.standard_normal((Khid, C)) / np.sqrt(Khid)).astype(np.float32)
+    b2 = rng.standard_normal(C, dtype=np.float32)
+    x0 = rng.standard_normal((B, C), dtype=np.float32)
+    gam = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    bet = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    eps = float(np.float32(1e-5))
+    ws, ks = Kn.gemm_partials(_T(hmid), _T(w2))
+    parts = ws.numpy()[:ks * B * C].reshape(ks, B, C)
+    ref = hmid.astype(np.float64) @ w2
+    assert np.abs(parts.sum(0) - ref).max() <= 1e-5 * np.sqrt(Khid) * (1 + np.abs(ref).max())
+    # reference: the reduce + LayerNorm launch on the same product
+    xr, yr = _T(x0), empty((B, C))
+    Kn.gemm_ln(_T(hmid), _T(w2), xr, _T(gam), _T(bet), eps, yr, bias=_T(b2))
+
+    wq = (rng.standard_normal((C, 3 * C)) / np.sqrt(C)).astype(np.float32)
+    bq = rng.standard_normal(3 * C, dtype=np.float32)
+    lengths = rng.integers(1, T + 1, B).astype(np.int32)
+    kc0 = rng.standard_normal((B, T, C), dtype=np.float32)
+    vc0 = rng.standard_normal((B, T, C), dtype=np.float32)
+    tl = _T(lengths, "int32")
+    scale = 1.0 / np.sqrt(D)
+    lnp = (_T(gam), _T(bet), eps)
+    # pending mode
+    tk1, tv1, o1, xo = _T(kc0), _T(vc0), empty((B, C)), empty((B, C))
+    Kn.qkv_attn_step(_T(x0), _T(wq), _T(bq), tk1, tv1, tl, H, scale, o1, pending=(ws, ks, _T(b2)), x_out=xo, ln=lnp)
+    # normalised-input mode on gemm_ln's y
+    tk2, tv2, o2 = _T(kc0), _T(vc0), empty((B, C))
+    Kn.qkv_attn_step(yr, _T(wq), _T(bq), tk2, tv2, tl, H, scale, o2)
+    np.testing.assert_array_equal(xo.numpy(), xr.numpy())
+    np.testing.assert_array_equal(o1.numpy(), o2.numpy())
+    np.testing.assert_array_equal(tk1.numpy(), tk2.numpy())
+    np.testing.assert_array_equal(tv1.numpy(), tv2.numpy())
+    # raw-row mode without pending partials: LayerNorm of x itself
+    o3 = empty((B, C))
+    Kn.qkv_attn_step(xr, _T(wq), _T(bq), _T(kc0), _T(vc0), tl, H, scale, o3, ln=lnp)
+    np.testing.assert_array_equal(o3.numpy(), o2.numpy())
+
+    # the head with the pick
+    V = 65
+    wh = (rng.standard_normal((C, V)) / np.sqrt(C)).astype(np.float32)
+    bh = rng.standard_normal(V, dtype=np.float32)
+    Tm = 40
+    res = []
+    for mode in ("pending", "normalised"):
+        cur = _T(np.zeros(B, np.int64), "int64")
+        ids = _T(np.zeros((Tm, B), np.int64), "int64")
+        mg = _T(np.zeros((Tm, B), np.float32))
+        tl2 = _T(np.full(B, 5, np.int32), "int32")
+        if mode == "pending":
+            Kn.head_pick(_T(x0), _T(wh), _T(bh), cur, ids, tl2, None, mg, pending=(ws, ks, _T(b2)), ln=lnp)
+        else:
+            Kn.head_pick(yr, _T(wh), _T(bh), cur, ids, tl2, None, mg)
+        res.append((cur.numpy(), ids.numpy(), mg.numpy()))
+    for a, b in zip(*res):
+        np.testing.assert_array_equal(a, b)

@@ -225,6 +225,31 @@ def test_greedy_graph_replay_matches_eager(dev):
     np.testing.assert_array_equal(m_graph, m_eager)
 
 
+@pytest.mark.parametrize("n_embd,n_head,n_layer,B", [(192, 3, 3, 5), (384, 6, 2, 64), (128, 1, 2, 3)])
+def test_greedy_deferred_residual_matches_per_block_reduce(dev, monkeypatch, n_embd, n_head, n_layer, B):
+    """Decode steps that leave each block's second residual add pending for
+    the next launch (mtx_gemm_partials_f32, then mtx_decode_qkv_attn_f32 or
+    mtx_head_pick_f32 sum the partial products, add bias and residual and
+    apply the LayerNorm) give bit-identical tokens and margins to steps that
+    finish every block with its own reduce + LayerNorm launch
+    (mtx_gemm_ln_f32): the same sums in the same order."""
+    import minitorch_amd.transformer as tr
+    from oracle.gpt import GPTConfig, init_params
+
+    _say(f"[gpt] greedy: deferred residual add vs per-block reduce, C={n_embd} H={n_head} L={n_layer} B={B}")
+    cfg = GPTConfig(vocab=65, block=64, n_embd=n_embd, n_head=n_head, n_layer=n_layer)
+    P = init_params(cfg, np.random.default_rng(35 + n_embd))
+    prompts = np.random.default_rng(36).integers(0, cfg.vocab, (B, 20))
+    model = gpu_gpt(cfg, P)
+    model.eval()
+    assert all(blk.deferred_step_fits(B, 20 + 30) for blk in model.blocks)
+    t_def, m_def = model.generate_greedy(prompts, 30, return_margins=True)
+    monkeypatch.setattr(tr, "_DEFERRED_STEP", False)
+    t_blk, m_blk = model.generate_greedy(prompts, 30, return_margins=True)
+    np.testing.assert_array_equal(t_def, t_blk)
+    np.testing.assert_array_equal(m_def, m_blk)
+
+
 def test_c4_greedy_full_config(dev):
     """Config C4 at full size: 64 prompts x 32 tokens, +224 greedy tokens with
     the C2 model, tokens identical to the oracle's (fixture
