@@ -6,7 +6,8 @@
 // closures of those nodes (tensor.py:210-218, 152-156, 115-119;
 // functional.py:69-73).
 //
-// Design (all kernels: 256 threads = 4 wave64s, 16x16 MFMA tiles):
+// Design (256-thread workgroups = 4 wave64s, 16x16 MFMA tiles; the bf16
+// dK/dV pass takes MTX_DKDV_WAVES waves):
 //  * "Transposed" products.  The forward and the dQ pass compute S^T = K Q^T, so
 //    a lane's accumulator column is one query: lane l owns query l%16 and keys
 //    4*(l/16)+r of each 16-key sub-tile.  Row max / row sum then need only two
@@ -17,10 +18,12 @@
 //    dK/dV for the workgroup's key block in registers over all query tiles.
 //  * dQ is a separate query-outer pass (recomputes S and dP) instead of fp32
 //    atomics: deterministic, and no dQ workspace traffic.
-//  * K/V (or Q/dO) tiles are staged through LDS row-major (global -> registers
-//    -> LDS, double-buffered, one barrier per tile); operands that need the
-//    transposed tile are read with gfx950's transposing LDS load
-//    (ds_read_b64_tr_b16), so each tile is stored once.
+//  * K/V (or Q/dO) tiles are staged through LDS row-major, double-buffered,
+//    one barrier per tile: bf16 tiles by direct global -> LDS loads (16 bytes
+//    per lane, XOR-permuted 16-byte chunks), fp32 tiles through registers into
+//    padded rows; operands that need the transposed tile are read with
+//    gfx950's transposing LDS load (ds_read_b64_tr_b16), so each tile is
+//    stored once.
 //  * Causal: tiles above the diagonal are skipped at workgroup and wave level;
 //    only diagonal tiles pay for the per-element mask.  Blocks are issued
 //    longest-first and all blocks of one (b,h) go to one XCD (workgroup ids are
@@ -31,16 +34,14 @@
 #include <mutex>
 #include <type_traits>
 
-// 1: the dK/dV tile body is instantiated twice (masked diagonal tiles,
-// unmasked interior tiles); 0: one body with a run-time mask test
-// waves per SIMD the dQ kernel is compiled for (bf16, D <= 64; fp32 D = 128:
-// 1, for its accumulators; others 2)
 // fp32, D <= 64: one tile buffer (staged through registers, two barriers
 // per tile) halves the LDS per workgroup (35 KB), so twice as many
 // workgroups share a CU; measured 9% faster than two buffers at C1
 #ifndef MTX_F32_NBUF1
 #define MTX_F32_NBUF1 1
 #endif
+// waves per SIMD the dQ kernel is compiled for (bf16, D <= 64; fp32 D = 128:
+// 1, for its accumulators; others 2)
 #ifndef MTX_DQ_WAVES
 #define MTX_DQ_WAVES 3
 #endif
@@ -49,6 +50,8 @@
 #ifndef MTX_FWD_WAVES
 #define MTX_FWD_WAVES 4
 #endif
+// 1: the dK/dV tile body is instantiated twice (masked diagonal tiles,
+// unmasked interior tiles); 0: one body with a run-time mask test
 #ifndef MTX_DKDV_SPLIT
 #define MTX_DKDV_SPLIT 1
 #endif
