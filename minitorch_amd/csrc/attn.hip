@@ -18,10 +18,11 @@
 //    dK/dV for the workgroup's key block in registers over all query tiles.
 //  * dQ is a separate query-outer pass (recomputes S and dP) instead of fp32
 //    atomics: deterministic, and no dQ workspace traffic.
-//  * K/V (or Q/dO) tiles are staged through LDS row-major, double-buffered,
-//    one barrier per tile: bf16 tiles by direct global -> LDS loads (16 bytes
-//    per lane, XOR-permuted 16-byte chunks), fp32 tiles through registers into
-//    padded rows; operands that need the transposed tile are read with
+//  * K/V (or Q/dO) tiles are staged through LDS row-major: bf16 tiles by
+//    direct global -> LDS loads (16 bytes per lane, XOR-permuted 16-byte
+//    chunks; two buffers, one barrier per tile), fp32 tiles through registers
+//    into padded rows (D <= 64: one buffer, two barriers per tile); operands
+//    that need the transposed tile are read with
 //    gfx950's transposing LDS load (ds_read_b64_tr_b16), so each tile is
 //    stored once.
 //  * Causal: tiles above the diagonal are skipped at workgroup and wave level;
