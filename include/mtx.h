@@ -559,12 +559,16 @@ int mtx_layernorm_fwd_f32(const float* x, int64_t ldx, const float* gamma, const
 size_t mtx_layernorm_bwd_workspace_bytes(int64_t rows, int C);
 /* LayerNorm backward: dx (if non-NULL) and dgamma/dbeta (if non-NULL), in one
  * pass over x and dy when both are asked for.  accumulate: bit 0 adds into dx,
- * bit 1 adds into dgamma and dbeta.  workspace: at least
- * mtx_layernorm_bwd_workspace_bytes(rows, C) when dgamma is given. */
+ * bit 1 adds into dgamma and dbeta.  addend (may be NULL; needs dx and bit 0
+ * clear; row stride ldadd): dx = the LayerNorm gradient + addend, the other
+ * contribution to x's gradient (the reference's _accum_grad, tensor.py:29-33,
+ * for the residual stream that feeds both a LayerNorm and the block's residual
+ * add, transformer.py:64-65) without first copying it into dx.  workspace: at
+ * least mtx_layernorm_bwd_workspace_bytes(rows, C) when dgamma is given. */
 int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* gamma, const float* mean,
                           const float* std_, const float* dy, int64_t lddy, float* dx, int64_t lddx,
-                          float* dgamma, float* dbeta, int64_t rows, int C, int accumulate,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          const float* addend, int64_t ldadd, float* dgamma, float* dbeta, int64_t rows, int C,
+                          int accumulate, void* workspace, size_t workspace_bytes, void* stream);
 
 /* GELU (tanh form, functional.py:54-59), contiguous n elements. */
 int mtx_gelu_fwd_f32(const float* x, float* y, int64_t n, void* stream);

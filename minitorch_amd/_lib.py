@@ -110,8 +110,8 @@ SIGNATURES = {
     "mtx_softmax_bwd_f32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I, _I, _I, _P]),
     "mtx_layernorm_fwd_f32": (_I, [_P, _I64, _P, _P, _P, _I64, _P, _P, _I64, _I, _F, _P]),
     "mtx_layernorm_bwd_workspace_bytes": (_SZ, [_I64, _I]),
-    "mtx_layernorm_bwd_f32": (_I, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _I64, _I, _I,
-                                   _P, _SZ, _P]),
+    "mtx_layernorm_bwd_f32": (_I, [_P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I,
+                                   _I, _P, _SZ, _P]),
     "mtx_gelu_fwd_f32": (_I, [_P, _P, _I64, _P]),
     "mtx_gelu_bwd_f32": (_I, [_P, _P, _P, _I64, _I, _P]),
     "mtx_xent_fwd_f32": (_I, [_P, _I64, _P, _P, _P, _I64, _I, _P]),

@@ -107,15 +107,17 @@ __global__ __launch_bounds__(256) void layernorm_fwd_kernel(const float* __restr
   }
 }
 
-// dx = (1/std) * (g - mean(g) - xh * mean(g * xh)), g = dy * gamma
+// dx = (1/std) * (g - mean(g) - xh * mean(g * xh)), g = dy * gamma, plus
+// add (when set; add may be dx itself: each element is read before the same
+// thread writes it, so neither pointer is restrict)
 template <int VPL>
 __global__ __launch_bounds__(256) void layernorm_bwd_kernel(const float* __restrict__ x, int64_t ldx,
                                                             const float* __restrict__ gamma,
                                                             const float* __restrict__ mean_in,
                                                             const float* __restrict__ std_in,
                                                             const float* __restrict__ dy, int64_t lddy,
-                                                            float* __restrict__ dx, int64_t lddx,
-                                                            int64_t rows, int C, int accumulate) {
+                                                            float* dx, int64_t lddx, const float* add,
+                                                            int64_t ldadd, int64_t rows, int C) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -140,12 +142,13 @@ __global__ __launch_bounds__(256) void layernorm_bwd_kernel(const float* __restr
   s1 = wave_sum(s1) / (float)C;
   s2 = wave_sum(s2) / (float)C;
   float* dr = dx + row * lddx;
+  const float* ar = add ? add + row * ldadd : nullptr;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int j = lane + 64 * i;
     if (j < C) {
       float v = (gg[i] - s1 - xh[i] * s2) / sd;
-      if (accumulate) v += dr[j];
+      if (ar) v += ar[j];
       dr[j] = v;
     }
   }
@@ -164,12 +167,12 @@ constexpr int LNP_WAVES = 8;
 template <int VPL>
 __global__ __launch_bounds__(64 * LNP_WAVES) void layernorm_bwd_param_kernel(
     const float* __restrict__ x, int64_t ldx, const float* __restrict__ gamma, const float* __restrict__ mean_in,
-    const float* __restrict__ std_in, const float* __restrict__ dy, int64_t lddy, float* __restrict__ dx,
-    int64_t lddx, float* __restrict__ ws, int64_t rows, int C, int64_t chunk, int acc_dx) {
+    const float* __restrict__ std_in, const float* __restrict__ dy, int64_t lddy, float* dx, int64_t lddx,
+    const float* add, int64_t ldadd, float* __restrict__ ws, int64_t rows, int C, int64_t chunk) {
   extern __shared__ float red[];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t r0 = (int64_t)blockIdx.x * chunk, r1 = min(rows, r0 + chunk);
-  const bool rd_dx = dx != nullptr && acc_dx != 0;
+  const bool rd_dx = dx != nullptr && add != nullptr;
   // rows of up to 768 columns keep gamma in registers and prefetch the next
   // row (x, dy and the dx being added to); wider rows would spill
   constexpr bool PF = VPL <= 12;
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(64 * LNP_WAVES) void layernorm_bwd_param_kernel(
       const bool ok = rr < r1 && j < C;
       px[i] = ok ? x[rr * ldx + j] : 0.f;
       pg[i] = ok ? dy[rr * lddy + j] : 0.f;
-      pd[i] = PF && ok && rd_dx ? dx[rr * lddx + j] : 0.f;
+      pd[i] = PF && ok && rd_dx ? add[rr * ldadd + j] : 0.f;
     }
   };
   int64_t r = r0 + w;
@@ -222,7 +225,7 @@ __global__ __launch_bounds__(64 * LNP_WAVES) void layernorm_bwd_param_kernel(
         const int j = lane + 64 * i;
         if (j < C) {
           float v = (cg[i] - s1 - cx[i] * s2) / sd;
-          if (acc_dx) v += PF ? cd[i] : dr[j];
+          if (rd_dx) v += PF ? cd[i] : add[r * ldadd + j];
           dr[j] = v;
         }
       }
@@ -446,17 +449,23 @@ extern "C" size_t mtx_layernorm_bwd_workspace_bytes(int64_t rows, int C) {
 
 extern "C" int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* gamma, const float* mean,
                                      const float* std_, const float* dy, int64_t lddy, float* dx, int64_t lddx,
-                                     float* dgamma, float* dbeta, int64_t rows, int C, int accumulate,
-                                     void* workspace, size_t workspace_bytes, void* stream) {
+                                     const float* addend, int64_t ldadd, float* dgamma, float* dbeta, int64_t rows,
+                                     int C, int accumulate, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
   MTX_CHECK_ARG(x && gamma && mean && std_ && dy, "layernorm_bwd: null pointer");
   MTX_CHECK_SHAPE(rows >= 0 && C >= 1 && C <= 2048 && ldx >= C && lddy >= C, "layernorm_bwd: bad shape");
   MTX_CHECK_ARG(!dx || lddx >= C, "layernorm_bwd: bad lddx");
   MTX_CHECK_ARG((dgamma == nullptr) == (dbeta == nullptr), "layernorm_bwd: dgamma and dbeta go together");
   MTX_CHECK_ARG(accumulate >= 0 && accumulate <= 3, "layernorm_bwd: accumulate takes bits 0 (dx) and 1 (params)");
+  MTX_CHECK_ARG(!addend || (dx && !(accumulate & 1) && ldadd >= C),
+                "layernorm_bwd: an addend needs dx, no dx accumulation and ldadd >= C");
   if (rows == 0) return MTX_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int vpl = (C + 63) / 64;
-  const int acc_dx = accumulate & 1, acc_p = (accumulate >> 1) & 1;
+  const int acc_p = (accumulate >> 1) & 1;
+  // accumulating into dx is dx = dx_ln + dx: the addend read from dx itself
+  const float* add = (accumulate & 1) ? dx : addend;
+  const int64_t lda = (accumulate & 1) ? lddx : ldadd;
   if (dgamma) {
     const size_t need = mtx_layernorm_bwd_workspace_bytes(rows, C);
     MTX_CHECK_ARG(workspace && workspace_bytes >= need, "layernorm_bwd: workspace too small (%zu < %zu)",
@@ -465,7 +474,7 @@ extern "C" int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* g
     const int64_t chunk = (rows + nsplit - 1) / nsplit;
     float* ws = static_cast<float*>(workspace);
     const size_t lds = (size_t)8 * C * sizeof(float);
-#define LN_P(V) hipLaunchKernelGGL(layernorm_bwd_param_kernel<V>, dim3(nsplit), dim3(64 * LNP_WAVES), lds, st, x, ldx, gamma, mean, std_, dy, lddy, dx, lddx, ws, rows, C, chunk, acc_dx)
+#define LN_P(V) hipLaunchKernelGGL(layernorm_bwd_param_kernel<V>, dim3(nsplit), dim3(64 * LNP_WAVES), lds, st, x, ldx, gamma, mean, std_, dy, lddy, dx, lddx, add, lda, ws, rows, C, chunk)
     if (vpl <= 1) LN_P(1);
     else if (vpl <= 2) LN_P(2);
     else if (vpl <= 4) LN_P(4);
@@ -481,7 +490,7 @@ extern "C" int mtx_layernorm_bwd_f32(const float* x, int64_t ldx, const float* g
     MTX_LAUNCHED();
   } else if (dx) {
     dim3 gr(rows_grid(rows)), bl(256);
-#define LN_B(V) hipLaunchKernelGGL(layernorm_bwd_kernel<V>, gr, bl, 0, st, x, ldx, gamma, mean, std_, dy, lddy, dx, lddx, rows, C, acc_dx)
+#define LN_B(V) hipLaunchKernelGGL(layernorm_bwd_kernel<V>, gr, bl, 0, st, x, ldx, gamma, mean, std_, dy, lddy, dx, lddx, add, lda, rows, C)
     if (vpl <= 1) LN_B(1);
     else if (vpl <= 2) LN_B(2);
     else if (vpl <= 4) LN_B(4);

@@ -717,16 +717,18 @@ def layernorm_fwd(x, gamma, beta, y, mean, std, eps):
 
 
 def layernorm_bwd(x, gamma, mean, std, dy, dx=None, dgamma=None, dbeta=None, accumulate=False,
-                  accumulate_params=None):
+                  accumulate_params=None, addend=None):
     """dx and/or dgamma, dbeta in one pass over x and dy.  `accumulate` adds
     into dx; `accumulate_params` (default: same as `accumulate`) adds into
-    dgamma and dbeta."""
+    dgamma and dbeta; `addend` (rows, C) is added to dx instead (dx = the
+    LayerNorm gradient + addend; not with `accumulate`)."""
     if accumulate_params is None:
         accumulate_params = accumulate
     flags = (1 if accumulate else 0) | (2 if accumulate_params else 0)
     r, C, ldx = _rows(x)
     _, _, lddy = _rows(dy)
     lddx = _rows(dx)[2] if dx is not None else C
+    ldadd = _rows(addend)[2] if addend is not None else 0
     ws = None
     ws_bytes = 0
     if dgamma is not None:
@@ -734,6 +736,7 @@ def layernorm_bwd(x, gamma, mean, std, dy, dx=None, dgamma=None, dbeta=None, acc
         ws = dev.empty_buf((ws_bytes,), "uint8")
     L.call("mtx_layernorm_bwd_f32", L.ptr(x), ldx, L.ptr(gamma), L.ptr(mean), L.ptr(std),
            L.ptr(dy), lddy, L.ptr(dx) if dx is not None else None, lddx,
+           L.ptr(addend) if addend is not None else None, ldadd,
            L.ptr(dgamma) if dgamma is not None else None, L.ptr(dbeta) if dbeta is not None else None,
            r, C, flags, L.ptr(ws) if ws is not None else None, ws_bytes,
            L.stream_handle())

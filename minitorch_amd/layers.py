@@ -15,7 +15,7 @@ from . import functional as F
 from . import kernels as K
 from .device import DeviceArray
 from .module import Module
-from .tensor import Tensor, _grad_target, grad_enabled, _parents
+from .tensor import Tensor, _grad_target, _grad_target_addend, grad_enabled, _parents
 
 
 class Linear(Module):
@@ -94,11 +94,14 @@ class LayerNorm(Module):
         if track:
             def _backward():
                 g = out.grad.contiguous().t.view(rows, C)
-                dx = dgam = dbet = None
+                dx = dgam = dbet = add = None
                 acc_x = acc_p = False
                 if x.requires_grad:
-                    tx, acc_x = _grad_target(x)
+                    # x's other contribution (the residual add's) is read as
+                    # an addend when it is still held by reference
+                    tx, acc_x, ad = _grad_target_addend(x)
                     dx = tx.t.view(rows, C)
+                    add = ad.t.view(rows, C) if ad is not None else None
                 if gamma.requires_grad or beta.requires_grad:
                     tg, ag = _grad_target(gamma)
                     tb, ab = _grad_target(beta)
@@ -107,7 +110,8 @@ class LayerNorm(Module):
                     dgam, dbet, acc_p = tg.t, tb.t, ag
                 if dx is not None or dgam is not None:
                     K.layernorm_bwd(xc.t.view(rows, C), gamma.data.t, mean.t, std.t, g, dx=dx,
-                                    dgamma=dgam, dbeta=dbet, accumulate=acc_x, accumulate_params=acc_p)
+                                    dgamma=dgam, dbeta=dbet, accumulate=acc_x, accumulate_params=acc_p,
+                                    addend=add)
 
             out._backward = _backward
             out._prev = _parents((x, gamma, beta))

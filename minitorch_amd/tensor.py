@@ -77,6 +77,9 @@ def _sum_to_shape(g: DeviceArray, shape) -> DeviceArray:
 # ids of the non-leaf tensors that have exactly one consumer in the graph the
 # running backward() walks (set by Tensor.backward)
 _single_consumer: set = set()
+# a non-leaf tensor with several consumers takes its first gradient by
+# reference too (False: as a copy)
+_ALIAS_FIRST_GRAD = True
 
 
 def _accum_grad(tensor: "Tensor", grad: DeviceArray, owned: bool = False):
@@ -92,7 +95,11 @@ def _accum_grad(tensor: "Tensor", grad: DeviceArray, owned: bool = False):
             tensor.grad = grad
             tensor._grad_alias = False
             return
-        if id(tensor) in _single_consumer and grad.shape == tensor.shape:
+        if (id(tensor) in _single_consumer or (_ALIAS_FIRST_GRAD and tensor._prev)) and grad.shape == tensor.shape:
+            # a non-leaf's first gradient is taken by reference: nothing
+            # writes that buffer again in this backward pass, and every later
+            # in-place write to tensor.grad copies it first (_own_grad) or
+            # reads it as an addend (_grad_target_addend)
             tensor.grad = grad
             tensor._grad_alias = True
             return
@@ -124,6 +131,22 @@ def _grad_target(tensor: "Tensor"):
         return tensor.grad, False
     _own_grad(tensor)
     return tensor.grad, True
+
+
+def _grad_target_addend(tensor: "Tensor"):
+    """(buffer, accumulate, addend) for a kernel that writes tensor's
+    gradient directly and can add a second input: when tensor.grad is a
+    reference to another buffer (its first contribution, see _accum_grad), a
+    new buffer plus that reference as the addend, so the kernel writes
+    new = own + addend with no copy; otherwise _grad_target's answer and no
+    addend."""
+    if tensor.grad is not None and getattr(tensor, "_grad_alias", False) and tensor.grad.t.is_contiguous():
+        addend = tensor.grad
+        tensor.grad = dev.empty(tensor.shape)
+        tensor._grad_alias = False
+        return tensor.grad, False, addend
+    t, acc = _grad_target(tensor)
+    return t, acc, None
 
 
 def _as_tensor(x) -> "Tensor":

@@ -213,6 +213,19 @@ def test_layernorm(dev, rows, C):
     close(H(dx2), hx.g, atol=1e-4 * np.sqrt(C) / 10, name="ln_dx_fused")
     close(H(dg2), 2 * hg.g, atol=2 * dot_tol(rows), name="ln_dgamma_acc")
     close(H(db2), 2 * hb.g, atol=2 * dot_tol(rows), name="ln_dbeta_acc")
+    # an addend instead of accumulation: the same bits as accumulating into a
+    # copy of it, with and without the parameter gradients; the addend unchanged
+    for with_params in (False, True):
+        acc_buf = T(base)
+        kw = dict(dgamma=empty((C,)), dbeta=empty((C,))) if with_params else {}
+        Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dx=acc_buf, accumulate=True, accumulate_params=False, **kw)
+        add_src, out = T(base), empty((rows, C))
+        kw = dict(dgamma=empty((C,)), dbeta=empty((C,))) if with_params else {}
+        Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dx=out, addend=add_src, **kw)
+        assert np.array_equal(H(out), H(acc_buf)), f"addend vs accumulate (params={with_params})"
+        assert np.array_equal(H(add_src), base)
+    with pytest.raises(ValueError):
+        Kn.layernorm_bwd(tx, T(gam), mean, std, T(dy), dx=dx2, accumulate=True, addend=T(base))
 
 
 def test_gelu(dev):
