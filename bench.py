@@ -517,6 +517,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--gemm-mode", choices=("bf16x3", "fp32"), default="bf16x3",
+                    help="--only gpt2/gpt0: the product kernel for shapes of >= 128 x 128")
     ap.add_argument("--only", choices=("all", "c3", "c3series", "c1", "c0attn", "c4", "c4eager", "c4kernel", "gpt2", "gpt0"),
                     default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
@@ -550,10 +552,14 @@ def main():
         print(f"[bench] copied {args.calibrate_copy} MiB x5", file=sys.stderr)
         return
     if args.only in ("gpt2", "gpt0"):
+        from minitorch_amd import kernels as _K
+
         c = C2_CFG if args.only == "gpt2" else C0_CFG
+        if args.gemm_mode == "fp32":
+            _K.set_gemm_mode(_K.GEMM_FP32)
         for graph in (True, False):
             ms, losses = bench_gpt(c, 2, args.steps, args.warmup, graph=graph)
-            print(f"[bench] {args.only} ({'graph' if graph else 'eager'}): {ms:.3f} ms/step, "
+            print(f"[bench] {args.only} ({'graph' if graph else 'eager'}, gemm {args.gemm_mode}): {ms:.3f} ms/step, "
                   f"{c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, losses {losses}", file=sys.stderr)
         return
     if args.only == "c3series":
@@ -627,6 +633,15 @@ def main():
     # the mean over 20 steps, the length of the compared loss curve
     ms_c2, losses_c2 = bench_gpt(C2_CFG, 2, 20, 3, graph=True)
     ms_c2_eager, _ = bench_gpt(C2_CFG, 2, 5, 2)
+    # the same replayed step with the products of >= 128 x 128 on the fp32
+    # MFMA kernel instead of the default three-piece bf16 split
+    from minitorch_amd import kernels as _K
+
+    prev_mode = _K.set_gemm_mode(_K.GEMM_FP32)
+    try:
+        ms_c2_f32, losses_c2_f32 = bench_gpt(C2_CFG, 2, 20, 3, graph=True)
+    finally:
+        _K.set_gemm_mode(prev_mode)
     tok_c2 = C2_CFG["B"] * C2_CFG["block"] / (ms_c2 * 1e-3)
     fl_c2 = gpt_flops_per_step(C2_CFG)
     print(f"[bench] C2 {ms_c2:.2f} ms/step = {tok_c2:.0f} tokens/s, losses {losses_c2}", file=sys.stderr,
@@ -703,7 +718,14 @@ def main():
                        "config": "vocab 65, n_embd 384, 6 heads, 6 layers, T=256, B=64, fp32, Adam 3e-4",
                        "losses": [round(x, 5) for x in losses_c2],
                        "mode": "step replayed from a HIP graph (CapturedStep)",
-                       "ms_per_step_eager": round(ms_c2_eager, 3)},
+                       "gemm": "fp32 products of >= 128 x 128 as three-piece bf16 splits on the bf16 "
+                               "matrix cores (fp32-accurate; mtx_gemm_set_mode MTX_GEMM_BF16X3, the default)",
+                       "ms_per_step_eager": round(ms_c2_eager, 3),
+                       "fp32_mfma_gemm": {"ms_per_step": round(ms_c2_f32, 3),
+                                          "tokens_per_s": round(C2_CFG["B"] * C2_CFG["block"] / (ms_c2_f32 * 1e-3), 1),
+                                          "losses": [round(x, 5) for x in losses_c2_f32],
+                                          "note": "the same replayed step with every product on the fp32 "
+                                                  "MFMA kernel (MTX_GEMM_FP32)"}},
                 "C0": {"tokens_per_s": round(tok_c0, 1), "ms_per_step": round(ms_c0, 3),
                        "config": "vocab 65, n_embd 64, 4 heads, 2 layers, T=32, B=16, fp32",
                        "mode": "step replayed from a HIP graph (CapturedStep)",

@@ -380,7 +380,19 @@ int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const
  * as stride swaps) and Linear.forward (layers.py:31-37, bias fused).  With a
  * workspace of mtx_gemm_workspace_bytes() bytes, long-K products are split
  * over K and reduced deterministically; without one they run unsplit.
+ *
+ * Products with M >= 128 and N >= 128 run, by default (MTX_GEMM_BF16X3), on
+ * the bf16 matrix cores with every fp32 operand value split into three bf16
+ * pieces (x = x0 + x1 + x2 to 2^-24 |x|) and the six piece products of
+ * weight >= 2^-16 accumulated in fp32: a dot product's error is the fp32
+ * accumulation error plus at most ~2^-22 sum|a_k b_k| (NaN for non-finite
+ * inputs).  MTX_GEMM_FP32 selects the fp32 MFMA kernel for them instead.
+ * The mode is process-wide and read when a product is launched (or
+ * recorded into a graph); every entry point of this section follows it.
  */
+enum mtx_gemm_mode { MTX_GEMM_FP32 = 0, MTX_GEMM_BF16X3 = 1 };
+int mtx_gemm_set_mode(int mode);
+int mtx_gemm_get_mode(void);
 size_t mtx_gemm_workspace_bytes(int M, int N, int K, int batch);
 int mtx_gemm_f32(int M, int N, int K, int batch,
                  float alpha, const float* a, int64_t sa_m, int64_t sa_k, int64_t sa_b,

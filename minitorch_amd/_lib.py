@@ -19,6 +19,7 @@ LIB_PATH = _PKG / "libmtx_hip.so"
 
 MTX_OK, MTX_ERR_ARG, MTX_ERR_SHAPE, MTX_ERR_DTYPE, MTX_ERR_HIP = range(5)
 MTX_F32, MTX_BF16 = 0, 1
+MTX_GEMM_FP32, MTX_GEMM_BF16X3 = 0, 1
 ATTN_SCRATCH_BYTES = 8 << 20  # MTX_ATTN_SCRATCH_BYTES (include/mtx.h)
 ATTN_BWD_DELTA, ATTN_BWD_DKDV, ATTN_BWD_DQ, ATTN_BWD_ALL = 1, 2, 4, 7
 
@@ -86,6 +87,8 @@ SIGNATURES = {
     "mtx_gemm_partials_f32": (_I, [_I, _I, _I, _P, _I64, _I64, _P, _I64, _I64, _P, _SZ, _P, _P]),
     "mtx_embedding2_fwd_f32": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I, _P]),
     "mtx_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "mtx_gemm_set_mode": (_I, [_I]),
+    "mtx_gemm_get_mode": (_I, []),
     "mtx_gemm_step_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _F, _P, _I64, _P, _I, _I,
                                _P, _P, _I64, _I64, _I, _P, _P]),
     "mtx_gemm_f32": (_I, [_I, _I, _I, _I,

@@ -20,6 +20,8 @@
 // alpha, beta and bias.
 #include "mtx_common.h"
 
+#include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace mtx {
@@ -397,6 +399,396 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// fp32 products on the bf16 matrix cores (the default for tiles of 128 x 128).
+//
+// Every fp32 operand value x is split into three bf16 pieces while its tile
+// is staged into LDS: x0 = bf16(x), x1 = bf16(x - x0), x2 = bf16(x - x0 - x1)
+// (each conversion rounds to nearest even; each difference is exact in fp32),
+// so x = x0 + x1 + x2 + r with |r| <= 2^-24 |x|: the pieces carry x's 24-bit
+// significand.  A product x*y is accumulated as the six piece products of
+// weight >= 2^-16 (x2y0, x1y1, x0y2, x1y0, x0y1, x0y0, smallest first); the
+// three dropped ones (x1y2, x2y1, x2y2) weigh at most ~2^-23 |xy| together.
+// Each piece product is exact in fp32 and the matrix core adds it into the
+// fp32 accumulator, so a dot product's error is the fp32 accumulation error
+// (as with fp32 multiply-adds) plus at most ~2^-22 sum|x_k y_k|.  Six
+// v_mfma_f32_32x32x16_bf16 (6 x 32 cycles) do the work of sixteen
+// v_mfma_f32_16x16x4_f32 (16 x 32 cycles): 2.7x the fp32 matrix rate.
+// Non-finite inputs give NaN (x - x0 is Inf - Inf).
+//
+// Tiling: 256 threads = 4 waves in a 2x2 grid, block tile 128 x 128 x 16,
+// wave tile 64 x 64 = 2 x 2 MFMA tiles of 32 x 32.  The next k-tile is
+// fetched into registers while the current one is multiplied out of LDS.
+// An operand contiguous along k is staged as [piece][row][k] (rows of 24
+// bf16: the 16 rows a fragment read touches per pass sit in 16 distinct
+// 16-byte bank groups) and read with ds_read_b128; an operand contiguous
+// along its rows (m or n) as [piece][k][row] (rows of 144 bf16) and read with
+// gfx950's transposing ds_read_b64_tr_b16, so staging never transposes in
+// registers.  MFMA 32x32x16 operands: lane l holds row l%32 and
+// k = 8(l/32) + 0..7; accumulator element e of lane l is
+// C[8(e/4) + 4(l/32) + e%4][l%32].
+// ---------------------------------------------------------------------------
+namespace x3 {
+constexpr int T = 128;             // tile rows and columns
+constexpr int BK = 16;             // k-tile depth (one MFMA k step)
+constexpr int LDK = BK + 8;        // row stride (bf16) of a k-contiguous plane
+constexpr int LDR = T + 16;        // row stride (bf16) of a row-contiguous plane
+constexpr int NV = T * BK / 4 / kGT;  // float4 per thread per operand tile
+}  // namespace x3
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ uint32_t pk_bf16(float x, float y) {
+  bf16x2 v = {(__bf16)x, (__bf16)y};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// x = h + m + l (+ 2^-24 |x|), for four values, each plane as four bf16
+__device__ __forceinline__ void split3(f32x4 v, uint2& h, uint2& m, uint2& l) {
+  h.x = pk_bf16(v[0], v[1]);
+  h.y = pk_bf16(v[2], v[3]);
+  float r0 = v[0] - __uint_as_float(h.x << 16), r1 = v[1] - __uint_as_float(h.x & 0xffff0000u);
+  float r2 = v[2] - __uint_as_float(h.y << 16), r3 = v[3] - __uint_as_float(h.y & 0xffff0000u);
+  m.x = pk_bf16(r0, r1);
+  m.y = pk_bf16(r2, r3);
+  r0 -= __uint_as_float(m.x << 16);
+  r1 -= __uint_as_float(m.x & 0xffff0000u);
+  r2 -= __uint_as_float(m.y << 16);
+  r3 -= __uint_as_float(m.y & 0xffff0000u);
+  l.x = pk_bf16(r0, r1);
+  l.y = pk_bf16(r2, r3);
+}
+
+// One operand's 128 x 16 tile (rows = m for A, n for B).  KC: contiguous
+// along k in global memory (rows strided by srow); else contiguous along the
+// rows (k strided by sk).  Thread slot i covers, KC: row idx/4, k 4(idx%4)..+3;
+// else: k idx/32, rows 4(idx%32)..+3 (idx = tid + 256 i).
+template <bool KC>
+struct X3Stage {
+  static constexpr int PS = KC ? x3::T * x3::LDK : x3::BK * x3::LDR;  // plane size (bf16)
+  const float* __restrict__ base;
+  int64_t srow, sk;
+  int rows, r0;
+  int64_t off[x3::NV];
+  f32x4 r[x3::NV];
+
+  __device__ __forceinline__ void init(const float* b, int64_t s_row, int64_t s_k, int nrows, int row0, int tid) {
+    base = b;
+    srow = s_row;
+    sk = s_k;
+    rows = nrows;
+    r0 = row0;
+#pragma unroll
+    for (int i = 0; i < x3::NV; ++i) {
+      const int idx = tid + i * kGT;
+      off[i] = KC ? (int64_t)(r0 + idx / 4) * srow + 4 * (idx % 4) : (int64_t)(idx / 32) * sk + r0 + 4 * (idx % 32);
+    }
+  }
+  // every row of the tile and every k of [k0, k0+16) in range, float4
+  // loads aligned (checked by the caller)
+  __device__ __forceinline__ void fetch_fast(int k0) {
+#pragma unroll
+    for (int i = 0; i < x3::NV; ++i)
+      r[i] = *reinterpret_cast<const f32x4*>(base + off[i] + (int64_t)k0 * (KC ? 1 : sk));
+  }
+  // rows past `rows` and k past kend read as zero; unaligned vectors by element
+  __device__ __forceinline__ void fetch_checked(int k0, int kend, int tid) {
+#pragma unroll
+    for (int i = 0; i < x3::NV; ++i) {
+      const int idx = tid + i * kGT;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KC) {
+        const int row = r0 + idx / 4, k = k0 + 4 * (idx % 4);
+        if (row < rows) {
+          const float* p = base + (int64_t)row * srow + k;
+          if (k + 3 < kend && (((uintptr_t)p) & 15u) == 0) {
+            v = *reinterpret_cast<const f32x4*>(p);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (k + j < kend) v[j] = p[j];
+          }
+        }
+      } else {
+        const int k = k0 + idx / 32, row = r0 + 4 * (idx % 32);
+        if (k < kend) {
+          const float* p = base + (int64_t)k * sk + row;
+          if (row + 3 < rows && (((uintptr_t)p) & 15u) == 0) {
+            v = *reinterpret_cast<const f32x4*>(p);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (row + j < rows) v[j] = p[j];
+          }
+        }
+      }
+      r[i] = v;
+    }
+  }
+  __device__ __forceinline__ void put(__bf16* __restrict__ lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < x3::NV; ++i) {
+      const int idx = tid + i * kGT;
+      const int o = KC ? (idx / 4) * x3::LDK + 4 * (idx % 4) : (idx / 32) * x3::LDR + 4 * (idx % 32);
+      uint2 h, m, l;
+      split3(r[i], h, m, l);
+      *reinterpret_cast<uint2*>(lds + o) = h;
+      *reinterpret_cast<uint2*>(lds + PS + o) = m;
+      *reinterpret_cast<uint2*>(lds + 2 * PS + o) = l;
+    }
+  }
+  // piece p's MFMA operand for tile rows rb .. rb+31: lane l gets row
+  // rb + l%32 and k = 8(l/32) + 0..7
+  __device__ __forceinline__ bf16x8 frag(const __bf16* __restrict__ lds, int p, int rb, int lane) const {
+    if constexpr (KC) {
+      return *reinterpret_cast<const bf16x8*>(lds + p * PS + (rb + (lane & 31)) * x3::LDK + 8 * (lane >> 5));
+    } else {
+      // transposing read: in each 16-lane group G, lane j = 4i + q addresses
+      // k row 8(G/2) + i (+4 for the second half) at rows rb + 16(G%2) + 4q;
+      // lane j then receives row rb + 16(G%2) + j at those four k
+      const int G = lane >> 4, j = lane & 15;
+      const __bf16* p0 = lds + p * PS + (8 * (G >> 1) + (j >> 2)) * x3::LDR + rb + 16 * (G & 1) + 4 * (j & 3);
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 4 * x3::LDR));
+      const uint2 ul = __builtin_bit_cast(uint2, lo), uh = __builtin_bit_cast(uint2, hi);
+      return __builtin_bit_cast(bf16x8, make_uint4(ul.x, ul.y, uh.x, uh.y));
+    }
+  }
+  // ACT 3 column sums: this thread's share of the staged B values, by
+  // column (KC: the 4 k of slot i belong to column idx/4; else slot i holds
+  // columns 4(idx%32)..+3, the same for every slot)
+  __device__ __forceinline__ void colsum_add(float (&cs)[4]) const {
+#pragma unroll
+    for (int i = 0; i < x3::NV; ++i) {
+      if constexpr (KC) {
+        cs[i] += (r[i][0] + r[i][1]) + (r[i][2] + r[i][3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cs[j] += r[i][j];
+      }
+    }
+  }
+};
+
+template <bool AK, bool BN1, int ACT>
+__global__ __launch_bounds__(kGT, 2) void gemm_x3_kernel(const GemmArgs g) {
+  using SA = X3Stage<AK>;
+  using SB = X3Stage<!BN1>;  // B^T: rows = n, contiguous along k iff !BN1
+  // the operand planes, reused by the epilogue for half the C tile (64 x 128 fp32)
+  constexpr int kAB = 3 * (SA::PS + SB::PS) * 2, kEp = 64 * x3::T * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kAB > kEp ? kAB : kEp];
+  __bf16* As = reinterpret_cast<__bf16*>(smem);
+  __bf16* Bs = As + 3 * SA::PS;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int wm = (wid >> 1) * 64, wn = (wid & 1) * 64;
+  const int m0 = blockIdx.y * x3::T, n0 = blockIdx.x * x3::T;
+  const int zb = blockIdx.z;
+  const int bidx = zb % g.batch, split = zb / g.batch;
+  const int kbeg = split * g.kchunk;
+  const int kend = min(g.K, kbeg + g.kchunk);
+
+  SA sa;
+  SB sb;
+  sa.init(g.a + (int64_t)bidx * g.sab, g.sam, g.sak, g.M, m0, tid);
+  sb.init(g.b + (int64_t)bidx * g.sbb, g.sbn, g.sbk, g.N, n0, tid);
+  const bool interior = g.vec_ok && m0 + x3::T <= g.M && n0 + x3::T <= g.N;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  // ACT 3: the first row of tiles sums the B columns it stages
+  const bool cs_block = ACT == 3 && blockIdx.y == 0;
+  float cs[4] = {0.f, 0.f, 0.f, 0.f};
+
+  // one k-tile: stage the fetched values, request the next tile (pref),
+  // multiply out of LDS
+  auto tile = [&](auto&& pref) {
+    __syncthreads();
+    sa.put(As, tid);
+    sb.put(Bs, tid);
+    if constexpr (ACT == 3) {
+      if (cs_block) sb.colsum_add(cs);
+    }
+    __syncthreads();
+    pref();
+    bf16x8 a[3][2], b[3][2];
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[p][i] = sa.frag(As, p, wm + 32 * i, lane);
+        b[p][i] = sb.frag(Bs, p, wn + 32 * i, lane);
+      }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f32x16 c = acc[i][j];
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2][i], b[0][j], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[1][j], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[2][j], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0][j], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1][j], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0][j], c, 0, 0, 0);
+        acc[i][j] = c;
+      }
+  };
+  auto checked_next = [&](int kn) {
+    if (kn < kend) {
+      sa.fetch_checked(kn, kend, tid);
+      sb.fetch_checked(kn, kend, tid);
+    }
+  };
+  int k0 = kbeg;
+  if (interior) {
+    // whole k-tiles through the unchecked loads in a branch-free loop; the
+    // last whole tile and a ragged tail after it
+    const int kfull = kbeg + (kend - kbeg) / x3::BK * x3::BK;
+    if (k0 < kfull) {
+      sa.fetch_fast(k0);
+      sb.fetch_fast(k0);
+    } else {
+      checked_next(k0);
+    }
+    for (; k0 + x3::BK < kfull; k0 += x3::BK)
+      tile([&] {
+        sa.fetch_fast(k0 + x3::BK);
+        sb.fetch_fast(k0 + x3::BK);
+      });
+  } else {
+    checked_next(k0);
+  }
+  for (; k0 < kend; k0 += x3::BK) tile([&] { checked_next(k0 + x3::BK); });
+
+  if constexpr (ACT == 3) {
+    // reduce the per-thread column sums through LDS (As is free after the
+    // barrier): KC: 4 threads per column, else 8 threads per 4 columns;
+    // contributors are added in a fixed order
+    if (cs_block) {
+      float* red = reinterpret_cast<float*>(As);  // [8][128]
+      __syncthreads();
+      if constexpr (!BN1) {
+#pragma unroll
+        for (int i = 0; i < x3::NV; ++i) {
+          const int idx = tid + i * kGT;
+          red[(idx % 4) * x3::T + idx / 4] = cs[i];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[(tid / 32) * x3::T + 4 * (tid % 32) + j] = cs[j];
+      }
+      __syncthreads();
+      if (tid < x3::T) {
+        constexpr int NC = BN1 ? 8 : 4;
+        float v = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) v += red[c * x3::T + tid];
+        const int n = n0 + tid;
+        if (n < g.N) {
+          if (g.ksplit > 1) g.ws[(int64_t)g.ksplit * g.M * g.N + (int64_t)split * g.N + n] = v;
+          else g.colsum[n] = g.colsum_acc ? g.colsum[n] + v : v;
+        }
+      }
+    }
+  }
+
+  // Epilogue, in two halves of 64 rows: the waves put acc[half] into LDS
+  // (row r of the half holds tile row 64(r/32) + 32 half + r%32; columns
+  // XOR-permuted by 32 on rows 4..7 mod 8, so the two rows a store
+  // instruction writes use disjoint banks), then each thread finishes float4
+  // runs of C rows: coalesced loads and stores, no per-element addresses.
+  // acc[i][j][e] = tile element (wm + 32i + 8(e/4) + 4(lane/32) + e%4, wn + 32j + lane%32).
+  float* ep = reinterpret_cast<float*>(smem);
+  const int lr = lane & 31, lh = lane >> 5;
+  const bool to_ws = g.ksplit > 1;
+  float* W = g.ws + ((int64_t)split * g.batch + bidx) * (int64_t)g.M * g.N;
+  float* Cp = g.c + (int64_t)bidx * g.scb;
+  float* X = g.aux + (int64_t)bidx * g.sxb;
+  const bool rd_c = !to_ws && g.beta != 0.f;
+  const bool use_x = !to_ws && (ACT == 2 || ACT == 4 || (ACT == 1 && g.aux != nullptr));
+  // whole float4 runs of C (and aux) are aligned vectors
+  const bool cvec = to_ws ? (g.N % 4 == 0)
+                          : (g.scn == 1 && g.scm % 4 == 0 && g.scb % 4 == 0 && (((uintptr_t)g.c) & 15u) == 0 &&
+                             (!use_x || (g.sxn == 1 && g.sxm % 4 == 0 && g.sxb % 4 == 0 &&
+                                         (((uintptr_t)g.aux) & 15u) == 0)));
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = (wm >> 1) + 8 * (e >> 2) + 4 * lh + (e & 3);
+        ep[r * x3::T + ((wn + 32 * j + lr) ^ ((r & 4) << 3))] = acc[half][j][e];
+      }
+    __syncthreads();
+#pragma unroll 2
+    for (int q = 0; q < 8; ++q) {
+      const int idx = tid + q * kGT;
+      const int r = idx >> 5, c = 4 * (idx & 31);
+      const int m = m0 + 64 * (r >> 5) + 32 * half + (r & 31);
+      const int n = n0 + c;
+      if (m >= g.M || n >= g.N) continue;
+      const f32x4 a4 = *reinterpret_cast<const f32x4*>(ep + r * x3::T + (c ^ ((r & 4) << 3)));
+      const int nv = min(4, g.N - n);
+      if (to_ws) {
+        float* w = W + (int64_t)m * g.N + n;
+        if (cvec && nv == 4) {
+          *reinterpret_cast<f32x4*>(w) = a4;
+        } else {
+          for (int t = 0; t < nv; ++t) w[t] = a4[t];
+        }
+        continue;
+      }
+      float* cp = Cp + (int64_t)m * g.scm + (int64_t)n * g.scn;
+      float* xp = X + (int64_t)m * g.sxm + (int64_t)n * g.sxn;
+      f32x4 v, old = {0.f, 0.f, 0.f, 0.f}, xa = {0.f, 0.f, 0.f, 0.f}, bv = {0.f, 0.f, 0.f, 0.f};
+      const bool vec = cvec && nv == 4;
+      if (vec) {
+        if (rd_c) old = *reinterpret_cast<const f32x4*>(cp);
+        if constexpr (ACT == 2 || ACT == 4) xa = *reinterpret_cast<const f32x4*>(xp);
+      } else {
+        for (int t = 0; t < nv; ++t) {
+          if (rd_c) old[t] = cp[(int64_t)t * g.scn];
+          if constexpr (ACT == 2 || ACT == 4) xa[t] = xp[(int64_t)t * g.sxn];
+        }
+      }
+      if (g.bias) {
+        for (int t = 0; t < nv; ++t) bv[t] = g.bias[n + t];
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        float u = g.alpha * a4[t] + bv[t];
+        if (rd_c) u += g.beta * old[t];
+        v[t] = u;
+      }
+      if constexpr (ACT == 1) {
+        if (g.aux) {
+          if (vec) *reinterpret_cast<f32x4*>(xp) = v;
+          else
+            for (int t = 0; t < nv; ++t) xp[(int64_t)t * g.sxn] = v[t];
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = gelu_tanh_fast(v[t]);
+      } else if constexpr (ACT == 2) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] *= gelu_grad_fast(xa[t]);
+      } else if constexpr (ACT == 4) {
+        v += xa;
+      }
+      if (vec) *reinterpret_cast<f32x4*>(cp) = v;
+      else
+        for (int t = 0; t < nv; ++t) cp[(int64_t)t * g.scn] = v[t];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny products: M <= 64 rows (a decode step's sequences), K <= 4096 (in
 // up to 8 ranges of 512, one workgroup each, when longer than 512).
 // One workgroup of 16 waves owns 16 output columns for every row; the waves
@@ -724,6 +1116,56 @@ int launch_tile(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
   return MTX_OK;
 }
 
+// Which kernel computes fp32 products of at least 128 x 128 (mtx_gemm_set_mode):
+// MTX_GEMM_BF16X3 (default) the three-piece bf16 split on the bf16 matrix
+// cores, MTX_GEMM_FP32 the fp32 MFMA tile kernel.  Smaller products, and
+// the decode step's skinny ones, always take the fp32 kernels.
+std::atomic<int> g_gemm_mode{MTX_GEMM_BF16X3};
+
+bool use_x3(int M, int N) { return g_gemm_mode.load(std::memory_order_relaxed) == MTX_GEMM_BF16X3 && M >= 128 && N >= 128; }
+
+// Split K only when the 128 x 128 tiles leave the CUs idle (weight gradients,
+// K = B*T): aim at MTX_X3_SPLIT_TARGET workgroups (two fit a CU), each split
+// keeping >= MTX_SPLIT_MINK of K.
+#ifndef MTX_X3_SPLIT_TARGET
+#define MTX_X3_SPLIT_TARGET 576
+#endif
+Plan plan_x3(int M, int N, int K, int batch, size_t ws_bytes) {
+  Plan p{x3::T, x3::T, 1, K};
+  const int64_t t = (int64_t)cdiv(M, x3::T) * cdiv(N, x3::T) * batch;
+  if (t < 256 && K >= 1024) {
+    int want = (int)std::min<int64_t>(K >= 4096 ? 64 : 16, (MTX_X3_SPLIT_TARGET + t - 1) / t);
+    want = std::min(want, std::max(1, K / MTX_SPLIT_MINK));
+    const size_t need = (size_t)want * batch * (size_t)(M + 1) * N * sizeof(float);
+    if (want > 1 && need <= ws_bytes) {
+      p.kchunk = cdiv(cdiv(K, want), x3::BK) * x3::BK;
+      p.ksplit = cdiv(K, p.kchunk);
+    }
+  }
+  return p;
+}
+
+template <int ACT>
+void launch_x3_act(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
+  const dim3 grid(cdiv(g.N, x3::T), cdiv(g.M, x3::T), g.batch * g.ksplit);
+  if (ak && bn1) hipLaunchKernelGGL((gemm_x3_kernel<true, true, ACT>), grid, dim3(kGT), 0, st, g);
+  else if (ak) hipLaunchKernelGGL((gemm_x3_kernel<true, false, ACT>), grid, dim3(kGT), 0, st, g);
+  else if (bn1) hipLaunchKernelGGL((gemm_x3_kernel<false, true, ACT>), grid, dim3(kGT), 0, st, g);
+  else hipLaunchKernelGGL((gemm_x3_kernel<false, false, ACT>), grid, dim3(kGT), 0, st, g);
+}
+
+// as launch_tile: with split K the reduce kernel applies the activation
+int launch_x3(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
+  const int act = g.ksplit > 1 ? 0 : g.act;
+  if (g.colsum) launch_x3_act<3>(g, ak, bn1, st);
+  else if (act == 1) launch_x3_act<1>(g, ak, bn1, st);
+  else if (act == 2) launch_x3_act<2>(g, ak, bn1, st);
+  else if (act == 4) launch_x3_act<4>(g, ak, bn1, st);
+  else launch_x3_act<0>(g, ak, bn1, st);
+  MTX_LAUNCHED();
+  return MTX_OK;
+}
+
 }  // namespace
 }  // namespace mtx
 
@@ -740,8 +1182,20 @@ extern "C" size_t mtx_gemm_workspace_bytes(int M, int N, int K, int batch) {
   // split partials [split][batch][M][N], then the weight-gradient variant's
   // column sums [split][N]
   const size_t tiled = p.ksplit > 1 ? (size_t)p.ksplit * batch * (size_t)(M + 1) * N * sizeof(float) : 0;
-  return skinny > tiled ? skinny : tiled;
+  // the bf16-split kernel's plan (either mode may be set when the product runs)
+  Plan q = plan_x3(M, N, K, batch, (size_t)-1);
+  const size_t split3 = q.ksplit > 1 ? (size_t)q.ksplit * batch * (size_t)(M + 1) * N * sizeof(float) : 0;
+  return std::max({skinny, tiled, split3});
 }
+
+extern "C" int mtx_gemm_set_mode(int mode) {
+  MTX_CHECK_ARG(mode == MTX_GEMM_FP32 || mode == MTX_GEMM_BF16X3,
+                "gemm mode %d must be MTX_GEMM_FP32 (0) or MTX_GEMM_BF16X3 (1)", mode);
+  g_gemm_mode.store(mode);
+  return MTX_OK;
+}
+
+extern "C" int mtx_gemm_get_mode(void) { return g_gemm_mode.load(); }
 
 namespace {
 int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64_t sa_m, int64_t sa_k,
@@ -807,11 +1261,14 @@ int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64
     }
     return MTX_OK;
   }
-  Plan p = plan_gemm(M, N, K, batch, workspace ? workspace_bytes : 0);
+  const bool ak = sa_k == 1, bn1 = sb_n == 1;
+  const bool split3 = use_x3(M, N);
+  Plan p = split3 ? plan_x3(M, N, K, batch, workspace ? workspace_bytes : 0)
+                  : plan_gemm(M, N, K, batch, workspace ? workspace_bytes : 0);
   g.ksplit = p.ksplit;
   g.kchunk = p.kchunk;
-  const bool ak = sa_k == 1, bn1 = sb_n == 1;
-  int rc = (p.bm == 128) ? launch_tile<128, 128>(g, ak, bn1, st) : launch_tile<64, 64>(g, ak, bn1, st);
+  int rc = split3 ? launch_x3(g, ak, bn1, st)
+                  : (p.bm == 128) ? launch_tile<128, 128>(g, ak, bn1, st) : launch_tile<64, 64>(g, ak, bn1, st);
   if (rc) return rc;
   if (p.ksplit > 1) {
     const int64_t total = (int64_t)M * N * batch + (colsum ? N : 0);

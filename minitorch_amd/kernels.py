@@ -466,6 +466,23 @@ def gemm_ln(a, b, c, gamma, beta_ln, eps, y, bias=None, alpha=1.0, beta=1.0):
     return y
 
 
+GEMM_FP32, GEMM_BF16X3 = L.MTX_GEMM_FP32, L.MTX_GEMM_BF16X3
+
+
+def set_gemm_mode(mode: int) -> int:
+    """Select how products of at least 128 x 128 are computed
+    (mtx_gemm_set_mode): GEMM_BF16X3 (the default: fp32 values split into
+    three bf16 pieces on the bf16 matrix cores, fp32-accurate) or GEMM_FP32
+    (fp32 MFMA).  Returns the previous mode."""
+    prev = int(L.lib().mtx_gemm_get_mode())
+    L.call("mtx_gemm_set_mode", int(mode))
+    return prev
+
+
+def get_gemm_mode() -> int:
+    return int(L.lib().mtx_gemm_get_mode())
+
+
 def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=1,
          sa=None, sb=None, sc=None, act=GEMM_ACT_NONE, aux=None, colsum=None, colsum_accumulate=False):
     """C = alpha*A@B + beta*C (+bias) with explicit (row, col, batch) strides

@@ -31,6 +31,17 @@ def close(got, ref, rtol=1e-4, atol=1e-5, name=""):
     assert np.all(err <= lim), f"{name}: max err {err.max():.3e} (max |ref| {np.abs(ref).max():.3e})"
 
 
+@pytest.fixture(params=["bf16x3", "fp32"])
+def gemm_mode(request, dev):
+    """Each GEMM test runs under both product kernels for shapes of at least
+    128 x 128: the bf16 three-piece split (the default) and fp32 MFMA."""
+    from minitorch_amd import kernels as Kn
+
+    prev = Kn.set_gemm_mode(Kn.GEMM_BF16X3 if request.param == "bf16x3" else Kn.GEMM_FP32)
+    yield request.param
+    Kn.set_gemm_mode(prev)
+
+
 def dot_tol(K):
     """Elementwise tolerance for a float32 dot product of length K with N(0,1)
     entries: rounding error grows like sqrt(K) * 2^-24 * |terms|."""
@@ -54,11 +65,17 @@ def dot_tol(K):
     (64, 384, 1536, False, False, 1, True),     # skinny, K split over 3 workgroups
     (17, 40, 1000, True, False, 2, True),       # skinny split, scalar A loads, batched
     (64, 64, 4100, False, False, 1, False),     # K past the skinny range: tiled split-K
+    # >= 128 x 128: the bf16-split kernel in its default mode
+    (256, 384, 1000, False, True, 1, True),     # ragged last k-tile, B contiguous along k
+    (300, 200, 77, True, True, 2, True),        # edge tiles on both sides, both operands transposed
+    (200, 150, 33, False, False, 1, True),      # row strides of 33: no aligned vector loads
+    (1000, 130, 5000, True, False, 1, False),   # split K with edge tiles
+    (512, 512, 16, False, False, 4, True),      # one k-tile, batched
 ])
-def test_gemm(dev, M, N, K, ta, tb, batch, bias):
+def test_gemm(dev, gemm_mode, M, N, K, ta, tb, batch, bias):
     from minitorch_amd import kernels as Kn
 
-    _say(f"[gemm] M={M} N={N} K={K} ta={ta} tb={tb} batch={batch} bias={bias}")
+    _say(f"[gemm] {gemm_mode} M={M} N={N} K={K} ta={ta} tb={tb} batch={batch} bias={bias}")
     rng = np.random.default_rng(M * 7 + N + K)
     a = rng.standard_normal((batch, K, M) if ta else (batch, M, K), dtype=np.float32)
     b = rng.standard_normal((batch, N, K) if tb else (batch, K, N), dtype=np.float32)
@@ -473,8 +490,8 @@ def test_pack3_unpack3(dev, rows, cols):
             np.testing.assert_array_equal(outs[i].numpy(), expect)
 
 
-@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (512, 1536, 384), (96, 80, 8192)])
-def test_gemm_gelu_epilogues(dev, M, N, K):
+@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (512, 1536, 384), (96, 80, 8192), (300, 260, 5000)])
+def test_gemm_gelu_epilogues(dev, gemm_mode, M, N, K):
     """mtx_gemm_act_f32: act 1 = gelu(A@B + bias) with the pre-activation in
     aux, act 2 = (A@B) * gelu'(aux), against NumPy float64 (the K = 8192 case
     takes the split-K path, whose reduce applies the epilogue)."""
@@ -505,8 +522,9 @@ def test_gemm_gelu_epilogues(dev, M, N, K):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K,acc", [(384, 1152, 16384, False), (384, 65, 4096, True), (200, 130, 777, False),
-                                       (64, 48, 300, True), (7, 5, 3, False), (384, 384, 0, True)])
-def test_gemm_wgrad_colsum(dev, M, N, K, acc):
+                                       (64, 48, 300, True), (7, 5, 3, False), (384, 384, 0, True),
+                                       (130, 300, 2001, True), (1536, 384, 16384, False)])
+def test_gemm_wgrad_colsum(dev, gemm_mode, M, N, K, acc):
     """mtx_gemm_wgrad_f32: dW = A @ B (+ beta C) and the column sums of B (a
     Linear's bias gradient) from one launch, against NumPy float64.  The
     first case takes the split-K path (the sums go through the reduce), the
@@ -540,8 +558,9 @@ def test_gemm_wgrad_colsum(dev, M, N, K, acc):
         close(H(c2), H(c), atol=dot_tol(max(K, 1)) * 2, name="wgrad_vs_plain")
 
 
-@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (16384, 384, 384), (96, 80, 8192), (64, 384, 2048)])
-def test_gemm_residual_epilogue(dev, M, N, K):
+@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (16384, 384, 384), (96, 80, 8192), (64, 384, 2048),
+                                   (200, 300, 3000)])
+def test_gemm_residual_epilogue(dev, gemm_mode, M, N, K):
     """mtx_gemm_act_f32 act 4: C = A@B + bias + aux (a residual stream),
     against NumPy float64; the K = 8192 case takes the split-K path, whose
     reduce applies the add."""
