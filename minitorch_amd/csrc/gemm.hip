@@ -427,6 +427,9 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
 // k = 8(l/32) + 0..7; accumulator element e of lane l is
 // C[8(e/4) + 4(l/32) + e%4][l%32].
 // ---------------------------------------------------------------------------
+#ifndef MTX_X3_XCD
+#define MTX_X3_XCD 1
+#endif
 namespace x3 {
 constexpr int T = 128;             // tile rows and columns
 constexpr int BK = 16;             // k-tile depth (one MFMA k step)
@@ -582,8 +585,27 @@ __global__ __launch_bounds__(kGT, 2) void gemm_x3_kernel(const GemmArgs g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wid = tid >> 6;
   const int wm = (wid >> 1) * 64, wn = (wid & 1) * 64;
+#if MTX_X3_XCD
+  // Workgroups are dealt round-robin over the 8 XCDs in dispatch order;
+  // give each XCD a contiguous run of row-major tiles, so the column tiles
+  // that share an A row panel read it through the same L2
+  int tx = blockIdx.x, ty = blockIdx.y, tz = blockIdx.z;
+  {
+    const int nt = gridDim.x * gridDim.y * gridDim.z;
+    if ((nt & 7) == 0) {
+      const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+      const int t = (lin & 7) * (nt >> 3) + (lin >> 3);
+      tx = t % gridDim.x;
+      ty = (t / gridDim.x) % gridDim.y;
+      tz = t / (gridDim.x * gridDim.y);
+    }
+  }
+  const int m0 = ty * x3::T, n0 = tx * x3::T;
+  const int zb = tz;
+#else
   const int m0 = blockIdx.y * x3::T, n0 = blockIdx.x * x3::T;
   const int zb = blockIdx.z;
+#endif
   const int bidx = zb % g.batch, split = zb / g.batch;
   const int kbeg = split * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
@@ -602,7 +624,7 @@ __global__ __launch_bounds__(kGT, 2) void gemm_x3_kernel(const GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   // ACT 3: the first row of tiles sums the B columns it stages
-  const bool cs_block = ACT == 3 && blockIdx.y == 0;
+  const bool cs_block = ACT == 3 && m0 == 0;
   float cs[4] = {0.f, 0.f, 0.f, 0.f};
 
   // one k-tile: stage the fetched values, request the next tile (pref),
