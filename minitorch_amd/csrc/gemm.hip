@@ -418,12 +418,12 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
 // Tiling: 256 threads = 4 waves in a 2x2 grid, block tile 128 x 128 x 16,
 // wave tile 64 x 64 = 2 x 2 MFMA tiles of 32 x 32.  The next k-tile is
 // fetched into registers while the current one is multiplied out of LDS.
-// An operand contiguous along k is staged as [piece][row][k] (rows of 24
-// bf16: the 16 rows a fragment read touches per pass sit in 16 distinct
-// 16-byte bank groups) and read with ds_read_b128; an operand contiguous
-// along its rows (m or n) as [piece][k][row] (rows of 144 bf16) and read with
-// gfx950's transposing ds_read_b64_tr_b16, so staging never transposes in
-// registers.  MFMA 32x32x16 operands: lane l holds row l%32 and
+// An operand contiguous along k is staged as [piece][row][k] (rows of 16
+// bf16, the two 16-byte chunks swapped on rows 8..15 mod 16) and read with
+// ds_read_b128; an operand contiguous along its rows (m or n) as
+// [piece][k][row] (rows of 160 bf16) and read with gfx950's transposing
+// ds_read_b64_tr_b16, so staging never transposes in registers.  Both
+// layouts are free of LDS bank conflicts (SQ_LDS_BANK_CONFLICT = 0).  MFMA 32x32x16 operands: lane l holds row l%32 and
 // k = 8(l/32) + 0..7; accumulator element e of lane l is
 // C[8(e/4) + 4(l/32) + e%4][l%32].
 // ---------------------------------------------------------------------------
@@ -433,8 +433,12 @@ __global__ __launch_bounds__(kGT) void gemm_f32_kernel(const GemmArgs g) {
 namespace x3 {
 constexpr int T = 128;             // tile rows and columns
 constexpr int BK = 16;             // k-tile depth (one MFMA k step)
-constexpr int LDK = BK + 8;        // row stride (bf16) of a k-contiguous plane
-constexpr int LDR = T + 16;        // row stride (bf16) of a row-contiguous plane
+constexpr int LDK = BK;            // row stride (bf16) of a k-contiguous plane
+constexpr int LDR = T + 32;        // row stride (bf16) of a row-contiguous plane
+// k-contiguous rows hold two 16-byte chunks, swapped on rows 8..15 mod 16:
+// a fragment read's 16 rows then cover 16 distinct 16-byte bank groups and
+// a staging store's 8 rows x 4 quarters 32 distinct 8-byte ones
+__device__ __forceinline__ int kswz(int row) { return ((row >> 3) & 1) * 8; }
 constexpr int NV = T * BK / 4 / kGT;  // float4 per thread per operand tile
 }  // namespace x3
 
@@ -532,7 +536,8 @@ struct X3Stage {
 #pragma unroll
     for (int i = 0; i < x3::NV; ++i) {
       const int idx = tid + i * kGT;
-      const int o = KC ? (idx / 4) * x3::LDK + 4 * (idx % 4) : (idx / 32) * x3::LDR + 4 * (idx % 32);
+      const int o = KC ? (idx / 4) * x3::LDK + ((4 * (idx % 4)) ^ x3::kswz(idx / 4))
+                       : (idx / 32) * x3::LDR + 4 * (idx % 32);
       uint2 h, m, l;
       split3(r[i], h, m, l);
       *reinterpret_cast<uint2*>(lds + o) = h;
@@ -544,7 +549,8 @@ struct X3Stage {
   // rb + l%32 and k = 8(l/32) + 0..7
   __device__ __forceinline__ bf16x8 frag(const __bf16* __restrict__ lds, int p, int rb, int lane) const {
     if constexpr (KC) {
-      return *reinterpret_cast<const bf16x8*>(lds + p * PS + (rb + (lane & 31)) * x3::LDK + 8 * (lane >> 5));
+      const int row = rb + (lane & 31);
+      return *reinterpret_cast<const bf16x8*>(lds + p * PS + row * x3::LDK + ((8 * (lane >> 5)) ^ x3::kswz(row)));
     } else {
       // transposing read: in each 16-lane group G, lane j = 4i + q addresses
       // k row 8(G/2) + i (+4 for the second half) at rows rb + 16(G%2) + 4q;
