@@ -519,6 +519,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--gemm-mode", choices=("bf16x3", "fp32"), default="bf16x3",
                     help="--only gpt2/gpt0: the product kernel for shapes of >= 128 x 128")
+    ap.add_argument("--attn-mode", choices=("bf16x3", "fp32"), default="bf16x3",
+                    help="--only c1/gpt2/gpt0: the product kernel of fp32 attention (64-wide heads)")
     ap.add_argument("--only", choices=("all", "c3", "c3series", "c1", "c0attn", "c4", "c4eager", "c4kernel", "gpt2", "gpt0"),
                     default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
@@ -589,6 +591,10 @@ def main():
     if args.only == "c4":
         print(f"[bench] C4 {bench_c4()}", file=sys.stderr)
         return
+    if args.attn_mode == "fp32":
+        from minitorch_amd import kernels as _K
+
+        _K.set_attn_mode(_K.GEMM_FP32)
     if args.only == "c1":
         r1, _ = bench_attention(32, 8, 256, 64, "float32", 1, 1.0, args.steps, args.warmup)
         print(f"[bench] C1 {r1}", file=sys.stderr)

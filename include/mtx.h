@@ -77,6 +77,18 @@ int mtx_attn_fwd(int dtype, int B, int H, int Tq, int Tk, int D,
                  void* o, const int64_t* o_strides,
                  float* lse, float scale, int causal, void* stream);
 
+/*
+ * How fp32 attention (dtype MTX_F32, D = 64) computes its products,
+ * process-wide, read at launch or graph recording: MTX_GEMM_BF16X3 (the
+ * default) on the bf16 matrix cores with every fp32 operand value, P and dS
+ * split into three bf16 pieces and the six piece products of weight >= 2^-16
+ * accumulated in fp32 (as the GEMMs' mode of the same name); MTX_GEMM_FP32 on
+ * fp32 MFMA.  Other head sizes and bf16 attention are not affected.  No reference
+ * counterpart (the reference computes in NumPy float64 after the scale).
+ */
+int mtx_attn_set_mode(int mode);
+int mtx_attn_get_mode(void);
+
 /* Bytes of workspace mtx_attn_bwd needs (the per-row delta = rowsum(dO*O)). */
 size_t mtx_attn_bwd_workspace_bytes(int B, int H, int Tq);
 
@@ -381,7 +393,7 @@ int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const
  * workspace of mtx_gemm_workspace_bytes() bytes, long-K products are split
  * over K and reduced deterministically; without one they run unsplit.
  *
- * Products with M >= 128 and N >= 128 run, by default (MTX_GEMM_BF16X3), on
+ * Products with M >= 128, N >= 128 and M*N*K*batch >= 2^27 run, by default (MTX_GEMM_BF16X3), on
  * the bf16 matrix cores with every fp32 operand value split into three bf16
  * pieces (x = x0 + x1 + x2 to 2^-24 |x|) and the six piece products of
  * weight >= 2^-16 accumulated in fp32: a dot product's error is the fp32

@@ -88,6 +88,8 @@ SIGNATURES = {
     "mtx_embedding2_fwd_f32": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I, _P]),
     "mtx_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "mtx_gemm_set_mode": (_I, [_I]),
+    "mtx_attn_set_mode": (_I, [_I]),
+    "mtx_attn_get_mode": (_I, []),
     "mtx_gemm_get_mode": (_I, []),
     "mtx_gemm_step_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _F, _P, _I64, _P, _I, _I,
                                _P, _P, _I64, _I64, _I, _P, _P]),

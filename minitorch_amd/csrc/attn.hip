@@ -31,6 +31,7 @@
 //    dealt round-robin over the 8 XCDs), so K/V re-reads hit that XCD's L2.
 #include "mtx_common.h"
 
+#include <atomic>
 #include <cmath>
 #include <mutex>
 #include <type_traits>
@@ -53,6 +54,20 @@
 #endif
 // 1: the dK/dV tile body is instantiated twice (masked diagonal tiles,
 // unmasked interior tiles); 0: one body with a run-time mask test
+// split-bf16 fp32 passes at D = 64: one wave per SIMD (the whole register
+// file) for dK/dV and dQ, and the 16-key / 16-query sub-blocks per wave
+#ifndef MTX_X3_DKDV_WAVES1
+#define MTX_X3_DKDV_WAVES1 1
+#endif
+#ifndef MTX_X3_DQ_WAVES1
+#define MTX_X3_DQ_WAVES1 1
+#endif
+#ifndef MTX_X3_NK
+#define MTX_X3_NK 2
+#endif
+#ifndef MTX_X3_NQ
+#define MTX_X3_NQ 2
+#endif
 #ifndef MTX_DKDV_SPLIT
 #define MTX_DKDV_SPLIT 1
 #endif
@@ -195,6 +210,123 @@ struct Lay {
   }
 };
 
+// ---------------------------------------------------------------------------
+// fp32 attention on the bf16 matrix cores (T = f32x3_t)
+// ---------------------------------------------------------------------------
+// The kernels run on fp32 data the way the GEMMs' default mode does: each
+// fp32 operand value x is split into x0 = bf16(x), x1 = bf16(x - x0),
+// x2 = bf16(x - x0 - x1) (round to nearest even, each difference exact), so
+// x = x0 + x1 + x2 to 2^-24 |x|, and a product is the sum of the six piece
+// products of weight >= 2^-16 (x2y0, x1y1, x0y2, x1y0, x0y1, x0y0), each
+// exact in fp32 and added into the fp32 accumulator by the matrix core: six
+// v_mfma_f32_16x16x32_bf16 (6 x 16 cycles) do the work of eight
+// v_mfma_f32_16x16x4_f32 (8 x 32 cycles).  Tiles are fetched as fp32 into
+// registers and split while stored, as three bf16 planes in the bf16 kernels'
+// LDS layout; the register operands (the pre-scaled Q or K, dO, V) and the
+// probabilities P and dS are split the same way.  Global data stays fp32.
+struct f32x3_t {};
+struct Frag3 {
+  bf16x8 p[3];
+};
+}  // namespace
+// (an explicit specialisation lives in the template's own namespace)
+template <> struct Mfma<f32x3_t> {
+  static constexpr int KI = 32;
+  static constexpr int KPL = 8;
+  typedef Frag3 frag;
+  __device__ __forceinline__ static f32x4 mma(const frag& a, const frag& b, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.p[2], b.p[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.p[1], b.p[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.p[0], b.p[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.p[1], b.p[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.p[0], b.p[1], c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.p[0], b.p[0], c, 0, 0, 0);
+  }
+};
+namespace {
+template <typename T> constexpr bool is_x3() { return std::is_same<T, f32x3_t>::value; }
+// element type in global memory and in LDS tiles
+template <typename T> struct GEl { using type = T; };
+template <> struct GEl<f32x3_t> { using type = float; };
+template <typename T> struct LEl { using type = T; };
+template <> struct LEl<f32x3_t> { using type = bf16_t; };
+// planes per LDS tile; every tile of these kernels has 64 rows
+template <typename T> constexpr int planes() { return is_x3<T>() ? 3 : 1; }
+constexpr int kTileRows = 64;
+// the bf16 kernels' swizzled row layout, filled through registers
+template <int D>
+struct Lay<f32x3_t, D> : Lay<bf16_t, D> {
+  static constexpr bool DIRECT = false;
+  static constexpr int PS = kTileRows * D;  // plane stride (bf16 elements)
+};
+
+// eight fp32 values -> three bf16x8 pieces
+__device__ __forceinline__ Frag3 split8(const float (&v)[8]) {
+  Frag3 f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h = (__bf16)v[e];
+    const float r1 = v[e] - (float)h;
+    const __bf16 m = (__bf16)r1;
+    f.p[0][e] = h;
+    f.p[1][e] = m;
+    f.p[2][e] = (__bf16)(r1 - (float)m);
+  }
+  return f;
+}
+
+// an fp32 tile of R rows through registers into three bf16 planes (the
+// fetch of TileRegs<float>; the put splits every value)
+template <int R, int D>
+struct TileRegsX3 {
+  using LY = Lay<bf16_t, D>;
+  static constexpr int CPR = D / 4;                            // 16-byte fp32 chunks per row
+  static constexpr int NCH = R * CPR;
+  static constexpr int PER = (NCH + kThreads - 1) / kThreads;
+  f32x4 r[PER];
+  __device__ __forceinline__ void fetch(const float* __restrict__ g, int64_t ts, int r0, int nrows, int tid) {
+    const float* __restrict__ base = g + (int64_t)r0 * ts;
+    const int its = (int)ts;
+    const int nrel = nrows - r0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * kThreads;
+      const int rr = c / CPR, cc = c % CPR;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if ((NCH % kThreads == 0 || c < NCH) && (r0 + R <= nrows || rr < nrel))
+        v = *reinterpret_cast<const f32x4*>(base + rr * its + cc * 4);
+      r[i] = v;
+    }
+  }
+  __device__ __forceinline__ void put(bf16_t* __restrict__ buf, int, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * kThreads;
+      if (NCH % kThreads != 0 && c >= NCH) continue;
+      const int rr = c / CPR, cc = c % CPR;
+      const int o = LY::at(rr, 4 * cc);
+      uint2 h, m, l;
+      h.x = pack_bf2(r[i][0], r[i][1]);
+      h.y = pack_bf2(r[i][2], r[i][3]);
+      float d0 = r[i][0] - __uint_as_float(h.x << 16), d1 = r[i][1] - __uint_as_float(h.x & 0xffff0000u);
+      float d2 = r[i][2] - __uint_as_float(h.y << 16), d3 = r[i][3] - __uint_as_float(h.y & 0xffff0000u);
+      m.x = pack_bf2(d0, d1);
+      m.y = pack_bf2(d2, d3);
+      d0 -= __uint_as_float(m.x << 16);
+      d1 -= __uint_as_float(m.x & 0xffff0000u);
+      d2 -= __uint_as_float(m.y << 16);
+      d3 -= __uint_as_float(m.y & 0xffff0000u);
+      l.x = pack_bf2(d0, d1);
+      l.y = pack_bf2(d2, d3);
+      *reinterpret_cast<uint2*>(buf + o) = h;
+      *reinterpret_cast<uint2*>(buf + Lay<f32x3_t, D>::PS + o) = m;
+      *reinterpret_cast<uint2*>(buf + 2 * Lay<f32x3_t, D>::PS + o) = l;
+    }
+  }
+};
+template <typename T, int R, int D> struct TileRegsSel { using type = TileRegs<T, R, D>; };
+template <int R, int D> struct TileRegsSel<f32x3_t, R, D> { using type = TileRegsX3<R, D>; };
+
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 
@@ -296,11 +428,29 @@ struct DMap {
   static constexpr int KC = (QPL + KPL - 1) / KPL;
 };
 
+// the 8 fp32 values of the bf16 quarter-map fragment kc of a global row
+// (D = 16: 4 values, then zeros)
+template <int D>
+__device__ __forceinline__ void load8(const float* __restrict__ p, int g, int kc, float (&v)[8]) {
+  constexpr int QPL = D / 4;
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p + g * QPL + 8 * kc);
+  const f32x4 b = QPL >= 8 ? *reinterpret_cast<const f32x4*>(p + g * QPL + 8 * kc + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = a[e];
+    v[e + 4] = b[e];
+  }
+}
+
 // Fragment of a row stored row-major (in LDS or global): row pointer p.
 template <typename T, int D>
-__device__ __forceinline__ typename Mfma<T>::frag dfrag(const T* __restrict__ p, int g, int kc) {
+__device__ __forceinline__ typename Mfma<T>::frag dfrag(const typename GEl<T>::type* __restrict__ p, int g, int kc) {
   constexpr int QPL = D / 4;
-  if constexpr (sizeof(T) == 4) {
+  if constexpr (is_x3<T>()) {
+    float v[8];
+    load8<D>(p, g, kc, v);
+    return split8(v);
+  } else if constexpr (sizeof(T) == 4) {
     return p[g * QPL + kc];
   } else if constexpr (QPL >= 8) {
     const uint4 u = *reinterpret_cast<const uint4*>(p + g * QPL + 8 * kc);
@@ -351,9 +501,20 @@ struct LaneOffs {
   }
 };
 
+template <int D>
+struct LaneOffs<f32x3_t, D> : LaneOffs<bf16_t, D> {
+  __device__ __forceinline__ LaneOffs(int n, int g) : LaneOffs<bf16_t, D>(n, g) {}
+};
+
 template <typename T, int D>
-__device__ __forceinline__ typename Mfma<T>::frag lfrag(const T* __restrict__ p) {
-  if constexpr (sizeof(T) == 4) {
+__device__ __forceinline__ typename Mfma<T>::frag lfrag(const typename LEl<T>::type* __restrict__ p) {
+  if constexpr (is_x3<T>()) {
+    constexpr int PS = Lay<f32x3_t, D>::PS;
+    Frag3 f;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) f.p[k] = lfrag<bf16_t, D>(p + k * PS);
+    return f;
+  } else if constexpr (sizeof(T) == 4) {
     return *p;
   } else if constexpr (D / 4 >= 8) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
@@ -365,9 +526,15 @@ __device__ __forceinline__ typename Mfma<T>::frag lfrag(const T* __restrict__ p)
 
 // transposed operand for k-step s; `to` = LaneOffs::t(dt)
 template <typename T, int D>
-__device__ __forceinline__ typename Mfma<T>::frag ltfrag(const T* __restrict__ buf, int s, int to) {
+__device__ __forceinline__ typename Mfma<T>::frag ltfrag(const typename LEl<T>::type* __restrict__ buf, int s, int to) {
   constexpr int LD = Lay<T, D>::LD;
-  if constexpr (sizeof(T) == 4) {
+  if constexpr (is_x3<T>()) {
+    constexpr int PS = Lay<f32x3_t, D>::PS;
+    Frag3 f;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) f.p[k] = ltfrag<bf16_t, D>(buf + k * PS, s, to);
+    return f;
+  } else if constexpr (sizeof(T) == 4) {
     return buf[(16 * (s >> 2) + (s & 3)) * LD + to];
   } else {
     const T* p = buf + 32 * s * LD + to;
@@ -390,6 +557,22 @@ __device__ __forceinline__ typename Mfma<T>::frag scale_frag(typename Mfma<T>::f
   }
 }
 
+// Fragment of a global row multiplied by c: for T = f32x3_t the product is
+// formed in fp32 and then split (scaling the pieces would round each).
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::frag dfrag_scaled(const typename GEl<T>::type* __restrict__ p, int g,
+                                                               int kc, float c) {
+  if constexpr (is_x3<T>()) {
+    float v[8];
+    load8<D>(p, g, kc, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] *= c;
+    return split8(v);
+  } else {
+    return scale_frag<T>(dfrag<T, D>(p, g, kc), c);
+  }
+}
+
 // acc + sum of the elements of an operand fragment (bf16: v_dot2 with ones).
 template <typename T>
 __device__ __forceinline__ float frag_sum(typename Mfma<T>::frag f, float acc) {
@@ -409,7 +592,11 @@ __device__ __forceinline__ float frag_sum(typename Mfma<T>::frag f, float acc) {
 // B operand from C-layout accumulators c[j16] (16x16 sub-tiles along j), step s.
 template <typename T, int NJ16>
 __device__ __forceinline__ typename Mfma<T>::frag pfrag(const f32x4 (&c)[NJ16], int s) {
-  if constexpr (sizeof(T) == 4) {
+  if constexpr (is_x3<T>()) {
+    const f32x4 a = c[2 * s], b = c[2 * s + 1];
+    const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return split8(v);
+  } else if constexpr (sizeof(T) == 4) {
     return c[s >> 2][s & 3];
   } else {
     const f32x4 a = c[2 * s], b = c[2 * s + 1];
@@ -469,23 +656,26 @@ void attn_fwd_kernel(const FwdArgs a) {
   using LY = Lay<T, D>;
   constexpr int LD = LY::LD;  // LDS row stride
   constexpr int KSZ = BK * LD;
-  constexpr int NBUF = (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * KSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
+  using G = typename GEl<T>::type;   // element type in global memory
+  using LT = typename LEl<T>::type;  // element type of the LDS tiles
+  constexpr int NPLN = planes<T>();
+  constexpr int NBUF = is_x3<T>() ? 1 : (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * KSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
   static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
   // separate arrays per buffer, picked with compile-time parities: the
   // compiler then sees the direct loads into one buffer and the reads of the
   // other as disjoint and does not wait for the loads before the reads
-  __shared__ __attribute__((aligned(16))) T K0[KSZ], V0[KSZ];
-  __shared__ __attribute__((aligned(16))) T K1[NBUF == 2 ? KSZ : 1], V1[NBUF == 2 ? KSZ : 1];
+  __shared__ __attribute__((aligned(16))) LT K0[KSZ * NPLN], V0[KSZ * NPLN];
+  __shared__ __attribute__((aligned(16))) LT K1[NBUF == 2 ? KSZ * NPLN : 1], V1[NBUF == 2 ? KSZ * NPLN : 1];
 
   const int BH = a.B * a.H;
   const int nqb = (a.Tq + BQ - 1) / BQ;
   int qb, bh;
   map_block(blockIdx.x, nqb, BH, a.causal != 0, qb, bh);
   const int b = bh / a.H, h = bh % a.H;
-  const T* __restrict__ qp = static_cast<const T*>(a.q) + b * a.sq.b + h * a.sq.h;
-  const T* __restrict__ kp = static_cast<const T*>(a.k) + b * a.sk.b + h * a.sk.h;
-  const T* __restrict__ vp = static_cast<const T*>(a.v) + b * a.sv.b + h * a.sv.h;
-  T* __restrict__ op = static_cast<T*>(a.o) + b * a.so.b + h * a.so.h;
+  const G* __restrict__ qp = static_cast<const G*>(a.q) + b * a.sq.b + h * a.sq.h;
+  const G* __restrict__ kp = static_cast<const G*>(a.k) + b * a.sk.b + h * a.sk.h;
+  const G* __restrict__ vp = static_cast<const G*>(a.v) + b * a.sv.b + h * a.sv.h;
+  G* __restrict__ op = static_cast<G*>(a.o) + b * a.so.b + h * a.so.h;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -505,7 +695,7 @@ void attn_fwd_kernel(const FwdArgs a) {
     const int rr = row < a.Tq ? row : a.Tq - 1;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      frag f = scale_frag<T>(dfrag<T, D>(qp + (int64_t)rr * a.sq.t, g, kc), c);
+      frag f = dfrag_scaled<T, D>(qp + (int64_t)rr * a.sq.t, g, kc, c);
       if (row >= a.Tq) f = frag{};
       qf[qs][kc] = f;
     }
@@ -535,7 +725,7 @@ void attn_fwd_kernel(const FwdArgs a) {
   const int ntile = (kend + BK - 1) / BK;
   const LaneOffs<T, D> lo(n, g);
   TileDma<T, BK, D> kdma, vdma;  // bf16: direct global -> LDS
-  TileRegs<T, BK, D> kreg, vreg;  // fp32: through registers
+  typename TileRegsSel<T, BK, D>::type kreg, vreg;  // fp32: through registers
   if constexpr (LY::DIRECT) {
     kdma.init(kp, a.sk.t, a.Tk, wid, lane);
     vdma.init(vp, a.sv.t, a.Tk, wid, lane);
@@ -553,8 +743,8 @@ void attn_fwd_kernel(const FwdArgs a) {
     const int P = int(par) % NBUF;  // a constant for the unrolled (direct-load) loop
     const int PN = (P + 1) % NBUF;
     const int kb = it * BK;
-    T* __restrict__ Kb = P ? K1 : K0;
-    T* __restrict__ Vb = P ? V1 : V0;
+    LT* __restrict__ Kb = P ? K1 : K0;
+    LT* __restrict__ Vb = P ? V1 : V0;
     if constexpr (LY::DIRECT) {
       wait_dma();
     } else {
@@ -661,10 +851,21 @@ void attn_fwd_kernel(const FwdArgs a) {
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) s[qs][kt][r] = __builtin_amdgcn_exp2f(s[qs][kt][r]);
+        if constexpr (is_x3<T>()) {
+          // the fp32 probabilities (which the three pieces carry to 2^-24),
+          // in the order the dropout variant adds them
 #pragma unroll
-        for (int st = 0; st < NS; ++st) {
-          pf[qs][st] = pfrag<T, 4>(s[qs], st);
-          l[qs] = frag_sum<T>(pf[qs][st], l[qs]);
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) l[qs] += s[qs][kt][r];
+#pragma unroll
+          for (int st = 0; st < NS; ++st) pf[qs][st] = pfrag<T, 4>(s[qs], st);
+        } else {
+#pragma unroll
+          for (int st = 0; st < NS; ++st) {
+            pf[qs][st] = pfrag<T, 4>(s[qs], st);
+            l[qs] = frag_sum<T>(pf[qs][st], l[qs]);
+          }
         }
       }
     }
@@ -697,7 +898,7 @@ void attn_fwd_kernel(const FwdArgs a) {
       const float inv = 1.0f / lt;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        store4<T>(op + (int64_t)qi * a.so.t + 16 * dt + 4 * g, acc[qs][dt] * inv);
+        store4<G>(op + (int64_t)qi * a.so.t + 16 * dt + 4 * g, acc[qs][dt] * inv);
       if (g == 0) a.lse[(int64_t)bh * a.Tq + qi] = (m[qs] + __log2f(lt)) * kLn2;
     }
   }
@@ -741,7 +942,7 @@ template <typename T>
 constexpr int dkdv_waves() { return sizeof(T) == 2 ? MTX_DKDV_WAVES : kWaves; }
 
 template <typename T, int D, int NK, bool DROP>
-__global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 1 : 2) void attn_dkdv_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4) || (is_x3<T>() && D == 64 && MTX_X3_DKDV_WAVES1)) ? 1 : 2) void attn_dkdv_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using DM = DMap<T, D>;
@@ -755,12 +956,15 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
   using LY = Lay<T, D>;
   constexpr int LD = LY::LD;
   constexpr int RSZ = BQ * LD;
-  constexpr int NBUF = (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
+  using G = typename GEl<T>::type;   // element type in global memory
+  using LT = typename LEl<T>::type;  // element type of the LDS tiles
+  constexpr int NPLN = planes<T>();
+  constexpr int NBUF = is_x3<T>() ? 1 : (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
   static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
   // separate arrays per buffer, picked with compile-time parities (see the
   // forward kernel)
-  __shared__ __attribute__((aligned(16))) T Q0[RSZ], D0[RSZ];
-  __shared__ __attribute__((aligned(16))) T Q1[NBUF == 2 ? RSZ : 1], D1[NBUF == 2 ? RSZ : 1];
+  __shared__ __attribute__((aligned(16))) LT Q0[RSZ * NPLN], D0[RSZ * NPLN];
+  __shared__ __attribute__((aligned(16))) LT Q1[NBUF == 2 ? RSZ * NPLN : 1], D1[NBUF == 2 ? RSZ * NPLN : 1];
   // per query of the tile: -lse*log2(e) and -delta, the starting accumulators
   // of the S and dP MFMAs, so they yield log2(P) and dP - delta directly
   __shared__ __attribute__((aligned(16))) float L0[BQ], E0[BQ], L1[BQ], E1[BQ];
@@ -770,10 +974,10 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
   int kbk, bh;
   map_block(blockIdx.x, nkb, BH, false, kbk, bh);
   const int b = bh / a.H, h = bh % a.H;
-  const T* __restrict__ qp = static_cast<const T*>(a.q) + b * a.sq.b + h * a.sq.h;
-  const T* __restrict__ kp = static_cast<const T*>(a.k) + b * a.sk.b + h * a.sk.h;
-  const T* __restrict__ vp = static_cast<const T*>(a.v) + b * a.sv.b + h * a.sv.h;
-  const T* __restrict__ dop = static_cast<const T*>(a.dout) + b * a.sdo.b + h * a.sdo.h;
+  const G* __restrict__ qp = static_cast<const G*>(a.q) + b * a.sq.b + h * a.sq.h;
+  const G* __restrict__ kp = static_cast<const G*>(a.k) + b * a.sk.b + h * a.sk.h;
+  const G* __restrict__ vp = static_cast<const G*>(a.v) + b * a.sv.b + h * a.sv.h;
+  const G* __restrict__ dop = static_cast<const G*>(a.dout) + b * a.sdo.b + h * a.sdo.h;
   const float* __restrict__ lsep = a.lse + (int64_t)bh * a.Tq;
   const float* __restrict__ delp = a.delta + (int64_t)bh * a.Tq;
 
@@ -798,7 +1002,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
   const int ntile = qstart < a.Tq ? (a.Tq - qstart + BQ - 1) / BQ : 0;
   const LaneOffs<T, D> lo(n, g);
   TileDma<T, BQ, D, NWV> qdma, ddma;  // bf16: direct global -> LDS
-  TileRegs<T, BQ, D> qreg, dreg;       // fp32: through registers
+  typename TileRegsSel<T, BQ, D>::type qreg, dreg;       // fp32: through registers
   if constexpr (LY::DIRECT) {
     qdma.init(qp, a.sq.t, a.Tq, wid, lane);
     ddma.init(dop, a.sdo.t, a.Tq, wid, lane);
@@ -807,7 +1011,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
   // the next tile's loads: lse / delta (through registers, raw; converted
   // when stored, so the loads are not waited for here) first, so that waiting
   // for them never waits for the direct tile loads issued after them
-  auto fetch = [&](int qt, T* qdst, T* ddst) {
+  auto fetch = [&](int qt, LT* qdst, LT* ddst) {
     if (tid < BQ) {
       const int qi = min(qt + tid, a.Tq - 1);
       lse_r = lsep[qi];
@@ -833,7 +1037,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
     const int rr = row < a.Tk ? row : a.Tk - 1;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      frag fk = scale_frag<T>(dfrag<T, D>(kp + (int64_t)rr * a.sk.t, g, kc), c);
+      frag fk = dfrag_scaled<T, D>(kp + (int64_t)rr * a.sk.t, g, kc, c);
       frag fv = dfrag<T, D>(vp + (int64_t)rr * a.sv.t, g, kc);
       if (row >= a.Tk) { fk = frag{}; fv = frag{}; }
       kf[ks][kc] = fk;
@@ -851,8 +1055,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
     const int P = int(par) % NBUF;
     const int PN = (P + 1) % NBUF;
     const int qt = qstart + it * BQ;
-    T* __restrict__ Qb = P ? Q1 : Q0;
-    T* __restrict__ Db = P ? D1 : D0;
+    LT* __restrict__ Qb = P ? Q1 : Q0;
+    LT* __restrict__ Db = P ? D1 : D0;
     float* __restrict__ lse_b = P ? L1 : L0;
     float* __restrict__ del_b = P ? E1 : E0;
     if constexpr (LY::DIRECT) {
@@ -1023,7 +1227,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), D == 128 && sizeof(T) == 4 ? 
 // FD: also computes delta[i] = sum_d dO[i,d] O[i,d] for its rows (from the
 // same fragments it loads anyway) and writes it for the dK/dV pass.
 template <typename T, int D, int NQ, bool FD, bool DROP>
-__global__ __launch_bounds__(kThreads, (sizeof(T) == 2 && D <= 64) ? MTX_DQ_WAVES : (D == 128 && sizeof(T) == 4 ? 1 : 2))
+__global__ __launch_bounds__(kThreads, (sizeof(T) == 2 && D <= 64) ? MTX_DQ_WAVES : (((D == 128 && sizeof(T) == 4) || (is_x3<T>() && D == 64 && MTX_X3_DQ_WAVES1)) ? 1 : 2))
 void attn_dq_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
@@ -1037,22 +1241,25 @@ void attn_dq_kernel(const BwdArgs a) {
   using LY = Lay<T, D>;
   constexpr int LD = LY::LD;
   constexpr int RSZ = BK * LD;
-  constexpr int NBUF = (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
+  using G = typename GEl<T>::type;   // element type in global memory
+  using LT = typename LEl<T>::type;  // element type of the LDS tiles
+  constexpr int NPLN = planes<T>();
+  constexpr int NBUF = is_x3<T>() ? 1 : (sizeof(T) == 4 && D <= 64 && MTX_F32_NBUF1) ? 1 : (2 * RSZ * (int)sizeof(T) * 2 <= 80 * 1024 ? 2 : 1);
   static_assert(!LY::DIRECT || NBUF == 2, "direct tile loads need two buffers");
   // separate arrays per buffer, picked with compile-time parities (see the
   // forward kernel)
-  __shared__ __attribute__((aligned(16))) T K0[RSZ], V0[RSZ];
-  __shared__ __attribute__((aligned(16))) T K1[NBUF == 2 ? RSZ : 1], V1[NBUF == 2 ? RSZ : 1];
+  __shared__ __attribute__((aligned(16))) LT K0[RSZ * NPLN], V0[RSZ * NPLN];
+  __shared__ __attribute__((aligned(16))) LT K1[NBUF == 2 ? RSZ * NPLN : 1], V1[NBUF == 2 ? RSZ * NPLN : 1];
 
   const int BH = a.B * a.H;
   const int nqb = (a.Tq + BQ - 1) / BQ;
   int qb, bh;
   map_block(blockIdx.x, nqb, BH, a.causal != 0, qb, bh);
   const int b = bh / a.H, h = bh % a.H;
-  const T* __restrict__ qp = static_cast<const T*>(a.q) + b * a.sq.b + h * a.sq.h;
-  const T* __restrict__ kp = static_cast<const T*>(a.k) + b * a.sk.b + h * a.sk.h;
-  const T* __restrict__ vp = static_cast<const T*>(a.v) + b * a.sv.b + h * a.sv.h;
-  const T* __restrict__ dop = static_cast<const T*>(a.dout) + b * a.sdo.b + h * a.sdo.h;
+  const G* __restrict__ qp = static_cast<const G*>(a.q) + b * a.sq.b + h * a.sq.h;
+  const G* __restrict__ kp = static_cast<const G*>(a.k) + b * a.sk.b + h * a.sk.h;
+  const G* __restrict__ vp = static_cast<const G*>(a.v) + b * a.sv.b + h * a.sv.h;
+  const G* __restrict__ dop = static_cast<const G*>(a.dout) + b * a.sdo.b + h * a.sdo.h;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1074,7 +1281,7 @@ void attn_dq_kernel(const BwdArgs a) {
     const int rr = ok ? row : a.Tq - 1;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      frag fq = scale_frag<T>(dfrag<T, D>(qp + (int64_t)rr * a.sq.t, g, kc), c);
+      frag fq = dfrag_scaled<T, D>(qp + (int64_t)rr * a.sq.t, g, kc, c);
       frag fd = dfrag<T, D>(dop + (int64_t)rr * a.sdo.t, g, kc);
       if (!ok) { fq = frag{}; fd = frag{}; }
       qf[qs][kc] = fq;
@@ -1084,14 +1291,22 @@ void attn_dq_kernel(const BwdArgs a) {
     float dl;
     if constexpr (FD) {
       // this lane's quarter of the row, then the sum over the 4 lanes of the row
-      const T* __restrict__ orow = static_cast<const T*>(a.o) + b * a.so.b + h * a.so.h + (int64_t)rr * a.so.t;
+      const G* __restrict__ orow = static_cast<const G*>(a.o) + b * a.so.b + h * a.so.h + (int64_t)rr * a.so.t;
       dl = 0.f;
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        const frag fo = dfrag<T, D>(orow, g, kc);
-        if constexpr (sizeof(T) == 4) {
+        if constexpr (is_x3<T>()) {
+          // delta from the fp32 values (dO reloaded: its fragments are split)
+          float ov[8], dv[8];
+          load8<D>(orow, g, kc, ov);
+          load8<D>(dop + (int64_t)rr * a.sdo.t, g, kc, dv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dl = fmaf(ov[e], dv[e], dl);
+        } else if constexpr (sizeof(T) == 4) {
+          const frag fo = dfrag<T, D>(orow, g, kc);
           dl = fmaf(fo, df[qs][kc], dl);
         } else {
+          const frag fo = dfrag<T, D>(orow, g, kc);
 #pragma unroll
           for (int e = 0; e < 8; ++e) dl = fmaf((float)fo[e], (float)df[qs][kc][e], dl);
         }
@@ -1116,7 +1331,7 @@ void attn_dq_kernel(const BwdArgs a) {
   const int ntile = (kend + BK - 1) / BK;
   const LaneOffs<T, D> lo(n, g);
   TileDma<T, BK, D> kdma, vdma;  // bf16: direct global -> LDS
-  TileRegs<T, BK, D> kreg, vreg;  // fp32: through registers
+  typename TileRegsSel<T, BK, D>::type kreg, vreg;  // fp32: through registers
   if constexpr (LY::DIRECT) {
     kdma.init(kp, a.sk.t, a.Tk, wid, lane);
     vdma.init(vp, a.sv.t, a.Tk, wid, lane);
@@ -1138,8 +1353,8 @@ void attn_dq_kernel(const BwdArgs a) {
     const int P = int(par) % NBUF;  // a constant for the unrolled (direct-load) loop
     const int PN = (P + 1) % NBUF;
     const int kb = it * BK;
-    T* __restrict__ Kb = P ? K1 : K0;
-    T* __restrict__ Vb = P ? V1 : V0;
+    LT* __restrict__ Kb = P ? K1 : K0;
+    LT* __restrict__ Vb = P ? V1 : V0;
     if constexpr (LY::DIRECT) {
       wait_dma();
     } else {
@@ -1289,6 +1504,9 @@ void attn_dq_kernel(const BwdArgs a) {
 #endif
 template <typename T, int D> struct Cfg;
 template <int D> struct Cfg<float, D> { static constexpr int NQ = 1, NK = 1, NQF = 1; };
+template <int D> struct Cfg<f32x3_t, D> {
+  static constexpr int NQ = D == 64 ? MTX_X3_NQ : 1, NK = D == 64 ? MTX_X3_NK : 1, NQF = 1;
+};
 template <int D> struct Cfg<bf16_t, D> {
   static constexpr int NQ = D <= 64 ? MTX_DQ_NQ_BF16 : 1;
   static constexpr int NQF = D <= 64 ? MTX_FWD_NQ_BF16 : 2;
@@ -1354,7 +1572,7 @@ int launch_bwd(const BwdArgs& a, int phases, hipStream_t st) {
   const bool fuse = (phases & MTX_ATTN_BWD_DELTA) && (phases & MTX_ATTN_BWD_DQ);
   if ((phases & MTX_ATTN_BWD_DELTA) && !fuse) {
     const int64_t rows = (int64_t)a.B * a.H * a.Tq;
-    hipLaunchKernelGGL((attn_delta_kernel<T, D>), dim3((unsigned)((rows + kThreads - 1) / kThreads)),
+    hipLaunchKernelGGL((attn_delta_kernel<typename GEl<T>::type, D>), dim3((unsigned)((rows + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, st, a);
     MTX_LAUNCHED();
   }
@@ -1405,10 +1623,34 @@ int dispatch_bwd(int D, const BwdArgs& a, int phases, hipStream_t st) {
   }
 }
 
+// fp32 attention with 64-wide heads runs on the bf16 matrix cores
+// (T = f32x3_t) unless mtx_attn_set_mode chose the fp32 MFMA kernels.
+// Smaller heads stay on fp32 MFMA: at D = 16, T = 32 (the C0 model's
+// attention, latency bound) the split's staging work made the training step
+// 17% slower.
+std::atomic<int> g_attn_mode{MTX_GEMM_BF16X3};
+
+bool use_x3(int dtype, int D) {
+  return dtype == MTX_F32 && D == 64 && g_attn_mode.load(std::memory_order_relaxed) == MTX_GEMM_BF16X3;
+}
+
+int dispatch_fwd_x3(const FwdArgs& a, hipStream_t st) { return launch_fwd<f32x3_t, 64>(a, st); }
+
+int dispatch_bwd_x3(const BwdArgs& a, int phases, hipStream_t st) { return launch_bwd<f32x3_t, 64>(a, phases, st); }
+
 }  // namespace
 }  // namespace mtx
 
 using namespace mtx;
+
+extern "C" int mtx_attn_set_mode(int mode) {
+  MTX_CHECK_ARG(mode == MTX_GEMM_FP32 || mode == MTX_GEMM_BF16X3,
+                "attention mode %d must be MTX_GEMM_FP32 (0) or MTX_GEMM_BF16X3 (1)", mode);
+  g_attn_mode.store(mode);
+  return MTX_OK;
+}
+
+extern "C" int mtx_attn_get_mode(void) { return g_attn_mode.load(); }
 
 namespace {
 int check_keep(const uint8_t* keep, int64_t keep_ld, float keep_scale, int Tk) {
@@ -1440,6 +1682,7 @@ int attn_fwd_impl(int dtype, int B, int H, int Tq, int Tk, int D,
   FwdArgs a{q, s3(q_strides), k, s3(k_strides), v, s3(v_strides), o, s3(o_strides),
             lse, B, H, Tq, Tk, scale, causal ? 1 : 0, keep, keep_ld, keep_scale};
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_x3(dtype, D)) return dispatch_fwd_x3(a, st);
   return dtype == MTX_F32 ? dispatch_fwd<float>(D, a, st) : dispatch_fwd<bf16_t>(D, a, st);
 }
 }  // namespace
@@ -1556,6 +1799,7 @@ int attn_bwd_impl(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
             dq, s3(dq_strides), dk, s3(dk_strides), dv, s3(dv_strides),
             B, H, Tq, Tk, scale, causal ? 1 : 0, accumulate ? 1 : 0, keep, keep_ld, keep_scale};
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_x3(dtype, D)) return dispatch_bwd_x3(a, phases, st);
   return dtype == MTX_F32 ? dispatch_bwd<float>(D, a, phases, st)
                           : dispatch_bwd<bf16_t>(D, a, phases, st);
 }

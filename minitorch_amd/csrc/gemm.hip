@@ -1150,7 +1150,14 @@ int launch_tile(const GemmArgs& g, bool ak, bool bn1, hipStream_t st) {
 // the decode step's skinny ones, always take the fp32 kernels.
 std::atomic<int> g_gemm_mode{MTX_GEMM_BF16X3};
 
-bool use_x3(int M, int N) { return g_gemm_mode.load(std::memory_order_relaxed) == MTX_GEMM_BF16X3 && M >= 128 && N >= 128; }
+// Products below 2^27 multiply-adds (the C0 model's 512-row ones: a handful
+// of 128 x 128 tiles, latency bound) stay on the fp32 kernel's 64 x 64
+// tiles: on the split kernel the C0 training step took 0.445 ms against
+// 0.379 ms.
+bool use_x3(int M, int N, int K, int batch) {
+  return g_gemm_mode.load(std::memory_order_relaxed) == MTX_GEMM_BF16X3 && M >= 128 && N >= 128 &&
+         (int64_t)M * N * K * batch >= ((int64_t)1 << 27);
+}
 
 // Split K only when the 128 x 128 tiles leave the CUs idle (weight gradients,
 // K = B*T): aim at MTX_X3_SPLIT_TARGET workgroups (two fit a CU), each split
@@ -1290,7 +1297,7 @@ int gemm_impl(int M, int N, int K, int batch, float alpha, const float* a, int64
     return MTX_OK;
   }
   const bool ak = sa_k == 1, bn1 = sb_n == 1;
-  const bool split3 = use_x3(M, N);
+  const bool split3 = use_x3(M, N, K, batch);
   Plan p = split3 ? plan_x3(M, N, K, batch, workspace ? workspace_bytes : 0)
                   : plan_gemm(M, N, K, batch, workspace ? workspace_bytes : 0);
   g.ksplit = p.ksplit;

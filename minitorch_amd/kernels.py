@@ -483,6 +483,20 @@ def get_gemm_mode() -> int:
     return int(L.lib().mtx_gemm_get_mode())
 
 
+def set_attn_mode(mode: int) -> int:
+    """Select how fp32 attention with 64-wide heads computes its
+    products (mtx_attn_set_mode): GEMM_BF16X3 (the default: three bf16
+    pieces per fp32 value on the bf16 matrix cores) or GEMM_FP32 (fp32
+    MFMA).  Returns the previous mode."""
+    prev = int(L.lib().mtx_attn_get_mode())
+    L.call("mtx_attn_set_mode", int(mode))
+    return prev
+
+
+def get_attn_mode() -> int:
+    return int(L.lib().mtx_attn_get_mode())
+
+
 def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=1,
          sa=None, sb=None, sc=None, act=GEMM_ACT_NONE, aux=None, colsum=None, colsum_accumulate=False):
     """C = alpha*A@B + beta*C (+bias) with explicit (row, col, batch) strides

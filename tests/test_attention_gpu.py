@@ -98,6 +98,17 @@ def _run(dev, q, k, v, do, scale, causal, dtype, views=None):
     return f(o), f(dq), f(dk), f(dv), f(lse)
 
 
+@pytest.fixture(params=["bf16x3", "fp32"])
+def attn_mode(request, dev):
+    """fp32 attention tests run under both product kernels (they differ for
+    64-wide heads): the three-piece bf16 split (the default) and fp32 MFMA."""
+    from minitorch_amd import kernels as Kn
+
+    prev = Kn.set_attn_mode(Kn.GEMM_BF16X3 if request.param == "bf16x3" else Kn.GEMM_FP32)
+    yield request.param
+    Kn.set_attn_mode(prev)
+
+
 CASES = [
     # (B, H, Tq, Tk, D, causal)
     (1, 1, 1, 1, 64, True),
@@ -114,8 +125,8 @@ CASES = [
 
 
 @pytest.mark.parametrize("B,H,Tq,Tk,D,causal", CASES)
-def test_fp32_small(dev, B, H, Tq, Tk, D, causal):
-    _say(f"[attn fp32] B={B} H={H} Tq={Tq} Tk={Tk} D={D} causal={causal}")
+def test_fp32_small(dev, attn_mode, B, H, Tq, Tk, D, causal):
+    _say(f"[attn fp32 {attn_mode}] B={B} H={H} Tq={Tq} Tk={Tk} D={D} causal={causal}")
     rng = np.random.default_rng(1000 + Tq + 7 * Tk + D)
     q = rng.standard_normal((B, H, Tq, D), dtype=np.float32)
     k = rng.standard_normal((B, H, Tk, D), dtype=np.float32)
@@ -161,7 +172,7 @@ def test_bf16_small(dev, B, H, Tq, Tk, D, causal):
                 _emu_bar(got[b, h], e[b, h], f"{name}[{b},{h}]")
 
 
-def test_fp32_strided_split_heads(dev):
+def test_fp32_strided_split_heads(dev, attn_mode):
     """q/k/v as the (B,H,T,D) strided views _split_heads makes of a (B,T,C)
     projection (transformer.py:26-28): strides (T*C, D, C, 1), no copies."""
     B, T, H, D = 2, 96, 6, 64
@@ -179,7 +190,7 @@ def test_fp32_strided_split_heads(dev):
     _fp32_bar(dv, rdv, "dv")
 
 
-def test_accumulate_flag(dev):
+def test_accumulate_flag(dev, attn_mode):
     """accumulate=1 adds into existing gradients (_accum_grad, tensor.py:29-33)."""
     from minitorch_amd import kernels as K
 
@@ -197,7 +208,7 @@ def test_accumulate_flag(dev):
 
 
 @pytest.mark.parametrize("dtype_name", ["float32", "bfloat16"])
-def test_phases_split_match_fused(dev, dtype_name):
+def test_phases_split_match_fused(dev, attn_mode, dtype_name):
     """mtx_attn_bwd_phase run as three calls (standalone delta kernel, then
     dQ, then dK/dV) gives the oracle's gradients and agrees with the fused
     DELTA|DQ path of mtx_attn_bwd up to the summation order of delta."""
@@ -229,10 +240,10 @@ def test_phases_split_match_fused(dev, dtype_name):
         (_fp32_bar if dtype == "float32" else _bf16_bar)(b, r, name)
 
 
-def test_c1_full(dev):
+def test_c1_full(dev, attn_mode):
     """Config C1: B=32, H=8, T=256, D=64 fp32, q,k,v,dO ~ N(0,1) drawn in that
     order from default_rng(1); scale 1/8.  Full tensors vs the oracle."""
-    _say("[attn C1 full] B=32 H=8 T=256 D=64 fp32")
+    _say(f"[attn C1 full {attn_mode}] B=32 H=8 T=256 D=64 fp32")
     rng = np.random.default_rng(1)
     shp = (32, 8, 256, 64)
     q, k, v, do = (rng.standard_normal(shp, dtype=np.float32) for _ in range(4))

@@ -65,12 +65,12 @@ def dot_tol(K):
     (64, 384, 1536, False, False, 1, True),     # skinny, K split over 3 workgroups
     (17, 40, 1000, True, False, 2, True),       # skinny split, scalar A loads, batched
     (64, 64, 4100, False, False, 1, False),     # K past the skinny range: tiled split-K
-    # >= 128 x 128: the bf16-split kernel in its default mode
-    (256, 384, 1000, False, True, 1, True),     # ragged last k-tile, B contiguous along k
-    (300, 200, 77, True, True, 2, True),        # edge tiles on both sides, both operands transposed
-    (200, 150, 33, False, False, 1, True),      # row strides of 33: no aligned vector loads
+    # >= 128 x 128 and >= 2^27 multiply-adds: the bf16-split kernel in its default mode
+    (256, 384, 1400, False, True, 1, True),     # ragged last k-tile, B contiguous along k
+    (300, 260, 1111, True, True, 2, True),      # edge tiles on both sides, both operands transposed
+    (4100, 1000, 33, False, False, 1, True),    # row strides of 33: no aligned vector loads
     (1000, 130, 5000, True, False, 1, False),   # split K with edge tiles
-    (512, 512, 16, False, False, 4, True),      # one k-tile, batched
+    (1024, 1024, 16, False, False, 8, True),    # one k-tile, batched
 ])
 def test_gemm(dev, gemm_mode, M, N, K, ta, tb, batch, bias):
     from minitorch_amd import kernels as Kn
@@ -523,7 +523,7 @@ def test_gemm_gelu_epilogues(dev, gemm_mode, M, N, K):
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K,acc", [(384, 1152, 16384, False), (384, 65, 4096, True), (200, 130, 777, False),
                                        (64, 48, 300, True), (7, 5, 3, False), (384, 384, 0, True),
-                                       (130, 300, 2001, True), (1536, 384, 16384, False)])
+                                       (130, 300, 4001, True), (1536, 384, 16384, False)])
 def test_gemm_wgrad_colsum(dev, gemm_mode, M, N, K, acc):
     """mtx_gemm_wgrad_f32: dW = A @ B (+ beta C) and the column sums of B (a
     Linear's bias gradient) from one launch, against NumPy float64.  The
