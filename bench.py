@@ -561,10 +561,13 @@ def main():
             _K.set_gemm_mode(_K.GEMM_FP32)
         if args.attn_mode == "fp32":
             _K.set_attn_mode(_K.GEMM_FP32)
+        # the modes as the library reports them, not as requested
+        gm = "bf16x3" if _K.get_gemm_mode() == _K.GEMM_BF16X3 else "fp32"
+        am = "bf16x3" if _K.get_attn_mode() == _K.GEMM_BF16X3 else "fp32"
         for graph in (True, False):
             ms, losses = bench_gpt(c, 2, args.steps, args.warmup, graph=graph)
-            print(f"[bench] {args.only} ({'graph' if graph else 'eager'}, gemm {args.gemm_mode}, "
-                  f"attention {args.attn_mode}): {ms:.3f} ms/step, "
+            print(f"[bench] {args.only} ({'graph' if graph else 'eager'}, gemm {gm}, "
+                  f"attention {am}): {ms:.3f} ms/step, "
                   f"{c['B'] * c['block'] / (ms * 1e-3):.0f} tokens/s, losses {losses}", file=sys.stderr)
         return
     if args.only == "c3series":
