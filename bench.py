@@ -165,11 +165,18 @@ def bench_attention(B, H, T, D, dtype, seed, scale_qkv, steps, warmup, cold=Fals
 
     cold_ms = time_loop(step, steps, warmup, settle_ms=0) if cold else None
     ms_step = time_loop(step, steps, warmup)
-    # per-kernel averages (each phase is one kernel launch; the dQ pass also
-    # computes delta = rowsum(dO*O), which the dK/dV pass reads)
+    # per-kernel averages (each phase is one kernel launch).  Two-pass: the dQ
+    # pass also computes delta = rowsum(dO*O), which the dK/dV pass reads.
+    # One-pass: "prep" computes delta and zeroes dq, "dkdvq" is the key-outer
+    # kernel that writes dK/dV and adds dQ.
     ms_fwd = time_loop(lambda: K.attn_fwd(q, k, v, scale, True, out=o, lse=lse), steps, 2)
     ph = {}
-    for name, mask in (("dq", L.ATTN_BWD_DELTA | L.ATTN_BWD_DQ), ("dkdv", L.ATTN_BWD_DKDV)):
+    if K.attn_bwd_onepass_used(dtype, D):
+        phases = (("prep", L.ATTN_BWD_ONEPASS | L.ATTN_BWD_DELTA),
+                  ("dkdvq", L.ATTN_BWD_ONEPASS | L.ATTN_BWD_DQ | L.ATTN_BWD_DKDV))
+    else:
+        phases = (("dq", L.ATTN_BWD_DELTA | L.ATTN_BWD_DQ), ("dkdv", L.ATTN_BWD_DKDV))
+    for name, mask in phases:
         ph[name] = time_loop(lambda m=mask: K.attn_bwd(q, k, v, o, do, lse, scale, True, dq=dq, dk=dk,
                                                        dv=dv, workspace=ws, phases=m), steps, 2)
     _sync()
@@ -620,17 +627,34 @@ def main():
     ms_cold = r3.pop("ms_step_cold")
     f3, b3 = attn_flops(B, H, T, D)
     tflops = (f3 + b3) / (r3["ms_step"] * 1e-3) / 1e12
-    # dominant kernel and its algorithmic FLOPs: fwd kernel = 2u; dK/dV pass =
-    # S, dP, dV, dK = 4u; dQ pass = the dQ product only (its S/dP recompute is
-    # already counted in the dK/dV pass, and its delta rowsum is O(T*D)) = 1u.
+    # dominant kernel and its algorithmic FLOPs: fwd kernel = 2u; one-pass
+    # key-outer kernel = S, dP, dV, dK, dQ = 5u (its prep kernel is HBM-bound
+    # O(T*D) work); two-pass: dK/dV pass = S, dP, dV, dK = 4u, dQ pass = the
+    # dQ product only (its S/dP recompute is already counted in the dK/dV
+    # pass, and its delta rowsum is O(T*D)) = 1u.
     u = B * H * T * T * D
-    kern = {"attn_fwd": (r3["ms_fwd"], 2 * u), "attn_dkdv": (r3["ms_dkdv"], 4 * u),
-            "attn_dq": (r3["ms_dq"], 1 * u)}
+    kern = {"attn_fwd": (r3["ms_fwd"], 2 * u)}
+    if "ms_dkdvq" in r3:
+        kern.update({"attn_dkdvq": (r3["ms_dkdvq"], 5 * u), "attn_prep": (r3["ms_prep"], 0)})
+    else:
+        kern.update({"attn_dkdv": (r3["ms_dkdv"], 4 * u), "attn_dq": (r3["ms_dq"], 1 * u)})
     dom = max(kern, key=lambda k_: kern[k_][0])
     ms_dom, fl_dom = kern[dom]
     achieved = fl_dom / (ms_dom * 1e-3) / 1e12
     print(f"[bench] C3 step {r3['ms_step']:.3f} ms = {tflops:.1f} TFLOP/s (cold start {ms_cold:.3f} ms = "
           f"{(f3 + b3) / (ms_cold * 1e-3) / 1e12:.1f}); phases {r3}", file=sys.stderr, flush=True)
+    # the same step with the deterministic two-pass backward, for comparison
+    from minitorch_amd import kernels as _K
+
+    r3b = None
+    if _K.get_attn_bwd_mode() == _K.ATTN_BWD_ONEPASS:
+        prev_bwd = _K.set_attn_bwd_mode(_K.ATTN_BWD_TWOPASS)
+        try:
+            r3b, _ = bench_attention(B, H, T, D, "bfloat16", 3, 0.5, args.steps, args.warmup)
+        finally:
+            _K.set_attn_bwd_mode(prev_bwd)
+        print(f"[bench] C3 two-pass step {r3b['ms_step']:.3f} ms = "
+              f"{(f3 + b3) / (r3b['ms_step'] * 1e-3) / 1e12:.1f} TFLOP/s; phases {r3b}", file=sys.stderr, flush=True)
     if args.only == "c3":
         return
 
@@ -715,6 +739,15 @@ def main():
         "settle_ms": SETTLE_MS,
         "also": {
             "C3_phase_ms": {k_: round(v_, 4) for k_, v_ in r3.items()},
+            "C3_backward": ("one-pass (mtx_attn_set_bwd_mode MTX_ATTN_BWD_ONEPASS, the default): a "
+                            "delta kernel that zeroes dq, then one key-outer kernel writing dK/dV and "
+                            "adding dQ with fp32 atomics" if "ms_dkdvq" in r3 else
+                            "two passes (dQ query-outer with delta, then dK/dV key-outer)"),
+            "C3_twopass": None if r3b is None else {
+                "ms_per_step": round(r3b["ms_step"], 4),
+                "tflops": round((f3 + b3) / (r3b["ms_step"] * 1e-3) / 1e12, 2),
+                "phase_ms": {k_: round(v_, 4) for k_, v_ in r3b.items()},
+                "note": "the same step with the deterministic two-pass backward (MTX_ATTN_BWD_TWOPASS)"},
             "C3_cold_start": {"ms_per_step": round(ms_cold, 4),
                               "tflops": round((f3 + b3) / (ms_cold * 1e-3) / 1e12, 2),
                               "note": f"{args.warmup} warm-up + {args.steps} timed steps right after the "

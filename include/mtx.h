@@ -89,6 +89,19 @@ int mtx_attn_fwd(int dtype, int B, int H, int Tq, int Tk, int D,
 int mtx_attn_set_mode(int mode);
 int mtx_attn_get_mode(void);
 
+/*
+ * How mtx_attn_bwd (and the dropout-free mtx_attn_bwd_noalloc) computes the
+ * gradient of bf16 attention with D <= 64: MTX_ATTN_BWD_TWOPASS (default;
+ * deterministic: bit-identical on every run) or MTX_ATTN_BWD_ONEPASS (one
+ * key-outer kernel with fp32 atomics for dQ; slower on MI355X).  Other
+ * dtypes and head sizes always run two passes.  Returns MTX_OK or
+ * MTX_ERR_ARG for an unknown mode.  Process-wide.  No reference counterpart (the reference runs the backward
+ * as NumPy closures, tensor.py:210-218, functional.py:69-73).
+ */
+enum mtx_attn_bwd_modes { MTX_ATTN_BWD_TWOPASS = 0, MTX_ATTN_BWD_ONEPASS = 8 };
+int mtx_attn_set_bwd_mode(int mode);
+int mtx_attn_get_bwd_mode(void);
+
 /* Bytes of workspace mtx_attn_bwd needs (the per-row delta = rowsum(dO*O)). */
 size_t mtx_attn_bwd_workspace_bytes(int B, int H, int Tq);
 
@@ -102,7 +115,12 @@ size_t mtx_attn_bwd_workspace_bytes(int B, int H, int Tq);
  * The reference's rowsum(P*dP) equals rowsum(dO*O) exactly in real arithmetic.
  * Gradients are fp32 for both dtypes.  accumulate != 0 adds into dq/dk/dv
  * (the reference's _accum_grad, tensor.py:29-33); 0 overwrites them.
- * Deterministic: no atomics (dK/dV and dQ come from two separate passes).
+ * Structure (mtx_attn_set_bwd_mode): by default two deterministic passes
+ * (dQ query-outer, dK/dV key-outer, no atomics).  bf16 inputs with D <= 64
+ * can instead run a one-pass backward (MTX_ATTN_BWD_ONEPASS: a delta kernel
+ * that also zeroes dq, then one key-outer kernel that writes dK/dV and adds
+ * dQ into dq with fp32 atomics; dQ's summation order over key blocks then
+ * varies from run to run in the last bits).
  */
 int mtx_attn_bwd(int dtype, int B, int H, int Tq, int Tk, int D,
                  const void* q, const int64_t* q_strides,
@@ -118,8 +136,9 @@ int mtx_attn_bwd(int dtype, int B, int H, int Tq, int Tk, int D,
                  float scale, int causal, int accumulate, void* stream);
 
 /*
- * mtx_attn_bwd without allocation: the same kernels and results (bit for bit),
- * with the per-row delta held in a fixed device array the library owns
+ * mtx_attn_bwd without allocation: the same kernels and results (bit for bit
+ * in two-pass mode; the one-pass mode's dQ differs from run to run in the
+ * last bits, for both entry points alike), with the per-row delta held in a fixed device array the library owns
  * (MTX_ATTN_SCRATCH_BYTES per GPU, kept until the process ends) instead of a
  * caller workspace.  The caller passes inputs and outputs only; the call
  * allocates nothing (no hipMalloc, no library allocation).  B*H*Tq must be at
@@ -147,8 +166,12 @@ int mtx_attn_bwd_noalloc(int dtype, int B, int H, int Tq, int Tk, int D,
  * delta = rowsum(dO*O) to the workspace; DKDV and DQ read it.  When DELTA and
  * DQ are both selected they run as one kernel (the dQ pass computes delta for
  * its rows and stores it); selected passes run in the order DELTA, DQ, DKDV,
- * and mtx_attn_bwd is DELTA|DQ|DKDV.  (No reference counterpart: the reference
- * runs this backward as the per-node closures listed at mtx_attn_bwd.)
+ * and DELTA|DQ|DKDV (= ALL) is mtx_attn_bwd, whose structure follows
+ * mtx_attn_set_bwd_mode.  Adding the bit MTX_ATTN_BWD_ONEPASS (8) selects the
+ * one-pass kernels explicitly (bf16, D <= 64, else MTX_ERR_SHAPE): DELTA then
+ * computes delta and zeroes dq (unless accumulate), DQ|DKDV (together) writes
+ * dK/dV and adds dQ into dq.  (No reference counterpart: the reference runs
+ * this backward as the per-node closures listed at mtx_attn_bwd.)
  */
 enum mtx_attn_bwd_phases {
   MTX_ATTN_BWD_DELTA = 1,

@@ -22,6 +22,7 @@ MTX_F32, MTX_BF16 = 0, 1
 MTX_GEMM_FP32, MTX_GEMM_BF16X3 = 0, 1
 ATTN_SCRATCH_BYTES = 8 << 20  # MTX_ATTN_SCRATCH_BYTES (include/mtx.h)
 ATTN_BWD_DELTA, ATTN_BWD_DKDV, ATTN_BWD_DQ, ATTN_BWD_ALL = 1, 2, 4, 7
+ATTN_BWD_TWOPASS, ATTN_BWD_ONEPASS = 0, 8  # mtx_attn_set_bwd_mode; ONEPASS is also a phase bit
 
 _P = C.c_void_p
 _I = C.c_int
@@ -90,6 +91,8 @@ SIGNATURES = {
     "mtx_gemm_set_mode": (_I, [_I]),
     "mtx_attn_set_mode": (_I, [_I]),
     "mtx_attn_get_mode": (_I, []),
+    "mtx_attn_set_bwd_mode": (_I, [_I]),
+    "mtx_attn_get_bwd_mode": (_I, []),
     "mtx_gemm_get_mode": (_I, []),
     "mtx_gemm_step_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _F, _P, _I64, _P, _I, _I,
                                _P, _P, _I64, _I64, _I, _P, _P]),

@@ -932,6 +932,53 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// one-pass backward, preparation: delta[i] = sum_d dO[i,d] O[i,d] and, unless
+// the gradients accumulate, dq[i,:] = 0 (the one-pass dK/dV/dQ kernel adds
+// into dq).  Four lanes per row, each summing D/4 consecutive products with
+// fmaf in order, then (s0 + s1) + (s2 + s3): the dQ pass's order (its lane
+// quarters and v_permlane swaps), so both structures see the same delta.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void attn_prep_kernel(const BwdArgs a) {
+  constexpr int QPL = D / 4;  // elements per lane
+  const int64_t rows = (int64_t)a.B * a.H * a.Tq;
+  const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t i = gid >> 2;
+  const int c = (int)(gid & 3);
+  const bool ok = i < rows;
+  float sum = 0.f;
+  int b = 0, h = 0, t = 0;
+  if (ok) {
+    t = (int)(i % a.Tq);
+    const int64_t bh = i / a.Tq;
+    b = (int)(bh / a.H);
+    h = (int)(bh % a.H);
+    const T* op = static_cast<const T*>(a.o) + b * a.so.b + h * a.so.h + (int64_t)t * a.so.t + c * QPL;
+    const T* dp = static_cast<const T*>(a.dout) + b * a.sdo.b + h * a.sdo.h + (int64_t)t * a.sdo.t + c * QPL;
+    constexpr int NW = QPL * (int)sizeof(T) / 8;  // 8-byte words per lane
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint2 ou = reinterpret_cast<const uint2*>(op)[w];
+      const uint2 du = reinterpret_cast<const uint2*>(dp)[w];
+      const T* oe = reinterpret_cast<const T*>(&ou);
+      const T* de = reinterpret_cast<const T*>(&du);
+#pragma unroll
+      for (int e = 0; e < 8 / (int)sizeof(T); ++e) sum = fmaf(Elem<T>::to_f(oe[e]), Elem<T>::to_f(de[e]), sum);
+    }
+  }
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  if (ok) {
+    if (c == 0) a.delta[i] = sum;
+    if (!a.accumulate) {
+      float* dq = a.dq + b * a.sdq.b + h * a.sdq.h + (int64_t)t * a.sdq.t + c * QPL;
+#pragma unroll
+      for (int j = 0; j < QPL; j += 4) *reinterpret_cast<f32x4*>(dq + j) = zero4();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // backward, pass 1: dK, dV (key-outer).  Each wave owns NK*16 keys.
 // ---------------------------------------------------------------------------
 // waves per workgroup of the bf16 dK/dV pass (they share each Q/dO tile)
@@ -941,7 +988,18 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const BwdArgs a) {
 template <typename T>
 constexpr int dkdv_waves() { return sizeof(T) == 2 ? MTX_DKDV_WAVES : kWaves; }
 
-template <typename T, int D, int NK, bool DROP>
+// FQ (one-pass backward, bf16): the pass also produces dQ.  Each tile's dS
+// (bf16, the operand the dK product uses) is stored transposed in LDS (rows:
+// the block's 128 keys, columns: the tile's 64 queries); after a barrier
+// every wave multiplies it with the block's K (staged in LDS once) for its
+// share of the dQ tile (dQ = scale dS K over the block's keys) and adds that
+// share into dq with fp32 atomics.  dq must hold zeros (or the gradient to
+// add to) and delta must be computed before the launch (attn_prep_kernel).
+// Nothing of the dQ product stays in registers across tiles: the dK/dV pass
+// already holds 2 waves per SIMD at the register file's limit.
+// (An issue order that keeps all key blocks of a slice consecutively on one
+// XCD, so that fewer slices take atomic adds at a time, measured the same.)
+template <typename T, int D, int NK, bool DROP, bool FQ = false>
 __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4) || (is_x3<T>() && D == 64 && MTX_X3_DKDV_WAVES1)) ? 1 : 2) void attn_dkdv_kernel(const BwdArgs a) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
@@ -968,6 +1026,12 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
   // per query of the tile: -lse*log2(e) and -delta, the starting accumulators
   // of the S and dP MFMAs, so they yield log2(P) and dP - delta directly
   __shared__ __attribute__((aligned(16))) float L0[BQ], E0[BQ], L1[BQ], E1[BQ];
+  // FQ: the tile's dS^T, and the block's K rows (row-major, the Q/dO tiles'
+  // layout)
+  static_assert(!FQ || (BF && !DROP && NWV == 4 && NK == 2 && D <= 64 && MF::KI == 32),
+                "the one-pass backward is built for bf16, D <= 64, 4 waves x 32 keys");
+  using LS = Lay<T, BQ>;  // dS^T rows: BQ bf16 each, swizzled like the Q/dO tiles
+  __shared__ __attribute__((aligned(16))) LT S0[FQ ? BKV * BQ : 1], KS[FQ ? BKV * LD : 1];
 
   const int BH = a.B * a.H;
   const int nkb = (a.Tk + BKV - 1) / BKV;
@@ -1026,6 +1090,14 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
     }
   };
   if (ntile > 0) fetch(qstart, Q0, D0);
+  if constexpr (FQ) {
+    // the block's K rows into KS (waited for with the first tile)
+    if (ntile > 0) {
+      TileDma<T, BKV, D, NWV> kdma;
+      kdma.init(kp, a.sk.t, a.Tk, wid, lane);
+      kdma.issue(k0, KS, wid);
+    }
+  }
   // the K/V fragments are loaded after the first tile is requested, so both
   // latencies overlap (measured 1.5% faster at C3)
   // K and V fragments of this wave's keys (B operands of S = Q K^T, dP = dO V^T);
@@ -1044,6 +1116,40 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
       vf[ks][kc] = fv;
     }
   }
+  // FQ: wave w computes the dQ tile's d-block dtq = w % DT for its NQW
+  // query sub-tiles qsq .. qsq + NQW - 1 (D = 64: all four), over the
+  // block's keys.  A operands: dS rows from the dS^T tile; B operands: K
+  // from the KS tile (rows past Tk read as zeros), both by transposed reads
+  // (ltfrag), so the key order of the two agrees.
+  constexpr int NQW = FQ ? DT : 1;
+  const int dtq = wid % DT, qsq = (wid / DT) * DT;
+  float* __restrict__ dqp = a.dq + b * a.sdq.b + h * a.sdq.h;
+  const LaneOffs<T, BQ> lsq(n, g);
+  // dQ[qt + 16 (qsq + i) + 4g + r][16 dtq + n] += scale * (dS K) from the
+  // dS^T tile of query tile qt
+  auto dq_phase = [&](const int qt) {
+    if constexpr (FQ) {
+      f32x4 acc[NQW];
+#pragma unroll
+      for (int i = 0; i < NQW; ++i) acc[i] = zero4();
+#pragma unroll
+      for (int s = 0; s < BKV / 32; ++s) {
+        const frag kb = ltfrag<T, D>(KS, s, lo.t(dtq));
+#pragma unroll
+        for (int i = 0; i < NQW; ++i) acc[i] = MF::mma(ltfrag<T, BQ>(S0, s, lsq.t(qsq + i)), kb, acc[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < NQW; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qi = qt + 16 * (qsq + i) + 4 * g + r;
+          if (qi < a.Tq) unsafeAtomicAdd(dqp + (int64_t)qi * a.sdq.t + 16 * dtq + n, acc[i][r] * a.scale);
+        }
+    }
+  };
+  // FQ: a key block that runs past Tk masks those keys in every tile (their
+  // P would be exp(-lse), unbounded, and dS enters dQ)
+  const bool rag = FQ && k0 + BKV > a.Tk;
   // one query tile; P = buffer parity (for direct loads the loop below is
   // unrolled by two so that P is a compile-time constant)
   // `open`: the tile is known to be fully visible to every wave of the
@@ -1073,10 +1179,24 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
     }
     __syncthreads();
     if (it + 1 < ntile) fetch(qt + BQ, PN ? Q1 : Q0, PN ? D1 : D0);
+    // FQ: every wave has finished the previous tile's dQ reads of S0 (barrier above)
+    LT* __restrict__ Sb = S0;
 
     // wave-level causal skip: every key of the wave is after every query of the tile
-    if (!OPEN && a.causal && kw0 > qt + BQ - 1 + off) return;
-    const bool need_mask = !OPEN && a.causal && (kw0 + NK * 16 - 1 > qt + off);
+    if (!OPEN && a.causal && kw0 > qt + BQ - 1 + off) {
+      if constexpr (FQ) {
+        // this wave's dS^T rows are zero
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+          for (int qs = 0; qs < BQ / 16; ++qs)
+            *reinterpret_cast<uint2*>(Sb + LS::at(NK * 16 * wid + 16 * ks + n, 16 * qs + 4 * g)) = make_uint2(0u, 0u);
+        __syncthreads();  // every wave passes one such barrier per tile
+        dq_phase(qt);
+      }
+      return;
+    }
+    const bool need_mask = !OPEN && ((a.causal && (kw0 + NK * 16 - 1 > qt + off)) || rag);
     // dropout keep bytes of this lane's keys for queries qt + 16qs + 4g + r,
     // packed one query quad per word
     uint32_t kwd[BQ / 16][NK];
@@ -1129,10 +1249,11 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
           }
           // key kj is hidden from query qt + ql iff r < kj - qt - off - 16qs - 4g
           const int hid = kw0 + 16 * ks + n - qt - off - 16 * qs - 4 * g;
+          const bool kout = FQ && kw0 + 16 * ks + n >= a.Tk;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float pv = __builtin_amdgcn_exp2f(sv[r]);
-            if (MASKED && need_mask && r < hid) pv = 0.f;
+            if (MASKED && need_mask && ((a.causal && r < hid) || kout)) pv = 0.f;
             if constexpr (DROP) {
               // dV takes the kept P; dS = P (z dP' - delta) with z = keep*kscale
               // and dP' = dO V^T (the product with the kept P); the MFMA gave
@@ -1155,6 +1276,15 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
         for (int ks = 0; ks < NK; ++ks) {
           pb[ks] = pfrag<T, GQ>(p[ks], ls);
           db[ks] = pfrag<T, GQ>(ds[ks], ls);
+          if constexpr (FQ) {
+            // dS^T row (key) NK*16 wid + 16 ks + n, queries 16 qs + 4g + 0..3
+            // for the group's two sub-tiles qs = 2 gq, 2 gq + 1
+            static_assert(!FQ || (GQ == 2 && SPG == 1), "one k-step per query group");
+            const uint4 u = __builtin_bit_cast(uint4, db[ks]);
+            const int row = NK * 16 * wid + 16 * ks + n;
+            *reinterpret_cast<uint2*>(Sb + LS::at(row, 32 * gq + 4 * g)) = make_uint2(u.x, u.y);
+            *reinterpret_cast<uint2*>(Sb + LS::at(row, 32 * gq + 16 + 4 * g)) = make_uint2(u.z, u.w);
+          }
         }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
@@ -1179,6 +1309,10 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
       tile(std::true_type{});
 #endif
     }
+    if constexpr (FQ) {
+      __syncthreads();  // the tile's dS^T is complete
+      dq_phase(qt);
+    }
   };
   // Tiles from query qfull on see every key of the block: the first tiles
   // (at most BKV / BQ + 1 of them, rounded up to an even count for the
@@ -1189,6 +1323,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
     itA = qfull > qstart ? (qfull - qstart + BQ - 1) / BQ : 0;
     itA = min(ntile, (itA + 1) & ~1);
   }
+  if (rag) itA = ntile;
   if constexpr (LY::DIRECT) {
     for (int it = 0; it < itA; it += 2) {
       step(std::integral_constant<int, 0>{}, it, std::false_type{});
@@ -1563,12 +1698,56 @@ int launch_fwd(const FwdArgs& a, hipStream_t st) {
   return MTX_OK;
 }
 
+// Backward structure for the full gradient (MTX_ATTN_BWD_ALL): the
+// deterministic two passes (the default), or for bf16 with D <= 64 the
+// one-pass kernel (mtx_attn_set_bwd_mode MTX_ATTN_BWD_ONEPASS).  Measured at
+// B=8, H=16, T=2048, D=64: one-pass 26 us (delta, dq zeroed) + 485 us
+// (key-outer with dQ atomics; 314 us with the atomics taken out) against
+// 103 us (dQ pass) + 141 us (dK/dV pass): 570 MB of fp32 atomic adds into dq
+// cost more than the dQ pass's recomputed S and dP.
+std::atomic<int> g_bwd_mode{MTX_ATTN_BWD_TWOPASS};
+
+template <typename T, int D>
+constexpr bool has_onepass() {
+  return sizeof(T) == 2 && D <= 64 && Cfg<T, D>::NK == 2 && dkdv_waves<T>() == 4;
+}
+
+// One-pass phases: MTX_ATTN_BWD_ONEPASS | DELTA runs the preparation kernel
+// (delta; dq zeroed unless accumulating), ONEPASS | DQ | DKDV the one-pass
+// kernel (dK, dV written, dQ added into dq).
+template <typename T, int D>
+int launch_onepass(const BwdArgs& a, int phases, hipStream_t st) {
+  if constexpr (has_onepass<T, D>()) {
+    constexpr int NK = Cfg<T, D>::NK;
+    if (phases & MTX_ATTN_BWD_DELTA) {
+      const int64_t lanes = (int64_t)a.B * a.H * a.Tq * 4;
+      hipLaunchKernelGGL((attn_prep_kernel<T, D>), dim3((unsigned)((lanes + kThreads - 1) / kThreads)),
+                         dim3(kThreads), 0, st, a);
+      MTX_LAUNCHED();
+    }
+    if (phases & (MTX_ATTN_BWD_DQ | MTX_ATTN_BWD_DKDV)) {
+      constexpr int NWV = dkdv_waves<T>();
+      const int gk = cdiv(a.Tk, NWV * NK * 16) * a.B * a.H;
+      hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NK, false, true>), dim3(gk), dim3(64 * NWV), 0, st, a);
+      MTX_LAUNCHED();
+    }
+    return MTX_OK;
+  } else {
+    return fail(MTX_ERR_SHAPE, "the one-pass backward needs bf16 inputs and D <= 64");
+  }
+}
+
 // Phase order: delta, dQ, dK/dV.  DELTA together with DQ runs as one
 // kernel (the dQ pass computes delta for its rows and stores it), which the
 // dK/dV pass then reads.
 template <typename T, int D>
 int launch_bwd(const BwdArgs& a, int phases, hipStream_t st) {
   constexpr int NQ = Cfg<T, D>::NQ, NK = Cfg<T, D>::NK;
+  if (phases & MTX_ATTN_BWD_ONEPASS) return launch_onepass<T, D>(a, phases, st);
+  if constexpr (has_onepass<T, D>()) {
+    if (phases == MTX_ATTN_BWD_ALL && !a.keep && g_bwd_mode.load(std::memory_order_relaxed) == MTX_ATTN_BWD_ONEPASS)
+      return launch_onepass<T, D>(a, phases, st);
+  }
   const bool fuse = (phases & MTX_ATTN_BWD_DELTA) && (phases & MTX_ATTN_BWD_DQ);
   if ((phases & MTX_ATTN_BWD_DELTA) && !fuse) {
     const int64_t rows = (int64_t)a.B * a.H * a.Tq;
@@ -1651,6 +1830,16 @@ extern "C" int mtx_attn_set_mode(int mode) {
 }
 
 extern "C" int mtx_attn_get_mode(void) { return g_attn_mode.load(); }
+
+extern "C" int mtx_attn_set_bwd_mode(int mode) {
+  MTX_CHECK_ARG(mode == MTX_ATTN_BWD_ONEPASS || mode == MTX_ATTN_BWD_TWOPASS,
+                "bwd mode must be MTX_ATTN_BWD_ONEPASS (%d) or MTX_ATTN_BWD_TWOPASS (%d), got %d",
+                MTX_ATTN_BWD_ONEPASS, MTX_ATTN_BWD_TWOPASS, mode);
+  g_bwd_mode.store(mode);
+  return MTX_OK;
+}
+
+extern "C" int mtx_attn_get_bwd_mode(void) { return g_bwd_mode.load(); }
 
 namespace {
 int check_keep(const uint8_t* keep, int64_t keep_ld, float keep_scale, int Tk) {
@@ -1768,7 +1957,15 @@ int attn_bwd_impl(int phases, int dtype, int B, int H, int Tq, int Tk, int D,
                             float scale, int causal, int accumulate,
                             const uint8_t* keep, int64_t keep_ld, float keep_scale, void* stream,
                             bool use_scratch = false) {
-  MTX_CHECK_ARG(phases > 0 && (phases & ~MTX_ATTN_BWD_ALL) == 0, "bad phase mask %d", phases);
+  MTX_CHECK_ARG(phases > 0 && (phases & ~(MTX_ATTN_BWD_ALL | MTX_ATTN_BWD_ONEPASS)) == 0 &&
+                    (phases & MTX_ATTN_BWD_ALL) != 0,
+                "bad phase mask %d", phases);
+  if (phases & MTX_ATTN_BWD_ONEPASS) {
+    MTX_CHECK_SHAPE(dtype == MTX_BF16 && D <= 64 && keep == nullptr,
+                    "MTX_ATTN_BWD_ONEPASS phases need bf16 inputs, D <= 64 and no dropout");
+    MTX_CHECK_ARG((phases & MTX_ATTN_BWD_DQ) == 0 || (phases & MTX_ATTN_BWD_DKDV) != 0,
+                  "the one-pass kernel computes dQ and dK/dV together (phases DQ | DKDV)");
+  }
   int rc = check_dims(dtype, B, H, Tq, Tk, D, causal);
   if (rc) return rc;
   const int es = dtype == MTX_F32 ? 4 : 2;

@@ -497,6 +497,30 @@ def get_attn_mode() -> int:
     return int(L.lib().mtx_attn_get_mode())
 
 
+ATTN_BWD_TWOPASS, ATTN_BWD_ONEPASS = L.ATTN_BWD_TWOPASS, L.ATTN_BWD_ONEPASS
+
+
+def set_attn_bwd_mode(mode: int) -> int:
+    """Select how the backward of bf16 attention with D <= 64 runs
+    (mtx_attn_set_bwd_mode): ATTN_BWD_TWOPASS (the default: deterministic
+    dQ and dK/dV passes) or ATTN_BWD_ONEPASS (one key-outer kernel writes
+    dK/dV and adds dQ with fp32 atomics, after a delta kernel that zeroes
+    dq).  Returns the previous mode."""
+    prev = int(L.lib().mtx_attn_get_bwd_mode())
+    L.call("mtx_attn_set_bwd_mode", int(mode))
+    return prev
+
+
+def get_attn_bwd_mode() -> int:
+    return int(L.lib().mtx_attn_get_bwd_mode())
+
+
+def attn_bwd_onepass_used(dtype: str, D: int) -> bool:
+    """Whether attn_bwd (all phases, no dropout) takes the one-pass kernels
+    for this input dtype and head size."""
+    return dtype == "bfloat16" and D <= 64 and get_attn_bwd_mode() == ATTN_BWD_ONEPASS
+
+
 def gemm(a, b, c, alpha=1.0, beta=0.0, bias=None, M=None, N=None, K=None, batch=1,
          sa=None, sb=None, sc=None, act=GEMM_ACT_NONE, aux=None, colsum=None, colsum_accumulate=False):
     """C = alpha*A@B + beta*C (+bias) with explicit (row, col, batch) strides

@@ -259,7 +259,8 @@ def _lazy_reference(s2, tile, tau):
     return out
 
 
-def attention_bf16_emulated(q, k, v, dout, scale, causal=True, rounding=True, tile=64, tau=8.0):
+def attention_bf16_emulated(q, k, v, dout, scale, causal=True, rounding=True, tile=64, tau=8.0,
+                            onepass=False):
     """The bf16 kernels' arithmetic (mtx_attn_fwd / mtx_attn_bwd with bf16
     inputs) restated in float64 with bf16 round-to-nearest-even at exactly
     the points where the kernels round, for elementwise checks of the GPU
@@ -277,6 +278,8 @@ def attention_bf16_emulated(q, k, v, dout, scale, causal=True, rounding=True, ti
       * P before dV = P^T dO, and dS = P (dP - delta) before dK = scale dS^T Q
         and dQ = scale dS K (P and dS themselves are formed in fp32 from the
         unrounded scores).
+    onepass=True: dQ as the one-pass backward forms it, from the dK/dV pass's
+      dS (scores from K*c) instead of a dQ pass's (scores from Q*c).
     rounding=False skips every rounding (then the result is attention_f64's
     up to float64 rounding).  Returns (out, lse, dq, dk, dv) in float64."""
     R = bf16_round if rounding else (lambda x: np.asarray(x, dtype=F64))
@@ -315,8 +318,12 @@ def attention_bf16_emulated(q, k, v, dout, scale, causal=True, rounding=True, ti
     dsk = pk * (dp - delta)
     dv = np.swapaxes(R(pk).astype(F64), -1, -2) @ g64
     dk = scale * (np.swapaxes(R(dsk).astype(F64), -1, -2) @ q64)
-    # dQ pass: S^T = K (Q c)^T
-    pq = np.where(hidden, 0.0, np.exp2(np.where(hidden, 0.0, qs @ np.swapaxes(k64, -1, -2)) - nl))
-    dsq = pq * (dp - delta)
-    dq = scale * (R(dsq).astype(F64) @ k64)
+    if onepass:
+        # the key-outer pass's dS, rounded for its dK product, times K
+        dq = scale * (R(dsk).astype(F64) @ k64)
+    else:
+        # dQ pass: S^T = K (Q c)^T
+        pq = np.where(hidden, 0.0, np.exp2(np.where(hidden, 0.0, qs @ np.swapaxes(k64, -1, -2)) - nl))
+        dsq = pq * (dp - delta)
+        dq = scale * (R(dsq).astype(F64) @ k64)
     return ob if rounding else out, lse, dq, dk, dv

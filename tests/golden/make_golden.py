@@ -6,6 +6,7 @@ Run in the build container only (the reference is mounted at
 
     python tests/golden/make_golden.py            # attention, MHA, C0 train (+ dropout), greedy
     python tests/golden/make_golden.py --c2       # also the C2 20-step loss curve (slow)
+    python tests/golden/make_golden.py --only-c4  # the C4 greedy tokens (slow, ~30 min)
 
 These are the functions no closed form, finite difference or library
 cross-check pins (the composed training step as the reference executes it,
@@ -189,6 +190,35 @@ def greedy(path, seed=100, B=4, T0=8, n_new=24):
     print(f"wrote {path.name}: min top-2 margin {np.min(margins):.3e}")
 
 
+def greedy_c4(path, n_new=224):
+    """Config C4 through the reference's own forward: the C2 model (weights
+    from init_params(C2, default_rng(2))), eval mode, no_grad, prompts
+    default_rng(4).integers(0, 65, (64, 32)), 224 greedy steps, each the
+    argmax of model(idx[:, -block:]).data[:, -1, :] (transformer.py:93-98,
+    full recompute as the reference generates).  Written after every step
+    (write + rename), so a long run leaves a usable prefix; `steps` says how
+    many tokens each row holds beyond the prompt."""
+    model = ref_model(C2, np.random.default_rng(2))
+    model.eval()
+    prompts = np.random.default_rng(4).integers(0, C2.vocab, (64, 32))
+    idx = prompts.copy()
+    margins = []
+    t0 = time.time()
+    with mt.no_grad():
+        for it in range(n_new):
+            logits = model(idx[:, -C2.block:]).data[:, -1, :]
+            nxt = np.argmax(logits, axis=-1)
+            top2 = np.sort(logits, axis=-1)[:, -2:]
+            margins.append(top2[:, 1] - top2[:, 0])
+            idx = np.concatenate([idx, nxt[:, None]], axis=1)
+            tmp = path.with_name(path.stem + ".part.npz")
+            np.savez_compressed(tmp, prompts=prompts, tokens=idx, margins=np.stack(margins, 1),
+                                steps=it + 1)
+            tmp.replace(path)
+            print(f"  C4 step {it:3d}  ({time.time() - t0:.1f}s)", flush=True)
+    print(f"wrote {path.name}: min top-2 margin {np.min(margins):.3e}")
+
+
 def sampling(path, seed=300, B=4, T0=8, temperature=0.8):
     """The reference's sampling GPT.generate (transformer.py:93-104) on a
     C0-size model, NumPy's global RNG seeded with np.random.seed: 16 new
@@ -213,6 +243,8 @@ def main():
     ap.add_argument("--only-c2", action="store_true")
     ap.add_argument("--only-sampling", action="store_true")
     ap.add_argument("--only-dropout", action="store_true")
+    ap.add_argument("--only-c4", action="store_true",
+                    help="only the C4 greedy run through the reference forward (slow)")
     ap.add_argument("--c2-out", default=str(HERE / "c2_train.npz"),
                     help="where the C2 curve goes (a long run can write beside the committed fixture)")
     args = ap.parse_args()
@@ -221,6 +253,9 @@ def main():
         return
     if args.only_dropout:
         train_curve_dropout(C0, 0, 16, 10, 0.1, 1234, HERE / "c0_train_dropout.npz")
+        return
+    if args.only_c4:
+        greedy_c4(HERE / "c4_greedy_ref.npz")
         return
     if not args.only_c2:
         attention_subgraph(HERE / "attn_subgraph.npz")

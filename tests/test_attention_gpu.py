@@ -15,6 +15,7 @@ flow, transformer.py:36-44).  Full-size bf16 (C3) runs are checked on a subset
 of (b, h) slices against the oracle and in full through identities that hold
 for any size: sum_j dV_j = sum_i dO_i and sum_j dK_j = 0 per (b, h).
 """
+import ctypes
 import math
 import sys
 
@@ -25,6 +26,7 @@ from devarrays import T as _T, empty, full, sync
 from oracle.attention import attention_bf16_emulated, bf16_round, reference_attention
 
 pytestmark = pytest.mark.gpu
+C_i64 = ctypes.c_int64
 
 
 def _say(msg):
@@ -82,6 +84,26 @@ def _emu_bar(got, emu, name):
 
 def _to_dev(x, dev, dtype):
     return _T(x, dtype)
+
+
+def _onepass(dtype, D):
+    """Whether attn_bwd runs the one-pass backward for these inputs (its dQ
+    is then emulated from the key-outer pass's dS: attention_bf16_emulated
+    onepass=True)."""
+    from minitorch_amd import kernels as K
+
+    return K.attn_bwd_onepass_used(dtype, D)
+
+
+@pytest.fixture(params=["onepass", "twopass"])
+def bwd_mode(request, dev):
+    """bf16 backward tests run under both structures: the deterministic two
+    passes (the default) and the one-pass kernel (dQ by atomics)."""
+    from minitorch_amd import kernels as K
+
+    prev = K.set_attn_bwd_mode(K.ATTN_BWD_ONEPASS if request.param == "onepass" else K.ATTN_BWD_TWOPASS)
+    yield request.param
+    K.set_attn_bwd_mode(prev)
 
 
 def _run(dev, q, k, v, do, scale, causal, dtype, views=None):
@@ -151,8 +173,8 @@ def test_fp32_small(dev, attn_mode, B, H, Tq, Tk, D, causal):
 
 
 @pytest.mark.parametrize("B,H,Tq,Tk,D,causal", [c for c in CASES if c[4] != 128] + [(1, 2, 100, 100, 128, True)])
-def test_bf16_small(dev, B, H, Tq, Tk, D, causal):
-    _say(f"[attn bf16] B={B} H={H} Tq={Tq} Tk={Tk} D={D} causal={causal}")
+def test_bf16_small(dev, bwd_mode, B, H, Tq, Tk, D, causal):
+    _say(f"[attn bf16 {bwd_mode}] B={B} H={H} Tq={Tq} Tk={Tk} D={D} causal={causal}")
     rng = np.random.default_rng(2000 + Tq + 7 * Tk + D)
     q = bf16_round(0.5 * rng.standard_normal((B, H, Tq, D), dtype=np.float32))
     k = bf16_round(0.5 * rng.standard_normal((B, H, Tk, D), dtype=np.float32))
@@ -165,7 +187,7 @@ def test_bf16_small(dev, B, H, Tq, Tk, D, causal):
     _bf16_bar(dq, rdq, "dq")
     _bf16_bar(dk, rdk, "dk")
     _bf16_bar(dv, rdv, "dv")
-    emu = attention_bf16_emulated(q, k, v, do, scale, causal)
+    emu = attention_bf16_emulated(q, k, v, do, scale, causal, onepass=_onepass("bfloat16", D))
     for b in range(B):
         for h in range(H):
             for name, got, e in zip(("o", "lse", "dq", "dk", "dv"), (o, lse, dq, dk, dv), emu):
@@ -211,18 +233,27 @@ def test_accumulate_flag(dev, attn_mode):
 def test_phases_split_match_fused(dev, attn_mode, dtype_name):
     """mtx_attn_bwd_phase run as three calls (standalone delta kernel, then
     dQ, then dK/dV) gives the oracle's gradients and agrees with the fused
-    DELTA|DQ path of mtx_attn_bwd up to the summation order of delta."""
+    DELTA|DQ path of mtx_attn_bwd (two-pass mode) up to the summation order
+    of delta."""
     from minitorch_amd import _lib as L
     from minitorch_amd import kernels as K
 
     dtype = dtype_name
     _say(f"[attn phases split vs fused] {dtype_name}")
+    prev = K.set_attn_bwd_mode(K.ATTN_BWD_TWOPASS)
+    try:
+        _phases_split(L, K, dtype)
+    finally:
+        K.set_attn_bwd_mode(prev)
+
+
+def _phases_split(L, K, dtype):
     rng = np.random.default_rng(17)
     B, H, Tq, Tk, D = 2, 3, 150, 190, 64
     arrs = [rng.standard_normal((B, H, T, D), dtype=np.float32) for T in (Tq, Tk, Tk, Tq)]
     if dtype == "bfloat16":
         arrs = [bf16_round(0.5 * x) for x in arrs]
-    q, k, v, do = (_to_dev(x, dev, dtype) for x in arrs)
+    q, k, v, do = (_to_dev(x, None, dtype) for x in arrs)
     o, lse = K.attn_fwd(q, k, v, 0.125, True)
     fused = K.attn_bwd(q, k, v, o, do, lse, 0.125, True)
     split = [full(t.shape, float("nan")) for t in fused]
@@ -240,6 +271,111 @@ def test_phases_split_match_fused(dev, attn_mode, dtype_name):
         (_fp32_bar if dtype == "float32" else _bf16_bar)(b, r, name)
 
 
+ONEPASS_CASES = [
+    # (B, H, Tq, Tk, D, causal)
+    (1, 1, 1, 1, 64, True),
+    (2, 3, 150, 190, 64, True),    # Tq < Tk, ragged key block
+    (1, 2, 1000, 1000, 64, True),  # ragged last query tile and key block
+    (2, 2, 200, 200, 64, False),
+    (2, 2, 65, 70, 64, False),     # non-causal, ragged key block
+    (1, 2, 17, 100, 64, True),
+    (2, 4, 256, 256, 16, True),
+    (1, 2, 64, 64, 32, True),
+    (1, 2, 130, 130, 32, False),
+]
+
+
+@pytest.mark.parametrize("B,H,Tq,Tk,D,causal", ONEPASS_CASES)
+def test_onepass_matches_twopass_and_emulation(dev, B, H, Tq, Tk, D, causal):
+    """bf16 one-pass backward (dK/dV written, dQ added with fp32 atomics by
+    the key-outer kernel): dK and dV bit-identical to the two-pass kernels'
+    (the same products in the same order), dQ elementwise against the
+    rounding emulation of the one-pass form and within the bf16 bar of the
+    reference."""
+    from minitorch_amd import kernels as K
+
+    _say(f"[attn bf16 one-pass vs two-pass] B={B} H={H} Tq={Tq} Tk={Tk} D={D} causal={causal}")
+    rng = np.random.default_rng(3000 + Tq + 7 * Tk + D)
+    q = bf16_round(0.5 * rng.standard_normal((B, H, Tq, D), dtype=np.float32))
+    k = bf16_round(0.5 * rng.standard_normal((B, H, Tk, D), dtype=np.float32))
+    v = bf16_round(0.5 * rng.standard_normal((B, H, Tk, D), dtype=np.float32))
+    do = bf16_round(rng.standard_normal((B, H, Tq, D), dtype=np.float32))
+    scale = 1.0 / math.sqrt(D)
+    prev = K.set_attn_bwd_mode(K.ATTN_BWD_ONEPASS)
+    try:
+        o1, dq1, dk1, dv1, lse = _run(dev, q, k, v, do, scale, causal, "bfloat16")
+        K.set_attn_bwd_mode(K.ATTN_BWD_TWOPASS)
+        o2, dq2, dk2, dv2, _ = _run(dev, q, k, v, do, scale, causal, "bfloat16")
+    finally:
+        K.set_attn_bwd_mode(prev)
+    assert np.array_equal(o1, o2)
+    assert np.array_equal(dk1, dk2), float(np.abs(dk1 - dk2).max())
+    assert np.array_equal(dv1, dv2), float(np.abs(dv1 - dv2).max())
+    assert np.all(np.isfinite(dq1))
+    _, rdq, _, _ = reference_attention(q, k, v, do, scale, causal)
+    _bf16_bar(dq1, rdq, "dq one-pass")
+    emu = attention_bf16_emulated(q, k, v, do, scale, causal, onepass=True)
+    for b in range(B):
+        for h in range(H):
+            _emu_bar(dq1[b, h], emu[2][b, h], f"dq[{b},{h}]")
+
+
+def test_onepass_phases_and_accumulate(dev):
+    """The one-pass kernels through explicit phases (ONEPASS|DELTA: delta and
+    dq zeroed; ONEPASS|DQ|DKDV: the key-outer kernel) equal mtx_attn_bwd in
+    one-pass mode; with accumulate=1 the gradients are added (dq starts from
+    the given values: the delta kernel leaves it alone); two runs agree up to
+    the atomics' summation order (dK/dV bit for bit)."""
+    from minitorch_amd import _lib as L
+    from minitorch_amd import kernels as K
+
+    _say("[attn bf16 one-pass phases / accumulate]")
+    rng = np.random.default_rng(41)
+    B, H, Tq, Tk, D = 2, 3, 300, 300, 64
+    arrs = [bf16_round(0.5 * rng.standard_normal((B, H, T, D), dtype=np.float32)) for T in (Tq, Tk, Tk, Tq)]
+    q, k, v, do = (_to_dev(x, None, "bfloat16") for x in arrs)
+    prev = K.set_attn_bwd_mode(K.ATTN_BWD_ONEPASS)
+    try:
+        o, lse = K.attn_fwd(q, k, v, 0.125, True)
+        ref = [t.numpy() for t in K.attn_bwd(q, k, v, o, do, lse, 0.125, True)]
+        again = [t.numpy() for t in K.attn_bwd(q, k, v, o, do, lse, 0.125, True)]
+        ws = empty((L.lib().mtx_attn_bwd_workspace_bytes(B, H, Tq),), "uint8")
+        got = [full((B, H, t, D), float("nan")) for t in (Tq, Tk, Tk)]
+        for ph in (L.ATTN_BWD_ONEPASS | L.ATTN_BWD_DELTA, L.ATTN_BWD_ONEPASS | L.ATTN_BWD_DQ | L.ATTN_BWD_DKDV):
+            K.attn_bwd(q, k, v, o, do, lse, 0.125, True, dq=got[0], dk=got[1], dv=got[2], workspace=ws, phases=ph)
+        sync()
+        got = [t.numpy() for t in got]
+        acc = [_to_dev(x, None, "float32") for x in ref]
+        K.attn_bwd(q, k, v, o, do, lse, 0.125, True, dq=acc[0], dk=acc[1], dv=acc[2], accumulate=True)
+        sync()
+        acc = [t.numpy() for t in acc]
+    finally:
+        K.set_attn_bwd_mode(prev)
+    for name, r, a, g, c in zip(("dq", "dk", "dv"), ref, again, got, acc):
+        amax = float(np.abs(r).max())
+        if name == "dq":
+            assert np.abs(a - r).max() <= 1e-6 * amax, (name, float(np.abs(a - r).max()), amax)
+            assert np.abs(g - r).max() <= 1e-6 * amax, (name, float(np.abs(g - r).max()), amax)
+        else:
+            assert np.array_equal(a, r) and np.array_equal(g, r), name
+        assert np.abs(c - 2 * r).max() <= 2e-6 * amax, (name, float(np.abs(c - 2 * r).max()), amax)
+
+
+def test_onepass_phase_rejections(dev):
+    """The one-pass phase bit is refused, before any device work, for fp32
+    inputs and for DQ without DKDV."""
+    from minitorch_amd import _lib as L
+
+    s = (C_i64 * 4)(64, 64, 64, 1)
+    lib = L.lib()
+    for dtype, phases in ((L.MTX_F32, L.ATTN_BWD_ONEPASS | L.ATTN_BWD_ALL),
+                          (L.MTX_BF16, L.ATTN_BWD_ONEPASS | L.ATTN_BWD_DQ)):
+        rc = lib.mtx_attn_bwd_phase(phases, dtype, 1, 1, 64, 64, 64, None, s, None, s, None, s, None, s,
+                                    None, s, None, None, s, None, s, None, s, None, 0, 0.125, 1, 0, None)
+        assert rc != 0
+        assert "ONEPASS" in lib.mtx_last_error().decode() or "one-pass" in lib.mtx_last_error().decode()
+
+
 def test_c1_full(dev, attn_mode):
     """Config C1: B=32, H=8, T=256, D=64 fp32, q,k,v,dO ~ N(0,1) drawn in that
     order from default_rng(1); scale 1/8.  Full tensors vs the oracle."""
@@ -254,10 +390,11 @@ def test_c1_full(dev, attn_mode):
 
 
 def _emu_slices(tag, q, k, v, do, scale, outs, slices):
+    onepass = _onepass("bfloat16", q.shape[-1])
     worst = {}
     for b, h in slices:
         sl = (slice(b, b + 1), slice(h, h + 1))
-        emu = attention_bf16_emulated(q[sl], k[sl], v[sl], do[sl], scale, True)
+        emu = attention_bf16_emulated(q[sl], k[sl], v[sl], do[sl], scale, True, onepass=onepass)
         for name, got, e in zip(("o", "lse", "dq", "dk", "dv"), outs, emu):
             r = _emu_bar(got[sl], e, f"{tag} {name}[{b},{h}]")
             worst[name] = max(worst.get(name, 0.0), r)

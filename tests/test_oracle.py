@@ -154,13 +154,21 @@ def test_bf16_emulation_pinned():
         ref = A.attention_f64(q, k, v, do, 1 / np.sqrt(D), causal)
         _, lse = A.flash_forward(q, k, v, 1 / np.sqrt(D), causal)
         refs = (ref[0], lse, ref[2], ref[3], ref[4])
-        exact = A.attention_bf16_emulated(q, k, v, do, 1 / np.sqrt(D), causal, rounding=False)
-        rounded = A.attention_bf16_emulated(q, k, v, do, 1 / np.sqrt(D), causal)
-        for name, e, r, b in zip(("out", "lse", "dq", "dk", "dv"), exact, refs, rounded):
-            amax = np.abs(r).max()
-            assert np.abs(e - r).max() <= 1e-12 * amax, name
-            rel = np.linalg.norm(b - r) / np.linalg.norm(r)
-            assert 1e-6 < rel < 1e-2, (name, rel)
+        for onepass in (False, True):
+            exact = A.attention_bf16_emulated(q, k, v, do, 1 / np.sqrt(D), causal, rounding=False,
+                                              onepass=onepass)
+            rounded = A.attention_bf16_emulated(q, k, v, do, 1 / np.sqrt(D), causal, onepass=onepass)
+            for name, e, r, b in zip(("out", "lse", "dq", "dk", "dv"), exact, refs, rounded):
+                amax = np.abs(r).max()
+                assert np.abs(e - r).max() <= 1e-12 * amax, (name, onepass)
+                rel = np.linalg.norm(b - r) / np.linalg.norm(r)
+                assert 1e-6 < rel < 1e-2, (name, onepass, rel)
+        # the two dQ forms round different scores (K*c vs Q*c): their dQ
+        # differ by a bf16-rounding-sized amount, not by a structural one
+        two = A.attention_bf16_emulated(q, k, v, do, 1 / np.sqrt(D), causal)[2]
+        one = A.attention_bf16_emulated(q, k, v, do, 1 / np.sqrt(D), causal, onepass=True)[2]
+        d = np.linalg.norm(one - two) / np.linalg.norm(refs[2])
+        assert 0 < d < 1e-2, d
     # a tile reference that moves (scores growing along the keys) still
     # reproduces the exact softmax: the tile weights exp2(m_t - m_final)
     T = 200

@@ -1,9 +1,12 @@
 """mtx_attn_bwd_noalloc (the backward entry point that allocates nothing:
 delta lives in the library's fixed per-GPU device array) against
 mtx_attn_bwd with a caller workspace.  Same kernels, so the results must be
-identical bit for bit; checked on two calls in a row, the second with a
-smaller input (the array keeps the first call's contents), for fp32 and
-bf16, plus the host-side rejection of inputs beyond the array's size."""
+identical bit for bit (for bf16 in one-pass mode dQ is summed with atomics
+in a run-dependent order: there dK/dV are compared bit for bit and dQ to
+1e-6 of its largest entry); checked on two calls in a row, the second with
+a smaller input (the array keeps the first call's contents), for fp32 and
+bf16 under both backward modes, plus the host-side rejection of inputs
+beyond the array's size."""
 import ctypes as C
 import sys
 
@@ -28,25 +31,33 @@ def _inputs(rng, shp_q, shp_k, bf16):
     return [T(a, "bfloat16" if bf16 else "float32") for a in arrs]
 
 
-@pytest.mark.parametrize("bf16", [False, True])
-def test_noalloc_matches_workspace_entry_point(dev, bf16):
+@pytest.mark.parametrize("bf16,onepass", [(False, False), (True, False), (True, True)])
+def test_noalloc_matches_workspace_entry_point(dev, bf16, onepass):
     from minitorch_amd import kernels as K
 
     rng = np.random.default_rng(77)
-    # second call smaller than the first: rows of the first call stay behind
-    # in the scratch array and must not leak into the second
-    for (B, H, Tq, Tk, D) in [(4, 6, 300, 300, 64), (2, 3, 129, 200, 64)]:
-        _say(f"[noalloc] bf16={bf16} B={B} H={H} Tq={Tq} Tk={Tk} D={D}")
-        q, k, v, do = _inputs(rng, (B, H, Tq, D), (B, H, Tk, D), bf16)
-        o, lse = K.attn_fwd(q, k, v, 0.125, True)
-        ref = K.attn_bwd(q, k, v, o, do, lse, 0.125, True)
-        got = [full((B, H, t, D), float("nan")) for t in (Tq, Tk, Tk)]
-        K.attn_bwd_noalloc(q, k, v, o, do, lse, 0.125, True, *got)
-        sync()
-        for name, a, b in zip(("dq", "dk", "dv"), ref, got):
-            a, b = a.numpy(), b.numpy()
-            assert np.all(np.isfinite(b)), name
-            assert np.array_equal(a, b), (name, float(np.abs(a - b).max()))
+    prev = K.set_attn_bwd_mode(K.ATTN_BWD_ONEPASS if onepass else K.ATTN_BWD_TWOPASS)
+    try:
+        # second call smaller than the first: rows of the first call stay
+        # behind in the scratch array and must not leak into the second
+        for (B, H, Tq, Tk, D) in [(4, 6, 300, 300, 64), (2, 3, 129, 200, 64)]:
+            _say(f"[noalloc] bf16={bf16} onepass={onepass} B={B} H={H} Tq={Tq} Tk={Tk} D={D}")
+            q, k, v, do = _inputs(rng, (B, H, Tq, D), (B, H, Tk, D), bf16)
+            o, lse = K.attn_fwd(q, k, v, 0.125, True)
+            ref = K.attn_bwd(q, k, v, o, do, lse, 0.125, True)
+            got = [full((B, H, t, D), float("nan")) for t in (Tq, Tk, Tk)]
+            K.attn_bwd_noalloc(q, k, v, o, do, lse, 0.125, True, *got)
+            sync()
+            for name, a, b in zip(("dq", "dk", "dv"), ref, got):
+                a, b = a.numpy(), b.numpy()
+                assert np.all(np.isfinite(b)), name
+                if onepass and name == "dq":
+                    amax = float(np.abs(a).max())
+                    assert np.abs(a - b).max() <= 1e-6 * amax, (name, float(np.abs(a - b).max()), amax)
+                else:
+                    assert np.array_equal(a, b), (name, float(np.abs(a - b).max()))
+    finally:
+        K.set_attn_bwd_mode(prev)
 
 
 def test_noalloc_rejects_oversize(dev):
@@ -54,7 +65,9 @@ def test_noalloc_rejects_oversize(dev):
 
     rows_max = L.ATTN_SCRATCH_BYTES // 4
     s = (C.c_int64 * 4)(64, 64, 64, 1)
-    p = C.c_void_p(256)
+    # null device pointers: the size check is what is tested, and a call
+    # that got past it would stop at the null-pointer checks on the host
+    p = None
     B, H, Tq = 1, 1, rows_max + 1
     rc = L.lib().mtx_attn_bwd_noalloc(L.MTX_F32, B, H, Tq, Tq, 64, p, s, p, s, p, s, p, s, p, s, p,
                                       p, s, p, s, p, s, 0.125, 1, 0, None)
