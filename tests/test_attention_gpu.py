@@ -402,6 +402,49 @@ def _emu_slices(tag, q, k, v, do, scale, outs, slices):
          + ", ".join(f"{n} {w:.2e}" for n, w in worst.items()))
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_forward_reference_moves(dev, dtype):
+    """Scores that grow along the keys (q = 1, k_j = j/16: 0.72 log2 units
+    per key at D = 64): every key tile's max exceeds the row's reference by
+    more than 8, so the forward moves the reference on every tile (the
+    rescale branch, which random inputs take only on the first tile).  bf16
+    against the rounding emulation (which models where the reference moves),
+    fp32 against the oracle: the forward outputs and dV.
+    (dQ and dK are only checked finite: with scores up to ~180 log2 units
+    the bf16 rounding of the pre-scaled operand moves P by tens of percent
+    and dS cancels, so the emulation itself is 47% / 24% away from float64
+    there and last-bit differences are amplified past any elementwise bar.)"""
+    from oracle.attention import _lazy_reference, causal_mask, LOG2E
+
+    _say(f"[attn moving reference] {dtype}")
+    B, H, T, D = 1, 2, 256, 64
+    rng = np.random.default_rng(57)
+    q = np.ones((B, H, T, D), np.float32)
+    k = np.broadcast_to((np.arange(T, dtype=np.float32) / 16)[:, None], (B, H, T, D)).copy()
+    v = bf16_round(rng.standard_normal((B, H, T, D), dtype=np.float32))
+    do = bf16_round(rng.standard_normal((B, H, T, D), dtype=np.float32))
+    s2 = np.where(causal_mask(T, T), -np.inf, (q[0, 0].astype(np.float64) * (0.125 * LOG2E)) @ k[0, 0].T)
+    mt = _lazy_reference(s2, 64, 8.0)
+    assert len(np.unique(mt[-1])) == 4  # the last row's reference moves on every tile
+    o, dq, dk, dv, lse = _run(dev, q, k, v, do, 0.125, True, dtype)
+    assert np.all(np.isfinite(dq)) and np.all(np.isfinite(dk))
+    if dtype == "bfloat16":
+        emu = attention_bf16_emulated(q, k, v, do, 0.125, True, onepass=_onepass(dtype, D))
+        for b in range(B):
+            for h in range(H):
+                for name, got, e in zip(("o", "lse", "dv"), (o, lse, dv), (emu[0], emu[1], emu[4])):
+                    _emu_bar(got[b, h], e[b, h], f"{name}[{b},{h}]")
+    else:
+        # fp32 scores of up to ~127 (natural units) carry rounding of about
+        # |s| 2^-22, which exp turns into that relative error in P: beyond
+        # the 1e-4 elementwise bar for any fp32 implementation, so 1e-3 of
+        # the largest entry here (a wrongly moved reference is off by O(1))
+        ro, _, _, rdv = reference_attention(q, k, v, do, 0.125, True)
+        for name, got, r in (("o", o, ro), ("dv", dv, rdv)):
+            err = float(np.abs(got - r).max())
+            assert err <= 1e-3 * float(np.abs(r).max()), (name, err)
+
+
 def test_bf16_elementwise_ragged_t(dev):
     """bf16 kernels elementwise against the rounding emulation at a T that is
     not a multiple of the 64-row tiles (ragged last query and key tiles,
