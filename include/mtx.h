@@ -420,8 +420,11 @@ int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const
  * the bf16 matrix cores with every fp32 operand value split into three bf16
  * pieces (x = x0 + x1 + x2 to 2^-24 |x|) and the six piece products of
  * weight >= 2^-16 accumulated in fp32: a dot product's error is the fp32
- * accumulation error plus at most ~2^-22 sum|a_k b_k| (NaN for non-finite
- * inputs).  MTX_GEMM_FP32 selects the fp32 MFMA kernel for them instead.
+ * accumulation error plus at most ~2^-22 sum|a_k b_k|.  Non-finite inputs,
+ * and finite ones of magnitude above bf16's largest value (~3.39e38, whose
+ * high piece rounds to Inf), give NaN where fp32 arithmetic could give a
+ * finite value or +-Inf.  MTX_GEMM_FP32 selects the fp32 MFMA kernel for
+ * them instead.
  * The mode is process-wide and read when a product is launched (or
  * recorded into a graph); every entry point of this section follows it.
  */

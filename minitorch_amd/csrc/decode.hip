@@ -419,17 +419,51 @@ __global__ __launch_bounds__(kQaThreads) void qkv_attn_kernel(int B, int H, int 
 }
 
 // ---- greedy pick: first maximum per row and top-2 margin ----
+// np.argmax's order: a NaN ranks above every number (the first NaN is the
+// pick), otherwise the first maximum; a row of -Inf picks its first index.
+// i1 == n_cols marks "nothing seen yet" (a lane with no columns).
 struct Top2 {
   float m1, m2;
   int i1;
 };
 
-__device__ __forceinline__ Top2 merge(Top2 x, Top2 y) {
+// a ranks above b
+__device__ __forceinline__ bool above(float a, float b) { return a > b || (a != a && b == b); }
+__device__ __forceinline__ float top(float a, float b) { return above(b, a) ? b : a; }
+
+// column c (scanned in increasing order) with value v
+__device__ __forceinline__ void scan(Top2& t, float v, int c, int ncols) {
+  if (t.i1 == ncols || above(v, t.m1)) {
+    if (t.i1 != ncols) t.m2 = t.m1;
+    t.m1 = v;
+    t.i1 = c;
+  } else {
+    t.m2 = top(t.m2, v);
+  }
+}
+
+__device__ __forceinline__ Top2 merge(Top2 x, Top2 y, int ncols) {
+  if (y.i1 == ncols) return x;
+  if (x.i1 == ncols) return y;
   Top2 r;
-  r.m1 = fmaxf(x.m1, y.m1);
-  r.i1 = x.m1 > y.m1 ? x.i1 : (y.m1 > x.m1 ? y.i1 : min(x.i1, y.i1));
-  r.m2 = x.m1 >= y.m1 ? fmaxf(x.m2, y.m1) : fmaxf(x.m1, y.m2);
+  const bool xa = above(x.m1, y.m1), ya = above(y.m1, x.m1);
+  const bool xw = xa || (!ya && x.i1 < y.i1);  // ties: the lower index
+  r.m1 = xw ? x.m1 : y.m1;
+  r.i1 = xw ? x.i1 : y.i1;
+  r.m2 = xw ? top(x.m2, y.m1) : top(y.m2, x.m1);
   return r;
+}
+
+__device__ __forceinline__ Top2 reduce_top2(Top2 t, int ncols) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    Top2 o;
+    o.m1 = __shfl_xor(t.m1, m, 64);
+    o.m2 = __shfl_xor(t.m2, m, 64);
+    o.i1 = __shfl_xor(t.i1, m, 64);
+    t = merge(t, o, ncols);
+  }
+  return t;
 }
 
 __global__ __launch_bounds__(256) void argmax_kernel(int rows, int cols, const float* __restrict__ x,
@@ -440,24 +474,8 @@ __global__ __launch_bounds__(256) void argmax_kernel(int rows, int cols, const f
   if (row >= rows) return;  // wave-uniform
   const float* __restrict__ xr = x + (int64_t)row * ld;
   Top2 t{-INFINITY, -INFINITY, cols};
-  for (int c = lane; c < cols; c += 64) {
-    const float v = xr[c];
-    if (v > t.m1) {
-      t.m2 = t.m1;
-      t.m1 = v;
-      t.i1 = c;
-    } else if (v > t.m2) {
-      t.m2 = v;
-    }
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    Top2 o;
-    o.m1 = __shfl_xor(t.m1, m, 64);
-    o.m2 = __shfl_xor(t.m2, m, 64);
-    o.i1 = __shfl_xor(t.i1, m, 64);
-    t = merge(t, o);
-  }
+  for (int c = lane; c < cols; c += 64) scan(t, xr[c], c, cols);
+  t = reduce_top2(t, cols);
   if (lane == 0) {
     idx[(int64_t)row * idx_stride] = t.i1;
     if (margin != nullptr) margin[(int64_t)row * margin_stride] = t.m1 - t.m2;
@@ -493,24 +511,8 @@ __global__ __launch_bounds__(256) void greedy_pick_kernel(int rows, int cols, co
   if (row >= rows) return;  // wave-uniform
   const float* __restrict__ xr = x + (int64_t)row * ld;
   Top2 t{-INFINITY, -INFINITY, cols};
-  for (int c = lane; c < cols; c += 64) {
-    const float v = xr[c];
-    if (v > t.m1) {
-      t.m2 = t.m1;
-      t.m1 = v;
-      t.i1 = c;
-    } else if (v > t.m2) {
-      t.m2 = v;
-    }
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    Top2 o;
-    o.m1 = __shfl_xor(t.m1, m, 64);
-    o.m2 = __shfl_xor(t.m2, m, 64);
-    o.i1 = __shfl_xor(t.i1, m, 64);
-    t = merge(t, o);
-  }
+  for (int c = lane; c < cols; c += 64) scan(t, xr[c], c, cols);
+  t = reduce_top2(t, cols);
   if (lane == 0) {
     const int L = lengths[row];
     cur[row] = t.i1;
@@ -636,23 +638,10 @@ __global__ __launch_bounds__(64 * kHpW) void head_pick_kernel(int rows, int K, i
 #pragma unroll
       for (int q = 0; q < kHpW; ++q) v += part[q * 64 * VPL + c];
       if (bias) v += bias[c];
-      if (v > t.m1) {
-        t.m2 = t.m1;
-        t.m1 = v;
-        t.i1 = c;
-      } else if (v > t.m2) {
-        t.m2 = v;
-      }
+      scan(t, v, c, V);
     }
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    Top2 o;
-    o.m1 = __shfl_xor(t.m1, m, 64);
-    o.m2 = __shfl_xor(t.m2, m, 64);
-    o.i1 = __shfl_xor(t.i1, m, 64);
-    t = merge(t, o);
-  }
+  t = reduce_top2(t, V);
   if (lane == 0) pick_record(row, rows, t, cur, ids, Tmax, margins, t_base, nm, lengths, pos);
 }
 

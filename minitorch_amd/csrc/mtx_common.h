@@ -27,11 +27,16 @@ int fail(int code, const char* fmt, ...);
   do {                                                            \
     if (!(cond)) return ::mtx::fail(MTX_ERR_SHAPE, __VA_ARGS__);  \
   } while (0)
+// A failing runtime call also leaves its error as the thread's last error;
+// it is reported here and cleared, so that the next launch check
+// (MTX_LAUNCHED) does not take it for that launch's
 #define MTX_HIP(expr)                                                           \
   do {                                                                          \
     hipError_t _e = (expr);                                                     \
-    if (_e != hipSuccess)                                                       \
+    if (_e != hipSuccess) {                                                     \
+      (void)hipGetLastError();                                                  \
       return ::mtx::fail(MTX_ERR_HIP, "%s: %s", #expr, hipGetErrorString(_e));  \
+    }                                                                           \
   } while (0)
 // check the launch that was just issued
 #define MTX_LAUNCHED()                                                          \

@@ -362,6 +362,26 @@ struct GraphRec {
   hipGraphExec_t exec;
   int pool;
 };
+
+// A graph pool ends (its graph destroyed, or its capture failed): it leaves
+// the live list and its free blocks join the general pool; blocks of it still
+// in use go to the general pool when freed (mtx_free checks pool_alive).
+void retire_pool(Allocator& A, int pool) {
+  std::lock_guard<std::mutex> lk(A.mu);
+  for (size_t i = 0; i < A.live_pools.size(); ++i)
+    if (A.live_pools[i] == pool) {
+      A.live_pools.erase(A.live_pools.begin() + i);
+      break;
+    }
+  auto fl = A.free_lists.find(pool);
+  if (fl != A.free_lists.end()) {
+    for (auto& kv : fl->second) {
+      A.cached[kv.second].pool = 0;
+      A.free_lists[0].emplace(kv.first, kv.second);
+    }
+    A.free_lists.erase(pool);
+  }
+}
 }  // namespace
 
 extern "C" int mtx_graph_begin(void* stream) {
@@ -375,8 +395,14 @@ extern "C" int mtx_graph_begin(void* stream) {
   }
   const hipError_t rc = hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeRelaxed);
   if (rc != hipSuccess) {
-    std::lock_guard<std::mutex> lk(A.mu);
-    A.capture_pool = 0;
+    int pool;
+    {
+      std::lock_guard<std::mutex> lk(A.mu);
+      pool = A.capture_pool;
+      A.capture_pool = 0;
+    }
+    retire_pool(A, pool);
+    (void)hipGetLastError();
     return fail(MTX_ERR_HIP, "hipStreamBeginCapture: %s", hipGetErrorString(rc));
   }
   return MTX_OK;
@@ -392,12 +418,22 @@ extern "C" int mtx_graph_end(void* stream, void** out) {
     pool = A.capture_pool;
     A.capture_pool = 0;
   }
+  // on failure (a capture invalidated by an illegal call, an instantiation
+  // error) the capture's pool ends here: nothing will replay it
   hipGraph_t g = nullptr;
-  MTX_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &g));
+  const hipError_t ec = hipStreamEndCapture(static_cast<hipStream_t>(stream), &g);
+  if (ec != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    retire_pool(A, pool);
+    (void)hipGetLastError();  // reported here, not by the next launch check
+    return fail(MTX_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(ec));
+  }
   hipGraphExec_t ex = nullptr;
   const hipError_t rc = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
   if (rc != hipSuccess) {
     (void)hipGraphDestroy(g);
+    retire_pool(A, pool);
+    (void)hipGetLastError();
     return fail(MTX_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(rc));
   }
   *out = new GraphRec{g, ex, pool};
@@ -416,23 +452,7 @@ extern "C" int mtx_graph_destroy(void* graph) {
   MTX_HIP(hipDeviceSynchronize());  // no replay of it is still running
   MTX_HIP(hipGraphExecDestroy(r->exec));
   MTX_HIP(hipGraphDestroy(r->graph));
-  Allocator& A = alloc();
-  {
-    std::lock_guard<std::mutex> lk(A.mu);
-    for (size_t i = 0; i < A.live_pools.size(); ++i)
-      if (A.live_pools[i] == r->pool) {
-        A.live_pools.erase(A.live_pools.begin() + i);
-        break;
-      }
-    auto fl = A.free_lists.find(r->pool);
-    if (fl != A.free_lists.end()) {
-      for (auto& kv : fl->second) {
-        A.cached[kv.second].pool = 0;
-        A.free_lists[0].emplace(kv.first, kv.second);
-      }
-      A.free_lists.erase(r->pool);
-    }
-  }
+  retire_pool(alloc(), r->pool);
   delete r;
   return MTX_OK;
 }

@@ -406,11 +406,17 @@ class DevBuf:
 
 def host_array(a, dtype: str) -> np.ndarray:
     """A contiguous host array in the device layout of `dtype` (bfloat16:
-    round-to-nearest-even to uint16 bit patterns)."""
+    round-to-nearest-even to uint16 bit patterns; a NaN stays a NaN of the
+    same sign -- the quiet NaN 0x7FC0 / 0xFFC0, as the rounding add would
+    otherwise carry a payload into the exponent)."""
     if dtype == "bfloat16":
         x = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
         u = x.view(np.uint32).astype(np.uint64)
-        return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+        r = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+        nan = np.isnan(x)
+        if nan.any():
+            r[nan] = (0x7FC0 | ((u[nan] >> 16) & 0x8000)).astype(np.uint16)
+        return r
     return np.ascontiguousarray(np.asarray(a, dtype=_HOST[dtype]))
 
 

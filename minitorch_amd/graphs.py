@@ -72,6 +72,9 @@ class Graph:
                 self._h = h
             elif rc == 0:
                 L.lib().mtx_graph_destroy(h)
+            # else: the block raised and the capture failed too; the library
+            # has already released the capture's memory pool, and the
+            # block's own exception is the one that propagates
 
     def replay(self):
         if self._h is None:

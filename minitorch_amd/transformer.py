@@ -480,13 +480,8 @@ class GPT(Module):
         V = self.lm_head.weight.shape[1]
         C = self.tok_emb.weight.shape[1]
         temp = dev.const(float(temperature))
-        def walk(m):
-            yield m
-            for _, c in m._children():
-                if isinstance(c, Module):
-                    yield from walk(c)
-
-        dropout_on = any(isinstance(m, Dropout) and m._training and m.p > 0.0 for m in walk(self))
+        mods = [self] + [m for kind, _, m, _ in self._walk() if kind == "module"]
+        dropout_on = any(isinstance(m, Dropout) and m._training and m.p > 0.0 for m in mods)
 
         def sample(logits2d):
             scaled = dev.empty((B, V))

@@ -197,15 +197,24 @@ def greedy_c4(path, n_new=224):
     argmax of model(idx[:, -block:]).data[:, -1, :] (transformer.py:93-98,
     full recompute as the reference generates).  Written after every step
     (write + rename), so a long run leaves a usable prefix; `steps` says how
-    many tokens each row holds beyond the prompt."""
+    many tokens each row holds beyond the prompt.  A run resumes from such a
+    prefix (each step depends only on the ids so far)."""
     model = ref_model(C2, np.random.default_rng(2))
     model.eval()
     prompts = np.random.default_rng(4).integers(0, C2.vocab, (64, 32))
     idx = prompts.copy()
     margins = []
+    start = 0
+    if path.exists():
+        z = np.load(path, allow_pickle=False)
+        assert np.array_equal(z["prompts"], prompts), "saved prefix is for other prompts"
+        start = int(z["steps"])
+        idx = z["tokens"].copy()
+        margins = list(z["margins"].T)
+        print(f"  resuming after {start} steps", flush=True)
     t0 = time.time()
     with mt.no_grad():
-        for it in range(n_new):
+        for it in range(start, n_new):
             logits = model(idx[:, -C2.block:]).data[:, -1, :]
             nxt = np.argmax(logits, axis=-1)
             top2 = np.sort(logits, axis=-1)[:, -2:]

@@ -118,12 +118,21 @@ def test_argmax_matches_numpy(dev):
         x[1, -1] = 50.0                   # maximum in the last column
         x[2, :] = 1.0                     # all equal
         x[3, 64 % cols] = x[3, 0] = 7.0   # tie across lanes
+        # np.argmax's order past the numbers: the first NaN wins (above
+        # +Inf), a row of -Inf picks index 0; margins come out NaN there
+        x[4, 10] = x[4, 50] = np.nan
+        x[5, :] = -np.inf
+        x[6, 7] = np.inf
+        x[6, 30] = np.nan
+        x[7, 63] = np.inf                 # +Inf in one lane, numbers elsewhere
         t = T(x)
         margin = empty((70,))
         idx, _ = K.argmax_rows(t, margin=margin)
         np.testing.assert_array_equal(idx.numpy(), np.argmax(x, axis=1))
         top2 = np.sort(x, axis=1)[:, -2:]
-        np.testing.assert_array_equal(margin.numpy(), top2[:, 1] - top2[:, 0])
+        with np.errstate(invalid="ignore"):  # -Inf - -Inf and NaN rows: NaN margins
+            want = top2[:, 1] - top2[:, 0]
+        np.testing.assert_array_equal(margin.numpy(), want)
 
 
 def _gelu64(x):
@@ -198,6 +207,7 @@ def test_greedy_pick_matches_argmax_advance_and_records(dev):
     rows, cols, Tmax, T0, n = 64, 65, 40, 10, 30
     x = rng.standard_normal((rows, cols)).astype(np.float32)
     x[5, 3] = x[5, 9] = 10.0  # tie: first index
+    x[6, 20] = x[6, 2] = np.nan  # a NaN logit: the first NaN (np.argmax), never an out-of-range id
     lengths = rng.integers(T0 + 1, Tmax, rows).astype(np.int32)
     lengths[7] = Tmax + 3     # past the id buffer: no record
     ids0 = rng.integers(0, 65, (Tmax, rows)).astype(np.int64)

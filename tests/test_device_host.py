@@ -94,6 +94,15 @@ def test_dtype_names_and_bf16_host_rounding():
     assert bits.dtype == np.uint16
     back = (bits.astype(np.uint32) << 16).view(np.float32)
     np.testing.assert_array_equal(back, bf16_round(x))
+    # NaNs with payloads (which round-to-nearest would carry into +-Inf or
+    # +-0) stay NaNs of their sign; Inf and the largest finite values round
+    # as IEEE rounding does (to Inf past the bf16 maximum)
+    pats = np.array([0x7F800001, 0x7FFFFFFF, 0xFFFFFFFF, 0xFF800001, 0x7FC00000, 0x7F800000, 0xFF800000,
+                     0x7F7FFFFF, 0x7F7F0000, 0x00000001, 0x80000000], dtype=np.uint32)
+    got = dev.host_array(pats.view(np.float32), "bfloat16")
+    want = np.array([0x7FC0, 0x7FC0, 0xFFC0, 0xFFC0, 0x7FC0, 0x7F80, 0xFF80, 0x7F80, 0x7F7F, 0x0000, 0x8000],
+                    dtype=np.uint16)
+    np.testing.assert_array_equal(got, want)
 
 
 def test_runtime_argument_checks_without_gpu():

@@ -618,3 +618,79 @@ def test_gemm_ln_matches_gemm_then_layernorm(dev, M, N, K):
     close(H(xs), xr, atol=dot_tol(K), name="gemm x")
     yr = ln_fwd(H(xf).astype(np.float64), gam.astype(np.float64), bet.astype(np.float64), 1e-5)[0]
     close(H(yf), yr, rtol=1e-4, atol=1e-4, name="gemm_ln y")
+
+
+def test_gemm_nonfinite_and_near_overflow(dev, gemm_mode):
+    """Inputs at the edge of the fp32 range, under both product kernels (a
+    512^3 product runs on the bf16-split kernel in its default mode).  Row 0
+    of A holds 3.4e38 (finite, but above bf16's largest finite value
+    3.39e38), row 1 holds +Inf; B's first row is 0.5.  fp32 MFMA: row 0 is
+    the finite fp32 result, row 1 is +Inf.  Split mode: both rows are NaN
+    (the high bf16 piece of 3.4e38 rounds to Inf, and Inf - Inf follows), as
+    documented for mtx_gemm_set_mode.  Every other row is unaffected."""
+    from minitorch_amd import kernels as Kn
+
+    _say(f"[gemm edge values] {gemm_mode}")
+    M = N = K = 512
+    rng = np.random.default_rng(99)
+    a = 0.1 * rng.standard_normal((M, K), dtype=np.float32)
+    b = 0.1 * rng.standard_normal((K, N), dtype=np.float32)
+    a[0, 0] = np.float32(3.4e38)
+    a[1, 0] = np.inf
+    b[0, :] = 0.5
+    tc = T(np.zeros((M, N), np.float32))
+    Kn.gemm(T(a), T(b), tc)
+    c = H(tc)
+    ref = a[2:].astype(np.float64) @ b
+    close(c[2:], ref, rtol=1e-4, atol=dot_tol(K), name="rows 2..")
+    if gemm_mode == "fp32":
+        ref0 = a[0].astype(np.float64) @ b
+        assert np.all(np.isfinite(c[0]))
+        np.testing.assert_allclose(c[0], ref0, rtol=1e-5)
+        assert np.all(c[1] == np.inf)
+    else:
+        assert np.all(np.isnan(c[0])) and np.all(np.isnan(c[1]))
+
+
+def test_failed_capture_releases_its_pool(dev):
+    """A capture that fails at mtx_graph_end (invalidated by synchronising
+    the capturing stream) releases its memory pool: a block freed into that
+    pool during the capture is reused by the next allocation of its size."""
+    import ctypes as C
+
+    from minitorch_amd import _lib as L
+
+    _say("[graph capture failure]")
+    lib = L.lib()
+    L.call("mtx_device_sync")
+    L.call("mtx_empty_cache")  # no cached general-pool block of this size
+    s = C.c_void_p()
+    L.call("mtx_stream_create", C.byref(s))
+    nbytes = 37 << 20
+    p = C.c_void_p()
+    L.call("mtx_malloc", C.byref(p), nbytes)
+    try:
+        L.call("mtx_graph_begin", s)
+        h = C.c_void_p()
+        try:
+            L.call("mtx_free", p)  # goes to the capture's pool
+            rc_sync = lib.mtx_stream_sync(s)
+        finally:
+            rc_end = lib.mtx_graph_end(s, C.byref(h))
+        if rc_end == 0:
+            lib.mtx_graph_destroy(h)
+            pytest.skip(f"the runtime did not invalidate the capture (sync rc {rc_sync})")
+        assert rc_sync != 0
+        q = C.c_void_p()
+        L.call("mtx_malloc", C.byref(q), nbytes)
+        assert q.value == p.value, "the failed capture's pool kept the block"
+        L.call("mtx_free", q)
+        # the failure is not reported again by the next launch
+        t = T(np.ones(1000, np.float32))
+        from minitorch_amd import kernels as Kn
+
+        Kn.ewise("COPY", t, t)
+        L.call("mtx_device_sync")
+    finally:
+        L.call("mtx_device_sync")
+        L.call("mtx_stream_destroy", s)
