@@ -528,6 +528,8 @@ def main():
                     help="--only gpt2/gpt0: the product kernel for shapes of >= 128 x 128")
     ap.add_argument("--attn-mode", choices=("bf16x3", "fp32"), default="bf16x3",
                     help="--only c1/gpt2/gpt0: the product kernel of fp32 attention (64-wide heads)")
+    ap.add_argument("--bwd-mode", choices=("default", "onepass", "twopass"), default="default",
+                    help="the attention backward structure for the C3/C1 legs (mtx_attn_set_bwd_mode)")
     ap.add_argument("--only", choices=("all", "c3", "c3series", "c1", "c0attn", "c4", "c4eager", "c4kernel", "gpt2", "gpt0"),
                     default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
@@ -549,6 +551,10 @@ def main():
         print(f"no GPU visible: {e}", file=sys.stderr)
         sys.exit(1)
 
+    if args.bwd_mode != "default":
+        from minitorch_amd import kernels as _K
+
+        _K.set_attn_bwd_mode(_K.ATTN_BWD_ONEPASS if args.bwd_mode == "onepass" else _K.ATTN_BWD_TWOPASS)
     if args.calibrate_copy:
         from minitorch_amd import kernels as K
 
@@ -643,18 +649,19 @@ def main():
     achieved = fl_dom / (ms_dom * 1e-3) / 1e12
     print(f"[bench] C3 step {r3['ms_step']:.3f} ms = {tflops:.1f} TFLOP/s (cold start {ms_cold:.3f} ms = "
           f"{(f3 + b3) / (ms_cold * 1e-3) / 1e12:.1f}); phases {r3}", file=sys.stderr, flush=True)
-    # the same step with the deterministic two-pass backward, for comparison
+    # the same step with the other backward structure, for comparison
     from minitorch_amd import kernels as _K
 
-    r3b = None
-    if _K.get_attn_bwd_mode() == _K.ATTN_BWD_ONEPASS:
-        prev_bwd = _K.set_attn_bwd_mode(_K.ATTN_BWD_TWOPASS)
-        try:
-            r3b, _ = bench_attention(B, H, T, D, "bfloat16", 3, 0.5, args.steps, args.warmup)
-        finally:
-            _K.set_attn_bwd_mode(prev_bwd)
-        print(f"[bench] C3 two-pass step {r3b['ms_step']:.3f} ms = "
-              f"{(f3 + b3) / (r3b['ms_step'] * 1e-3) / 1e12:.1f} TFLOP/s; phases {r3b}", file=sys.stderr, flush=True)
+    cur_bwd = _K.get_attn_bwd_mode()
+    other_bwd = _K.ATTN_BWD_TWOPASS if cur_bwd == _K.ATTN_BWD_ONEPASS else _K.ATTN_BWD_ONEPASS
+    other_name = "two-pass" if other_bwd == _K.ATTN_BWD_TWOPASS else "one-pass"
+    _K.set_attn_bwd_mode(other_bwd)
+    try:
+        r3b, _ = bench_attention(B, H, T, D, "bfloat16", 3, 0.5, args.steps, args.warmup)
+    finally:
+        _K.set_attn_bwd_mode(cur_bwd)
+    print(f"[bench] C3 {other_name} step {r3b['ms_step']:.3f} ms = "
+          f"{(f3 + b3) / (r3b['ms_step'] * 1e-3) / 1e12:.1f} TFLOP/s; phases {r3b}", file=sys.stderr, flush=True)
     if args.only == "c3":
         return
 
@@ -739,15 +746,19 @@ def main():
         "settle_ms": SETTLE_MS,
         "also": {
             "C3_phase_ms": {k_: round(v_, 4) for k_, v_ in r3.items()},
-            "C3_backward": ("one-pass (mtx_attn_set_bwd_mode MTX_ATTN_BWD_ONEPASS, the default): a "
-                            "delta kernel that zeroes dq, then one key-outer kernel writing dK/dV and "
-                            "adding dQ with fp32 atomics" if "ms_dkdvq" in r3 else
-                            "two passes (dQ query-outer with delta, then dK/dV key-outer)"),
-            "C3_twopass": None if r3b is None else {
+            "C3_backward": ("one-pass (mtx_attn_set_bwd_mode MTX_ATTN_BWD_ONEPASS): a delta kernel "
+                            "that zeroes dq, then one key-outer kernel writing dK/dV and adding dQ with "
+                            "fp32 atomics" if "ms_dkdvq" in r3 else
+                            "two passes (the default, MTX_ATTN_BWD_TWOPASS: dQ query-outer with delta, "
+                            "then dK/dV key-outer; deterministic)"),
+            "C3_other_backward": {
+                "mode": other_name,
                 "ms_per_step": round(r3b["ms_step"], 4),
                 "tflops": round((f3 + b3) / (r3b["ms_step"] * 1e-3) / 1e12, 2),
                 "phase_ms": {k_: round(v_, 4) for k_, v_ in r3b.items()},
-                "note": "the same step with the deterministic two-pass backward (MTX_ATTN_BWD_TWOPASS)"},
+                "note": "the same step with the other backward structure (mtx_attn_set_bwd_mode); "
+                        "one-pass phases: prep = delta + dq zeroed, dkdvq = key-outer kernel with "
+                        "dQ atomics"},
             "C3_cold_start": {"ms_per_step": round(ms_cold, 4),
                               "tflops": round((f3 + b3) / (ms_cold * 1e-3) / 1e12, 2),
                               "note": f"{args.warmup} warm-up + {args.steps} timed steps right after the "

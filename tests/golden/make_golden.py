@@ -220,6 +220,10 @@ def greedy_c4(path, n_new=224):
             top2 = np.sort(logits, axis=-1)[:, -2:]
             margins.append(top2[:, 1] - top2[:, 0])
             idx = np.concatenate([idx, nxt[:, None]], axis=1)
+            # the step's graph holds reference cycles (node <-> closure): free
+            # it now, or ~0.5 GB per step accumulates until the cyclic collector runs
+            del logits
+            gc.collect()
             tmp = path.with_name(path.stem + ".part.npz")
             np.savez_compressed(tmp, prompts=prompts, tokens=idx, margins=np.stack(margins, 1),
                                 steps=it + 1)
