@@ -301,18 +301,39 @@ def bench_c4(n_new=224):
     model.init_weights(np.random.default_rng(2))
     model.eval()
     prompts = np.random.default_rng(4).integers(0, c["vocab"], (64, 32))
-    model.generate_greedy(prompts, 8)  # warm-up (library load, allocator)
-    _sync()
-    best = None
-    for _ in range(2):
-        t0 = time.perf_counter()
-        toks = model.generate_greedy(prompts, n_new)
-        dt = time.perf_counter() - t0
-        best = dt if best is None else min(best, dt)
+    import minitorch_amd.transformer as tr
+
+    def timed():
+        model.generate_greedy(prompts, 8)  # warm-up (library load, allocator)
+        _sync()
+        best, toks = None, None
+        for _ in range(2):
+            t0 = time.perf_counter()
+            toks = model.generate_greedy(prompts, n_new)
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        return best, toks
+
+    def name(persistent):
+        return ("persistent: the 223 token steps after the prefill's pick in one cooperative launch "
+                "(mtx_decode_step_f32)" if persistent
+                else "chain: 32 launches per token step, recorded once as a HIP graph and replayed")
+
+    mode = tr._PERSISTENT_STEP
+    best, toks = timed()
     assert toks.shape == (64, 32 + n_new)
+    tr._PERSISTENT_STEP = not mode
+    try:
+        other, toks2 = timed()
+    finally:
+        tr._PERSISTENT_STEP = mode
+    assert np.array_equal(toks, toks2), "the two decode-step structures disagree"
     dk = bench_decode_kernel(c)
     return {"tokens_per_s": round(64 * n_new / best, 1), "ms_total": round(best * 1e3, 2),
             "ms_per_token_step": round(best * 1e3 / n_new, 4),
+            "decode_step": name(mode),
+            "other_decode_step": {"structure": name(not mode), "ms_per_token_step": round(other * 1e3 / n_new, 4),
+                                  "tokens_per_s": round(64 * n_new / other, 1), "same_tokens": True},
             "decode_kernel": dk,
             "config": "C2 model (6x384, 6 heads), 64 prompts x 32 ids, +224 greedy tokens, fp32, KV cache"}
 
@@ -528,9 +549,12 @@ def main():
                     help="--only gpt2/gpt0: the product kernel for shapes of >= 128 x 128")
     ap.add_argument("--attn-mode", choices=("bf16x3", "fp32"), default="bf16x3",
                     help="--only c1/gpt2/gpt0: the product kernel of fp32 attention (64-wide heads)")
+    ap.add_argument("--decode", choices=("default", "persistent", "chain"), default="default",
+                    help="the greedy decode step of the C4 leg: one persistent launch or the chain of launches")
     ap.add_argument("--bwd-mode", choices=("default", "onepass", "twopass"), default="default",
                     help="the attention backward structure for the C3/C1 legs (mtx_attn_set_bwd_mode)")
-    ap.add_argument("--only", choices=("all", "c3", "c3series", "c1", "c0attn", "c4", "c4eager", "c4kernel", "gpt2", "gpt0"),
+    ap.add_argument("--only", choices=("all", "c3", "c3series", "c1", "c0attn", "c4", "c4eager", "c4step", "c4kernel",
+                                       "gpt2", "gpt0"),
                     default="all",
                     help="profiling aid: run only one attention config and print no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -551,6 +575,10 @@ def main():
         print(f"no GPU visible: {e}", file=sys.stderr)
         sys.exit(1)
 
+    if args.decode != "default":
+        import minitorch_amd.transformer as _tr
+
+        _tr._PERSISTENT_STEP = args.decode == "persistent"
     if args.bwd_mode != "default":
         from minitorch_amd import kernels as _K
 
@@ -587,9 +615,12 @@ def main():
         c3_series()
         return
     if args.only == "c4eager":
-        # the C4 run with every decode step launched eagerly (no HIP graph):
-        # the same kernels, for a kernel-by-kernel trace
+        # the C4 run with the chain of launches, every decode step launched
+        # eagerly (no HIP graph): the same kernels, for a kernel-by-kernel trace
         import minitorch_amd as mt
+        import minitorch_amd.transformer as _tr
+
+        _tr._PERSISTENT_STEP = False
 
         c = C2_CFG
         model = mt.GPT(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"], dropout=0.0)
@@ -602,6 +633,25 @@ def main():
         model.generate_greedy(prompts, 224, graph=False)
         dt = time.perf_counter() - t0
         print(f"[bench] C4 eager steps: {dt * 1e3 / 224:.3f} ms per token step", file=sys.stderr)
+        return
+    if args.only == "c4step":
+        # the C4 run with the persistent decode step only (one launch per
+        # token step, no graph): a short workload for kernel traces
+        import minitorch_amd as mt
+        import minitorch_amd.transformer as _tr
+
+        _tr._PERSISTENT_STEP = True
+        c = C2_CFG
+        model = mt.GPT(c["vocab"], c["block"], c["n_embd"], c["n_head"], c["n_layer"], dropout=0.0)
+        model.init_weights(np.random.default_rng(2))
+        model.eval()
+        prompts = np.random.default_rng(4).integers(0, c["vocab"], (64, 32))
+        model.generate_greedy(prompts, 8)
+        _sync()
+        t0 = time.perf_counter()
+        model.generate_greedy(prompts, 224)
+        dt = time.perf_counter() - t0
+        print(f"[bench] C4 persistent steps: {dt * 1e3 / 224:.4f} ms per token step", file=sys.stderr)
         return
     if args.only == "c4kernel":
         bench_decode_kernel(C2_CFG, graph=False)

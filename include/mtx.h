@@ -402,6 +402,86 @@ int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const
                       int64_t ldw, const float* bias, int64_t* cur, int64_t* ids, int Tmax, float* margins,
                       int t_base, int n_margins, int* lengths, int64_t* pos, void* stream);
 
+/*
+ * `steps` consecutive greedy decode steps of a GPT in ONE launch (persistent,
+ * cooperative; each step's pick feeds the next step inside the launch, past
+ * one more grid-wide barrier): the token + position embeddings, every block (ln1, fused
+ * q/k/v projection with the cache writes, decode attention, out_proj,
+ * residual, ln2, fc1 + GELU, fc2, residual) and ln_f + lm_head + the pick
+ * with its bookkeeping (as mtx_head_pick_f32: cur, ids, margins, lengths,
+ * pos).  Replaces one iteration of GPT.generate's loop (transformer.py:93-104:
+ * the forward of transformer.py:80-91 at the last position, then np.argmax)
+ * for the KV-cache decode; the multi-launch chain of mtx_decode_qkv_attn_f32,
+ * mtx_gemm_ln_f32, mtx_gemm_step_f32, mtx_gemm_partials_f32 and
+ * mtx_head_pick_f32 computes the same step in 2 + 5 per block launches.
+ *
+ * Model (plain pointers, fp32, row-major and contiguous): C = n_head * 64
+ * (head size 64) in {128, 256, 384, 512}, MLP width F = 4C (the block's
+ * Linear(C, 4C), transformer.py:57-59), V <= 256, 1 <= n_layer <= 16, Tmax
+ * <= 1024 cache rows, B >= 1; k_cache, v_cache and w_out 16-byte aligned.
+ * Weights are (in, out): w_qkv (C, 3C) with columns q | k | v, b_qkv (3C);
+ * w_out (C, C); w_fc1 (C, F); w_fc2 (F, C); w_head (C, V).  k_cache/v_cache
+ * are (B, Tmax, C).  Row b's new token sits at row lengths[b] - 1 of its
+ * caches and attends to rows [0, lengths[b]); the embedding reads token
+ * cur[b] (clamped to n_tok) and position pos[0] (clamped to n_pos).
+ *
+ * Grid-wide ordering: the launch is cooperative (every workgroup resident,
+ * or the launch fails), and the blocks' stages are separated by grid-wide
+ * barriers (two per block) in device memory held in the workspace.  Every
+ * barrier wait is bounded: a wait longer than wait_limit_us microseconds
+ * (0: the default, 2 s; negative: every wait fails at once, for tests of the
+ * failure path) sets an error word, every workgroup leaves the kernel, and
+ * every later step on that workspace returns at its start.  Read it with
+ * mtx_decode_step_status (which synchronises the stream);
+ * mtx_decode_step_reset clears it.
+ *
+ * Workspace: mtx_decode_step_workspace_bytes(B, C, n_head, F) bytes of
+ * device memory, 256-byte aligned, zeroed once before the first step (or by
+ * mtx_decode_step_reset); it holds the barrier words, the residual rows and
+ * the partial products between stages.  Steps that share a workspace must
+ * not overlap (one stream).  Deterministic: fixed summation orders.
+ */
+typedef struct mtx_decode_layer {
+  const float* ln1_gamma;
+  const float* ln1_beta;
+  const float* w_qkv;
+  const float* b_qkv;
+  const float* w_out;
+  const float* b_out;
+  const float* ln2_gamma;
+  const float* ln2_beta;
+  const float* w_fc1;
+  const float* b_fc1;
+  const float* w_fc2;
+  const float* b_fc2;
+  float* k_cache;
+  float* v_cache;
+  float ln1_eps;
+  float ln2_eps;
+} mtx_decode_layer;
+
+typedef struct mtx_decode_model {
+  int n_layer, B, C, n_head, F, V, Tmax;
+  const float* tok_emb;
+  int64_t n_tok;
+  const float* pos_emb;
+  int64_t n_pos;
+  const mtx_decode_layer* layers; /* host array of n_layer entries */
+  const float* lnf_gamma;
+  const float* lnf_beta;
+  float lnf_eps;
+  const float* w_head;
+  const float* b_head;
+} mtx_decode_model;
+
+size_t mtx_decode_step_workspace_bytes(int B, int C, int n_head, int F);
+int mtx_decode_step_f32(const mtx_decode_model* m, int steps, int64_t* cur, int64_t* ids, float* margins,
+                        int t_base, int n_margins, int* lengths, int64_t* pos, void* workspace,
+                        size_t workspace_bytes, int64_t wait_limit_us, void* stream);
+/* MTX_OK, or MTX_ERR_HIP with a message when a step's barrier wait ran out. */
+int mtx_decode_step_status(const void* workspace, void* stream);
+int mtx_decode_step_reset(void* workspace, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* GEMM                                                                     */
 /* ------------------------------------------------------------------------ */

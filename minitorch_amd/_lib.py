@@ -38,6 +38,23 @@ EW = dict(COPY=0, ADD=1, SUB=2, MUL=3, DIV=4, POW=5, AXPBY=6, SCALE_SHIFT=7, EXP
           ABS=20, SIGN=21)
 RED_SUM, RED_MAX = 0, 1
 
+
+
+class DecodeLayer(C.Structure):
+    """mtx_decode_layer (include/mtx.h): one block's weights and caches."""
+    _fields_ = [(n, _P) for n in ("ln1_gamma", "ln1_beta", "w_qkv", "b_qkv", "w_out", "b_out", "ln2_gamma",
+                                  "ln2_beta", "w_fc1", "b_fc1", "w_fc2", "b_fc2", "k_cache", "v_cache")] + [
+        ("ln1_eps", _F), ("ln2_eps", _F)]
+
+
+class DecodeModel(C.Structure):
+    """mtx_decode_model (include/mtx.h): the model a persistent decode step runs."""
+    _fields_ = [("n_layer", _I), ("B", _I), ("C", _I), ("n_head", _I), ("F", _I), ("V", _I), ("Tmax", _I),
+                ("tok_emb", _P), ("n_tok", _I64), ("pos_emb", _P), ("n_pos", _I64),
+                ("layers", C.POINTER(DecodeLayer)), ("lnf_gamma", _P), ("lnf_beta", _P), ("lnf_eps", _F),
+                ("w_head", _P), ("b_head", _P)]
+
+
 # name -> (restype, argtypes); mirrors include/mtx.h
 SIGNATURES = {
     "mtx_last_error": (C.c_char_p, []),
@@ -78,6 +95,10 @@ SIGNATURES = {
     "mtx_argmax_f32": (_I, [_I, _I, _P, _I64, _P, _I64, _P, _I64, _P]),
     "mtx_kv_append_f32": (_I, [_I, _I, _I, _P, _I64, _P, _I64, _I64, _P, _P]),
     "mtx_decode_advance": (_I, [_I, _P, _P, _P]),
+    "mtx_decode_step_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "mtx_decode_step_f32": (_I, [_P, _I, _P, _P, _P, _I, _I, _P, _P, _P, _SZ, _I64, _P]),
+    "mtx_decode_step_status": (_I, [_P, _P]),
+    "mtx_decode_step_reset": (_I, [_P, _P]),
     "mtx_greedy_pick_f32": (_I, [_I, _I, _P, _I64, _P, _P, _I, _P, _I, _I, _P, _P, _P]),
     "mtx_embedding2_ln_fwd_f32": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I,
                                        _P, _P, _F, _P, _I64, _P]),

@@ -8,6 +8,8 @@ arguments, found before any HIP call) or ``MtxError`` (HIP failure).
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 
 from . import _lib as L
@@ -155,6 +157,112 @@ def attn_decode(q, k, v, scale: float, out=None, lse=None, lengths=None):
            L.ptr(lengths) if lengths is not None else None, float(scale),
            L.stream_handle())
     return out, lse
+
+
+DECODE_STEP_WIDTHS = (128, 256, 384, 512)
+_DECODE_LAYER_KEYS = ("ln1_gamma", "ln1_beta", "w_qkv", "b_qkv", "w_out", "b_out", "ln2_gamma", "ln2_beta",
+                      "w_fc1", "b_fc1", "w_fc2", "b_fc2", "k_cache", "v_cache")
+
+
+def decode_step_fits(n_layer, C, n_head, F, V, Tmax):
+    """Whether mtx_decode_step_f32 runs the model: head size 64 with C in
+    {128, 256, 384, 512}, MLP width F = 4C, V <= 256, up to 16 blocks and
+    1024 cache rows."""
+    return (C in DECODE_STEP_WIDTHS and C == 64 * n_head and F == 4 * C
+            and 1 <= V <= 256 and 1 <= n_layer <= 16 and 1 <= Tmax <= 1024)
+
+
+class DecodeStep:
+    """A GPT's greedy decode step as one persistent, cooperative launch
+    (mtx_decode_step_f32): embeddings, every block, ln_f, lm_head and the
+    pick, with grid-wide barriers between stages.
+
+    layers: one dict per block of fp32 device arrays, contiguous, weights
+    (in, out): ln1_gamma, ln1_beta, w_qkv (C, 3C) [q | k | v], b_qkv, w_out
+    (C, C), b_out, ln2_gamma, ln2_beta, w_fc1 (C, F), b_fc1, w_fc2 (F, C),
+    b_fc2, k_cache and v_cache (B, Tmax, C), plus ln1_eps and ln2_eps
+    floats.  tok_emb (n_tok, C), pos_emb (n_pos, C), lnf = (gamma, beta,
+    eps), w_head (C, V), b_head (V,).  The workspace (barrier words, residual
+    rows, partial products) is allocated and zeroed here; the steps of one
+    DecodeStep run in order on one stream."""
+
+    def __init__(self, layers, tok_emb, pos_emb, lnf, w_head, b_head, B, Tmax):
+        C = tok_emb.shape[1]
+        F = layers[0]["w_fc1"].shape[1]
+        V = w_head.shape[1]
+        H = C // 64
+        if not decode_step_fits(len(layers), C, H, F, V, Tmax):
+            raise ValueError("decode_step: model outside the persistent step's limits")
+        arrays = [tok_emb, pos_emb, lnf[0], lnf[1], w_head, b_head]
+        for y in layers:
+            arrays += [y[k] for k in _DECODE_LAYER_KEYS]
+        for t in arrays:
+            _need_cuda(t)
+            if _dt(t) != "float32" or not t.is_contiguous():
+                raise ValueError("decode_step: model arrays must be contiguous fp32 device arrays")
+        shapes = {"w_qkv": (C, 3 * C), "b_qkv": (3 * C,), "w_out": (C, C), "b_out": (C,), "w_fc1": (C, F),
+                  "b_fc1": (F,), "w_fc2": (F, C), "b_fc2": (C,), "ln1_gamma": (C,), "ln1_beta": (C,),
+                  "ln2_gamma": (C,), "ln2_beta": (C,), "k_cache": (B, Tmax, C), "v_cache": (B, Tmax, C)}
+        for i, y in enumerate(layers):
+            for k, s in shapes.items():
+                if tuple(y[k].shape) != s:
+                    raise ValueError(f"decode_step: layer {i} {k} has shape {tuple(y[k].shape)}, expected {s}")
+        if tuple(w_head.shape) != (C, V) or tuple(b_head.shape) != (V,) or pos_emb.shape[1] != C:
+            raise ValueError("decode_step: head or embedding shapes do not match")
+        self.B, self.C, self.Tmax, self.V = B, C, Tmax, V
+        self._arrays = arrays  # kept alive: the structs below hold their addresses
+        self._layers = (L.DecodeLayer * len(layers))()
+        for i, y in enumerate(layers):
+            for k in _DECODE_LAYER_KEYS:
+                setattr(self._layers[i], k, y[k].data_ptr())
+            self._layers[i].ln1_eps = float(y["ln1_eps"])
+            self._layers[i].ln2_eps = float(y["ln2_eps"])
+        m = L.DecodeModel()
+        m.n_layer, m.B, m.C, m.n_head, m.F, m.V, m.Tmax = len(layers), B, C, H, F, V, Tmax
+        m.tok_emb, m.n_tok = tok_emb.data_ptr(), tok_emb.shape[0]
+        m.pos_emb, m.n_pos = pos_emb.data_ptr(), pos_emb.shape[0]
+        m.layers = self._layers
+        m.lnf_gamma, m.lnf_beta, m.lnf_eps = lnf[0].data_ptr(), lnf[1].data_ptr(), float(lnf[2])
+        m.w_head, m.b_head = w_head.data_ptr(), b_head.data_ptr()
+        self._model = m
+        nbytes = L.lib().mtx_decode_step_workspace_bytes(B, C, H, F)
+        self.workspace = dev.zeros(((nbytes + 3) // 4,), "int32").t
+        self._ws_bytes = self.workspace.numel() * 4
+
+    def __call__(self, cur, ids, lengths, pos, margins=None, t_base=0, wait_limit_us=0, steps=1):
+        """`steps` token steps in one launch.  A step reads cur (B,) int64
+        and pos (1,) int64, appends to the caches at row lengths[b] - 1,
+        writes the pick to cur and ids (Tmax, B) at row lengths[b], the top-2
+        margin to margins (n, B) at row lengths[b] - t_base, then lengths +=
+        1 and pos += 1.  wait_limit_us bounds each grid-wide wait (0: the
+        library's 2 s; negative: every wait fails, for tests of the failure
+        path)."""
+        B = self.B
+        _need_cuda(cur, ids, lengths, pos)
+        if _dt(cur) != "int64" or cur.numel() != B or not cur.is_contiguous():
+            raise ValueError("decode_step: cur must be contiguous int64 (B,)")
+        if _dt(ids) != "int64" or ids.dim() != 2 or ids.shape[1] != B or not ids.is_contiguous():
+            raise ValueError("decode_step: ids must be contiguous int64 (Tmax, B)")
+        if _dt(lengths) != "int32" or lengths.numel() != B or not lengths.is_contiguous():
+            raise ValueError("decode_step: lengths must be contiguous int32 (B,)")
+        if _dt(pos) != "int64" or pos.numel() < 1:
+            raise ValueError("decode_step: pos must be int64")
+        if margins is not None and (_dt(margins) != "float32" or margins.dim() != 2 or margins.shape[1] != B
+                                    or not margins.is_contiguous()):
+            raise ValueError("decode_step: margins must be contiguous fp32 (n, B)")
+        L.call("mtx_decode_step_f32", ctypes.addressof(self._model), int(steps), L.ptr(cur), L.ptr(ids),
+               L.ptr(margins) if margins is not None else None, int(t_base),
+               margins.shape[0] if margins is not None else 0, L.ptr(lengths), L.ptr(pos),
+               L.ptr(self.workspace), self._ws_bytes, int(wait_limit_us), L.stream_handle())
+
+    def check(self):
+        """Synchronise and raise MtxError if a step's grid-wide wait ran out
+        (that step's results are incomplete; later steps did nothing)."""
+        L.call("mtx_decode_step_status", L.ptr(self.workspace), L.stream_handle())
+
+    def reset(self):
+        """Clear the barrier words and the error word."""
+        L.call("mtx_decode_step_reset", L.ptr(self.workspace), L.stream_handle())
 
 
 QKV_ATTN_MAX_C, QKV_ATTN_MAX_T = 1024, 2048

@@ -23,6 +23,9 @@ from .tensor import Tensor, no_grad
 # reads the rows (TransformerBlock.forward_step_deferred) where the size
 # limits allow; False keeps one reduce launch per block (forward_step)
 _DEFERRED_STEP = True
+# greedy decode steps run as one persistent launch each (mtx_decode_step_f32)
+# where the model fits its limits; False keeps the multi-launch step above
+_PERSISTENT_STEP = True
 
 
 def _linear_into(x, lin, out):
@@ -359,8 +362,10 @@ class GPT(Module):
         The loop stays on the device: each step's pick (mtx_greedy_pick_f32)
         lands in the id buffer the next step's embedding reads, and the same
         launch advances the step's positions (cache row, key count, position
-        id), device counters.  A step therefore replays unchanged:
-        with graph=True the first one-token step runs eagerly, the second is
+        id), device counters.  Where the model fits its limits each step is
+        one persistent launch (mtx_decode_step_f32, GPT._decode_step);
+        otherwise a step is a chain of launches that replays unchanged: with
+        graph=True the first one-token step runs eagerly, the second is
         recorded as a HIP graph and replayed for the rest.  The host
         synchronises once, at the end.  Needs T0 + max_new_tokens <=
         block_size (beyond it the reference crops the context and recomputes
@@ -440,23 +445,67 @@ class GPT(Module):
                     K.head_pick(hn.data.t.view(B, C), self.lm_head.weight.data.t, self.lm_head.bias.data.t, cur,
                                 ids.t, lengths, posd, margins.t, t_base=T0)
 
-                step()
-                if graph and n > 2:
+                ds = self._decode_step(caches, B, Tmax)
+                if ds is not None:
+                    # every remaining token step in one persistent launch;
+                    # the status word is read once
+                    ds(cur, ids.t, lengths, posd, margins=margins.t, t_base=T0, steps=n - 1)
+                    ds.check()
+                elif graph and n > 2:
                     from .graphs import Graph
 
+                    step()  # eager first: the recorded step then finds every buffer allocated
                     g = Graph()
                     with g.capture():
                         step()
                     for s in range(2, n):
                         g.replay()
                 else:
-                    for s in range(2, n):
+                    for s in range(1, n):
                         step()
         out = ids.t.numpy().T.copy()
         out[:, :T0] = idx
         if return_margins:
             return out, margins.t.numpy().T.astype(np.float64)
         return out
+
+    def _decode_step(self, caches, B, Tmax):
+        """The persistent one-launch decode step (kernels.DecodeStep) for
+        this model, or None where it does not apply: a block with an MLP
+        other than Linear-GELU-Linear, active dropout, a Linear without bias,
+        a head size other than 64 or a model beyond the kernel's limits."""
+        from . import kernels as K
+
+        C = self.tok_emb.weight.shape[1]
+        V = self.lm_head.weight.shape[1]
+        blocks = self.blocks
+        if not (_PERSISTENT_STEP and blocks):
+            return None
+        hid = blocks[0].mlp.layers[0].weight.shape[1]
+        if not K.decode_step_fits(len(blocks), C, C // 64, hid, V, Tmax) or self.lm_head.bias is None:
+            return None
+        layers = []
+        for blk, (kc, vc) in zip(blocks, caches):
+            fc1, act, fc2, drop = blk.mlp.layers
+            attn = blk.attn
+            if (attn.n_head * 64 != C or not isinstance(act, GELU) or (drop._training and drop.p > 0.0)
+                    or (attn.attn_drop._training and attn.attn_drop.p > 0.0) or fc1.weight.shape[1] != hid
+                    or any(lin.bias is None for lin in (fc1, fc2, attn.out_proj, attn.q_proj, attn.k_proj,
+                                                        attn.v_proj))):
+                return None
+            if attn._qkv is None:
+                attn.fuse_qkv()
+            W, b = attn._qkv
+            layers.append(dict(
+                ln1_gamma=blk.ln1.gamma.data.t, ln1_beta=blk.ln1.beta.data.t,
+                ln1_eps=float(np.float32(blk.ln1.eps)), w_qkv=W.data.t, b_qkv=b.data.t,
+                w_out=attn.out_proj.weight.data.t, b_out=attn.out_proj.bias.data.t,
+                ln2_gamma=blk.ln2.gamma.data.t, ln2_beta=blk.ln2.beta.data.t,
+                ln2_eps=float(np.float32(blk.ln2.eps)), w_fc1=fc1.weight.data.t, b_fc1=fc1.bias.data.t,
+                w_fc2=fc2.weight.data.t, b_fc2=fc2.bias.data.t, k_cache=kc.t, v_cache=vc.t))
+        lnf = (self.ln_f.gamma.data.t, self.ln_f.beta.data.t, float(np.float32(self.ln_f.eps)))
+        return K.DecodeStep(layers, self.tok_emb.weight.data.t, self.pos_emb.weight.data.t, lnf,
+                            self.lm_head.weight.data.t, self.lm_head.bias.data.t, B, Tmax)
 
     def generate(self, idx, max_new_tokens, temperature=1.0):
         """Sample tokens as the reference does (transformer.py:93-104): each

@@ -15,6 +15,34 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 
+def _keep_host_memory_mapped():
+    """The oracle's full-size checks allocate and free hundreds of MB of
+    float64 arrays per step.  On hosts where a fresh page costs a slow fault
+    (virtual machines with transparent huge pages) that dominates their run
+    time, so freed memory stays in the process (glibc: no mmap for large
+    blocks, no trimming) and NumPy stops asking for huge pages.  Run-time
+    settings only; results are unchanged."""
+    import ctypes
+
+    import numpy as np
+
+    try:
+        np._core.multiarray._set_madvise_hugepage(False)
+    except AttributeError:
+        pass
+    try:
+        libc = ctypes.CDLL("libc.so.6")
+        M_TRIM_THRESHOLD, M_TOP_PAD, M_MMAP_MAX = -1, -2, -4
+        libc.mallopt(M_MMAP_MAX, 0)
+        libc.mallopt(M_TRIM_THRESHOLD, 1 << 30)
+        libc.mallopt(M_TOP_PAD, 256 << 20)
+    except OSError:
+        pass
+
+
+_keep_host_memory_mapped()
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X GPU (HIP library calls)")
     config.addinivalue_line("markers", "slow: long-running CPU test")

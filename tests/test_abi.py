@@ -175,3 +175,57 @@ def test_captured_step_needs_an_eager_warmup():
 
     with pytest.raises(ValueError, match="warm-up"):
         CapturedStep(lambda: None, warmup=0)
+
+
+def _decode_model(n_layer=2, C=384, n_head=6, F=1536, V=65, Tmax=64, B=4, null=None):
+    """An mtx_decode_model of fake (never dereferenced) device addresses."""
+    layers = (L.DecodeLayer * n_layer)()
+    for y in layers:
+        for name, _ in L.DecodeLayer._fields_[:14]:
+            setattr(y, name, 0x100000)
+        y.ln1_eps = y.ln2_eps = 1e-5
+    if null is not None:
+        setattr(layers[0], null, None)
+    m = L.DecodeModel(n_layer, B, C, n_head, F, V, Tmax)
+    m.tok_emb = m.pos_emb = m.lnf_gamma = m.lnf_beta = m.w_head = m.b_head = 0x100000
+    m.n_tok, m.n_pos, m.lnf_eps = V, Tmax, 1e-5
+    m.layers = layers
+    return m, layers
+
+
+@pytest.mark.parametrize("over,code,frag", [
+    (dict(C=320, n_head=5), L.MTX_ERR_SHAPE, "C = 64 n_head"),
+    (dict(C=384, n_head=4), L.MTX_ERR_SHAPE, "head size 64"),
+    (dict(F=1024), L.MTX_ERR_SHAPE, "F = 4C"),
+    (dict(V=257), L.MTX_ERR_SHAPE, "V <="),
+    (dict(Tmax=1025), L.MTX_ERR_SHAPE, "Tmax"),
+    (dict(n_layer=17), L.MTX_ERR_SHAPE, "n_layer"),
+    (dict(null="w_fc2"), L.MTX_ERR_ARG, "null pointer in layer 0"),
+    (dict(ws=-256), L.MTX_ERR_ARG, "workspace"),
+    (dict(steps=0), L.MTX_ERR_ARG, "steps"),
+])
+def test_decode_step_rejects_bad_arguments(over, code, frag):
+    """mtx_decode_step_f32 validates the model, the buffers and the workspace
+    before any HIP call (no GPU needed)."""
+    lib = L.lib()
+    ws_delta = over.pop("ws", 0)
+    over_steps = over.pop("steps", 1)
+    m, keep = _decode_model(**over)
+    need = lib.mtx_decode_step_workspace_bytes(m.B, 384, 6, 1536)
+    assert need > 0
+    rc = lib.mtx_decode_step_f32(C.addressof(m), over_steps, 0x1000, 0x1000, None, 0, 0, 0x1000, 0x1000, 0x10000,
+                                 need + ws_delta, 0, None)
+    assert rc == code
+    assert frag in lib.mtx_last_error().decode()
+
+
+def test_decode_step_null_arguments():
+    lib = L.lib()
+    assert lib.mtx_decode_step_f32(None, 1, 0x1000, 0x1000, None, 0, 0, 0x1000, 0x1000, 0x10000, 1 << 30, 0,
+                                   None) == L.MTX_ERR_ARG
+    m, keep = _decode_model()
+    assert lib.mtx_decode_step_f32(C.addressof(m), 1, None, 0x1000, None, 0, 0, 0x1000, 0x1000, 0x10000,
+                                   1 << 30, 0, None) == L.MTX_ERR_ARG
+    assert lib.mtx_decode_step_status(None, None) == L.MTX_ERR_ARG
+    assert lib.mtx_decode_step_reset(None, None) == L.MTX_ERR_ARG
+    assert lib.mtx_decode_step_workspace_bytes(0, 384, 6, 1536) == 0

@@ -322,6 +322,20 @@ def test_cached_greedy_matches_reference_golden():
     np.testing.assert_allclose(margins, g["margins"], rtol=0, atol=2e-6)
 
 
+def test_c4_oracle_fixture_matches_reference_fixture():
+    """Config C4 at full size (the C2 model, 64 prompts x 32 ids, +224
+    greedy tokens): the oracle's cached decoding (c4_greedy.npz,
+    make_c4_fixture.py) gives the tokens the reference's own GPT.forward +
+    argmax loop wrote (c4_greedy_ref.npz, make_golden.py --only-c4), all
+    224 steps; margins agree to float32 rounding."""
+    r = load("c4_greedy_ref.npz")
+    o = load("c4_greedy.npz")
+    assert int(r["steps"]) == 224 and r["tokens"].shape == (64, 256)
+    np.testing.assert_array_equal(o["prompts"], r["prompts"])
+    np.testing.assert_array_equal(o["tokens"], r["tokens"])
+    np.testing.assert_allclose(o["margins"], r["margins"], rtol=0, atol=2e-6)
+
+
 def test_cached_greedy_equals_recompute_on_larger_model():
     cfg = G.GPTConfig(vocab=65, block=48, n_embd=96, n_head=6, n_layer=3)
     rng = np.random.default_rng(31)
