@@ -201,20 +201,20 @@ def _decode_model(n_layer=2, C=384, n_head=6, F=1536, V=65, Tmax=64, B=4, null=N
     (dict(Tmax=1025), L.MTX_ERR_SHAPE, "Tmax"),
     (dict(n_layer=17), L.MTX_ERR_SHAPE, "n_layer"),
     (dict(null="w_fc2"), L.MTX_ERR_ARG, "null pointer in layer 0"),
-    (dict(ws=-256), L.MTX_ERR_ARG, "workspace"),
+    (dict(ws=None), L.MTX_ERR_ARG, "workspace"),
     (dict(steps=0), L.MTX_ERR_ARG, "steps"),
 ])
 def test_decode_step_rejects_bad_arguments(over, code, frag):
     """mtx_decode_step_f32 validates the model, the buffers and the workspace
     before any HIP call (no GPU needed)."""
     lib = L.lib()
-    ws_delta = over.pop("ws", 0)
+    ws = over.pop("ws", 0x10000)  # a fake address: every case fails validation before any HIP call
     over_steps = over.pop("steps", 1)
     m, keep = _decode_model(**over)
     need = lib.mtx_decode_step_workspace_bytes(m.B, 384, 6, 1536)
     assert need > 0
-    rc = lib.mtx_decode_step_f32(C.addressof(m), over_steps, 0x1000, 0x1000, None, 0, 0, 0x1000, 0x1000, 0x10000,
-                                 need + ws_delta, 0, None)
+    rc = lib.mtx_decode_step_f32(C.addressof(m), over_steps, 0x1000, 0x1000, None, 0, 0, 0x1000, 0x1000, ws,
+                                 need, 0, None)
     assert rc == code
     assert frag in lib.mtx_last_error().decode()
 
