@@ -11,20 +11,20 @@ __version__ = "0.1.0"
 
 from . import functional as F  # noqa: E402
 from .graphs import CapturedStep  # noqa: E402
-from .layers import GELU, Dropout, Embedding, LayerNorm, Linear, ReLU, Sigmoid, Softmax, Tanh  # noqa: E402
-from .loss import cross_entropy_loss, mse_loss  # noqa: E402
+from .layers import GELU, Dropout, Embedding, LayerNorm, Linear  # noqa: E402
+from .loss import cross_entropy_loss  # noqa: E402
 from .module import Module, Sequential  # noqa: E402
-from .optim import SGD, Adam  # noqa: E402
-from .tensor import Tensor, cat, no_grad, stack  # noqa: E402
+from .optim import Adam  # noqa: E402
+from .tensor import Tensor, no_grad  # noqa: E402
 from .transformer import GPT, MultiHeadAttention, TransformerBlock  # noqa: E402
 
 __all__ = [
-    "Tensor", "no_grad", "cat", "stack",
+    "Tensor", "no_grad",
     "Module", "Sequential",
-    "Linear", "ReLU", "Sigmoid", "Tanh", "Softmax", "Dropout", "GELU", "LayerNorm", "Embedding",
+    "Linear", "Dropout", "GELU", "LayerNorm", "Embedding",
     "GPT", "TransformerBlock", "MultiHeadAttention",
-    "mse_loss", "cross_entropy_loss",
-    "SGD", "Adam",
+    "cross_entropy_loss",
+    "Adam",
     "CapturedStep",
     "F",
 ]

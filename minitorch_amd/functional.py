@@ -1,8 +1,9 @@
 """Stateless differentiable functions (the reference's functional.py, plus the
 fused ops the GPU path adds).
 
-Reference functions, same names and semantics: relu, sigmoid, tanh, gelu,
-softmax, log_softmax (functional.py:9-97).  Added fused ops, each one autograd
+Reference functions on the transformer's path, same names and semantics:
+tanh, gelu, softmax, log_softmax (functional.py:39-97; relu and sigmoid, off
+that path, are not provided).  Added fused ops, each one autograd
 node with a hand-written backward (the precedent is the reference's Conv2d,
 conv.py:66-95):
   linear(x, W, b)              x @ W + b with the bias in the GEMM epilogue
@@ -33,44 +34,6 @@ def _node(data, prev, op, backward, track):
         out._backward = backward
         out._prev = _parents(prev)
         out._op = op
-    return out
-
-
-def relu(x):
-    """max(0, x) (functional.py:9-21)."""
-    data = dev.empty(x.shape)
-    K.ewise("MAXIMUM", data.t, x.data.t, dev.const(0.0).t)
-    out = None
-
-    def _backward():
-        if x.requires_grad:
-            g = dev.empty(x.shape)
-            K.ewise("GT", g.t, x.data.t, dev.const(0.0).t)
-            K.ewise("MUL", g.t, g.t, out.grad.t)
-            _accum_grad(x, g, owned=True)
-
-    out = _node(data, (x,), "relu", _backward, _track(x))
-    return out
-
-
-def sigmoid(x):
-    """1 / (1 + exp(-x)) (functional.py:24-36)."""
-    data = dev.empty(x.shape)
-    K.ewise("NEG", data.t, x.data.t)
-    K.ewise("EXP", data.t, data.t)
-    K.ewise("SCALE_SHIFT", data.t, data.t, alpha=1.0, beta=1.0)
-    K.ewise("DIV", data.t, dev.const(1.0).t.expand(x.shape), data.t)
-    out = None
-
-    def _backward():
-        if x.requires_grad:
-            g = dev.empty(x.shape)
-            K.ewise("SCALE_SHIFT", g.t, out.data.t, alpha=-1.0, beta=1.0)
-            K.ewise("MUL", g.t, g.t, out.data.t)
-            K.ewise("MUL", g.t, g.t, out.grad.t)
-            _accum_grad(x, g, owned=True)
-
-    out = _node(data, (x,), "sigmoid", _backward, _track(x))
     return out
 
 

@@ -38,30 +38,6 @@ class Linear(Module):
         return F.linear(x, self.weight, self.bias)
 
 
-class ReLU(Module):
-    def forward(self, x):
-        return F.relu(x)
-
-
-class Sigmoid(Module):
-    def forward(self, x):
-        return F.sigmoid(x)
-
-
-class Tanh(Module):
-    def forward(self, x):
-        return F.tanh(x)
-
-
-class Softmax(Module):
-    def __init__(self, axis=-1):
-        super().__init__()
-        self.axis = axis
-
-    def forward(self, x):
-        return F.softmax(x, axis=self.axis)
-
-
 class GELU(Module):
     def forward(self, x):
         return F.gelu(x)

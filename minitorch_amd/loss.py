@@ -8,10 +8,6 @@ from .device import DeviceArray
 from .tensor import Tensor
 
 
-def mse_loss(input, target):
-    return ((input - target) ** 2).mean()
-
-
 def cross_entropy_loss(input, target):
     """Softmax cross-entropy of (N, V) logits (loss.py:17-27).  `target` holds
     class indices (a Tensor, array or list; one per row) or one-hot rows."""

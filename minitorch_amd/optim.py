@@ -162,23 +162,3 @@ class Adam(Optimizer):
         with np.load(path) as data:
             self.load_state_dict({k: data[k] for k in data.files})
         return self
-
-
-class SGD(Optimizer):
-    """SGD with momentum (optim.py:19-34): v = mu*v + g; p -= lr*v."""
-
-    def __init__(self, params, lr=1e-3, momentum=0.0, weight_decay=0.0):
-        super().__init__(params, lr, weight_decay)
-        self.momentum = momentum
-        self.velocities = [dev.zeros(p.shape) for p in self.params]
-
-    def step(self):
-        for p, v in zip(self.params, self.velocities):
-            if not p.requires_grad or p.grad is None:
-                continue
-            g = p.grad
-            if self.weight_decay:
-                g = g.copy()
-                K.ewise("AXPBY", g.t, g.t, p.data.t, alpha=1.0, beta=self.weight_decay)
-            K.ewise("AXPBY", v.t, v.t, g.t, alpha=self.momentum, beta=1.0)
-            K.ewise("AXPBY", p.data.t, p.data.t, v.t, alpha=1.0, beta=-self.lr)

@@ -210,10 +210,6 @@ class Tensor:
     def randn(*shape, requires_grad=False):
         return Tensor(np.random.randn(*shape).astype(np.float32), requires_grad=requires_grad)
 
-    @staticmethod
-    def eye(n, requires_grad=False):
-        return Tensor(np.eye(n, dtype=np.float32), requires_grad=requires_grad)
-
     def _should_track(self, *others):
         return _grad_enabled and any(t.requires_grad for t in (self, *others))
 
@@ -414,51 +410,6 @@ class Tensor:
         out = self._node(data, (self,), "mean", _backward, track)
         return out
 
-    def var(self, axis=None, keepdims=False):
-        m = self.mean(axis=axis, keepdims=True)
-        return ((self - m) ** 2).mean(axis=axis, keepdims=keepdims)
-
-    def std(self, axis=None, keepdims=False):
-        return (self.var(axis=axis, keepdims=keepdims) + 1e-12) ** 0.5
-
-    def _minmax(self, axis, keepdims, sign):
-        # max(x) = -min(-x); min computed through max of the negation
-        src = self.data
-        if sign < 0:
-            src = dev.empty(self.shape)
-            K.ewise("NEG", src.t, self.data.t)
-        axes = self._norm_axes(axis)
-        kept = [s for i, s in enumerate(self.shape) if i not in axes]
-        red = dev.empty(kept)
-        K.reduce(src.t, axes, red.t, op=1)
-        if sign < 0:
-            K.ewise("NEG", red.t, red.t)
-        kshape = [1 if i in axes else s for i, s in enumerate(self.shape)]
-        data = red.reshape(*kshape) if keepdims else red
-        track = self.requires_grad and _grad_enabled
-        out = None
-
-        def _backward():
-            if self.requires_grad:
-                # mask of the extreme entries, shared equally (tensor.py:283-289)
-                mask = dev.empty(self.shape)
-                K.ewise("EQ", mask.t, self.data.t, red.reshape(*kshape).broadcast_to(self.shape).t)
-                cnt = dev.empty(kept)
-                K.reduce(mask.t, axes, cnt.t)
-                g = dev.empty(self.shape)
-                K.ewise("DIV", g.t, mask.t, cnt.reshape(*kshape).broadcast_to(self.shape).t)
-                K.ewise("MUL", g.t, g.t, out.grad.reshape(*kshape).broadcast_to(self.shape).t)
-                _accum_grad(self, g, owned=True)
-
-        out = self._node(data, (self,), "max" if sign > 0 else "min", _backward, track)
-        return out
-
-    def max(self, axis=None, keepdims=False):
-        return self._minmax(axis, keepdims, 1)
-
-    def min(self, axis=None, keepdims=False):
-        return self._minmax(axis, keepdims, -1)
-
     # ---------------------------------------------------------------- shapes
     def reshape(self, *shape):
         """A view with a new shape when the layout allows, else a copy
@@ -490,26 +441,6 @@ class Tensor:
 
         out = self._node(data, (self,), "transpose", _backward, track)
         return out
-
-    def squeeze(self, axis=None):
-        shape = self.shape
-        if axis is None:
-            new = tuple(s for s in shape if s != 1)
-        else:
-            ax = (axis,) if isinstance(axis, int) else tuple(axis)
-            ax = {a % self.ndim for a in ax}
-            new = tuple(s for i, s in enumerate(shape) if i not in ax)
-        r = self.reshape(*new)
-        r._op = "squeeze"
-        return r
-
-    def unsqueeze(self, axis):
-        shape = list(self.shape)
-        axis = axis % (self.ndim + 1)
-        shape.insert(axis, 1)
-        r = self.reshape(*shape)
-        r._op = "unsqueeze"
-        return r
 
     def __getitem__(self, key):
         """Basic indexing (a strided view) or an integer index array on the
@@ -586,14 +517,6 @@ class Tensor:
             return g
         return self._unary("LOG", "log", gf)
 
-    def abs(self):
-        def gf(out):
-            g = dev.empty(self.shape)
-            K.ewise("SIGN", g.t, self.data.t)
-            K.ewise("MUL", g.t, g.t, out.grad.t)
-            return g
-        return self._unary("ABS", "abs", gf)
-
     # --------------------------------------------------------------- autograd
     def backward(self):
         """Reverse-mode autodiff from this scalar (tensor.py:453-477)."""
@@ -647,39 +570,3 @@ class Tensor:
 
     def __float__(self):
         return float(self.data.numpy())
-
-
-def cat(tensors, axis=0):
-    """Concatenate along an existing axis (tensor.py:502-518)."""
-    tensors = list(tensors)
-    shp = list(tensors[0].shape)
-    axis = axis % len(shp)
-    shp[axis] = sum(t.shape[axis] for t in tensors)
-    data = dev.empty(shp)
-    offs = []
-    o = 0
-    for t in tensors:
-        sl = [slice(None)] * len(shp)
-        sl[axis] = slice(o, o + t.shape[axis])
-        K.ewise("COPY", data.t[tuple(sl)], t.data.t)
-        offs.append(tuple(sl))
-        o += t.shape[axis]
-    track = _grad_enabled and any(t.requires_grad for t in tensors)
-    out = Tensor(data, requires_grad=track)
-
-    def _backward():
-        for t, sl in zip(tensors, offs):
-            if t.requires_grad:
-                _accum_grad(t, DeviceArray(out.grad.t[sl]))
-
-    if track:
-        out._backward = _backward
-        out._prev = _parents(tensors)
-        out._op = "cat"
-    return out
-
-
-def stack(tensors, axis=0):
-    """Stack along a new axis (tensor.py:521-537)."""
-    tensors = list(tensors)
-    return cat([t.unsqueeze(axis) for t in tensors], axis=axis)

@@ -60,6 +60,49 @@ def test_noalloc_matches_workspace_entry_point(dev, bf16, onepass):
         K.set_attn_bwd_mode(prev)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_noalloc_replayed_from_a_graph(dev, bf16):
+    """The callers the entry point is for record it: the backward captured
+    as a HIP graph and replayed three times, the outputs overwritten with NaN
+    by eager launches before every replay and the scratch array reused by an
+    eager call of another shape between replays; every replay equals the
+    eager call bit for bit (two-pass mode)."""
+    from minitorch_amd import kernels as K
+    from minitorch_amd.graphs import Graph
+
+    rng = np.random.default_rng(78)
+    prev = K.set_attn_bwd_mode(K.ATTN_BWD_TWOPASS)
+    try:
+        B, H, Tq, Tk, D = 2, 4, 200, 200, 64
+        _say(f"[noalloc] graph replay, bf16={bf16} B={B} H={H} T={Tq} D={D}")
+        q, k, v, do = _inputs(rng, (B, H, Tq, D), (B, H, Tk, D), bf16)
+        o, lse = K.attn_fwd(q, k, v, 0.125, True)
+        shapes = [(B, H, t, D) for t in (Tq, Tk, Tk)]
+        ref = [full(s, float("nan")) for s in shapes]
+        K.attn_bwd_noalloc(q, k, v, o, do, lse, 0.125, True, *ref)
+        sync()
+        ref = [r.numpy() for r in ref]
+        # another shape's inputs, run eagerly between replays
+        q2, k2, v2, do2 = _inputs(rng, (1, 3, 96, D), (1, 3, 96, D), bf16)
+        o2, lse2 = K.attn_fwd(q2, k2, v2, 0.125, True)
+        other = [full((1, 3, 96, D), 0.0) for _ in range(3)]
+        got = [full(s, float("nan")) for s in shapes]
+        g = Graph()
+        with g.capture():
+            K.attn_bwd_noalloc(q, k, v, o, do, lse, 0.125, True, *got)
+        for rep in range(3):
+            for t in got:
+                t.fill_(float("nan"))
+            g.replay()
+            K.attn_bwd_noalloc(q2, k2, v2, o2, do2, lse2, 0.125, True, *other)
+            sync()
+            for name, a, b in zip(("dq", "dk", "dv"), ref, got):
+                assert np.array_equal(a, b.numpy()), (rep, name)
+        del g
+    finally:
+        K.set_attn_bwd_mode(prev)
+
+
 def test_noalloc_rejects_oversize(dev):
     from minitorch_amd import _lib as L
 
