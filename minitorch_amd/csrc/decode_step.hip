@@ -1,4 +1,4 @@
-// One greedy decode step of a GPT in one persistent, cooperative launch, for
+// Greedy decode steps of a GPT in one persistent, cooperative launch, for
 // gfx950 (MI355X).
 //
 // mtx_decode_step_f32 replaces one iteration of the reference's generation
@@ -237,8 +237,10 @@ __device__ __forceinline__ bool ps_barrier(const PsArgs& a, int* flag) {
 
 // ---- stage A: (pair of sequences, head) ----
 // Weights of an item do not depend on the previous stage: a workgroup's
-// first item of a stage has them requested before the barrier that opens
-// the stage (PreA, PreB), so their latency overlaps the wait.
+// first stage-A item has its first weight batch requested before the
+// barrier that opens the stage (PreA), so that latency overlaps the wait.
+// (Stage B's weights requested that way pushed the kernel past 128 VGPRs
+// into spills; stage B requests its own at the item's start.)
 constexpr int kPsNPL = 3 * kPsD / 64;   // q, k, v columns of the head per lane
 constexpr int kPsBA = 36 / kPsNPL;      // weight rows per load batch in stage A
 struct PreA {
@@ -534,8 +536,7 @@ __device__ __forceinline__ void mlp_load2(const mtx_decode_layer& Ly, int F, int
 }
 
 template <int C>
-__device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, PsStageB& sm, PreB<C>& pre,
-                                            bool prefetched) {
+__device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, PsStageB& sm) {
   const mtx_decode_layer& Ly = a.L[l];
   const int B = a.B, F = a.F;
   const int ns = F / kPsHS;
@@ -545,7 +546,8 @@ __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, Ps
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   constexpr int kc = C / kPsW;
   const int k0 = w * kc;
-  if (!prefetched) mlp_load1<C>(Ly, F, item, pre);
+  PreB<C> pre;
+  mlp_load1<C>(Ly, F, item, pre);
   LnPar lp;
   if (w < kPsR) ln_load<C>(lp, Ly.ln2_gamma, Ly.ln2_beta, lane);
 
@@ -715,7 +717,6 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
   const int nb = ((a.B + kPsR - 1) / kPsR) * (a.F / kPsHS);
   const int first = blockIdx.x;
   PreA pa;
-  PreB<C> pb;
   if (first < na) attn_prefetch<C>(a, 0, first, pa);
   // token steps x blocks as one loop (a loop nest here makes the compiler
   // keep more values live across stages)
@@ -724,7 +725,7 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
     const int l = q % a.NL;
     for (int it = first; it < na; it += gridDim.x) ps_attn_item<C>(a, l, it, sm.a, pa, it == first);
     if (!ps_barrier(a, &flag)) return;
-    for (int it = first; it < nb; it += gridDim.x) ps_mlp_item<C>(a, l, it, sm.b, pb, false);
+    for (int it = first; it < nb; it += gridDim.x) ps_mlp_item<C>(a, l, it, sm.b);
     if (l + 1 == a.NL) {
       if (!ps_barrier(a, &flag)) return;
       for (int r = blockIdx.x; r < a.B; r += gridDim.x) ps_head_item<C, VPL>(a, r, sm.h);
