@@ -86,6 +86,7 @@ struct PsArgs {
   int steps;      // token steps in this launch
   mtx_decode_layer L[kPsMaxL];
 };
+static_assert(sizeof(PsArgs) <= 4096, "kernel arguments are limited to 4 KiB");
 
 constexpr int kPsOpart = 8192;  // out_proj group partial sums, floats
 struct PsStageA {
