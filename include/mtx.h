@@ -439,7 +439,9 @@ int mtx_head_pick_f32(int rows, int K, int V, const float* x, int64_t ldx, const
  * device memory, 256-byte aligned, zeroed once before the first step (or by
  * mtx_decode_step_reset); it holds the barrier words, the residual rows and
  * the partial products between stages.  Steps that share a workspace must
- * not overlap (one stream).  Deterministic: fixed summation orders.
+ * not overlap (one stream); they may differ in model and batch size (each
+ * launch counts its barriers from the base the launch before it left).
+ * Deterministic: fixed summation orders.
  */
 typedef struct mtx_decode_layer {
   const float* ln1_gamma;

@@ -22,14 +22,16 @@
 //   barrier;
 //   stage B, per block, items (8 rows, 64 hidden columns): the residual plus
 //     the head partials of out_proj and its bias (written back as the
-//     residual by the first column slab), ln2, fc1 + GELU on the slab, and
+//     residual by the first column slab), ln2, fc1 + GELU on the slab (its
+//     weight columns staged in LDS by direct loads while stage A runs), and
 //     fc2's partial product over the slab's 64 rows of its weight;
 //   barrier;
 //   after the last block, items (row): the residual plus the last fc2
 //     partials and bias, ln_f, lm_head and the pick with its bookkeeping.
 //
 // The barrier is a 64-bit arrival counter in device memory (the workspace),
-// touched by one thread per workgroup with agent-scope atomics.  Every
+// touched by one thread per workgroup with agent-scope atomics; each launch
+// counts from the base the launch before it left.  Every
 // wait is bounded by the 100 MHz wall clock: a wait that runs out sets the
 // workspace's error word and the workgroup leaves the kernel; waiting
 // workgroups see the word and leave too, and a later launch on the same
@@ -56,8 +58,9 @@ constexpr int kPsHS = 64;        // hidden columns per stage-B item
 constexpr int kPsMaxT = 1024;    // cache rows (scores of kPsS rows in LDS)
 constexpr int kPsMaxL = 16;
 constexpr int kPsMaxV = 256;
-// barrier words (unsigned), each on its own 128-byte line
-constexpr int kBarCount = 0, kBarErr = 64, kBarBytes = 512;
+// barrier words (unsigned), each on its own 128-byte line: the arrival
+// counter and the launch base (64-bit), the error word
+constexpr int kBarCount = 0, kBarBase = 32, kBarErr = 64, kBarBytes = 512;
 
 struct PsArgs {
   int NL, B, C, H, F, V, Tmax;
@@ -102,7 +105,6 @@ struct PsStageA {
 };
 struct PsStageB {
   float xs[kPsR][kPsMaxC];
-  float part[kPsW][kPsR][kPsHS];
   float hs[kPsR][kPsHS];
 };
 struct PsHead {
@@ -113,6 +115,22 @@ union PsSmem {
   PsStageA a;
   PsStageB b;
   PsHead h;
+};
+// Stage B's slab region: fc1's weights [C][64] (filled by direct loads),
+// then the fc1 partial sums [kPsW][kPsR][kPsHS], then the fc2 half sums
+// [2][kPsR][C].  Where it fits beside the union (C <= 384) it has LDS of its
+// own and a workgroup requests its first stage-B slab at the start of stage
+// A; otherwise it lies over stage A's data, after stage B's rows, and the
+// request waits for the end of stage A.
+template <int C>
+struct PsLds {
+  static constexpr int kUnion = (int)(sizeof(PsSmem) / sizeof(float));
+  static constexpr int kSlab = C * kPsHS;
+  static constexpr bool kApart = (kUnion + kSlab) * (int)sizeof(float) <= 160 * 1024 - 256;
+  static constexpr int kSlabOff = kApart ? kUnion : (int)(sizeof(PsStageB) / sizeof(float));
+  static constexpr int kTotal = kApart ? kUnion + kSlab : (kSlabOff + kSlab > kUnion ? kSlabOff + kSlab : kUnion);
+  static_assert(kPsW * kPsR * kPsHS <= kSlab && 2 * kPsR * C <= kSlab, "partial sums fit the slab region");
+  static_assert(kSlabOff % 4 == 0, "16-byte aligned slab");
 };
 
 // Data that crosses workgroups within a launch (the residual rows X0/X1, the
@@ -199,26 +217,29 @@ __device__ __forceinline__ float ps_pending(const PsArgs& a, const float* __rest
   return t;
 }
 
-// Grid-wide barrier over a 64-bit arrival counter that only grows: the
-// arrival that returns `prior` belongs to the round prior / G and the round
-// is complete when the counter reaches (prior / G + 1) G.  Each thread first
-// waits for its own stores (the device-scope stores are acknowledged once
-// they are visible across the device), the workgroup barrier then covers
-// every thread, and thread 0 arrives and polls; no cache write-back or
-// invalidation is needed, so the L2 caches keep the weights across stages.
-// Returns false when the step must end: this wait ran out, or another
-// workgroup's did.
-__device__ __forceinline__ bool ps_barrier(const PsArgs& a, int* flag) {
+// Grid-wide barrier over a 64-bit arrival counter that only grows.  A launch
+// reads the counter's value at its start from the base word (written by the
+// launch before it, so launches of different grid sizes may share a
+// workspace); its k-th barrier (k = 1, 2, ...) is complete when the counter
+// reaches base + k G, and its workgroup 0 leaves the final count as the next
+// launch's base.  `next` (thread 0) is this workgroup's next target.  Each
+// thread first waits for its own stores (the device-scope stores are
+// acknowledged once they are visible across the device), the workgroup
+// barrier then covers every thread, and thread 0 arrives and polls; no cache
+// write-back or invalidation is needed, so the L2 caches keep the weights
+// across stages.  Returns false when the step must end: this wait ran out,
+// or another workgroup's did.
+__device__ __forceinline__ bool ps_barrier(const PsArgs& a, int* flag, unsigned long long& next) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
     unsigned long long* count = reinterpret_cast<unsigned long long*>(a.bar + kBarCount);
     unsigned* err = a.bar + kBarErr;
-    const unsigned long long G = gridDim.x;
+    const unsigned long long target = next;
+    next += gridDim.x;
     const unsigned long long prior = __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned long long target = (prior / G + 1ull) * G;
     int ok = 1;
-    if (prior + 1ull != target) {
+    if (prior + 1ull < target) {
       const int64_t t0 = wall_clock64();
       while (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
         if (a.limit < 0 || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
@@ -240,8 +261,10 @@ __device__ __forceinline__ bool ps_barrier(const PsArgs& a, int* flag) {
 // Weights of an item do not depend on the previous stage: a workgroup's
 // first stage-A item has its first weight batch requested before the
 // barrier that opens the stage (PreA), so that latency overlaps the wait.
-// (Stage B's weights requested that way pushed the kernel past 128 VGPRs
-// into spills; stage B requests its own at the item's start.)
+// (Stage B's weights requested into registers that way pushed the kernel
+// past 128 VGPRs into spills; its fc1 slab goes to LDS by direct loads
+// instead, requested at the start of stage A, and fc2's weights are
+// requested at the item's start.)
 constexpr int kPsNPL = 3 * kPsD / 64;   // q, k, v columns of the head per lane
 constexpr int kPsBA = 36 / kPsNPL;      // weight rows per load batch in stage A
 struct PreA {
@@ -504,24 +527,39 @@ __device__ __forceinline__ void ps_attn_item(const PsArgs& a, int l, int item, P
 
 // ---- stage B: (8 rows, 64 hidden columns) ----
 // fc1: wave w sums weight rows [w kc, w kc + kc) for hidden column j0 +
-// lane; fc2: thread (half, n), n < C, sums the slab's hidden columns
-// [32 half, 32 half + 32) for all 8 rows of column n, and the two halves
-// are added through LDS
+// lane, the slab staged in LDS; fc2: thread (half, n), n < C, sums the
+// slab's hidden columns [32 half, 32 half + 32) for all 8 rows of column n,
+// and the two halves are added through LDS
 template <int C>
 struct PreB {
-  float w1v[C / kPsW];
   float w2v[kPsHS / 2];
 };
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// fc1's weight slab of an item (rows 0 .. C-1, columns j0 .. j0+63) into
+// w1s[k][64] by direct buffer loads into LDS: no registers, so a workgroup's
+// first item has it requested before the barrier that opens the stage.  One
+// wave load moves four rows (1 KiB); completion is the wave's vmcnt.
 template <int C>
-__device__ __forceinline__ void mlp_load1(const mtx_decode_layer& Ly, int F, int item, PreB<C>& p) {
-  constexpr int kc = C / kPsW;
+__device__ __forceinline__ void mlp_dma(const mtx_decode_layer& Ly, int F, int item, float* w1s) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int NI = C / 4, PW = NI / kPsW;
+  static_assert(NI % kPsW == 0, "whole wave loads per wave");
   const int j0 = (item % (F / kPsHS)) * kPsHS;
   const int tid = ps_tid();
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const float* __restrict__ wr = Ly.w_fc1 + (int64_t)(w * kc) * F + j0;
+  const int bytes = ((C - 1) * F + kPsHS) * (int)sizeof(float);
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Ly.w_fc1 + j0), (short)0, bytes, 0x00020000);
+  const int r = lane >> 4, ch = lane & 15;
 #pragma unroll
-  for (int i = 0; i < kc; ++i, wr += F) p.w1v[i] = ld_off<float>(wr, 4u * lane);
+  for (int i = 0; i < PW; ++i) {
+    const int ins = w + i * kPsW;
+    const uint32_t voff = (uint32_t)(((4 * ins + r) * F + 4 * ch) * (int)sizeof(float));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(w1s + ins * 4 * kPsHS), 16, voff, 0, 0, 0);
+  }
+#endif
 }
 
 template <int C>
@@ -537,7 +575,7 @@ __device__ __forceinline__ void mlp_load2(const mtx_decode_layer& Ly, int F, int
 }
 
 template <int C>
-__device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, PsStageB& sm) {
+__device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, PsStageB& sm, float* big, bool prefetched) {
   const mtx_decode_layer& Ly = a.L[l];
   const int B = a.B, F = a.F;
   const int ns = F / kPsHS;
@@ -548,7 +586,10 @@ __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, Ps
   constexpr int kc = C / kPsW;
   const int k0 = w * kc;
   PreB<C> pre;
-  mlp_load1<C>(Ly, F, item, pre);
+  if (!prefetched) {
+    __syncthreads();  // the previous item's LDS reads are done
+    mlp_dma<C>(Ly, F, item, big);
+  }
   LnPar lp;
   if (w < kPsR) ln_load<C>(lp, Ly.ln2_gamma, Ly.ln2_beta, lane);
 
@@ -574,20 +615,24 @@ __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, Ps
   }
   __syncthreads();
   if (w < kPsR) ps_ln_row<C>(sm.xs[w], lane, lp, Ly.ln2_eps);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's slab rows have landed
   __syncthreads();
 
+  const float* __restrict__ w1s = big;
   float acc[kPsR];
 #pragma unroll
   for (int m = 0; m < kPsR; ++m) acc[m] = 0.f;
 #pragma unroll
   for (int i = 0; i < kc; ++i) {
 #pragma unroll
-    for (int m = 0; m < kPsR; ++m) acc[m] = fmaf(sm.xs[m][k0 + i], pre.w1v[i], acc[m]);
+    for (int m = 0; m < kPsR; ++m) acc[m] = fmaf(sm.xs[m][k0 + i], w1s[(k0 + i) * kPsHS + lane], acc[m]);
     // keep the scheduler from hoisting every row value's LDS read at once
     if (i % 4 == 3) __builtin_amdgcn_sched_barrier(0);
   }
+  float* __restrict__ part = big;  // [kPsW][kPsR][kPsHS], over the consumed slab
+  __syncthreads();  // every wave's slab reads are done
 #pragma unroll
-  for (int m = 0; m < kPsR; ++m) sm.part[w][m][lane] = acc[m];
+  for (int m = 0; m < kPsR; ++m) part[(w * kPsR + m) * kPsHS + lane] = acc[m];
 
   // fc2's weights, requested before the fc1 reduce
   mlp_load2<C>(Ly, F, item, pre);
@@ -598,13 +643,12 @@ __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, Ps
     const int m = tid / kPsHS, j = tid % kPsHS;
     float v = 0.f;
 #pragma unroll
-    for (int q = 0; q < kPsW; ++q) v += sm.part[q][m][j];
+    for (int q = 0; q < kPsW; ++q) v += part[(q * kPsR + m) * kPsHS + j];
     v += Ly.b_fc1[j0 + j];
     sm.hs[m][j] = gelu_tanh(v);
   }
   __syncthreads();
-  float* __restrict__ p2h = &sm.part[0][0][0];  // [2][kPsR][C] half sums (the fc1 partials are consumed)
-  static_assert(2 * kPsR * C <= kPsW * kPsR * kPsHS, "fc2 half sums fit the partial buffer");
+  float* __restrict__ p2h = big;  // [2][kPsR][C] half sums (the fc1 partials are consumed)
   if (fc2_thread) {
     // the eight rows of GELU(fc1), lane j holding column j; each term takes
     // its value from lane 32 half + j as a scalar operand (whole waves take
@@ -707,11 +751,18 @@ __device__ __forceinline__ void ps_head_item(const PsArgs& a, int row, PsHead& s
 template <int C, int VPL>
 __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
   static_assert(C % 64 == 0 && C <= kPsMaxC && 2 * C <= kPsT, "row width");
-  __shared__ PsSmem sm;
+  __shared__ __align__(16) float lds[PsLds<C>::kTotal];
   __shared__ int flag;
+  unsigned long long next = 0;  // thread 0: the next barrier's target
+  PsSmem& sm = *reinterpret_cast<PsSmem*>(lds);
+  float* const big = lds + PsLds<C>::kSlabOff;
   // a step after a failed wait on this workspace does nothing
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
     flag = __hip_atomic_load(a.bar + kBarErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u;
+    next = __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.bar + kBarBase), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT) +
+           gridDim.x;
+  }
   __syncthreads();
   if (!flag) return;
   const int na = ((a.B + kPsS - 1) / kPsS) * a.H;
@@ -724,11 +775,17 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
   const int nq = a.steps * a.NL;
   for (int q = 0; q < nq; ++q) {
     const int l = q % a.NL;
+    // the slab region is free: the last stage B's reads ended before the barrier
+    if (PsLds<C>::kApart && first < nb) mlp_dma<C>(a.L[l], a.F, first, big);
     for (int it = first; it < na; it += gridDim.x) ps_attn_item<C>(a, l, it, sm.a, pa, it == first);
-    if (!ps_barrier(a, &flag)) return;
-    for (int it = first; it < nb; it += gridDim.x) ps_mlp_item<C>(a, l, it, sm.b);
+    if (!PsLds<C>::kApart && first < nb) {
+      __syncthreads();  // stage A's LDS reads are done: the slab overwrites them
+      mlp_dma<C>(a.L[l], a.F, first, big);
+    }
+    if (!ps_barrier(a, &flag, next)) return;
+    for (int it = first; it < nb; it += gridDim.x) ps_mlp_item<C>(a, l, it, sm.b, big, it == first);
     if (l + 1 == a.NL) {
-      if (!ps_barrier(a, &flag)) return;
+      if (!ps_barrier(a, &flag, next)) return;
       for (int r = blockIdx.x; r < a.B; r += gridDim.x) ps_head_item<C, VPL>(a, r, sm.h);
       if (q + 1 == nq) break;
       // the next step reads the picks, lengths and position just written
@@ -737,8 +794,13 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
     // into the stage before, where their registers would add to its own)
     __builtin_amdgcn_sched_barrier(0);
     if (first < na) attn_prefetch<C>(a, l + 1 == a.NL ? 0 : l + 1, first, pa);
-    if (!ps_barrier(a, &flag)) return;
+    if (!ps_barrier(a, &flag, next)) return;
   }
+  // every workgroup has passed every barrier: the counter stands at the
+  // last target, the next launch's base
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(reinterpret_cast<unsigned long long*>(a.bar + kBarBase), next - gridDim.x,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void decode_reset_kernel(unsigned* bar) {

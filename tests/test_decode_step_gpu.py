@@ -6,7 +6,10 @@ greedy token step, grid-wide barriers between stages) on the GPU.
     1e-4 of the oracle's, for every kernel instance the models below reach:
     row widths C = 128, 256, 384, 512, logits per lane for V <= 128 and
     V <= 256, odd batch sizes (a stage-A item with one sequence, a stage-B
-    item with fewer than 8 rows), one to six blocks.
+    item with fewer than 8 rows), one to six blocks, and batches with more
+    stage-A and stage-B items than resident workgroups (C = 128, B = 300;
+    C = 384, B = 96), so that workgroups run several items of a stage and
+    request later items' weight slabs inside the stage.
   * The multi-launch step (the chain of mtx_decode_qkv_attn_f32 ...
     mtx_head_pick_f32) gives the same tokens, margins within 2e-5.
   * Deterministic: two runs give bit-identical tokens and margins.
@@ -15,6 +18,11 @@ greedy token step, grid-wide barriers between stages) on the GPU.
     reports the failure through mtx_decode_step_status, and the following
     steps on the same workspace do nothing until mtx_decode_step_reset;
     after the reset a step gives the chain's token.
+  * Steps per launch: five launches of one step and one launch of five
+    steps agree bit for bit.
+  * One workspace shared in turn by launches of different grid sizes gives
+    the results of workspaces of their own (each launch counts its barriers
+    from the base the launch before it left).
 """
 import sys
 
@@ -46,6 +54,8 @@ CASES = [
     ((200, 48, 256, 4, 2), 9, 3, 30),
     ((65, 40, 512, 8, 1), 3, 5, 20),
     ((65, 256, 384, 6, 6), 64, 32, 16),
+    ((65, 24, 128, 2, 2), 300, 3, 6),
+    ((65, 16, 384, 6, 1), 96, 3, 6),
 ]
 
 
@@ -147,13 +157,36 @@ def test_wait_failure_is_reported_and_cleared(dev, monkeypatch):
     np.testing.assert_array_equal(cur.numpy(), want)
 
 
+def _prefilled(model, prompts, Tmax, n_margins):
+    """The state generate_greedy builds before its first decode step: the
+    prompt's caches, the first pick in ids[T0] and cur, lengths T0 + 1,
+    position T0."""
+    from minitorch_amd import device as dv
+    from minitorch_amd import kernels as K
+    from minitorch_amd.tensor import Tensor, no_grad
+
+    B, T0 = prompts.shape
+    C = model.tok_emb.weight.shape[1]
+    caches = [(dv.empty((B, Tmax, C)), dv.empty((B, Tmax, C))) for _ in model.blocks]
+    ids = dv.empty((Tmax, B), dtype="int64")
+    margins = dv.empty((n_margins, B))
+    pos = model._positions(Tmax)
+    with no_grad():
+        x = model.tok_emb(dv.index_array(prompts)) + model.pos_emb(dv.DeviceArray(pos.t[:T0]))
+        for block, cache in zip(model.blocks, caches):
+            x = block.forward_cached(x, cache, 0)
+        h = model.ln_f(Tensor(x.data.t[:, T0 - 1:T0, :]))
+        K.argmax_rows(model.lm_head(h).data.t.view(B, -1), idx=ids.t[T0], margin=margins.t[0])
+    cur = ids.t[T0].clone()
+    lengths = dv.full((B,), T0 + 1, "int32").t
+    posd = dv.full((1,), T0, "int64").t
+    return caches, ids, margins, cur, lengths, posd
+
+
 def test_steps_per_launch_agree(dev):
     """Five token steps as five launches and as one launch (the picks,
     lengths and position passed between steps inside the kernel) give the
     same ids and margins, bit for bit."""
-    from minitorch_amd import device as dv
-    from minitorch_amd import kernels as K
-    from minitorch_amd.tensor import Tensor, no_grad
     from oracle.gpt import GPTConfig
 
     _say("[decode_step] 5 launches of one step vs one launch of 5 steps")
@@ -162,22 +195,9 @@ def test_steps_per_launch_agree(dev):
     model, _ = _model(cfg, 47)
     prompts = np.random.default_rng(48).integers(0, cfg.vocab, (B, T0))
     Tmax = T0 + 1 + n
-    C = cfg.n_embd
     outs = []
     for per_launch in (1, n):
-        caches = [(dv.empty((B, Tmax, C)), dv.empty((B, Tmax, C))) for _ in model.blocks]
-        ids = dv.empty((Tmax, B), dtype="int64")
-        margins = dv.empty((n + 1, B))
-        pos = model._positions(Tmax)
-        with no_grad():
-            x = model.tok_emb(dv.index_array(prompts)) + model.pos_emb(dv.DeviceArray(pos.t[:T0]))
-            for block, cache in zip(model.blocks, caches):
-                x = block.forward_cached(x, cache, 0)
-            h = model.ln_f(Tensor(x.data.t[:, T0 - 1:T0, :]))
-            K.argmax_rows(model.lm_head(h).data.t.view(B, -1), idx=ids.t[T0], margin=margins.t[0])
-        cur = ids.t[T0].clone()
-        lengths = dv.full((B,), T0 + 1, "int32").t
-        posd = dv.full((1,), T0, "int64").t
+        caches, ids, margins, cur, lengths, posd = _prefilled(model, prompts, Tmax, n + 1)
         ds = model._decode_step(caches, B, Tmax)
         for _ in range(n // per_launch):
             ds(cur, ids.t, lengths, posd, margins=margins.t, t_base=T0, steps=per_launch)
@@ -187,3 +207,38 @@ def test_steps_per_launch_agree(dev):
     np.testing.assert_array_equal(outs[0][1], outs[1][1])
     np.testing.assert_array_equal(outs[0][2], np.full(B, T0 + 1 + n))
     np.testing.assert_array_equal(outs[1][2], np.full(B, T0 + 1 + n))
+
+
+def test_workspace_shared_across_grid_sizes(dev):
+    """One workspace used in turn by steps of two batch sizes whose grids
+    differ (8 and 24 workgroups at C = 128, neither launch's barrier count a
+    multiple of the other grid): every step gives the ids and margins, bit
+    for bit, of the same steps on workspaces of their own."""
+    from oracle.gpt import GPTConfig
+
+    _say("[decode_step] one workspace, grids of 8 and 24 workgroups in turn")
+    cfg = GPTConfig(65, 32, 128, 2, 2)
+    T0, n = 4, 4
+    Tmax = T0 + 1 + n
+    model, _ = _model(cfg, 49)
+    prompts = {B: np.random.default_rng(50 + B).integers(0, cfg.vocab, (B, T0)) for B in (5, 17)}
+
+    def run(shared):
+        states, steps = {}, {}
+        for B in (5, 17):
+            states[B] = _prefilled(model, prompts[B], Tmax, n + 1)
+            steps[B] = model._decode_step(states[B][0], B, Tmax)
+        if shared:
+            steps[5].workspace, steps[5]._ws_bytes = steps[17].workspace, steps[17]._ws_bytes
+        for _ in range(n):
+            for B in (5, 17):
+                _, ids, margins, cur, lengths, posd = states[B]
+                steps[B](cur, ids.t, lengths, posd, margins=margins.t, t_base=T0)
+        for B in (5, 17):
+            steps[B].check()
+        return {B: (states[B][1].numpy()[T0:T0 + n + 1].copy(), states[B][2].numpy().copy()) for B in (5, 17)}
+
+    own, shared = run(False), run(True)
+    for B in (5, 17):
+        np.testing.assert_array_equal(shared[B][0], own[B][0])
+        np.testing.assert_array_equal(shared[B][1], own[B][1])
