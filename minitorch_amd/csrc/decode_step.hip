@@ -413,34 +413,58 @@ __device__ __forceinline__ void ps_attn_item(const PsArgs& a, int l, int item, P
     const int64_t cst = C, csb = (int64_t)a.Tmax * C;
     float* __restrict__ scs = sm.sc[sg];
     const float* __restrict__ qv = sm.qkv[sg];
-    // scores (log2 units): four threads per key, a quarter of D each
+    // scores (log2 units): four threads per key, a quarter of D each; a
+    // thread's keys two at a time, both rows requested together (one memory
+    // round trip for up to 2 TPS / 4 keys)
     const float c = a.scale * kLog2e;
-    constexpr int DQ = D / 4;
+    constexpr int DQ = D / 4, KP = TPS / 4;
     const int kq = lt >> 2, qd = lt & 3;
     float qr[DQ];
 #pragma unroll
     for (int e = 0; e < DQ; ++e) qr[e] = qv[qd * DQ + e] * c;
     const float* __restrict__ kb0 = Ly.k_cache + (int64_t)min(b, B - 1) * csb + h * D + qd * DQ;
     float mx = -INFINITY;
-    for (int j = kq; j < L; j += TPS / 4) {
-      float kr[DQ];
-      if (j == newrow) {
+    for (int j0 = kq; j0 < L; j0 += 2 * KP) {
+      float kr[2][DQ];
 #pragma unroll
-        for (int e = 0; e < DQ; ++e) kr[e] = qv[D + qd * DQ + e];
-      } else {
+      for (int u = 0; u < 2; ++u) {
+        const int j = min(j0 + u * KP, L - 1);  // a row past L is not used
 #pragma unroll
         for (int e = 0; e < DQ; e += 4) {
           const f32x4 v = *reinterpret_cast<const f32x4*>(kb0 + (int64_t)j * cst + e);
-          kr[e] = v[0]; kr[e + 1] = v[1]; kr[e + 2] = v[2]; kr[e + 3] = v[3];
+          kr[u][e] = v[0]; kr[u][e + 1] = v[1]; kr[u][e + 2] = v[2]; kr[u][e + 3] = v[3];
         }
       }
-      float sv = 0.f;
 #pragma unroll
-      for (int e = 0; e < DQ; ++e) sv = fmaf(qr[e], kr[e], sv);
-      sv += __shfl_xor(sv, 1, 64);
-      sv += __shfl_xor(sv, 2, 64);
-      if (qd == 0) scs[j] = sv;
-      mx = fmaxf(mx, sv);
+      for (int u = 0; u < 2; ++u) {
+        const int j = j0 + u * KP;
+        if (j == newrow) {
+#pragma unroll
+          for (int e = 0; e < DQ; ++e) kr[u][e] = qv[D + qd * DQ + e];
+        }
+        float sv = 0.f;
+#pragma unroll
+        for (int e = 0; e < DQ; ++e) sv = fmaf(qr[e], kr[u][e], sv);
+        sv += __shfl_xor(sv, 1, 64);
+        sv += __shfl_xor(sv, 2, 64);
+        if (j < L) {
+          if (qd == 0) scs[j] = sv;
+          mx = fmaxf(mx, sv);
+        }
+      }
+    }
+
+    // the value rows of the first 8 key groups, requested before the
+    // softmax so that their latency overlaps it (rows past L are not used;
+    // the row this step wrote is taken from LDS)
+    const int dv = lt % DV, kg = lt / DV;
+    const float* __restrict__ vb0 = Ly.v_cache + (int64_t)min(b, B - 1) * csb + h * D + 4 * dv;
+    constexpr int VPF = 8;
+    f32x4 vpre[VPF];
+    if (L > 0) {
+#pragma unroll
+      for (int i = 0; i < VPF; ++i)
+        vpre[i] = *reinterpret_cast<const f32x4*>(vb0 + (int64_t)min(kg + i * NGS, L - 1) * cst);
     }
     mx = wave_max(mx);
     if (lane == 0) sm.red[w] = mx;
@@ -463,11 +487,14 @@ __device__ __forceinline__ void ps_attn_item(const PsArgs& a, int l, int item, P
     for (int q = 0; q < WS; ++q) lsum += sm.red[sg * WS + q];
 
     // o[d] = sum_j p_j v[j][d] / l
-    const int dv = lt % DV, kg = lt / DV;
-    const float* __restrict__ vb0 = Ly.v_cache + (int64_t)min(b, B - 1) * csb + h * D + 4 * dv;
     f32x4 av = zero4();
+#pragma unroll
+    for (int i = 0; i < VPF; ++i) {
+      const int j = kg + i * NGS;
+      if (j < L) av += scs[j] * (j == newrow ? *reinterpret_cast<const f32x4*>(qv + 2 * D + 4 * dv) : vpre[i]);
+    }
 #pragma unroll 4
-    for (int j = kg; j < L; j += NGS) {
+    for (int j = kg + VPF * NGS; j < L; j += NGS) {
       const f32x4 vv = j == newrow ? *reinterpret_cast<const f32x4*>(qv + 2 * D + 4 * dv)
                                    : *reinterpret_cast<const f32x4*>(vb0 + (int64_t)j * cst);
       av += scs[j] * vv;
@@ -622,12 +649,22 @@ __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, Ps
   float acc[kPsR];
 #pragma unroll
   for (int m = 0; m < kPsR; ++m) acc[m] = 0.f;
+  // four weight rows at a time: the row values as one 16-byte broadcast read
+  // per row (terms still added in ascending k)
+  static_assert(kc % 4 == 0, "whole groups of four weight rows");
 #pragma unroll
-  for (int i = 0; i < kc; ++i) {
+  for (int i = 0; i < kc; i += 4) {
+    float wv[4];
 #pragma unroll
-    for (int m = 0; m < kPsR; ++m) acc[m] = fmaf(sm.xs[m][k0 + i], w1s[(k0 + i) * kPsHS + lane], acc[m]);
+    for (int u = 0; u < 4; ++u) wv[u] = w1s[(k0 + i + u) * kPsHS + lane];
+#pragma unroll
+    for (int m = 0; m < kPsR; ++m) {
+      const f32x4 x4 = *reinterpret_cast<const f32x4*>(&sm.xs[m][k0 + i]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[m] = fmaf(x4[u], wv[u], acc[m]);
+    }
     // keep the scheduler from hoisting every row value's LDS read at once
-    if (i % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+    if (i % 8 == 4) __builtin_amdgcn_sched_barrier(0);
   }
   float* __restrict__ part = big;  // [kPsW][kPsR][kPsHS], over the consumed slab
   __syncthreads();  // every wave's slab reads are done
@@ -650,22 +687,21 @@ __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, Ps
   __syncthreads();
   float* __restrict__ p2h = big;  // [2][kPsR][C] half sums (the fc1 partials are consumed)
   if (fc2_thread) {
-    // the eight rows of GELU(fc1), lane j holding column j; each term takes
-    // its value from lane 32 half + j as a scalar operand (whole waves take
-    // this branch: 2C is a multiple of 64, and half is uniform per wave)
-    float hrow[kPsR];
-#pragma unroll
-    for (int m = 0; m < kPsR; ++m) hrow[m] = sm.hs[m][lane];
+    // the eight rows of GELU(fc1) as 16-byte broadcast reads of four hidden
+    // columns, terms added in ascending hidden column (whole waves take this
+    // branch: 2C is a multiple of 64, and half is uniform per wave)
     float p2[kPsR];
 #pragma unroll
     for (int m = 0; m < kPsR; ++m) p2[m] = 0.f;
     const int jb = __builtin_amdgcn_readfirstlane(half) * (kPsHS / 2);
 #pragma unroll
-    for (int j = 0; j < kPsHS / 2; ++j) {
+    for (int j = 0; j < kPsHS / 2; j += 4) {
 #pragma unroll
-      for (int m = 0; m < kPsR; ++m)
-        p2[m] = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(hrow[m]), jb + j)), pre.w2v[j],
-                     p2[m]);
+      for (int m = 0; m < kPsR; ++m) {
+        const f32x4 h4 = *reinterpret_cast<const f32x4*>(&sm.hs[m][jb + j]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) p2[m] = fmaf(h4[u], pre.w2v[j + u], p2[m]);
+      }
     }
 #pragma unroll
     for (int m = 0; m < kPsR; ++m) p2h[(half * kPsR + m) * C + n2] = p2[m];
