@@ -29,9 +29,10 @@
 //   after the last block, items (row): the residual plus the last fc2
 //     partials and bias, ln_f, lm_head and the pick with its bookkeeping.
 //
-// The barrier is a 64-bit arrival counter in device memory (the workspace),
-// touched by one thread per workgroup with agent-scope atomics; each launch
-// counts from the base the launch before it left.  Every
+// The barrier is a set of 64-bit arrival counters in device memory (the
+// workspace), added to by one thread per workgroup and polled by one wave
+// with agent-scope atomics; each launch counts from the base the launch
+// before it left.  Every
 // wait is bounded by the 100 MHz wall clock: a wait that runs out sets the
 // workspace's error word and the workgroup leaves the kernel; waiting
 // workgroups see the word and leave too, and a later launch on the same
@@ -58,9 +59,12 @@ constexpr int kPsHS = 64;        // hidden columns per stage-B item
 constexpr int kPsMaxT = 1024;    // cache rows (scores of kPsS rows in LDS)
 constexpr int kPsMaxL = 16;
 constexpr int kPsMaxV = 256;
-// barrier words (unsigned), each on its own 128-byte line: the arrival
-// counter and the launch base (64-bit), the error word
-constexpr int kBarCount = 0, kBarBase = 32, kBarErr = 64, kBarBytes = 512;
+// barrier words (unsigned), each on its own 128-byte line: kBarNC arrival
+// counters (64-bit; workgroup i adds to counter i mod kBarNC, and wave 0 of a
+// waiting workgroup reads one per lane), the launch base (64-bit), the error
+// word
+constexpr int kBarNC = 64;
+constexpr int kBarCount = 0, kBarBase = 32 * kBarNC, kBarErr = kBarBase + 32, kBarBytes = 4 * (kBarErr + 32);
 
 struct PsArgs {
   int NL, B, C, H, F, V, Tmax;
@@ -217,44 +221,68 @@ __device__ __forceinline__ float ps_pending(const PsArgs& a, const float* __rest
   return t;
 }
 
-// Grid-wide barrier over a 64-bit arrival counter that only grows.  A launch
-// reads the counter's value at its start from the base word (written by the
-// launch before it, so launches of different grid sizes may share a
-// workspace); its k-th barrier (k = 1, 2, ...) is complete when the counter
-// reaches base + k G, and its workgroup 0 leaves the final count as the next
-// launch's base.  `next` (thread 0) is this workgroup's next target.  Each
-// thread first waits for its own stores (the device-scope stores are
-// acknowledged once they are visible across the device), the workgroup
-// barrier then covers every thread, and thread 0 arrives and polls; no cache
-// write-back or invalidation is needed, so the L2 caches keep the weights
-// across stages.  Returns false when the step must end: this wait ran out,
-// or another workgroup's did.
-__device__ __forceinline__ bool ps_barrier(const PsArgs& a, int* flag, unsigned long long& next) {
+// Grid-wide barrier over arrival counters that only grow, spread over kBarNC
+// counters on separate lines (with one counter for the whole grid, the
+// arrivals and polls on its one line queued behind each other and each
+// barrier took about 1 us longer).  A launch reads the counters' total at its
+// start from the base word (written by the launch before it, so launches of
+// different grid sizes may share a workspace); its k-th barrier (k = 1, 2,
+// ...) is complete when the total reaches base + k G, and its workgroup 0
+// leaves the final total as the next launch's base.  `next` (lanes of wave
+// 0) is this workgroup's next target.  Each thread first waits for its own
+// stores (the device-scope stores are acknowledged once they are visible
+// across the device), the workgroup barrier then covers every thread, thread
+// 0 adds to its counter, and wave 0 polls: lane i reads counter i and the
+// lanes sum them (each counter only grows, so a total that reaches the
+// target means every arrival happened).  No cache write-back or invalidation
+// is needed, so the L2 caches keep the weights across stages.
+// Arrival and wait are separate so that loads that do not depend on the
+// stage before (the next stage's first weights) can be issued between them:
+// issued before the arrival, the arrival's wait for this thread's stores
+// would wait for them too (one counter covers loads and stores).
+// ps_wait returns false when the step must end: this wait ran out, or
+// another workgroup's did.
+__device__ __forceinline__ void ps_arrive(const PsArgs& a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned long long* count = reinterpret_cast<unsigned long long*>(a.bar + kBarCount);
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(reinterpret_cast<unsigned long long*>(a.bar + kBarCount + 32 * (blockIdx.x % kBarNC)),
+                           1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool ps_wait(const PsArgs& a, int* flag, unsigned long long& next) {
+  static_assert(kBarNC <= 64 && (kBarNC & (kBarNC - 1)) == 0, "one counter per lane of wave 0");
+  const unsigned long long target = next;
+  next += gridDim.x;
+  if (threadIdx.x < kBarNC) {
+    unsigned long long* count = reinterpret_cast<unsigned long long*>(a.bar + kBarCount + 32 * threadIdx.x);
     unsigned* err = a.bar + kBarErr;
-    const unsigned long long target = next;
-    next += gridDim.x;
-    const unsigned long long prior = __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int ok = 1;
-    if (prior + 1ull < target) {
-      const int64_t t0 = wall_clock64();
-      while (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        if (a.limit < 0 || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
-            wall_clock64() - t0 > a.limit) {
-          __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ok = 0;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
+    const int64_t t0 = wall_clock64();
+    while (true) {
+      unsigned long long s = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int o = 1; o < kBarNC; o *= 2) s += __shfl_xor(s, o, 64);
+      if (s >= target) break;
+      if (a.limit < 0 || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
+          wall_clock64() - t0 > a.limit) {
+        if (threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = 0;
+        break;
       }
+      __builtin_amdgcn_s_sleep(1);
     }
-    *flag = ok;
+    if (threadIdx.x == 0) *flag = ok;
   }
   __syncthreads();
-  return *flag != 0;
+  if (*flag != 0) return true;
+  __builtin_amdgcn_s_waitcnt(0);  // no load issued between arrival and wait outlives the workgroup
+  return false;
+}
+
+__device__ __forceinline__ bool ps_barrier(const PsArgs& a, int* flag, unsigned long long& next) {
+  ps_arrive(a);
+  return ps_wait(a, flag, next);
 }
 
 // ---- stage A: (pair of sequences, head) ----
@@ -789,16 +817,16 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
   static_assert(C % 64 == 0 && C <= kPsMaxC && 2 * C <= kPsT, "row width");
   __shared__ __align__(16) float lds[PsLds<C>::kTotal];
   __shared__ int flag;
-  unsigned long long next = 0;  // thread 0: the next barrier's target
+  unsigned long long next = 0;  // threads 0 .. kBarNC-1: the next barrier's target
   PsSmem& sm = *reinterpret_cast<PsSmem*>(lds);
   float* const big = lds + PsLds<C>::kSlabOff;
   // a step after a failed wait on this workspace does nothing
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0)
     flag = __hip_atomic_load(a.bar + kBarErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u;
+  if (threadIdx.x < kBarNC)
     next = __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.bar + kBarBase), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT) +
            gridDim.x;
-  }
   __syncthreads();
   if (!flag) return;
   const int na = ((a.B + kPsS - 1) / kPsS) * a.H;
@@ -814,11 +842,13 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
     // the slab region is free: the last stage B's reads ended before the barrier
     if (PsLds<C>::kApart && first < nb) mlp_dma<C>(a.L[l], a.F, first, big);
     for (int it = first; it < na; it += gridDim.x) ps_attn_item<C>(a, l, it, sm.a, pa, it == first);
-    if (!PsLds<C>::kApart && first < nb) {
-      __syncthreads();  // stage A's LDS reads are done: the slab overwrites them
-      mlp_dma<C>(a.L[l], a.F, first, big);
+    {
+      ps_arrive(a);
+      // (after the arrival's workgroup barrier stage A's LDS reads are done,
+      // so a slab that lies over them can be requested)
+      if (!PsLds<C>::kApart && first < nb) mlp_dma<C>(a.L[l], a.F, first, big);
+      if (!ps_wait(a, &flag, next)) return;
     }
-    if (!ps_barrier(a, &flag, next)) return;
     for (int it = first; it < nb; it += gridDim.x) ps_mlp_item<C>(a, l, it, sm.b, big, it == first);
     if (l + 1 == a.NL) {
       if (!ps_barrier(a, &flag, next)) return;
@@ -826,11 +856,16 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
       if (q + 1 == nq) break;
       // the next step reads the picks, lengths and position just written
     }
-    // (the scheduling barrier keeps the prefetch loads from being hoisted
-    // into the stage before, where their registers would add to its own)
-    __builtin_amdgcn_sched_barrier(0);
-    if (first < na) attn_prefetch<C>(a, l + 1 == a.NL ? 0 : l + 1, first, pa);
-    if (!ps_barrier(a, &flag, next)) return;
+    // the next stage's first weights are requested after the arrival (the
+    // scheduling barriers keep their loads from moving into the stage before,
+    // where their registers would add to its own, or ahead of the arrival)
+    {
+      ps_arrive(a);
+      __builtin_amdgcn_sched_barrier(0);
+      if (first < na) attn_prefetch<C>(a, l + 1 == a.NL ? 0 : l + 1, first, pa);
+      __builtin_amdgcn_sched_barrier(0);
+      if (!ps_wait(a, &flag, next)) return;
+    }
   }
   // every workgroup has passed every barrier: the counter stands at the
   // last target, the next launch's base
@@ -840,7 +875,7 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
 }
 
 __global__ void decode_reset_kernel(unsigned* bar) {
-  if (threadIdx.x < kBarBytes / 4) bar[threadIdx.x] = 0u;
+  for (int i = threadIdx.x; i < kBarBytes / 4; i += blockDim.x) bar[i] = 0u;
 }
 
 // workspace layout: barrier words, X0, X1, P1, P2 (each 256-byte aligned)
@@ -1011,7 +1046,7 @@ extern "C" int mtx_decode_step_status(const void* workspace, void* stream) {
 
 extern "C" int mtx_decode_step_reset(void* workspace, void* stream) {
   MTX_CHECK_ARG(workspace != nullptr, "decode_step_reset: null workspace");
-  hipLaunchKernelGGL(decode_reset_kernel, dim3(1), dim3(kBarBytes / 4), 0, static_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL(decode_reset_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<unsigned*>(workspace));
   MTX_LAUNCHED();
   return MTX_OK;
