@@ -98,24 +98,33 @@ class MultiHeadAttention(Module):
         return self.out_proj(out)
 
 
-    def forward_cached(self, x, cache, t0):
+    def forward_cached(self, x, cache, t0, residual=None, fused=False):
         """Inference-only step over positions [t0, t0 + T) of x (B, T, C):
         keys/values of these positions are written into cache = (k, v), each a
         (B, Tmax, C) DeviceArray, and attention runs against cache[:, :t0 + T]
-        (bottom-right causal: query i sees keys <= t0 + i)."""
+        (bottom-right causal: query i sees keys <= t0 + i).  fused: the three
+        projections as one GEMM over the fused q/k/v weight, which the caller
+        has just refreshed (fuse_qkv).  With `residual` (shaped like x) the result is residual +
+        attention(x), the add in the output projection's epilogue (same
+        values as the separate add)."""
         from . import kernels as K
 
         B, T, C = x.shape
         H, D = self.n_head, self.head_dim
-        q = self.q_proj(x)
-        k = self.k_proj(x)
-        v = self.v_proj(x)
+        rows = B * T
+        if fused:
+            W, b = self._qkv
+            qkv = dev.empty((B, T, 3 * C))
+            K.gemm(x.data.t.reshape(rows, C), W.data.t, qkv.t.view(rows, 3 * C), bias=b.data.t)
+            q_t, k_t, v_t = qkv.t[:, :, :C], qkv.t[:, :, C:2 * C], qkv.t[:, :, 2 * C:]
+        else:
+            q_t, k_t, v_t = (p(x).data.t for p in (self.q_proj, self.k_proj, self.v_proj))
         kc, vc = cache
-        K.ewise("COPY", kc.t[:, t0:t0 + T, :], k.data.t)
-        K.ewise("COPY", vc.t[:, t0:t0 + T, :], v.data.t)
+        K.ewise("COPY", kc.t[:, t0:t0 + T, :], k_t)
+        K.ewise("COPY", vc.t[:, t0:t0 + T, :], v_t)
         Tk = t0 + T
         heads = lambda t: t.view(t.shape[0], t.shape[1], H, D).transpose(1, 2)
-        qh = heads(q.data.t)
+        qh = heads(q_t)
         kh = heads(kc.t[:, :Tk, :])
         vh = heads(vc.t[:, :Tk, :])
         out = dev.empty((B, T, H, D))
@@ -123,7 +132,14 @@ class MultiHeadAttention(Module):
             K.attn_decode(qh, kh, vh, 1.0 / math.sqrt(D), out=out.t.transpose(1, 2))
         else:
             K.attn_fwd(qh, kh, vh, 1.0 / math.sqrt(D), True, out=out.t.transpose(1, 2))
-        return self.out_proj(Tensor(out.reshape(B, T, C)))
+        o = Tensor(out.reshape(B, T, C))
+        if residual is None:
+            return self.out_proj(o)
+        y = dev.empty((B, T, C))
+        K.gemm(o.data.t.reshape(rows, C), self.out_proj.weight.data.t, y.t.view(rows, C),
+               bias=self.out_proj.bias.data.t if self.out_proj.bias is not None else None,
+               act=K.GEMM_ACT_ADD, aux=residual.data.t.reshape(rows, C))
+        return Tensor(y)
 
 
     def forward_step(self, x, cache, lengths, residual=None, ln=None):
@@ -226,10 +242,31 @@ class TransformerBlock(Module):
             x = x + self.mlp(self.ln2(x))
         return x
 
-    def forward_cached(self, x, cache, t0):
-        x = x + self.attn.forward_cached(self.ln1(x), cache, t0)
-        x = x + self.mlp(self.ln2(x))
-        return x
+    def forward_cached(self, x, cache, t0, fused=False):
+        """Inference-only forward over positions [t0, t0 + T) with the
+        attention's keys and values cached: the residual adds in the GEMM
+        epilogues of the output projection and fc2, fc1's GELU in its own
+        epilogue (no pre-activation kept), the values of the layer-by-layer
+        composition.  fused: the attention's q/k/v projections as one GEMM
+        over its fused weight, refreshed by the caller (attn.fuse_qkv)."""
+        from . import kernels as K
+
+        fc1, act, fc2, drop = self.mlp.layers
+        if not (isinstance(fc1, Linear) and isinstance(act, GELU) and isinstance(fc2, Linear)
+                and fc1.bias is not None and fc2.bias is not None
+                and (not drop._training or drop.p == 0.0)):
+            x = x + self.attn.forward_cached(self.ln1(x), cache, t0, fused=fused)
+            return x + self.mlp(self.ln2(x))
+        x = self.attn.forward_cached(self.ln1(x), cache, t0, residual=x, fused=fused)
+        B, T, C = x.shape
+        rows, Hd = B * T, fc1.weight.shape[1]
+        h = dev.empty((rows, Hd))
+        K.gemm(self.ln2(x).data.t.reshape(rows, C), fc1.weight.data.t, h.t, bias=fc1.bias.data.t,
+               act=K.GEMM_ACT_GELU)
+        y = dev.empty((B, T, C))
+        K.gemm(h.t, fc2.weight.data.t, y.t.view(rows, C), bias=fc2.bias.data.t, act=K.GEMM_ACT_ADD,
+               aux=x.data.t.reshape(rows, C))
+        return Tensor(y)
 
     def forward_step(self, x, cache, lengths, ln_in=None, next_ln=None):
         """Decode step (no autograd): x is updated in place, both residual
@@ -388,16 +425,18 @@ class GPT(Module):
         pos = self._positions(Tmax)
 
         with no_grad():
+            # the fused q/k/v weights (a snapshot of the current weights) serve
+            # the prefill and the decode steps
+            for block in self.blocks:
+                block.attn.fuse_qkv()
             # prefill over the prompt
             prompt = dev.index_array(idx)
             x = self.tok_emb(prompt) + self.pos_emb(DeviceArray(pos.t[:T0]))
             for block, cache in zip(self.blocks, caches):
-                x = block.forward_cached(x, cache, 0)
+                x = block.forward_cached(x, cache, 0, fused=True)
             x = self.ln_f(Tensor(x.data.t[:, T0 - 1:T0, :]))
             K.argmax_rows(self.lm_head(x).data.t.view(B, -1), idx=ids.t[T0], margin=margins.t[0])
             if n > 1:
-                for block in self.blocks:
-                    block.attn.fuse_qkv()
                 cur = ids.t[T0].clone()              # ids fed to the next step, then overwritten
                 lengths = dev.full((B,), T0 + 1, "int32").t
                 posd = dev.full((1,), T0, "int64").t
