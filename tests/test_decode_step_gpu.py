@@ -8,8 +8,9 @@ greedy token step, grid-wide barriers between stages) on the GPU.
     V <= 256, odd batch sizes (a stage-A item with one sequence, a stage-B
     item with fewer than 8 rows), one to six blocks, and batches with more
     stage-A and stage-B items than resident workgroups (C = 128, B = 300;
-    C = 384, B = 96), so that workgroups run several items of a stage and
-    request later items' weight slabs inside the stage.
+    C = 384, B = 96; C = 512, B = 72, where fc1's weight slab shares stage
+    A's LDS), so that workgroups run several items of a stage and request
+    later items' weight slabs inside the stage.
   * The multi-launch step (the chain of mtx_decode_qkv_attn_f32 ...
     mtx_head_pick_f32) gives the same tokens, margins within 2e-5.
   * Deterministic: two runs give bit-identical tokens and margins.
@@ -56,6 +57,7 @@ CASES = [
     ((65, 256, 384, 6, 6), 64, 32, 16),
     ((65, 24, 128, 2, 2), 300, 3, 6),
     ((65, 16, 384, 6, 1), 96, 3, 6),
+    ((65, 16, 512, 8, 1), 72, 3, 6),
 ]
 
 
