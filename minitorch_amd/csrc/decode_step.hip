@@ -260,10 +260,14 @@ __device__ __forceinline__ bool ps_wait(const PsArgs& a, int* flag, unsigned lon
     int ok = 1;
     const int64_t t0 = wall_clock64();
     while (true) {
-      unsigned long long s = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // (a negative limit fails before the first poll, so that the failure
+      // does not depend on how far the other workgroups have come)
+      if (a.limit >= 0) {
+        unsigned long long s = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-      for (int o = 1; o < kBarNC; o *= 2) s += __shfl_xor(s, o, 64);
-      if (s >= target) break;
+        for (int o = 1; o < kBarNC; o *= 2) s += __shfl_xor(s, o, 64);
+        if (s >= target) break;
+      }
       if (a.limit < 0 || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
           wall_clock64() - t0 > a.limit) {
         if (threadIdx.x == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
