@@ -291,12 +291,12 @@ __device__ __forceinline__ bool ps_barrier(const PsArgs& a, int* flag, unsigned 
 
 // ---- stage A: (pair of sequences, head) ----
 // Weights of an item do not depend on the previous stage: a workgroup's
-// first stage-A item has its first weight batch requested before the
-// barrier that opens the stage (PreA), so that latency overlaps the wait.
-// (Stage B's weights requested into registers that way pushed the kernel
-// past 128 VGPRs into spills; its fc1 slab goes to LDS by direct loads
-// instead, requested at the start of stage A, and fc2's weights are
-// requested at the item's start.)
+// first stage-A item has its first weight batch requested between the
+// arrival and the wait of the barrier that opens the stage (PreA), so that
+// latency overlaps the wait.  (Stage B's weights requested into registers
+// that way pushed the kernel past 128 VGPRs into spills; its fc1 slab goes
+// to LDS by direct loads instead, requested at the start of stage A, and
+// fc2's weights are requested after fc1.)
 constexpr int kPsNPL = 3 * kPsD / 64;   // q, k, v columns of the head per lane
 constexpr int kPsBA = 36 / kPsNPL;      // weight rows per load batch in stage A
 struct PreA {
@@ -598,8 +598,10 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 // fc1's weight slab of an item (rows 0 .. C-1, columns j0 .. j0+63) into
 // w1s[k][64] by direct buffer loads into LDS: no registers, so a workgroup's
-// first item has it requested before the barrier that opens the stage.  One
-// wave load moves four rows (1 KiB); completion is the wave's vmcnt.
+// first item has it requested before the stage (at the start of stage A, or
+// between the arrival and the wait of the barrier before the stage where the
+// slab lies over stage A's LDS).  One wave load moves four rows (1 KiB);
+// completion is the wave's vmcnt.
 template <int C>
 __device__ __forceinline__ void mlp_dma(const mtx_decode_layer& Ly, int F, int item, float* w1s) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -871,8 +873,8 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
       if (!ps_wait(a, &flag, next)) return;
     }
   }
-  // every workgroup has passed every barrier: the counter stands at the
-  // last target, the next launch's base
+  // every workgroup has passed every barrier: the counters' total stands at
+  // the last target, the next launch's base
   if (blockIdx.x == 0 && threadIdx.x == 0)
     __hip_atomic_store(reinterpret_cast<unsigned long long*>(a.bar + kBarBase), next - gridDim.x,
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
