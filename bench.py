@@ -274,6 +274,10 @@ def cpu_baseline_attention(arrs, T, D, budget_s=15.0):
 
 C0_CFG = dict(vocab=65, block=32, n_embd=64, n_head=4, n_layer=2, B=16)
 C2_CFG = dict(vocab=65, block=256, n_embd=384, n_head=6, n_layer=6, B=64)
+# sequences per step of the C2 CPU baseline (a full B=64 step of the NumPy
+# restatement took over 10 minutes on an 8-core host, too long for the default
+# run; 8 sequences take about 18 s there)
+C2_CPU_B = 8
 
 
 def gpt_flops_per_step(c):
@@ -758,8 +762,8 @@ def main():
                          f"NumPy restatement of the reference sub-graph (fp32 q@k^T, fp64 from the "
                          f"scale on), {dt:.1f}s; TFLOP/s on the algorithmic causal count",
                "host": host_info()}
-        print("[bench] CPU baseline, GPT C2 step on 1 sequence (NumPy restatement)", file=sys.stderr, flush=True)
-        tps2, n2, dt2 = cpu_baseline_gpt(C2_CFG, args.cpu_budget / 2, 1)
+        print("[bench] CPU baseline, GPT C2 step on 8 sequences (NumPy restatement)", file=sys.stderr, flush=True)
+        tps2, n2, dt2 = cpu_baseline_gpt(C2_CFG, args.cpu_budget / 2, C2_CPU_B)
         tps0, n0, dt0 = cpu_baseline_gpt(C0_CFG, 3.0, C0_CFG["B"])
         tps4, dt4 = cpu_baseline_c4()
         c4["cpu_baseline"] = {"value": round(tps4, 2), "unit": "tokens/s", "cores": blas_threads(), "kind": "port",
@@ -768,7 +772,8 @@ def main():
                                         f"full-recompute NumPy restatement of GPT.generate (oracle/gpt.py)"}
         cpu_gpt = {"C2_tokens_per_s": round(tps2, 2), "C0_tokens_per_s": round(tps0, 1),
                    "cores": blas_threads(), "kind": "port",
-                   "sample": f"C2 model, {n2} training steps on 1 sequence of 256 tokens ({dt2:.1f}s); "
+                   "sample": f"C2 model, {n2} training steps on {C2_CPU_B} sequences of 256 tokens ({dt2:.1f}s; "
+                             f"a B=64 step of the restatement took over 10 minutes on an 8-core host); "
                              f"C0, {n0} full B=16 steps ({dt0:.1f}s); NumPy restatement of the "
                              f"reference step (oracle/gpt.py)"}
 
