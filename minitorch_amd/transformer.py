@@ -199,13 +199,17 @@ class MultiHeadAttention(Module):
     def fuse_qkv(self):
         """Concatenate the q/k/v projections into one (C, 3C) weight and (3C,)
         bias for decode steps (one GEMM instead of three).  A snapshot: call
-        again after the weights change (generate_greedy does, per call)."""
+        again after the weights change (generate_greedy does, per call).  The
+        buffers are kept and refilled, so their addresses stay the same."""
         from . import kernels as K
 
         lins = (self.q_proj, self.k_proj, self.v_proj)
         Cin, C = self.q_proj.weight.shape
-        W = dev.empty((Cin, 3 * C))
-        b = dev.empty((3 * C,))
+        if self._qkv is not None and tuple(self._qkv[0].shape) == (Cin, 3 * C):
+            W, b = self._qkv[0].data, self._qkv[1].data
+        else:
+            W = dev.empty((Cin, 3 * C))
+            b = dev.empty((3 * C,))
         K.pack3([p.weight.data.t.contiguous() for p in lins], W.t)
         K.pack3([p.bias.data.t.contiguous().view(1, C) for p in lins], b.t.view(1, 3 * C))
         self._qkv = (Tensor(W), Tensor(b))
@@ -403,8 +407,13 @@ class GPT(Module):
         one persistent launch (mtx_decode_step_f32, GPT._decode_step);
         otherwise a step is a chain of launches that replays unchanged: with
         graph=True the first one-token step runs eagerly, the second is
-        recorded as a HIP graph and replayed for the rest.  The host
-        synchronises once, at the end.  Needs T0 + max_new_tokens <=
+        recorded as a HIP graph and replayed for the rest.  With the
+        persistent step the device state (caches, records, the step's inputs
+        and workspace) is kept for the most recent prompt shape and, with
+        graph=True, the prefill is recorded as a HIP graph on the second call
+        for that shape and replayed after that, while the parameters keep
+        their device buffers.  The host synchronises once, at the end.  Needs
+        T0 + max_new_tokens <=
         block_size (beyond it the reference crops the context and recomputes
         positions, which a cache cannot reuse; use generate() then).
         Returns ids (B, T0 + n) and, if asked, the top-2 logit margins (B, n)."""
@@ -419,6 +428,10 @@ class GPT(Module):
         if n < 1:
             return (idx.copy(), np.empty((B, 0))) if return_margins else idx.copy()
         C = self.tok_emb.weight.shape[1]
+        if _PERSISTENT_STEP:
+            out = self._generate_greedy_persistent(idx, n, return_margins, graph)
+            if out is not None:
+                return out
         caches = [(dev.empty((B, Tmax, C)), dev.empty((B, Tmax, C))) for _ in self.blocks]
         ids = dev.empty((Tmax, B), dtype="int64")  # time-major: a step's ids are contiguous
         margins = dev.empty((n, B))
@@ -506,6 +519,101 @@ class GPT(Module):
         out[:, :T0] = idx
         if return_margins:
             return out, margins.t.numpy().T.astype(np.float64)
+        return out
+
+    def _param_ptrs(self):
+        """Device addresses of every parameter and fused q/k/v buffer, and
+        every dropout's mode: a cached decode state built on them is valid
+        while they are unchanged (values may change in place)."""
+        ptrs = [p.data.t.data_ptr() for p in self.parameters()]
+        for blk in self.blocks:
+            if blk.attn._qkv is not None:
+                ptrs += [blk.attn._qkv[0].data.t.data_ptr(), blk.attn._qkv[1].data.t.data_ptr()]
+        drops = [(m._training, m.p) for kind, _, m, _ in self._walk() if kind == "module" and isinstance(m, Dropout)]
+        return tuple(ptrs), tuple(drops)
+
+    def _greedy_state(self, B, T0):
+        """Device state of greedy decoding with the persistent step for (B, T0)
+        prompts, kept between calls (the most recent shape only): caches of
+        block_size rows, the id and margin records, the step's inputs, the
+        DecodeStep and, from the second call on, the prefill recorded as a HIP
+        graph.  None where the persistent step does not apply."""
+        st = self.__dict__.get("_greedy_st")
+        if st is not None and st["key"] == (B, T0) and st["ptrs"] == self._param_ptrs():
+            return st
+        self.__dict__["_greedy_st"] = None  # the previous state (its graph, its buffers) goes first
+        st = None
+        Tm = self.block_size
+        C = self.tok_emb.weight.shape[1]
+        for block in self.blocks:
+            block.attn.fuse_qkv()
+        caches = [(dev.empty((B, Tm, C)), dev.empty((B, Tm, C))) for _ in self.blocks]
+        ds = self._decode_step(caches, B, Tm)
+        if ds is None:
+            return None
+        st = dict(key=(B, T0), ptrs=self._param_ptrs(), caches=caches, ds=ds, graph=None, calls=0,
+                  ids=dev.empty((Tm, B), dtype="int64"), margins=dev.empty((Tm, B)),
+                  prompt=dev.empty((B, T0), dtype="int64"), cur=dev.empty((B,), dtype="int64"),
+                  lengths=dev.empty((B,), dtype="int32"), posd=dev.empty((1,), dtype="int64"),
+                  lengths0=dev.full((B,), T0 + 1, "int32"), posd0=dev.full((1,), T0, "int64"))
+        self.__dict__["_greedy_st"] = st
+        return st
+
+    def _generate_greedy_persistent(self, idx, n, return_margins, graph):
+        """generate_greedy with the persistent decode step and the state of
+        _greedy_state: the prompt is copied into the state's buffer, the
+        prefill (fused q/k/v refreshed, the prompt's forward writing the
+        caches, the first pick, the step inputs reset) runs eagerly on the
+        first call for a shape and replays a recorded HIP graph after that
+        (graph=True), then one launch runs the remaining token steps.  None
+        where the persistent step does not apply."""
+        from . import kernels as K
+
+        B, T0 = idx.shape
+        st = self._greedy_state(B, T0)
+        if st is None:
+            return None
+        pos = self._positions(self.block_size)
+        ids, margins = st["ids"], st["margins"]
+
+        def prefill():
+            for block in self.blocks:
+                block.attn.fuse_qkv()
+            x = self.tok_emb(st["prompt"]) + self.pos_emb(DeviceArray(pos.t[:T0]))
+            for block, cache in zip(self.blocks, st["caches"]):
+                x = block.forward_cached(x, cache, 0, fused=True)
+            x = self.ln_f(Tensor(x.data.t[:, T0 - 1:T0, :]))
+            K.argmax_rows(self.lm_head(x).data.t.view(B, -1), idx=ids.t[T0], margin=margins.t[0])
+            st["cur"].t.copy_(ids.t[T0])
+            st["lengths"].t.copy_(st["lengths0"].t)
+            st["posd"].t.copy_(st["posd0"].t)
+
+        st["prompt"].t.copy_(np.ascontiguousarray(idx, dtype=np.int64))
+        with no_grad():
+            if graph and st["calls"] > 0:
+                if st["graph"] is None:
+                    from .graphs import Graph
+
+                    g = Graph()
+                    with g.capture():
+                        prefill()
+                    st["graph"] = g
+                st["graph"].replay()
+            else:
+                prefill()
+            st["calls"] += 1
+            if n > 1:
+                try:
+                    st["ds"](st["cur"].t, ids.t, st["lengths"].t, st["posd"].t, margins=margins.t, t_base=T0,
+                             steps=n - 1)
+                    st["ds"].check()
+                except Exception:
+                    self.__dict__["_greedy_st"] = None  # a failed step leaves its workspace unusable
+                    raise
+        out = ids.t[:T0 + n].numpy().T.copy()
+        out[:, :T0] = idx
+        if return_margins:
+            return out, margins.t[:n].numpy().T.astype(np.float64)
         return out
 
     def _decode_step(self, caches, B, Tmax):

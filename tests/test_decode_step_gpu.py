@@ -24,6 +24,10 @@ greedy token step, grid-wide barriers between stages) on the GPU.
   * One workspace shared in turn by launches of different grid sizes gives
     the results of workspaces of their own (each launch counts its barriers
     from the base the launch before it left).
+  * generate_greedy's kept state (prefill replayed from a HIP graph from the
+    second call of a shape) gives the oracle's tokens call after call, sees
+    weights changed in place, and is rebuilt for new parameter buffers or a
+    new prompt shape.
 """
 import sys
 
@@ -244,3 +248,43 @@ def test_workspace_shared_across_grid_sizes(dev):
     for B in (5, 17):
         np.testing.assert_array_equal(shared[B][0], own[B][0])
         np.testing.assert_array_equal(shared[B][1], own[B][1])
+
+
+def test_greedy_state_kept_across_calls(dev):
+    """generate_greedy keeps the persistent step's device state for the most
+    recent prompt shape: repeated calls (the prefill eager on the first call,
+    recorded as a HIP graph on the second, replayed after that) give the
+    oracle's tokens for each call's prompts; a weight changed in place is
+    read by the replayed prefill and the step; parameters given new buffers
+    (load_state_dict) or another prompt shape rebuild the state."""
+    from oracle.gpt import GPTConfig, greedy_generate_cached, init_params
+
+    _say("[decode_step] state kept across generate_greedy calls")
+    cfg = GPTConfig(65, 48, 128, 2, 2)
+    B, T0, n = 6, 5, 12
+    model, P = _model(cfg, 51)
+    rng = np.random.default_rng(52)
+
+    def check(P_, B_=B, T0_=T0):
+        prompts = rng.integers(0, cfg.vocab, (B_, T0_))
+        toks, marg = model.generate_greedy(prompts, n, return_margins=True)
+        ref, rmarg = greedy_generate_cached(P_, cfg, prompts, n)
+        np.testing.assert_array_equal(toks, ref)
+        np.testing.assert_allclose(marg, rmarg, rtol=0, atol=1e-4)
+
+    for _ in range(3):
+        check(P)
+    st = model.__dict__["_greedy_st"]
+    assert st is not None and st["graph"] is not None and st["calls"] == 3
+    newb = (rng.standard_normal(cfg.vocab) * 0.5).astype(np.float32)
+    model.lm_head.bias.data.t.copy_(newb)
+    P["lm_head.bias"] = newb
+    check(P)
+    assert model.__dict__["_greedy_st"] is st
+    P2 = init_params(cfg, np.random.default_rng(53))
+    model.load_state_dict(P2)
+    check(P2)
+    st2 = model.__dict__["_greedy_st"]
+    assert st2 is not st and st2["calls"] == 1
+    check(P2, B_=4, T0_=7)
+    assert model.__dict__["_greedy_st"]["key"] == (4, 7)
