@@ -265,10 +265,10 @@ def test_greedy_state_kept_across_calls(dev):
     model, P = _model(cfg, 51)
     rng = np.random.default_rng(52)
 
-    def check(P_, B_=B, T0_=T0):
+    def check(P_, B_=B, T0_=T0, n_=n, graph=True):
         prompts = rng.integers(0, cfg.vocab, (B_, T0_))
-        toks, marg = model.generate_greedy(prompts, n, return_margins=True)
-        ref, rmarg = greedy_generate_cached(P_, cfg, prompts, n)
+        toks, marg = model.generate_greedy(prompts, n_, return_margins=True, graph=graph)
+        ref, rmarg = greedy_generate_cached(P_, cfg, prompts, n_)
         np.testing.assert_array_equal(toks, ref)
         np.testing.assert_allclose(marg, rmarg, rtol=0, atol=1e-4)
 
@@ -288,3 +288,7 @@ def test_greedy_state_kept_across_calls(dev):
     assert st2 is not st and st2["calls"] == 1
     check(P2, B_=4, T0_=7)
     assert model.__dict__["_greedy_st"]["key"] == (4, 7)
+    # one new token (the prefill's pick only, no decode launch), then the
+    # prefill run eagerly on a kept state
+    check(P2, B_=4, T0_=7, n_=1)
+    check(P2, B_=4, T0_=7, graph=False)
