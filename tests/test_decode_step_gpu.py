@@ -5,8 +5,9 @@ greedy token step, grid-wide barriers between stages) on the GPU.
     pinned by the reference's own greedy tokens) and top-2 margins within
     1e-4 of the oracle's, for every kernel instance the models below reach:
     row widths C = 128, 256, 384, 512, logits per lane for V <= 128 and
-    V <= 256, odd batch sizes (a stage-A item with one sequence, a stage-B
-    item with fewer than 8 rows), one to six blocks, and batches with more
+    V <= 256 (V = 256: every lane's four logits in use), odd batch sizes (a
+    stage-A item with one sequence, a stage-B item with fewer than 8 rows;
+    a batch of one), one to six blocks, and batches with more
     stage-A and stage-B items than resident workgroups (C = 128, B = 300;
     C = 384, B = 96; C = 512, B = 72, where fc1's weight slab shares stage
     A's LDS), so that workgroups run several items of a stage and request
@@ -62,6 +63,7 @@ CASES = [
     ((65, 24, 128, 2, 2), 300, 3, 6),
     ((65, 16, 384, 6, 1), 96, 3, 6),
     ((65, 16, 512, 8, 1), 72, 3, 6),
+    ((256, 40, 256, 4, 2), 1, 4, 20),
 ]
 
 
