@@ -498,8 +498,10 @@ int mtx_decode_step_reset(void* workspace, void* stream);
  * workspace of mtx_gemm_workspace_bytes() bytes, long-K products are split
  * over K and reduced deterministically; without one they run unsplit.
  *
- * Products with M >= 128, N >= 128 and M*N*K*batch >= 2^27 run, by default (MTX_GEMM_BF16X3), on
- * the bf16 matrix cores with every fp32 operand value split into three bf16
+ * Products with M >= 128, N >= 128 and M*N*K*batch >= 2^27 run, by default
+ * (MTX_GEMM_BF16X3), on the bf16 matrix cores -- unless they have fewer than
+ * 256 tiles of 128 x 128 and K < 1024; those, like smaller products, take the
+ * fp32 kernel -- with every fp32 operand value split into three bf16
  * pieces (x = x0 + x1 + x2 to 2^-24 |x|) and the six piece products of
  * weight >= 2^-16 accumulated in fp32: a dot product's error is the fp32
  * accumulation error plus at most ~2^-22 sum|a_k b_k|.  Non-finite inputs,

@@ -1154,9 +1154,18 @@ std::atomic<int> g_gemm_mode{MTX_GEMM_BF16X3};
 // of 128 x 128 tiles, latency bound) stay on the fp32 kernel's 64 x 64
 // tiles: on the split kernel the C0 training step took 0.445 ms against
 // 0.379 ms.
+// Nor do products whose 128 x 128 tiles leave part of the 256 CUs idle
+// while K is too short to split (< 1024): at M = 2048 (a prefill over 64
+// prompts of 32 tokens) the fp32 kernel's 64 x 64 tiles took 28.5, 17.3 and
+// 32.0 us for q/k/v (N = 1152), out_proj (N = 384, + residual) and fc1 + GELU
+// (N = 1536), all K = 384, against 36.9, 35.7 and 41.6 us on 144, 48 and 192
+// split-kernel tiles.
 bool use_x3(int M, int N, int K, int batch) {
-  return g_gemm_mode.load(std::memory_order_relaxed) == MTX_GEMM_BF16X3 && M >= 128 && N >= 128 &&
-         (int64_t)M * N * K * batch >= ((int64_t)1 << 27);
+  if (g_gemm_mode.load(std::memory_order_relaxed) != MTX_GEMM_BF16X3 || M < 128 || N < 128 ||
+      (int64_t)M * N * K * batch < ((int64_t)1 << 27))
+    return false;
+  const int64_t tiles = (int64_t)cdiv(M, x3::T) * cdiv(N, x3::T) * batch;
+  return tiles >= 256 || K >= 1024;
 }
 
 // Split K only when the 128 x 128 tiles leave the CUs idle (weight gradients,

@@ -65,7 +65,8 @@ def dot_tol(K):
     (64, 384, 1536, False, False, 1, True),     # skinny, K split over 3 workgroups
     (17, 40, 1000, True, False, 2, True),       # skinny split, scalar A loads, batched
     (64, 64, 4100, False, False, 1, False),     # K past the skinny range: tiled split-K
-    # >= 128 x 128 and >= 2^27 multiply-adds: the bf16-split kernel in its default mode
+    # >= 128 x 128 and >= 2^27 multiply-adds, with K >= 1024 or >= 256 tiles of
+    # 128 x 128: the bf16-split kernel in its default mode
     (256, 384, 1400, False, True, 1, True),     # ragged last k-tile, B contiguous along k
     (300, 260, 1111, True, True, 2, True),      # edge tiles on both sides, both operands transposed
     (4100, 1000, 33, False, False, 1, True),    # row strides of 33: no aligned vector loads
@@ -490,11 +491,14 @@ def test_pack3_unpack3(dev, rows, cols):
             np.testing.assert_array_equal(outs[i].numpy(), expect)
 
 
-@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (512, 1536, 384), (96, 80, 8192), (300, 260, 5000)])
+@pytest.mark.parametrize("M,N,K", [(37, 50, 23), (512, 1536, 384), (2048, 2048, 384), (96, 80, 8192),
+                                   (300, 260, 5000)])
 def test_gemm_gelu_epilogues(dev, gemm_mode, M, N, K):
     """mtx_gemm_act_f32: act 1 = gelu(A@B + bias) with the pre-activation in
     aux, act 2 = (A@B) * gelu'(aux), against NumPy float64 (the K = 8192 case
-    takes the split-K path, whose reduce applies the epilogue)."""
+    takes the split-K path, whose reduce applies the epilogue; 2048 x 2048
+    the split-bf16 kernel's own epilogue in its default mode, 512 x 1536 --
+    48 tiles of 128 x 128 with K < 1024 -- the fp32 kernel in both)."""
 
     from minitorch_amd import kernels as K_
 
@@ -622,7 +626,8 @@ def test_gemm_ln_matches_gemm_then_layernorm(dev, M, N, K):
 
 def test_gemm_nonfinite_and_near_overflow(dev, gemm_mode):
     """Inputs at the edge of the fp32 range, under both product kernels (a
-    512^3 product runs on the bf16-split kernel in its default mode).  Row 0
+    512 x 512 x 1024 product runs on the bf16-split kernel in its default
+    mode, K split four ways).  Row 0
     of A holds 3.4e38 (finite, but above bf16's largest finite value
     3.39e38), row 1 holds +Inf; B's first row is 0.5.  fp32 MFMA: row 0 is
     the finite fp32 result, row 1 is +Inf.  Split mode: both rows are NaN
@@ -631,7 +636,8 @@ def test_gemm_nonfinite_and_near_overflow(dev, gemm_mode):
     from minitorch_amd import kernels as Kn
 
     _say(f"[gemm edge values] {gemm_mode}")
-    M = N = K = 512
+    M = N = 512
+    K = 1024
     rng = np.random.default_rng(99)
     a = 0.1 * rng.standard_normal((M, K), dtype=np.float32)
     b = 0.1 * rng.standard_normal((K, N), dtype=np.float32)
