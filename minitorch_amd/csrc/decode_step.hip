@@ -20,7 +20,8 @@
 //     the cached keys, and the head's share of out_proj (its 64 rows of the
 //     weight) as a partial product per head;
 //   barrier;
-//   stage B, per block, items (8 rows, 64 hidden columns): the residual plus
+//   stage B, per block, items (8 rows, 48 hidden columns at C = 384, else
+//     64): the residual plus
 //     the head partials of out_proj and its bias (written back as the
 //     residual by the first column slab), ln2, fc1 + GELU on the slab (its
 //     weight columns staged in LDS by direct loads while stage A runs), and
@@ -55,7 +56,7 @@ constexpr int kPsMaxC = 512;
 constexpr int kPsMaxH = kPsMaxC / kPsD;
 constexpr int kPsS = 2;          // sequences per stage-A item
 constexpr int kPsR = 8;          // rows per stage-B item
-constexpr int kPsHS = 64;        // hidden columns per stage-B item
+constexpr int kPsHS = 64;        // most hidden columns per stage-B item
 constexpr int kPsMaxT = 1024;    // cache rows (scores of kPsS rows in LDS)
 constexpr int kPsMaxL = 16;
 constexpr int kPsMaxV = 256;
@@ -64,6 +65,12 @@ constexpr int kPsMaxV = 256;
 // waiting workgroup reads one per lane), the launch base (64-bit), the error
 // word
 constexpr int kBarNC = 64;
+// hidden columns per stage-B item: 48 at C = 384 (the MLP width 1536 in 32
+// slabs: with 64 sequences, 8 row groups x 32 slabs = 256 items, one per CU,
+// where 64-column slabs leave 64 CUs idle in stage B), else 64
+template <int C>
+constexpr int ps_hs() { return C == 384 ? 48 : kPsHS; }
+inline int ps_hs_host(int C) { return C == 384 ? 48 : kPsHS; }
 constexpr int kBarCount = 0, kBarBase = 32 * kBarNC, kBarErr = kBarBase + 32, kBarBytes = 4 * (kBarErr + 32);
 
 struct PsArgs {
@@ -108,7 +115,7 @@ struct PsStageA {
   float sc[kPsS][kPsMaxT];
 };
 struct PsStageB {
-  float xs[kPsR][kPsMaxC];
+  float xs[kPsR][kPsMaxC + 4];  // (rows 16 bytes apart in the banks)
   float hs[kPsR][kPsHS];
 };
 struct PsHead {
@@ -120,8 +127,8 @@ union PsSmem {
   PsStageB b;
   PsHead h;
 };
-// Stage B's slab region: fc1's weights [C][64] (filled by direct loads),
-// then the fc1 partial sums [kPsW][kPsR][kPsHS], then the fc2 half sums
+// Stage B's slab region: fc1's weights [C][HS] (filled by direct loads),
+// then the fc1 partial sums [kPsW][kPsR][HS], then the fc2 half sums
 // [2][kPsR][C].  Where it fits beside the union (C <= 384) it has LDS of its
 // own and a workgroup requests its first stage-B slab at the start of stage
 // A; otherwise it lies over stage A's data, after stage B's rows, and the
@@ -129,11 +136,11 @@ union PsSmem {
 template <int C>
 struct PsLds {
   static constexpr int kUnion = (int)(sizeof(PsSmem) / sizeof(float));
-  static constexpr int kSlab = C * kPsHS;
+  static constexpr int kSlab = C * ps_hs<C>();
   static constexpr bool kApart = (kUnion + kSlab) * (int)sizeof(float) <= 160 * 1024 - 256;
   static constexpr int kSlabOff = kApart ? kUnion : (int)(sizeof(PsStageB) / sizeof(float));
   static constexpr int kTotal = kApart ? kUnion + kSlab : (kSlabOff + kSlab > kUnion ? kSlabOff + kSlab : kUnion);
-  static_assert(kPsW * kPsR * kPsHS <= kSlab && 2 * kPsR * C <= kSlab, "partial sums fit the slab region");
+  static_assert(kPsW * kPsR * ps_hs<C>() <= kSlab && 2 * kPsR * C <= kSlab, "partial sums fit the slab region");
   static_assert(kSlabOff % 4 == 0, "16-byte aligned slab");
 };
 
@@ -203,7 +210,7 @@ __device__ __forceinline__ void ps_ln_row(float* __restrict__ row, int lane, con
 // its bias -- (sum + bias) + residual, the grouping of the chain's reduce
 template <int C>
 __device__ __forceinline__ float ps_pending(const PsArgs& a, const float* __restrict__ bias, int b, int n) {
-  constexpr int ns = 4 * C / kPsHS;        // slabs of the MLP width F = 4C
+  constexpr int ns = 4 * C / ps_hs<C>();   // slabs of the MLP width F = 4C
   constexpr int NB = ns <= 24 ? ns : 16;   // loads in flight
   const int64_t stride = (int64_t)a.B * C;
   const unsigned off = (unsigned)(b * C + n);
@@ -584,17 +591,19 @@ __device__ __forceinline__ void ps_attn_item(const PsArgs& a, int l, int item, P
   }
 }
 
-// ---- stage B: (8 rows, 64 hidden columns) ----
-// fc1: wave w sums weight rows [w kc, w kc + kc) for hidden column j0 +
-// lane, the slab staged in LDS; fc2: thread (half, n), n < C, sums the
-// slab's hidden columns [32 half, 32 half + 32) for all 8 rows of column n,
-// and the two halves are added through LDS
-// fc2 weight rows (of a thread's 32) requested before fc1; the rest after it
-// (all 32 before fc1 measured slower, 0.1945 against 0.1937 ms per step)
-constexpr int kPsW2E = 24;
+// ---- stage B: (8 rows, HS = 48 or 64 hidden columns) ----
+// fc1: wave w sums weight rows [w kc, w kc + kc) for the slab's columns, the
+// slab staged in LDS; fc2: thread (half, n), n < C, sums the slab's hidden
+// columns [HS/2 half, HS/2 half + HS/2) for all 8 rows of column n, and the
+// two halves are added through LDS
+// fc2 weight rows (24 of a thread's 32 with 64-column slabs, 18 of 24 with
+// 48) requested before fc1; the rest after it (all 32 before fc1 measured
+// slower, 0.1945 against 0.1937 ms per step)
+template <int C>
+constexpr int ps_w2e() { return ps_hs<C>() == 64 ? 24 : 18; }
 template <int C>
 struct PreB {
-  float w2v[kPsHS / 2];
+  float w2v[ps_hs<C>() / 2];
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -608,20 +617,28 @@ typedef __attribute__((address_space(3))) void lds_void;
 template <int C>
 __device__ __forceinline__ void mlp_dma(const mtx_decode_layer& Ly, int F, int item, float* w1s) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int NI = C / 4, PW = NI / kPsW;
-  static_assert(NI % kPsW == 0, "whole wave loads per wave");
-  const int j0 = (item % (F / kPsHS)) * kPsHS;
+  constexpr int HS = ps_hs<C>();
+  constexpr int RB = HS * (int)sizeof(float);  // bytes per slab row
+  constexpr int NI = C * RB / 1024;            // wave loads of 1 KiB
+  constexpr int PW = (NI + kPsW - 1) / kPsW;
+  static_assert(C * RB % 1024 == 0 && RB % 16 == 0, "whole wave loads, 16-byte pieces within a row");
+  const int j0 = (item % (F / HS)) * HS;
   const int tid = ps_tid();
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bytes = ((C - 1) * F + kPsHS) * (int)sizeof(float);
+  const int bytes = ((C - 1) * F + HS) * (int)sizeof(float);
   const __amdgpu_buffer_rsrc_t rsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Ly.w_fc1 + j0), (short)0, bytes, 0x00020000);
-  const int r = lane >> 4, ch = lane & 15;
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
-    const int ins = w + i * kPsW;
-    const uint32_t voff = (uint32_t)(((4 * ins + r) * F + 4 * ch) * (int)sizeof(float));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(w1s + ins * 4 * kPsHS), 16, voff, 0, 0, 0);
+    const int ins = w + i * kPsW;  // (wave-uniform)
+    if (NI % kPsW == 0 || ins < NI) {
+      // the slab's bytes [1024 ins, 1024 ins + 1024), 16 per lane: row k,
+      // byte cb of the row
+      const int b = 1024 * ins + 16 * lane;
+      const int k = b / RB, cb = b % RB;
+      const uint32_t voff = (uint32_t)(k * F * (int)sizeof(float) + cb);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(w1s + ins * 256), 16, voff, 0, 0, 0);
+    }
   }
 #endif
 }
@@ -629,10 +646,11 @@ __device__ __forceinline__ void mlp_dma(const mtx_decode_layer& Ly, int F, int i
 // fc2's weights of the thread's rows [J0, J1) of its half
 template <int C, int J0, int J1>
 __device__ __forceinline__ void mlp_load2(const mtx_decode_layer& Ly, int F, int item, PreB<C>& p) {
-  const int j0 = (item % (F / kPsHS)) * kPsHS;
+  constexpr int HS = ps_hs<C>();
+  const int j0 = (item % (F / HS)) * HS;
   const int tid = ps_tid();
   if (tid < 2 * C) {
-    const float* __restrict__ wr = Ly.w_fc2 + (int64_t)(j0 + (kPsHS / 2) * (tid / C) + J0) * C;
+    const float* __restrict__ wr = Ly.w_fc2 + (int64_t)(j0 + (HS / 2) * (tid / C) + J0) * C;
     const unsigned n2 = 4u * (unsigned)(tid % C);
 #pragma unroll
     for (int j = J0; j < J1; ++j, wr += C) p.w2v[j] = ld_off<float>(wr, n2);
@@ -642,10 +660,11 @@ __device__ __forceinline__ void mlp_load2(const mtx_decode_layer& Ly, int F, int
 template <int C>
 __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, PsStageB& sm, float* big, bool prefetched) {
   const mtx_decode_layer& Ly = a.L[l];
+  constexpr int HS = ps_hs<C>();
   const int B = a.B, F = a.F;
-  const int ns = F / kPsHS;
+  const int ns = F / HS;
   const int rg = item / ns, sl = item % ns;
-  const int m0 = rg * kPsR, j0 = sl * kPsHS;
+  const int m0 = rg * kPsR, j0 = sl * HS;
   const int tid = ps_tid();
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   constexpr int kc = C / kPsW;
@@ -682,45 +701,81 @@ __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, Ps
   if (w < kPsR) ps_ln_row<C>(sm.xs[w], lane, lp, Ly.ln2_eps);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's slab rows have landed
   __syncthreads();
-  // the first kPsW2E of fc2's weight rows, requested before fc1
-  mlp_load2<C, 0, kPsW2E>(Ly, F, item, pre);
+  // the first of fc2's weight rows, requested before fc1
+  mlp_load2<C, 0, ps_w2e<C>()>(Ly, F, item, pre);
 
   const float* __restrict__ w1s = big;
-  float acc[kPsR];
-#pragma unroll
-  for (int m = 0; m < kPsR; ++m) acc[m] = 0.f;
-  // four weight rows at a time: the row values as one 16-byte broadcast read
-  // per row (terms still added in ascending k)
+  float* __restrict__ part = big;  // [kPsW][kPsR][HS], over the consumed slab
   static_assert(kc % 4 == 0, "whole groups of four weight rows");
+  if constexpr (HS == kPsHS) {
+    // lane = hidden column, all 8 rows; four weight rows at a time, the row
+    // values as one 16-byte broadcast read per row (terms added in
+    // ascending k)
+    float acc[kPsR];
 #pragma unroll
-  for (int i = 0; i < kc; i += 4) {
-    float wv[4];
+    for (int m = 0; m < kPsR; ++m) acc[m] = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) wv[u] = w1s[(k0 + i + u) * kPsHS + lane];
+    for (int i = 0; i < kc; i += 4) {
+      float wv[4];
 #pragma unroll
-    for (int m = 0; m < kPsR; ++m) {
-      const f32x4 x4 = *reinterpret_cast<const f32x4*>(&sm.xs[m][k0 + i]);
+      for (int u = 0; u < 4; ++u) wv[u] = w1s[(k0 + i + u) * HS + lane];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[m] = fmaf(x4[u], wv[u], acc[m]);
+      for (int m = 0; m < kPsR; ++m) {
+        const f32x4 x4 = *reinterpret_cast<const f32x4*>(&sm.xs[m][k0 + i]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[m] = fmaf(x4[u], wv[u], acc[m]);
+      }
+      // keep the scheduler from hoisting every row value's LDS read at once
+      if (i % 8 == 4) __builtin_amdgcn_sched_barrier(0);
     }
-    // keep the scheduler from hoisting every row value's LDS read at once
-    if (i % 8 == 4) __builtin_amdgcn_sched_barrier(0);
-  }
-  float* __restrict__ part = big;  // [kPsW][kPsR][kPsHS], over the consumed slab
-  __syncthreads();  // every wave's slab reads are done
+    __syncthreads();  // every wave's slab reads are done
 #pragma unroll
-  for (int m = 0; m < kPsR; ++m) part[(w * kPsR + m) * kPsHS + lane] = acc[m];
+    for (int m = 0; m < kPsR; ++m) part[(w * kPsR + m) * HS + lane] = acc[m];
+  } else {
+    // 48 columns: lane (cg, rp) takes columns cg, cg + 16, cg + 32 of rows
+    // 2 rp and 2 rp + 1, so that every lane works; per output the terms are
+    // still added in ascending k
+    static_assert(HS == 48 && kPsR == 8, "48 columns = 3 x 16 lanes, 8 rows = 4 x 2");
+    const int cg = lane & 15, rp = lane >> 4;
+    float acc[2][3];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int c = 0; c < 3; ++c) acc[r][c] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kc; i += 4) {
+      float wv[4][3];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) wv[u][c] = w1s[(k0 + i + u) * HS + cg + 16 * c];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const f32x4 x4 = *reinterpret_cast<const f32x4*>(&sm.xs[2 * rp + r][k0 + i]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int c = 0; c < 3; ++c) acc[r][c] = fmaf(x4[u], wv[u][c], acc[r][c]);
+      }
+      if (i % 8 == 4) __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // every wave's slab reads are done
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int c = 0; c < 3; ++c) part[(w * kPsR + 2 * rp + r) * HS + cg + 16 * c] = acc[r][c];
+  }
 
   // the rest of fc2's weights, requested before the fc1 reduce
-  mlp_load2<C, kPsW2E, kPsHS / 2>(Ly, F, item, pre);
+  mlp_load2<C, ps_w2e<C>(), HS / 2>(Ly, F, item, pre);
   const bool fc2_thread = tid < 2 * C;
   const int n2 = tid % C, half = tid / C;
   __syncthreads();
-  if (tid < kPsR * kPsHS) {
-    const int m = tid / kPsHS, j = tid % kPsHS;
+  if (tid < kPsR * HS) {
+    const int m = tid / HS, j = tid % HS;
     float v = 0.f;
 #pragma unroll
-    for (int q = 0; q < kPsW; ++q) v += part[(q * kPsR + m) * kPsHS + j];
+    for (int q = 0; q < kPsW; ++q) v += part[(q * kPsR + m) * HS + j];
     v += Ly.b_fc1[j0 + j];
     sm.hs[m][j] = gelu_tanh(v);
   }
@@ -733,9 +788,9 @@ __device__ __forceinline__ void ps_mlp_item(const PsArgs& a, int l, int item, Ps
     float p2[kPsR];
 #pragma unroll
     for (int m = 0; m < kPsR; ++m) p2[m] = 0.f;
-    const int jb = __builtin_amdgcn_readfirstlane(half) * (kPsHS / 2);
+    const int jb = __builtin_amdgcn_readfirstlane(half) * (HS / 2);
 #pragma unroll
-    for (int j = 0; j < kPsHS / 2; j += 4) {
+    for (int j = 0; j < HS / 2; j += 4) {
 #pragma unroll
       for (int m = 0; m < kPsR; ++m) {
         const f32x4 h4 = *reinterpret_cast<const f32x4*>(&sm.hs[m][jb + j]);
@@ -842,7 +897,7 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
   __syncthreads();
   if (!flag) return;
   const int na = ((a.B + kPsS - 1) / kPsS) * a.H;
-  const int nb = ((a.B + kPsR - 1) / kPsR) * (a.F / kPsHS);
+  const int nb = ((a.B + kPsR - 1) / kPsR) * (a.F / ps_hs<C>());
   const int first = blockIdx.x;
   PreA pa;
   if (first < na) attn_prefetch<C>(a, 0, first, pa);
@@ -906,7 +961,7 @@ PsLayout ps_layout(int B, int C, int H, int F) {
   L.p1 = off;
   off += al256((size_t)H * row);
   L.p2 = off;
-  off += al256((size_t)(F / kPsHS) * row);
+  off += al256((size_t)(F / ps_hs_host(C)) * row);
   L.total = off;
   return L;
 }
@@ -1012,7 +1067,7 @@ extern "C" int mtx_decode_step_f32(const mtx_decode_model* m, int steps, int64_t
   const int ci = C / 128 - 1, vi = V <= 128 ? 0 : 1;
   const int resident = d.per_cu[ci][vi] * d.ncu;
   MTX_CHECK_SHAPE(resident >= 1, "decode_step: the kernel does not fit a compute unit");
-  const int na = ((B + kPsS - 1) / kPsS) * H, nb = ((B + kPsR - 1) / kPsR) * (F / kPsHS);
+  const int na = ((B + kPsS - 1) / kPsS) * H, nb = ((B + kPsR - 1) / kPsR) * (F / ps_hs_host(C));
   const int G = std::min(resident, std::max(std::max(na, nb), B));
 
   char* ws = static_cast<char*>(workspace);
