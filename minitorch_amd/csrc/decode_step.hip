@@ -62,9 +62,14 @@ constexpr int kPsMaxL = 16;
 constexpr int kPsMaxV = 256;
 // barrier words (unsigned), each on its own 128-byte line: kBarNC arrival
 // counters (64-bit; workgroup i adds to counter i mod kBarNC, and wave 0 of a
-// waiting workgroup reads one per lane), the launch base (64-bit), the error
-// word
-constexpr int kBarNC = 64;
+// waiting workgroup reads kBarNC / 64 per lane), the launch base (64-bit),
+// the error word
+#ifndef MTX_DS_BAR_COUNTERS
+#define MTX_DS_BAR_COUNTERS 128
+#endif
+constexpr int kBarNC = MTX_DS_BAR_COUNTERS;
+constexpr int kBarPL = kBarNC / 64;  // counters per polling lane
+static_assert(kBarNC % 64 == 0 && (kBarNC & (kBarNC - 1)) == 0, "whole counters per lane of wave 0");
 // hidden columns per stage-B item: 48 at C = 384 (the MLP width 1536 in 32
 // slabs: with 64 sequences, 8 row groups x 32 slabs = 256 items, one per CU,
 // where 64-column slabs leave 64 CUs idle in stage B), else 64
@@ -231,7 +236,8 @@ __device__ __forceinline__ float ps_pending(const PsArgs& a, const float* __rest
 // Grid-wide barrier over arrival counters that only grow, spread over kBarNC
 // counters on separate lines (with one counter for the whole grid, the
 // arrivals and polls on its one line queued behind each other and each
-// barrier took about 1 us longer).  A launch reads the counters' total at its
+// barrier took about 1 us longer; with 64 counters for 256 workgroups a
+// token step took 2 us longer than with 128).  A launch reads the counters' total at its
 // start from the base word (written by the launch before it, so launches of
 // different grid sizes may share a workspace); its k-th barrier (k = 1, 2,
 // ...) is complete when the total reaches base + k G, and its workgroup 0
@@ -239,8 +245,8 @@ __device__ __forceinline__ float ps_pending(const PsArgs& a, const float* __rest
 // 0) is this workgroup's next target.  Each thread first waits for its own
 // stores (the device-scope stores are acknowledged once they are visible
 // across the device), the workgroup barrier then covers every thread, thread
-// 0 adds to its counter, and wave 0 polls: lane i reads counter i and the
-// lanes sum them (each counter only grows, so a total that reaches the
+// 0 adds to its counter, and wave 0 polls: lane i reads counters i, i + 64,
+// ... and the lanes sum them (each counter only grows, so a total that reaches the
 // target means every arrival happened).  No cache write-back or invalidation
 // is needed, so the L2 caches keep the weights across stages.
 // Arrival and wait are separate so that loads that do not depend on the
@@ -258,11 +264,9 @@ __device__ __forceinline__ void ps_arrive(const PsArgs& a) {
 }
 
 __device__ __forceinline__ bool ps_wait(const PsArgs& a, int* flag, unsigned long long& next) {
-  static_assert(kBarNC <= 64 && (kBarNC & (kBarNC - 1)) == 0, "one counter per lane of wave 0");
   const unsigned long long target = next;
   next += gridDim.x;
-  if (threadIdx.x < kBarNC) {
-    unsigned long long* count = reinterpret_cast<unsigned long long*>(a.bar + kBarCount + 32 * threadIdx.x);
+  if (threadIdx.x < 64) {
     unsigned* err = a.bar + kBarErr;
     int ok = 1;
     const int64_t t0 = wall_clock64();
@@ -270,9 +274,13 @@ __device__ __forceinline__ bool ps_wait(const PsArgs& a, int* flag, unsigned lon
       // (a negative limit fails before the first poll, so that the failure
       // does not depend on how far the other workgroups have come)
       if (a.limit >= 0) {
-        unsigned long long s = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned long long s = 0;
 #pragma unroll
-        for (int o = 1; o < kBarNC; o *= 2) s += __shfl_xor(s, o, 64);
+        for (int c = 0; c < kBarPL; ++c)
+          s += __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.bar + kBarCount + 32 * (threadIdx.x + 64 * c)),
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int o = 1; o < 64; o *= 2) s += __shfl_xor(s, o, 64);
         if (s >= target) break;
       }
       if (a.limit < 0 || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u ||
@@ -884,13 +892,13 @@ __global__ __launch_bounds__(kPsT) void decode_step_kernel(const PsArgs a) {
   static_assert(C % 64 == 0 && C <= kPsMaxC && 2 * C <= kPsT, "row width");
   __shared__ __align__(16) float lds[PsLds<C>::kTotal];
   __shared__ int flag;
-  unsigned long long next = 0;  // threads 0 .. kBarNC-1: the next barrier's target
+  unsigned long long next = 0;  // threads 0 .. 63: the next barrier's target
   PsSmem& sm = *reinterpret_cast<PsSmem*>(lds);
   float* const big = lds + PsLds<C>::kSlabOff;
   // a step after a failed wait on this workspace does nothing
   if (threadIdx.x == 0)
     flag = __hip_atomic_load(a.bar + kBarErr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u;
-  if (threadIdx.x < kBarNC)
+  if (threadIdx.x < 64)
     next = __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.bar + kBarBase), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT) +
            gridDim.x;
