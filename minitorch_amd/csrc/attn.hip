@@ -1032,6 +1032,12 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
                 "the one-pass backward is built for bf16, D <= 64, 4 waves x 32 keys");
   using LS = Lay<T, BQ>;  // dS^T rows: BQ bf16 each, swizzled like the Q/dO tiles
   __shared__ __attribute__((aligned(16))) LT S0[FQ ? BKV * BQ : 1], KS[FQ ? BKV * LD : 1];
+  // bf16 two-pass, D <= 64: each wave's rows of dK, then of dV, staged for
+  // whole-row stores (rows padded by 4 floats; the one-pass and D = 128
+  // kernels would lose their second workgroup per CU to this LDS)
+  constexpr bool GSTAGE = BF && !FQ && D <= 64;
+  constexpr int GLD = D + 4;
+  __shared__ __attribute__((aligned(16))) float GE[GSTAGE ? NWV * NK * 16 * GLD : 1];
 
   const int BH = a.B * a.H;
   const int nkb = (a.Tk + BKV - 1) / BKV;
@@ -1343,14 +1349,47 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
   float* __restrict__ dkp = a.dk + b * a.sdk.b + h * a.sdk.h;
   float* __restrict__ dvp = a.dv + b * a.sdv.b + h * a.sdv.h;
   const bool accf = a.accumulate != 0;
+  if constexpr (GSTAGE) {
+    // A store instruction straight from the accumulators writes 64 bytes of
+    // each of 16 rows, so every 128-byte line reached memory in two
+    // non-temporal pieces (1.41x the gradient bytes written).  The wave's
+    // NK*16 rows go through LDS instead and each instruction writes 4 whole
+    // rows of D floats (16 lanes x 16 bytes per row).
+    static_assert(D % 4 == 0 && 64 % (D / 4) == 0, "whole rows per wave store");
+    constexpr int LPR = D / 4;           // lanes per row
+    constexpr int RPI = 64 / LPR;        // rows per store instruction
+    constexpr int NR = NK * 16;          // the wave's rows
+    float* __restrict__ ge = GE + wid * NR * GLD;
 #pragma unroll
-  for (int ks = 0; ks < NK; ++ks) {
-    const int kj = kw0 + 16 * ks + n;
-    if (kj < a.Tk) {
+    for (int t = 0; t < 2; ++t) {
+      float* __restrict__ dst = t == 0 ? dkp : dvp;
+      const int64_t st = t == 0 ? a.sdk.t : a.sdv.t;
+      __syncthreads();  // (t = 1) every lane's reads of the dK rows are done
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        store_grad4(dkp + (int64_t)kj * a.sdk.t + 16 * dt + 4 * g, dka[ks][dt] * a.scale, accf);
-        store_grad4(dvp + (int64_t)kj * a.sdv.t + 16 * dt + 4 * g, dva[ks][dt], accf);
+      for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          *reinterpret_cast<f32x4*>(ge + (16 * ks + n) * GLD + 16 * dt + 4 * g) =
+              t == 0 ? dka[ks][dt] * a.scale : dva[ks][dt];
+      __syncthreads();
+      const int rl = lane / LPR, c4 = 4 * (lane % LPR);
+#pragma unroll
+      for (int r0 = 0; r0 < NR; r0 += RPI) {
+        const int kj = kw0 + r0 + rl;
+        if (kj < a.Tk)
+          store_grad4(dst + (int64_t)kj * st + c4, *reinterpret_cast<const f32x4*>(ge + (r0 + rl) * GLD + c4), accf);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) {
+      const int kj = kw0 + 16 * ks + n;
+      if (kj < a.Tk) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          store_grad4(dkp + (int64_t)kj * a.sdk.t + 16 * dt + 4 * g, dka[ks][dt] * a.scale, accf);
+          store_grad4(dvp + (int64_t)kj * a.sdv.t + 16 * dt + 4 * g, dva[ks][dt], accf);
+        }
       }
     }
   }
@@ -1609,13 +1648,43 @@ void attn_dq_kernel(const BwdArgs a) {
 
   float* __restrict__ dqp = a.dq + b * a.sdq.b + h * a.sdq.h;
   const bool accf = a.accumulate != 0;
+  if constexpr (BF && D == 64 && kWaves == 4 && NBUF == 2) {
+    // A store instruction straight from the accumulators writes 64 bytes of
+    // each of 16 rows, so every 128-byte line reached memory in two
+    // non-temporal pieces.  Each wave stages its NQ*16 rows of dQ in one of
+    // the four K/V tile buffers, free after the loop (rows of 64 floats, the
+    // 16-byte chunks of row r XOR-permuted by r % 16, so that neither the
+    // staging writes nor the row reads meet in a bank), and each store
+    // instruction writes 4 whole rows.
+    constexpr int NR = NQ * 16;
+    static_assert((int)sizeof(K0) >= NR * D * (int)sizeof(float), "a wave's rows fit one tile buffer");
+    __syncthreads();  // every wave's reads of the K/V tiles are done
+    float* __restrict__ ge = reinterpret_cast<float*>(wid == 0 ? K0 : wid == 1 ? V0 : wid == 2 ? K1 : V1);
 #pragma unroll
-  for (int qs = 0; qs < NQ; ++qs) {
-    const int qi = qw0 + 16 * qs + n;
-    if (qi < a.Tq) {
+    for (int qs = 0; qs < NQ; ++qs) {
+      const int r = 16 * qs + n;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        store_grad4(dqp + (int64_t)qi * a.sdq.t + 16 * dt + 4 * g, acc[qs][dt] * a.scale, accf);
+        *reinterpret_cast<f32x4*>(ge + r * D + 4 * ((4 * dt + g) ^ (r & 15))) = acc[qs][dt] * a.scale;
+    }
+    __syncthreads();
+    const int rl = lane >> 4, c = lane & 15;
+#pragma unroll
+    for (int r0 = 0; r0 < NR; r0 += 4) {
+      const int r = r0 + rl, qi = qw0 + r;
+      if (qi < a.Tq)
+        store_grad4(dqp + (int64_t)qi * a.sdq.t + 4 * c, *reinterpret_cast<const f32x4*>(ge + r * D + 4 * (c ^ (r & 15))),
+                    accf);
+    }
+  } else {
+#pragma unroll
+    for (int qs = 0; qs < NQ; ++qs) {
+      const int qi = qw0 + 16 * qs + n;
+      if (qi < a.Tq) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          store_grad4(dqp + (int64_t)qi * a.sdq.t + 16 * dt + 4 * g, acc[qs][dt] * a.scale, accf);
+      }
     }
   }
 }
