@@ -1033,11 +1033,10 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
   using LS = Lay<T, BQ>;  // dS^T rows: BQ bf16 each, swizzled like the Q/dO tiles
   __shared__ __attribute__((aligned(16))) LT S0[FQ ? BKV * BQ : 1], KS[FQ ? BKV * LD : 1];
   // bf16 two-pass, D <= 64: each wave's rows of dK, then of dV, staged for
-  // whole-row stores (rows padded by 4 floats; the one-pass and D = 128
-  // kernels would lose their second workgroup per CU to this LDS)
+  // whole-row stores (the one-pass and D = 128 kernels would lose their
+  // second workgroup per CU to this LDS)
   constexpr bool GSTAGE = BF && !FQ && D <= 64;
-  constexpr int GLD = D + 4;
-  __shared__ __attribute__((aligned(16))) float GE[GSTAGE ? NWV * NK * 16 * GLD : 1];
+  __shared__ __attribute__((aligned(16))) float GE[GSTAGE ? NWV * NK * 16 * D : 1];
 
   const int BH = a.B * a.H;
   const int nkb = (a.Tk + BKV - 1) / BKV;
@@ -1353,13 +1352,15 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
     // A store instruction straight from the accumulators writes 64 bytes of
     // each of 16 rows, so every 128-byte line reached memory in two
     // non-temporal pieces (1.41x the gradient bytes written).  The wave's
-    // NK*16 rows go through LDS instead and each instruction writes 4 whole
-    // rows of D floats (16 lanes x 16 bytes per row).
+    // NK*16 rows go through LDS instead (the 16-byte chunks of row r
+    // XOR-permuted by r mod D/4, so that at D = 64 neither the staging writes
+    // nor the row reads meet in a bank) and each instruction writes
+    // 64 / (D/4) whole rows of D floats.
     static_assert(D % 4 == 0 && 64 % (D / 4) == 0, "whole rows per wave store");
-    constexpr int LPR = D / 4;           // lanes per row
+    constexpr int LPR = D / 4;           // lanes per row (16-byte chunks per row)
     constexpr int RPI = 64 / LPR;        // rows per store instruction
     constexpr int NR = NK * 16;          // the wave's rows
-    float* __restrict__ ge = GE + wid * NR * GLD;
+    float* __restrict__ ge = GE + wid * NR * D;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       float* __restrict__ dst = t == 0 ? dkp : dvp;
@@ -1369,15 +1370,16 @@ __global__ __launch_bounds__(64 * dkdv_waves<T>(), ((D == 128 && sizeof(T) == 4)
       for (int ks = 0; ks < NK; ++ks)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-          *reinterpret_cast<f32x4*>(ge + (16 * ks + n) * GLD + 16 * dt + 4 * g) =
+          *reinterpret_cast<f32x4*>(ge + (16 * ks + n) * D + 4 * ((4 * dt + g) ^ ((16 * ks + n) % LPR))) =
               t == 0 ? dka[ks][dt] * a.scale : dva[ks][dt];
       __syncthreads();
-      const int rl = lane / LPR, c4 = 4 * (lane % LPR);
+      const int rl = lane / LPR, c = lane % LPR;
 #pragma unroll
       for (int r0 = 0; r0 < NR; r0 += RPI) {
-        const int kj = kw0 + r0 + rl;
+        const int r = r0 + rl, kj = kw0 + r;
         if (kj < a.Tk)
-          store_grad4(dst + (int64_t)kj * st + c4, *reinterpret_cast<const f32x4*>(ge + (r0 + rl) * GLD + c4), accf);
+          store_grad4(dst + (int64_t)kj * st + 4 * c, *reinterpret_cast<const f32x4*>(ge + r * D + 4 * (c ^ (r % LPR))),
+                      accf);
       }
     }
   } else {
